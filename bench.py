@@ -1,0 +1,239 @@
+"""Headline benchmark: INT8 IResNet-50 (ArcFace) faces/s at B=1024 on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 1024]
+
+A step is one forward pass of the whole network (stem .. FC head, one
+captured hipGraph) over a batch of synthetic faces already resident in HBM.
+Prints ONE JSON line.  Besides the headline value it reports the b=1 latency,
+the roofline position of the dominant kernel (the 26 convolutions
+256->256 3x3 s1 at 14x14, timed live with HIP events on the stream they run
+on) and the reference CPU path timed on this host's cores.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import re
+import statistics
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "faces/sec at B=1024 INT8 IResNet-50 (1 GPU); b=1 latency ms; % int8 MFMA peak"
+PEAK_INT8_TOPS = 5000.0          # MI355X dense int8, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def check(lib, rc, what):
+    if rc != 0:
+        import fastface_amd
+        raise RuntimeError("%s failed (%d): %s" % (what, rc, fastface_amd.last_error()))
+
+
+def cpu_baseline(ffw):
+    """The reference's own batched CPU binary (oracle/_ref, built from its
+    sources) on this host: --batch 8, its built-in bench (5 trials x 30
+    passes, best).  Falls back to the C restatement when the host lacks
+    AVX-VNNI (the reference build would SIGILL)."""
+    from oracle.oracle import host_has_avx_vnni
+    cores = min(16, os.cpu_count() or 1)
+    exe = os.path.join(ROOT, "oracle", "_ref", "fastface_int8_batched")
+    env = dict(os.environ, OMP_NUM_THREADS=str(cores), OMP_PROC_BIND="close", OMP_PLACES="cores")
+    if os.path.exists(exe) and host_has_avx_vnni():
+        log("cpu baseline: reference fastface_int8_batched --batch 8, %d threads" % cores)
+        r = subprocess.run([exe, ffw, "--batch", "8", "--threads", str(cores)], cwd=ROOT, env=env,
+                           capture_output=True, text=True, timeout=600)
+        m = re.search(r"Best:\s*([\d.]+) ms/batch = ([\d.]+) ms/face\s*\(([\d.]+) face/s\)", r.stdout)
+        if r.returncode == 0 and m:
+            return {"value": float(m.group(3)), "unit": "faces/s", "cores": cores,
+                    "kind": "reference",
+                    "sample": "reference fastface_int8_batched, B=8 synthetic faces, best of 5x30 "
+                              "passes (%s ms/face); synthetic FFW4 + committed OPSC2" % m.group(2)}
+        log("reference binary failed (rc %d): %s" % (r.returncode, r.stderr[-300:]))
+    from fastface_amd import synth
+    from oracle.oracle import Oracle
+    log("cpu baseline: C restatement (oracle), B=4")
+    orc = Oracle()
+    m = orc.load_model(ffw, synth.OPSC_PATH, synth.OPSC2_PATH)
+    x = synth.faces_uniform(4, 99)
+    t0 = time.perf_counter()
+    orc.forward(m, x)
+    dt = time.perf_counter() - t0
+    orc.free_model(m)
+    return {"value": 4 / dt, "unit": "faces/s", "cores": cores, "kind": "port",
+            "sample": "oracle/ff_oracle.c forward of 4 synthetic faces"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=1024)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-reps", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the path is per-face data "
+              "parallel; multi-GPU sharding is described in DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import fastface_amd
+    from fastface_amd import synth
+
+    lib = fastface_amd.load()
+    if lib.ffk_device_count() <= 0:
+        raise RuntimeError("no HIP device")
+    B, K, W = args.batch, args.steps, args.warmup
+    ffw = synth.synthetic_ffw4_path(3)
+    log("weights %s" % ffw)
+    ff = fastface_amd.FastFace(ffw, cwd=ROOT)
+    check(lib, lib.fastface_reserve(ff.ff, B), "reserve")
+    stream = lib.fastface_stream(ff.ff)
+
+    # inputs resident in HBM before timing (uniform faces)
+    x = synth.faces_uniform(B, 5)
+    d_in = lib.ffk_malloc(x.nbytes)
+    d_out = lib.ffk_malloc(B * 512 * 4)
+    check(lib, lib.ffk_memcpy_h2d(d_in, x.ctypes.data, x.nbytes, stream), "upload")
+    check(lib, lib.ffk_stream_sync(stream), "sync")
+
+    def step():
+        check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, B, d_out, stream), "embed")
+
+    log("warmup %d x B=%d" % (W, B))
+    for _ in range(max(W, 1)):
+        step()
+    check(lib, lib.ffk_stream_sync(stream), "sync")
+    ev0, ev1 = C.c_void_p(), C.c_void_p()
+    check(lib, lib.ffk_event_create(C.byref(ev0)), "event")
+    check(lib, lib.ffk_event_create(C.byref(ev1)), "event")
+    log("timing %d steps" % K)
+    t0 = time.perf_counter()
+    check(lib, lib.ffk_event_record(ev0, stream), "record")
+    for _ in range(K):
+        step()
+    check(lib, lib.ffk_event_record(ev1, stream), "record")
+    check(lib, lib.ffk_stream_sync(stream), "sync")
+    wall = time.perf_counter() - t0
+    ms = C.c_float()
+    check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
+    ms_per_step = ms.value / K
+    faces_per_s = B * K / (ms.value / 1e3)
+    log("%.3f ms/step, %.0f faces/s (wall %.3f s)" % (ms_per_step, faces_per_s, wall))
+    out = np.empty((B, 512), np.float32)
+    check(lib, lib.ffk_memcpy_d2h(out.ctypes.data, d_out, out.nbytes, stream), "download")
+    check(lib, lib.ffk_stream_sync(stream), "sync")
+    assert np.isfinite(out).all()
+
+    # per-launch durations of every step of the chain (events between launches)
+    n_steps = lib.fastface_num_steps(ff.ff)
+    step_ms = np.zeros(n_steps, np.float32)
+    x1 = np.ascontiguousarray(x[:1])
+    e1 = np.empty(512, np.float32)
+    check(lib, lib.fastface_embed_batch(ff.ff, x.ctypes.data, B, out.ctypes.data), "embed host")
+    rc = lib.fastface_profile_steps(ff.ff, B, args.profile_reps, step_ms.ctypes.data)
+    if rc != n_steps:
+        raise RuntimeError("profile_steps failed: %s" % fastface_amd.last_error())
+    info = fastface_amd.fastface_step_info()
+    steps = []
+    for s in range(n_steps):
+        check(lib, lib.fastface_get_step(ff.ff, s, C.byref(info)), "step info")
+        steps.append(dict(kind=info.kind, cin=info.cin, cout=info.cout, k=info.kh, s=info.stride,
+                          hin=info.hin, hout=info.hout, ops=info.ops_per_face,
+                          act=info.act_bytes_per_face, wbytes=info.weight_bytes,
+                          ms=float(step_ms[s])))
+    dom = [st for st in steps if st["kind"] == 1 and st["cin"] == 256 and st["cout"] == 256
+           and st["k"] == 3 and st["s"] == 1]
+    dom_ms = statistics.mean(st["ms"] for st in dom)
+    dom_ops = dom[0]["ops"] * B
+    dom_tops = dom_ops / (dom_ms * 1e-3) / 1e12
+    total_ops = sum(st["ops"] for st in steps) * B
+    chain_tops = total_ops / (ms_per_step * 1e-3) / 1e12
+    fc = [st for st in steps if st["kind"] == 2][0]
+    stages = {}
+    for st in steps:
+        if st["kind"] != 1:
+            continue
+        key = "stage%d" % {112: 1, 56: 1, 28: 2, 14: 3, 7: 4}[st["hout"]] if st["cin"] != 3 else "stem"
+        d = stages.setdefault(key, [0.0, 0.0])
+        d[0] += st["ops"] * B
+        d[1] += st["ms"]
+    stage_util = {k: round(v[0] / (v[1] * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4) for k, v in stages.items()}
+    log("dominant conv 256x256x3x3@14: %.4f ms/launch, %.1f TOP/s (%.1f%% of peak)"
+        % (dom_ms, dom_tops, 100 * dom_tops / PEAK_INT8_TOPS))
+
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "traffic_conv256_b1024.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+
+    # b=1 latency: host buffers in, host buffers out (fastface_embed), and the
+    # device-only chain
+    lat = []
+    for i in range(60):
+        t = time.perf_counter()
+        check(lib, lib.fastface_embed(ff.ff, x1.ctypes.data, e1.ctypes.data), "embed b1")
+        lat.append((time.perf_counter() - t) * 1e3)
+    lat = sorted(lat[10:])
+    b1_ms = statistics.median(lat)
+    check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 1, d_out, stream), "b1 dev")
+    check(lib, lib.ffk_stream_sync(stream), "sync")
+    check(lib, lib.ffk_event_record(ev0, stream), "record")
+    for _ in range(50):
+        check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 1, d_out, stream), "b1 dev")
+    check(lib, lib.ffk_event_record(ev1, stream), "record")
+    check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
+    b1_dev_ms = ms.value / 50
+    log("b=1: %.3f ms host-to-host median, %.3f ms device chain" % (b1_ms, b1_dev_ms))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(ffw)
+        log("cpu baseline: %.1f %s (%s)" % (cpu["value"], cpu["unit"], cpu["kind"]))
+
+    ff.close()
+    rec = {
+        "metric": METRIC,
+        "value": round(faces_per_s, 1),
+        "unit": "faces/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded uniform faces; synthetic FFW4 weights, committed OPSC/OPSC2 scales)",
+        "config": {"workload": "ArcFace IResNet-50 INT8 forward, B=%d (BASELINE config 5), "
+                               "inputs resident in HBM, one hipGraph per step" % B,
+                   "global_batch": B, "input": "112x112x3 fp32 NHWC", "parallelism": "single GPU"},
+        "b1_latency_ms": round(b1_ms, 4),
+        "b1_device_ms": round(b1_dev_ms, 4),
+        "chain_int8_tops": round(chain_tops, 2),
+        "chain_frac_of_int8_peak": round(chain_tops / PEAK_INT8_TOPS, 4),
+        "stage_frac_of_int8_peak": stage_util,
+        "fc_ms": round(fc["ms"], 4),
+        "fc_hbm_gbs": round((fc["wbytes"] + fc["act"] * B) / (fc["ms"] * 1e-3) / 1e9, 1),
+        "roofline": {"bound": "mfma", "kernel": "conv_i8_kernel<256,256,3,1,14,14,128,128>",
+                     "achieved": round(dom_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                     "frac": round(dom_tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
+                     "launch_ms": round(dom_ms, 5), "ops_per_launch": dom_ops},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,78 @@
+"""In-process Python binding of the fastface.h C API.
+
+Mirrors the reference SDK's `FastFace` class (fastface.py:41-162: embed,
+embed_batch, cos_sim, close, context manager) but calls the C library
+directly instead of piping frames to a `--server` subprocess.  Inputs are
+HWC [112, 112, 3] fp32 faces in [-1, 1]; outputs raw (not L2-normalized)
+512-d fp32 embeddings.
+"""
+from __future__ import annotations
+
+import os
+from typing import Sequence
+
+import numpy as np
+
+from . import FASTFACE_INPUT_N, FASTFACE_OUTPUT_N, load
+
+
+class FastFace:
+    def __init__(self, weights: str = "models/w600k_r50_ffw4.bin", batch: int = 1,
+                 cwd: str | None = None):
+        """`cwd`: directory holding models/op_scales.bin (the C API opens it
+        relative to the working directory, like the reference)."""
+        self.lib = load()
+        self.batch = int(batch)
+        old = os.getcwd()
+        if cwd:
+            os.chdir(cwd)
+        try:
+            self.ff = self.lib.fastface_create(os.path.abspath(weights).encode())
+        finally:
+            os.chdir(old)
+        if not self.ff:
+            raise RuntimeError("fastface_create failed for %s" % weights)
+        if self.batch > 1:
+            self.lib.fastface_reserve(self.ff, self.batch)
+
+    def embed(self, arr: np.ndarray) -> np.ndarray:
+        a = np.ascontiguousarray(arr, dtype=np.float32)
+        if a.size != FASTFACE_INPUT_N:
+            raise ValueError("arr must have %d elements, got %d" % (FASTFACE_INPUT_N, a.size))
+        out = np.empty(FASTFACE_OUTPUT_N, np.float32)
+        rc = self.lib.fastface_embed(self.ff, a.ctypes.data, out.ctypes.data)
+        if rc != 0:
+            raise RuntimeError("fastface_embed failed (%d)" % rc)
+        return out
+
+    def embed_batch(self, arrs: Sequence[np.ndarray] | np.ndarray) -> np.ndarray:
+        a = np.ascontiguousarray(np.asarray(arrs, dtype=np.float32))
+        b = a.size // FASTFACE_INPUT_N
+        if a.size != b * FASTFACE_INPUT_N:
+            raise ValueError("input is not a whole number of faces")
+        out = np.empty((b, FASTFACE_OUTPUT_N), np.float32)
+        rc = self.lib.fastface_embed_batch(self.ff, a.ctypes.data, b, out.ctypes.data)
+        if rc != 0:
+            raise RuntimeError("fastface_embed_batch failed (%d)" % rc)
+        return out
+
+    @staticmethod
+    def cos_sim(a: np.ndarray, b: np.ndarray) -> float:
+        return float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+    def close(self):
+        if getattr(self, "ff", None):
+            self.lib.fastface_destroy(self.ff)
+            self.ff = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

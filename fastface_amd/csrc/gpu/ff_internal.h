@@ -1,0 +1,25 @@
+// ff_internal.h -- shared between the HIP translation units (not exported).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../../include/fastface_kernels.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+void ffk_set_error(const char* fmt, const char* a, const char* b);
+int ffk_hip_fail(hipError_t e, const char* what);
+
+// Launch-time check: a kernel launch error (bad configuration) is reported
+// right away instead of surfacing at the next synchronization.
+static inline int ffk_check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? FFK_OK : ffk_hip_fail(e, what);
+}
+
+// Packed weight layout shared by every int8 MFMA kernel: the reduction index
+// k = (kh*KW + kw)*Cin + ci is cut into steps of 64; step s of output channel
+// n lives at  w[(s*Cout + n)*64 .. +64).  One K step of a whole output-channel
+// tile is therefore one contiguous block of BN*64 bytes.
+static constexpr int FF_KSTEP = 64;

@@ -1,0 +1,384 @@
+/* fastface.c -- the fastface.h C API on MI355X.
+ *
+ * create (reference libfastface.c:231-310): load FFW + OPSC/OPSC2, build the
+ * fused launch plan, pack all weights into one device arena and all
+ * per-channel parameters into another (two uploads), create the stream.
+ * embed (libfastface.c:312-470): copy the faces in, replay the captured
+ * launch chain for this batch size (one hipGraph per batch size, built on
+ * first use over preallocated activation buffers), copy the embeddings out.
+ * destroy (libfastface.c:472-490): free everything, including what the
+ * reference leaks (the mapping and the scale arrays).
+ *
+ * Errors: NULL from create, non-zero from embed -- never an abort.  A HIP
+ * failure message goes to stderr once, prefixed "fastface:".
+ */
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "ff_host.h"
+
+#define FF_MAX_GRAPHS 16
+
+typedef struct { int batch; void* exec; } GraphEntry;
+
+struct FastFace {
+    FfModel model;
+    FfPlan plan;
+    void* stream;
+    int8_t* d_weights;
+    float* d_params;
+    float* d_in_inv;
+    int capacity;               /* faces the activation buffers hold */
+    int8_t** d_bufs;            /* plan.n_buffers buffers */
+    float* d_input;             /* capacity * 37632 */
+    float* d_output;            /* capacity * 512 */
+    ffk_io* d_io;               /* device I/O descriptor */
+    ffk_io* h_io;               /* pinned staging */
+    ffk_io io_cur;              /* what d_io holds now */
+    int keep_all;
+    GraphEntry graphs[FF_MAX_GRAPHS];
+    int n_graphs, graph_rr;
+};
+
+static void report(const char* what, int rc)
+{
+    fprintf(stderr, "fastface: %s failed (%d): %s\n", what, rc, ffk_last_error());
+}
+
+static void drop_graphs(FastFace* ff)
+{
+    for (int i = 0; i < ff->n_graphs; i++) ffk_graph_destroy(ff->graphs[i].exec);
+    ff->n_graphs = 0;
+    ff->graph_rr = 0;
+}
+
+static void free_activations(FastFace* ff)
+{
+    drop_graphs(ff);
+    if (ff->d_bufs) {
+        for (int i = 0; i < ff->plan.n_buffers; i++) ffk_free(ff->d_bufs[i]);
+        free(ff->d_bufs);
+        ff->d_bufs = NULL;
+    }
+    ffk_free(ff->d_input); ff->d_input = NULL;
+    ffk_free(ff->d_output); ff->d_output = NULL;
+    ff->capacity = 0;
+}
+
+static int set_io(FastFace* ff, const float* in, float* out, void* stream)
+{
+    if (ff->io_cur.in == in && ff->io_cur.out == out) return 0;
+    /* the staging slot may still feed an earlier copy: drain first */
+    int rc = ffk_stream_sync(ff->stream);
+    if (!rc && stream != ff->stream) rc = ffk_stream_sync(stream);
+    if (rc) return rc;
+    ff->h_io->in = in;
+    ff->h_io->out = out;
+    rc = ffk_memcpy_h2d(ff->d_io, ff->h_io, sizeof(ffk_io), stream);
+    if (!rc) rc = ffk_stream_sync(stream);
+    if (rc) return rc;
+    ff->io_cur = *ff->h_io;
+    return 0;
+}
+
+static int ensure_capacity(FastFace* ff, int batch)
+{
+    if (batch <= ff->capacity) return 0;
+    int rc = ffk_stream_sync(ff->stream);
+    if (rc) return rc;
+    free_activations(ff);
+    FfPlan* p = &ff->plan;
+    ff->d_bufs = (int8_t**)calloc((size_t)p->n_buffers, sizeof(int8_t*));
+    if (!ff->d_bufs) return FFK_ERR_NOMEM;
+    const size_t buf_bytes = p->max_face_bytes * (size_t)batch + 256;
+    for (int i = 0; i < p->n_buffers; i++) {
+        ff->d_bufs[i] = (int8_t*)ffk_malloc(buf_bytes);
+        if (!ff->d_bufs[i]) { free_activations(ff); return FFK_ERR_NOMEM; }
+    }
+    ff->d_input = (float*)ffk_malloc((size_t)batch * FASTFACE_INPUT_N * sizeof(float));
+    ff->d_output = (float*)ffk_malloc((size_t)batch * FASTFACE_OUTPUT_N * sizeof(float));
+    if (!ff->d_input || !ff->d_output) { free_activations(ff); return FFK_ERR_NOMEM; }
+    ff->capacity = batch;
+    ff->io_cur.in = NULL; ff->io_cur.out = NULL;
+    return 0;
+}
+
+static int8_t* tensor_ptr(FastFace* ff, int t)
+{
+    if (t < 0) return NULL;
+    int b = ff->plan.tensors[t].buf;
+    return b >= 0 ? ff->d_bufs[b] : NULL;
+}
+
+static int launch_step(FastFace* ff, int s, int batch, void* stream)
+{
+    const FfStep* st = &ff->plan.steps[s];
+    if (st->kind == 1) {
+        ffk_conv_desc d;
+        memset(&d, 0, sizeof d);
+        d.batch = batch; d.cin = st->cin; d.cout = st->cout; d.kh = st->kh; d.kw = st->kw;
+        d.stride = st->stride; d.pad = st->pad; d.hin = st->hin; d.win = st->win;
+        if (st->t_in == FF_T_INPUT) {
+            d.in = NULL;
+            d.io = ff->d_io;
+            d.in_inv = ff->d_in_inv;
+        } else {
+            d.in = tensor_ptr(ff, st->t_in);
+        }
+        d.w = ff->d_weights + st->w_off;
+        d.params = ff->d_params + st->p_off;
+        d.add_src = tensor_ptr(ff, st->t_add);
+        d.out = tensor_ptr(ff, st->t_out);
+        d.out_bn = tensor_ptr(ff, st->t_bn);
+        d.flags = st->flags;
+        d.in_scale = st->in_scale;
+        return ffk_conv(&d, stream);
+    }
+    ffk_fc_desc f;
+    memset(&f, 0, sizeof f);
+    f.batch = batch; f.n = st->fc_n; f.k = st->fc_k;
+    f.a = tensor_ptr(ff, st->t_in);
+    f.w = ff->d_weights + st->w_off;
+    f.ws = ff->d_params + st->ws_off;
+    f.bias = ff->d_params + st->bias_off;
+    f.a_scale = st->a_scale;
+    f.out = NULL;
+    f.io = ff->d_io;
+    f.path = 0;
+    return ffk_fc(&f, stream);
+}
+
+static int run_direct(FastFace* ff, int batch, void* stream)
+{
+    for (int s = 0; s < ff->plan.n_steps; s++) {
+        int rc = launch_step(ff, s, batch, stream);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+static void* graph_for(FastFace* ff, int batch)
+{
+    for (int i = 0; i < ff->n_graphs; i++)
+        if (ff->graphs[i].batch == batch) return ff->graphs[i].exec;
+    if (ffk_graph_begin(ff->stream)) return NULL;
+    int rc = run_direct(ff, batch, ff->stream);
+    void* exec = NULL;
+    int rc2 = ffk_graph_end(ff->stream, &exec);
+    if (rc || rc2) { if (exec) ffk_graph_destroy(exec); return NULL; }
+    int slot;
+    if (ff->n_graphs < FF_MAX_GRAPHS) slot = ff->n_graphs++;
+    else { slot = ff->graph_rr; ff->graph_rr = (ff->graph_rr + 1) % FF_MAX_GRAPHS;
+           ffk_graph_destroy(ff->graphs[slot].exec); }
+    ff->graphs[slot].batch = batch;
+    ff->graphs[slot].exec = exec;
+    return exec;
+}
+
+/* enqueue one batch whose I/O pointers are already in d_io */
+static int enqueue(FastFace* ff, int batch, void* stream)
+{
+    if (ff->keep_all) return run_direct(ff, batch, stream);
+    void* g = graph_for(ff, batch);
+    if (!g) return FFK_ERR_HIP;
+    return ffk_graph_launch(g, stream);
+}
+
+FastFace* fastface_create(const char* ffw4_path)
+{
+    if (!ffw4_path) return NULL;
+    if (ffk_device_count() <= 0) {
+        fprintf(stderr, "fastface: no HIP device\n");
+        return NULL;
+    }
+    FastFace* ff = (FastFace*)calloc(1, sizeof(FastFace));
+    if (!ff) return NULL;
+    const char* v2 = getenv("OPSC2_PATH");
+    if (!v2) v2 = "models/op_scales_v2.bin";
+    if (ff_model_load(&ff->model, ffw4_path, "models/op_scales.bin", v2) != 0) {
+        free(ff);
+        return NULL;
+    }
+    if (ff_plan_build(&ff->model, &ff->plan) != 0) {
+        fprintf(stderr, "fastface: unsupported model: %s\n", ff->plan.err);
+        goto fail;
+    }
+    ff_plan_assign_buffers(&ff->plan, 0);
+    if (ffk_stream_create(&ff->stream)) { report("stream", FFK_ERR_HIP); goto fail; }
+    ff->d_weights = (int8_t*)ffk_malloc(ff->plan.w_bytes);
+    ff->d_params = (float*)ffk_malloc(ff->plan.p_floats * sizeof(float));
+    ff->d_in_inv = (float*)ffk_malloc(4 * sizeof(float));
+    ff->d_io = (ffk_io*)ffk_malloc(sizeof(ffk_io));
+    ff->h_io = (ffk_io*)ffk_host_alloc(sizeof(ffk_io));
+    if (!ff->d_weights || !ff->d_params || !ff->d_in_inv || !ff->d_io || !ff->h_io) {
+        report("device allocation", FFK_ERR_NOMEM);
+        goto fail;
+    }
+    if (ffk_memcpy_h2d(ff->d_weights, ff->plan.w_host, ff->plan.w_bytes, ff->stream) ||
+        ffk_memcpy_h2d(ff->d_params, ff->plan.p_host, ff->plan.p_floats * sizeof(float), ff->stream) ||
+        ffk_memcpy_h2d(ff->d_in_inv, ff->plan.in_inv, 4 * sizeof(float), ff->stream) ||
+        ffk_stream_sync(ff->stream)) {
+        report("weight upload", FFK_ERR_HIP);
+        goto fail;
+    }
+    /* host copies of the packed weights are no longer needed */
+    free(ff->plan.w_host); ff->plan.w_host = NULL;
+    {
+        const char* e = getenv("FASTFACE_MAX_BATCH");
+        int reserve = e ? atoi(e) : 1;
+        if (reserve < 1) reserve = 1;
+        if (ensure_capacity(ff, reserve)) { report("activation allocation", FFK_ERR_NOMEM); goto fail; }
+    }
+    return ff;
+fail:
+    fastface_destroy(ff);
+    return NULL;
+}
+
+void fastface_destroy(FastFace* ff)
+{
+    if (!ff) return;
+    if (ff->stream) ffk_stream_sync(ff->stream);
+    free_activations(ff);
+    ffk_free(ff->d_weights);
+    ffk_free(ff->d_params);
+    ffk_free(ff->d_in_inv);
+    ffk_free(ff->d_io);
+    ffk_host_free(ff->h_io);
+    if (ff->stream) ffk_stream_destroy(ff->stream);
+    ff_plan_free(&ff->plan);
+    ff_model_free(&ff->model);
+    free(ff);
+}
+
+int fastface_reserve(FastFace* ff, int max_batch)
+{
+    if (!ff || max_batch < 1) return -1;
+    return ensure_capacity(ff, max_batch) ? -2 : 0;
+}
+
+void* fastface_stream(FastFace* ff) { return ff ? ff->stream : NULL; }
+
+int fastface_embed_batch(FastFace* ff, const float* in, int batch, float* out)
+{
+    if (!ff || !in || !out || batch < 0) return -1;
+    if (batch == 0) return 0;
+    int rc = ensure_capacity(ff, batch);
+    if (rc) { report("activation allocation", rc); return -2; }
+    rc = set_io(ff, ff->d_input, ff->d_output, ff->stream);
+    if (!rc) rc = ffk_memcpy_h2d(ff->d_input, in, (size_t)batch * FASTFACE_INPUT_N * sizeof(float), ff->stream);
+    if (!rc) rc = enqueue(ff, batch, ff->stream);
+    if (!rc) rc = ffk_memcpy_d2h(out, ff->d_output, (size_t)batch * FASTFACE_OUTPUT_N * sizeof(float), ff->stream);
+    if (!rc) rc = ffk_stream_sync(ff->stream);
+    if (rc) { report("embed", rc); return -3; }
+    return 0;
+}
+
+int fastface_embed(FastFace* ff, const float* input_hwc, float* out_emb)
+{
+    if (!ff || !input_hwc || !out_emb) return -1;
+    return fastface_embed_batch(ff, input_hwc, 1, out_emb);
+}
+
+int fastface_embed_batch_device(FastFace* ff, const float* d_in, int batch, float* d_out, void* stream)
+{
+    if (!ff || !d_in || !d_out || batch < 0) return -1;
+    if (batch == 0) return 0;
+    if (!stream) stream = ff->stream;
+    int rc = ensure_capacity(ff, batch);
+    if (rc) { report("activation allocation", rc); return -2; }
+    rc = set_io(ff, d_in, d_out, stream);
+    if (!rc) rc = enqueue(ff, batch, stream);
+    if (rc) { report("embed_batch_device", rc); return -3; }
+    return 0;
+}
+
+int fastface_num_steps(const FastFace* ff) { return ff ? ff->plan.n_steps : -1; }
+
+int fastface_get_step(const FastFace* ff, int s, fastface_step_info* info)
+{
+    if (!ff || !info || s < 0 || s >= ff->plan.n_steps) return -1;
+    const FfStep* st = &ff->plan.steps[s];
+    memset(info, 0, sizeof *info);
+    info->kind = st->kind;
+    info->op_first = st->op_first;
+    info->op_last = st->op_last;
+    if (st->kind == 1) {
+        info->cin = st->cin; info->cout = st->cout; info->kh = st->kh; info->kw = st->kw;
+        info->stride = st->stride; info->pad = st->pad; info->hin = st->hin; info->win = st->win;
+        info->hout = st->hout; info->wout = st->wout; info->flags = st->flags;
+        info->stores_x = st->t_out >= 0;
+        const double pix_out = (double)st->hout * st->wout;
+        info->ops_per_face = 2.0 * pix_out * st->cout * st->kh * st->kw * st->cin;
+        /* distinct input pixels a kernel must read */
+        double pix_in = (st->kh == 1) ? pix_out : (double)st->hin * st->win;
+        double in_bytes = pix_in * st->cin * (st->cin == 3 ? 4.0 : 1.0);
+        double out_b = pix_out * st->cout;
+        info->act_bytes_per_face = in_bytes + out_b * ((st->t_out >= 0) + (st->t_bn >= 0) + (st->t_add >= 0));
+        info->weight_bytes = (double)ffk_conv_packed_bytes(st->cin, st->cout, st->kh, st->kw);
+    } else {
+        info->cin = st->fc_k; info->cout = st->fc_n; info->kh = info->kw = 1; info->stride = 1;
+        info->hin = info->win = info->hout = info->wout = 1;
+        info->ops_per_face = 2.0 * st->fc_k * st->fc_n;
+        info->act_bytes_per_face = st->fc_k + 4.0 * st->fc_n;
+        info->weight_bytes = (double)st->fc_k * st->fc_n;
+    }
+    return 0;
+}
+
+int fastface_profile_steps(FastFace* ff, int batch, int reps, float* step_ms)
+{
+    if (!ff || !step_ms || batch < 1 || reps < 1) return -1;
+    int rc = ensure_capacity(ff, batch);
+    if (!rc) rc = set_io(ff, ff->d_input, ff->d_output, ff->stream);
+    if (rc) return -2;
+    const int n = ff->plan.n_steps;
+    void** ev = (void**)calloc((size_t)n + 1, sizeof(void*));
+    for (int s = 0; s <= n && !rc; s++) rc = ffk_event_create(&ev[s]);
+    for (int s = 0; s < n; s++) step_ms[s] = 0.0f;
+    for (int r = 0; r < reps && !rc; r++) {
+        for (int s = 0; s < n && !rc; s++) {
+            rc = ffk_event_record(ev[s], ff->stream);
+            if (!rc) rc = launch_step(ff, s, batch, ff->stream);
+        }
+        if (!rc) rc = ffk_event_record(ev[n], ff->stream);
+        if (!rc) rc = ffk_stream_sync(ff->stream);
+        for (int s = 0; s < n && !rc; s++) {
+            float ms = 0.0f;
+            rc = ffk_event_elapsed_ms(ev[s], ev[s + 1], &ms);
+            step_ms[s] += ms / (float)reps;
+        }
+    }
+    for (int s = 0; s <= n; s++) if (ev[s]) ffk_event_destroy(ev[s]);
+    free(ev);
+    if (rc) { report("profile", rc); return -3; }
+    return n;
+}
+
+int fastface_debug_keep_tensors(FastFace* ff, int on)
+{
+    if (!ff) return -1;
+    int rc = ffk_stream_sync(ff->stream);
+    if (rc) return -3;
+    int cap = ff->capacity;
+    free_activations(ff);
+    ff->keep_all = on ? 1 : 0;
+    ff_plan_assign_buffers(&ff->plan, ff->keep_all);
+    return ensure_capacity(ff, cap > 0 ? cap : 1) ? -2 : 0;
+}
+
+long long fastface_debug_read(FastFace* ff, int op_idx, int batch, void* host, size_t bytes)
+{
+    if (!ff || !host || batch < 1 || batch > ff->capacity) return -1;
+    for (int t = ff->plan.n_tensors - 1; t > 0; t--) {
+        const FfTensor* T = &ff->plan.tensors[t];
+        if (T->op != op_idx || T->buf < 0) continue;
+        size_t n = (size_t)T->C * T->H * T->W * (size_t)batch;
+        if (n > bytes) return -4;
+        if (ffk_memcpy_d2h(host, ff->d_bufs[T->buf], n, ff->stream) || ffk_stream_sync(ff->stream))
+            return -3;
+        return (long long)n;
+    }
+    return -5;
+}

@@ -1,0 +1,373 @@
+/* ff_plan.c -- turn the FFW op list into a fused launch plan, once.
+ *
+ * The reference re-interprets the op list on every embed
+ * (libfastface.c:312-470; batched: arcface_forward_int8_batched.c:339-516):
+ * Conv looks ahead to fuse the next PReLU or Add (:370-382), per-channel
+ * forward/inverse scales are tracked op by op (:383-396, :402-411), BN
+ * requantizes in place (:401-413), BLOCK_START / SAVE_ID copy the current
+ * activation into the block buffer / one of 24 identity slots (:425-440),
+ * and FLATTEN transposes NHWC to NCHW before the FC (:456-464).
+ *
+ * Here the same walk runs once at create time over immutable tensors:
+ *   - every CONV (+PReLU | +Add) becomes one kernel launch;
+ *   - a BN that follows it (through SAVE_ID / BLOCK_START) becomes a second
+ *     output of that launch (the pre-BN tensor is still stored when the
+ *     identity slot or the block buffer refers to it);
+ *   - SAVE_ID / BLOCK_START become tensor references (no copies);
+ *   - FLATTEN disappears: the FC weight columns are permuted from the
+ *     reference's NCHW order (c*HW + hw) to NHWC (hw*C + c); the int32 dot
+ *     product is order-independent, so results are unchanged;
+ *   - every scalar fallback of the reference (no OPSC2 entry, length
+ *     mismatch) is resolved into explicit per-channel parameter rows,
+ *     computed in fp32 exactly as the reference computes them.
+ * Op sequences outside this pattern are rejected (create fails) instead of
+ * being run some other way.
+ */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "ff_host.h"
+
+typedef struct {
+    FfPlan* p;
+    size_t w_cap, p_cap;
+    int s_cap, t_cap;
+} Builder;
+
+static int fail(FfPlan* p, const char* msg, int op)
+{
+    snprintf(p->err, sizeof p->err, "%s (op %d)", msg, op);
+    return -1;
+}
+
+static int new_tensor(Builder* b, int C, int H, int W, int op)
+{
+    FfPlan* p = b->p;
+    if (p->n_tensors == b->t_cap) {
+        b->t_cap = b->t_cap ? 2 * b->t_cap : 64;
+        p->tensors = (FfTensor*)realloc(p->tensors, (size_t)b->t_cap * sizeof(FfTensor));
+    }
+    FfTensor* t = &p->tensors[p->n_tensors];
+    t->C = C; t->H = H; t->W = W; t->def_step = p->n_steps; t->last_use = -1; t->buf = -1;
+    t->op = op;
+    return p->n_tensors++;
+}
+
+static FfStep* new_step(Builder* b)
+{
+    FfPlan* p = b->p;
+    if (p->n_steps == b->s_cap) {
+        b->s_cap = b->s_cap ? 2 * b->s_cap : 64;
+        p->steps = (FfStep*)realloc(p->steps, (size_t)b->s_cap * sizeof(FfStep));
+    }
+    FfStep* s = &p->steps[p->n_steps++];
+    memset(s, 0, sizeof *s);
+    s->t_in = s->t_add = s->t_out = s->t_bn = s->t_x = -1;
+    return s;
+}
+
+static size_t alloc_params(Builder* b, size_t n)
+{
+    FfPlan* p = b->p;
+    size_t off = (p->p_floats + 63) & ~(size_t)63;     /* 256-byte aligned rows */
+    if (off + n > b->p_cap) {
+        while (off + n > b->p_cap) b->p_cap = b->p_cap ? 2 * b->p_cap : 65536;
+        p->p_host = (float*)realloc(p->p_host, b->p_cap * sizeof(float));
+    }
+    memset(p->p_host + p->p_floats, 0, (off + n - p->p_floats) * sizeof(float));
+    p->p_floats = off + n;
+    return off;
+}
+
+static size_t alloc_weights(Builder* b, size_t n)
+{
+    FfPlan* p = b->p;
+    size_t off = (p->w_bytes + 255) & ~(size_t)255;
+    if (off + n > b->w_cap) {
+        while (off + n > b->w_cap) b->w_cap = b->w_cap ? 2 * b->w_cap : ((size_t)1 << 24);
+        p->w_host = (int8_t*)realloc(p->w_host, b->w_cap);
+    }
+    p->w_bytes = off + n;
+    return off;
+}
+
+static void fill_row(float* row, int n, const uint8_t* src, float scalar)
+{
+    for (int i = 0; i < n; i++) row[i] = src ? ff_read_f32(src, i) : scalar;
+}
+static void fill_rowf(float* row, int n, const float* src, float scalar)
+{
+    for (int i = 0; i < n; i++) row[i] = src ? src[i] : scalar;
+}
+
+/* inverse of a scalar scale the way the reference forms it
+ * (int8_epilogue.c:39,122,262: 1.0f / (out_scale + 1e-9f)) */
+static float inv_of(float s)
+{
+    volatile float t = s + 1e-9f;
+    return 1.0f / t;
+}
+
+typedef struct { int C, H, W; } Shp;
+
+int ff_plan_build(const FfModel* m, FfPlan* p)
+{
+    memset(p, 0, sizeof *p);
+    Builder B = { p, 0, 0, 0, 0 };
+    const int n = m->n_ops;
+    const int v4 = m->version >= 4;
+    const int pc = v4 && m->has_v2;
+
+    /* input quantization (libfastface.c:335-338): per-channel for FFW4+OPSC2 */
+    for (int c = 0; c < 3; c++)
+        p->in_inv[c] = (pc && m->n_in >= 3) ? m->in_inv_pc[c] : inv_of(m->input_scale);
+    if (pc && m->n_in < 3) return fail(p, "OPSC2 input scales need 3 channels", -1);
+    new_tensor(&B, 3, 112, 112, -1);             /* FF_T_INPUT */
+
+    /* shortcut + shape pre-pass (libfastface.c:243-269) */
+    uint8_t* is_sc = (uint8_t*)calloc((size_t)n, 1);
+    Shp* sh_in = (Shp*)calloc((size_t)n, sizeof(Shp));
+    Shp* sh_out = (Shp*)calloc((size_t)n, sizeof(Shp));
+    for (int i = 1; i < n; i++)
+        if (m->ops[i].type == FF_OP_CONV && m->ops[i - 1].type == FF_OP_SAVE_ID) is_sc[i] = 1;
+    Shp cur = {3, 112, 112}, blk = cur;
+    for (int i = 0; i < n; i++) {
+        const FfOp* op = &m->ops[i];
+        Shp s = is_sc[i] ? blk : cur;
+        sh_in[i] = s;
+        if (op->type == FF_OP_CONV) {
+            if (op->stride <= 0) { free(is_sc); free(sh_in); free(sh_out); return fail(p, "bad stride", i); }
+            cur.C = op->Cout;
+            cur.H = (s.H + 2 * op->pad - op->Kh) / op->stride + 1;
+            cur.W = (s.W + 2 * op->pad - op->Kw) / op->stride + 1;
+        } else if (op->type == FF_OP_GEMM) {
+            cur.C = (int)op->N; cur.H = 1; cur.W = 1;
+        }
+        sh_out[i] = cur;
+        if (op->type == FF_OP_BLOCK_START) blk = cur;
+    }
+
+    int rc = 0;
+    int A = FF_T_INPUT;
+    float A_scale = m->input_scale;
+    const float* A_pc = pc ? m->in_scale_pc : NULL;
+    int blk_t = FF_T_INPUT;
+    float blk_scale = m->input_scale;
+    int slot_t[24]; float slot_scale[24]; const float* slot_pc[24];
+    for (int k = 0; k < 24; k++) { slot_t[k] = -1; slot_scale[k] = 0.0f; slot_pc[k] = NULL; }
+    int save_idx = 0, add_idx = 0;
+    int last_conv = -1;         /* step whose output A currently is */
+    int flat = 0, done = 0;
+
+    for (int i = 0; i < n && !rc; i++) {
+        const FfOp* op = &m->ops[i];
+        float next_scale = m->scales[i];
+        if (next_scale <= 0) next_scale = A_scale;
+        if (done) { rc = fail(p, "ops after the GEMM are not supported", i); break; }
+        switch (op->type) {
+        case FF_OP_CONV: {
+            const int in_t = is_sc[i] ? blk_t : A;
+            const float in_scale = v4 ? 1.0f : (is_sc[i] ? blk_scale : A_scale);
+            const Shp si = sh_in[i], so = sh_out[i];
+            if (op->Cin != si.C) { rc = fail(p, "conv Cin does not match its input", i); break; }
+            if ((in_t == FF_T_INPUT) != (op->Cin == 3)) {
+                rc = fail(p, "only a 3-channel stem conv may read the input faces", i); break;
+            }
+            if (!ffk_conv_supported(op->Cin, op->Cout, op->Kh, op->Kw, op->stride, op->pad, si.H, si.W)) {
+                rc = fail(p, "no kernel for this conv geometry", i); break;
+            }
+            const uint8_t* slope = NULL;
+            int add_k = -1, eff = i, skip = 0;
+            float eff_scale = next_scale;
+            if (i + 1 < n && m->ops[i + 1].type == FF_OP_PRELU) {
+                if (m->ops[i + 1].prelu_size != op->Cout) { rc = fail(p, "PReLU size != Cout", i + 1); break; }
+                slope = m->ops[i + 1].prelu_slope;
+                eff_scale = m->scales[i + 1];
+                if (eff_scale <= 0) eff_scale = next_scale;
+                eff = i + 1; skip = 1;
+            } else if (i + 1 < n && m->ops[i + 1].type == FF_OP_ADD) {
+                add_k = add_idx % 24;
+                if (slot_t[add_k] < 0) { rc = fail(p, "Add before any SAVE_ID", i + 1); break; }
+                const FfTensor* at = &p->tensors[slot_t[add_k]];
+                if (at->C != op->Cout || at->H != so.H || at->W != so.W) {
+                    rc = fail(p, "Add operands differ in shape", i + 1); break;
+                }
+                eff_scale = m->scales[i + 1];
+                if (eff_scale <= 0) eff_scale = next_scale;
+                eff = i + 1; skip = 1;
+            }
+            const float* inv_pc = pc ? m->inv_pc[eff] : NULL;
+            if (inv_pc && m->pc_len[eff] < (uint32_t)op->Cout) { rc = fail(p, "OPSC2 entry too short", eff); break; }
+
+            const int X = new_tensor(&B, op->Cout, so.H, so.W, eff);
+            FfStep* s = new_step(&B);
+            s->kind = 1; s->op_first = i; s->op_last = eff;
+            s->cin = op->Cin; s->cout = op->Cout; s->kh = op->Kh; s->kw = op->Kw;
+            s->stride = op->stride; s->pad = op->pad; s->hin = si.H; s->win = si.W;
+            s->hout = so.H; s->wout = so.W;
+            s->t_in = in_t; s->t_out = X; s->t_x = X;
+            s->in_scale = in_scale;
+            s->flags = FFK_EPI_BIAS | (in_scale != 1.0f ? FFK_EPI_INSCALE : 0);
+            s->w_off = alloc_weights(&B, ffk_conv_packed_bytes(op->Cin, op->Cout, op->Kh, op->Kw));
+            ffk_pack_conv_weights(op->conv_w, op->Cout, op->Cin, op->Kh, op->Kw, p->w_host + s->w_off);
+            s->p_off = alloc_params(&B, (size_t)FFK_NPARAM * op->Cout);
+            float* P = p->p_host + s->p_off;
+            const int C = op->Cout;
+            fill_row(P + FFK_P_WS * C, C, op->conv_scales, 0.0f);
+            fill_row(P + FFK_P_BIAS * C, C, op->conv_bias, 0.0f);   /* FFW2: no bias, +0 */
+            fill_rowf(P + FFK_P_INV * C, C, inv_pc, inv_of(eff_scale));
+            if (slope) {
+                s->flags |= FFK_EPI_PRELU;
+                fill_row(P + FFK_P_SLOPE * C, C, slope, 0.0f);
+            }
+            if (add_k >= 0) {
+                s->flags |= FFK_EPI_ADD;
+                s->t_add = slot_t[add_k];
+                /* per-channel shortcut scale for FFW4 (libfastface.c:378), else scalar */
+                fill_rowf(P + FFK_P_ADDSCALE * C, C, v4 ? slot_pc[add_k] : NULL, slot_scale[add_k]);
+                add_idx++;
+            }
+            A = X; A_scale = eff_scale;
+            if (pc && m->scale_pc[eff]) A_pc = m->scale_pc[eff];
+            last_conv = p->n_steps - 1;
+            if (skip) i++;
+            break;
+        }
+        case FF_OP_BN: {
+            const Shp si = sh_in[i];
+            if (last_conv < 0 || p->steps[last_conv].t_out != A || p->steps[last_conv].t_bn >= 0) {
+                rc = fail(p, "BN must follow a Conv (through SAVE_ID/BLOCK_START only)", i); break;
+            }
+            if (op->bn_size != si.C) { rc = fail(p, "BN size != channels", i); break; }
+            FfStep* s = &p->steps[last_conv];
+            float* P = p->p_host + s->p_off;
+            const int C = si.C;
+            /* libfastface.c:402-408 */
+            const float* bn_inv = (pc && m->inv_pc[i] && m->pc_len[i] == (uint32_t)C) ? m->inv_pc[i] : NULL;
+            const float* bn_in = (pc && A_pc) ? A_pc : NULL;
+            fill_rowf(P + FFK_P_BN_SIN * C, C, bn_in, A_scale);
+            fill_row(P + FFK_P_BN_S * C, C, op->bn_scale, 0.0f);
+            fill_row(P + FFK_P_BN_O * C, C, op->bn_offset, 0.0f);
+            fill_rowf(P + FFK_P_BN_INV * C, C, bn_inv, inv_of(next_scale));
+            s->flags |= FFK_EPI_BN;
+            const int Y = new_tensor(&B, C, si.H, si.W, i);
+            p->tensors[Y].def_step = last_conv;
+            s->t_bn = Y;
+            s->op_last = i;
+            A = Y; A_scale = next_scale;
+            if (pc && m->scale_pc[i]) A_pc = m->scale_pc[i];
+            break;
+        }
+        case FF_OP_PRELU:
+            rc = fail(p, "stand-alone PReLU (not after a Conv) is not supported", i);
+            break;
+        case FF_OP_ADD:
+            rc = fail(p, "stand-alone Add (not after a Conv) is not supported", i);
+            break;
+        case FF_OP_BLOCK_START:          /* libfastface.c:425-428 */
+            blk_t = A; blk_scale = A_scale;
+            break;
+        case FF_OP_SAVE_ID: {            /* libfastface.c:435-440 */
+            const int k = save_idx % 24;
+            slot_t[k] = A; slot_scale[k] = A_scale; slot_pc[k] = A_pc;
+            save_idx++;
+            break;
+        }
+        case FF_OP_FLATTEN:
+            flat = 1;
+            break;
+        case FF_OP_GEMM: {               /* libfastface.c:441-455 */
+            const FfTensor* at = &p->tensors[A];
+            const int K = (int)op->K, N = (int)op->N;
+            if (A == FF_T_INPUT || (long long)at->C * at->H * at->W != K) {
+                rc = fail(p, "GEMM K does not match its input", i); break;
+            }
+            if (K % 64 != 0) { rc = fail(p, "GEMM K must be a multiple of 64", i); break; }
+            FfStep* s = new_step(&B);
+            s->kind = 2; s->op_first = i; s->op_last = i;
+            s->t_in = A; s->fc_n = N; s->fc_k = K;
+            s->a_scale = v4 ? 1.0f : A_scale;
+            s->w_off = alloc_weights(&B, ffk_fc_packed_bytes(N, K));
+            int8_t* wt = (int8_t*)malloc((size_t)N * K);
+            if (!wt) { rc = fail(p, "out of host memory", i); break; }
+            const int HW = at->H * at->W, Cc = at->C;
+            for (int r = 0; r < N; r++) {
+                const int8_t* src = op->gemm_w + (size_t)r * K;
+                int8_t* dst = wt + (size_t)r * K;
+                if (flat)            /* reference column c*HW + hw -> NHWC column hw*C + c */
+                    for (int c = 0; c < Cc; c++)
+                        for (int hw = 0; hw < HW; hw++) dst[(size_t)hw * Cc + c] = src[(size_t)c * HW + hw];
+                else
+                    memcpy(dst, src, (size_t)K);
+            }
+            ffk_pack_fc_weights(wt, N, K, p->w_host + s->w_off);
+            free(wt);
+            s->ws_off = alloc_params(&B, (size_t)N);
+            fill_row(p->p_host + s->ws_off, N, op->gemm_scales, 0.0f);
+            s->bias_off = alloc_params(&B, (size_t)N);
+            fill_row(p->p_host + s->bias_off, N, op->gemm_bias, 0.0f);
+            p->emb_n = N;
+            done = 1;
+            break;
+        }
+        default:
+            rc = fail(p, "unknown op", i);
+        }
+    }
+    free(is_sc); free(sh_in); free(sh_out);
+    if (!rc && !done) rc = fail(p, "model has no GEMM head", n);
+    if (!rc && p->emb_n != FASTFACE_OUTPUT_N) rc = fail(p, "embedding size must be 512", n);
+    return rc;
+}
+
+int ff_plan_assign_buffers(FfPlan* p, int keep_all)
+{
+    for (int t = 0; t < p->n_tensors; t++) { p->tensors[t].last_use = -1; p->tensors[t].buf = -1; }
+    for (int s = 0; s < p->n_steps; s++) {
+        const FfStep* st = &p->steps[s];
+        if (st->t_in >= 0) p->tensors[st->t_in].last_use = s;
+        if (st->t_add >= 0) p->tensors[st->t_add].last_use = s;
+    }
+    p->max_face_bytes = 0;
+    for (int t = 1; t < p->n_tensors; t++) {
+        size_t b = (size_t)p->tensors[t].C * p->tensors[t].H * p->tensors[t].W;
+        if (b > p->max_face_bytes) p->max_face_bytes = b;
+    }
+    /* the pre-BN output of a dual-output step is stored only if read later */
+    for (int s = 0; s < p->n_steps; s++) {
+        FfStep* st = &p->steps[s];
+        if (st->kind != 1) continue;
+        st->t_out = st->t_x;
+        if (st->t_bn >= 0 && p->tensors[st->t_x].last_use < 0 && !keep_all) st->t_out = -1;
+    }
+    int* free_list = (int*)malloc((size_t)(p->n_tensors + 1) * sizeof(int));
+    int n_free = 0, n_buf = 0;
+    for (int s = 0; s < p->n_steps; s++) {
+        FfStep* st = &p->steps[s];
+        int outs[2] = { st->t_out, st->t_bn };
+        for (int k = 0; k < 2; k++) {
+            int t = outs[k];
+            if (t < 0) continue;
+            if (!keep_all && n_free > 0) p->tensors[t].buf = free_list[--n_free];
+            else p->tensors[t].buf = n_buf++;
+        }
+        if (keep_all) continue;
+        /* release what is dead after this step (inputs, and outputs never read) */
+        for (int t = 1; t < p->n_tensors; t++) {
+            FfTensor* T = &p->tensors[t];
+            if (T->buf < 0) continue;
+            if (T->last_use == s) free_list[n_free++] = T->buf;
+        }
+    }
+    free(free_list);
+    p->n_buffers = n_buf;
+    return 0;
+}
+
+void ff_plan_free(FfPlan* p)
+{
+    free(p->steps); free(p->tensors); free(p->w_host); free(p->p_host);
+    memset(p, 0, sizeof *p);
+}

@@ -1,0 +1,190 @@
+"""Synthetic FFW4 weights and seeded synthetic faces.
+
+The reference's real weights (`models/w600k_r50_ffw4.bin`) are not
+distributed with it, so tests and the bench run on a synthetic FFW4 with the
+same 177-op IResNet-50 schedule and byte layout that the reference's writer
+emits (prepare_weights_v3.py:280-307; loader kernels/ffw2_loader.c:71-159):
+
+    "FFW4" u32 n_ops, then per op: u8 type + payload
+      CONV  (1): 6 x u16 [Cin, Cout, Kh, Kw, stride, pad], i8[Cout*Cin*Kh*Kw]
+                 (OIHW), f32[Cout] weight scales, f32[Cout] bias
+      BN    (2): u16 n, f32[n] scale, f32[n] offset
+      PRELU (3): u16 n, f32[n] slope
+      GEMM  (5): u32 N, u32 K, i8[N*K], f32[N] scales, f32[N] bias
+      ADD (4), FLATTEN (6), SAVE_ID (7), BLOCK_START (8): no payload
+
+Schedule (op index order):
+    CONV stem 3->64 3x3 s1, PRELU
+    per block of stages [3, 4, 14, 3] at 64/128/256/512 channels:
+      BLOCK_START, BN(Cin), CONV c1 3x3 s1 Cin->C, PRELU,
+      first block of a stage: CONV c2 3x3 s2, SAVE_ID, CONV ds 1x1 s2 Cin->C, ADD
+      other blocks:           CONV c2 3x3 s1, ADD
+      SAVE_ID unless last block of the stage
+    BN(512), FLATTEN, GEMM 25088->512
+
+Values follow the recipe: int8 weights uniform in [-127, 127], per-channel
+fp32 scales, bias N(0, 0.05), PReLU slopes U(0, 0.3), seeded numpy PCG64.
+Weight scales are sized from the committed OPSC2 output scales so that the
+activations stay inside the int8 range rather than saturating.
+"""
+from __future__ import annotations
+
+import os
+import struct
+
+import numpy as np
+
+OP_CONV, OP_BN, OP_PRELU, OP_ADD, OP_GEMM, OP_FLATTEN, OP_SAVE_ID, OP_BLOCK_START = range(1, 9)
+
+STAGES = ((3, 64), (4, 128), (14, 256), (3, 512))
+INPUT_HW = 112
+INPUT_C = 3
+EMB_N = 512
+FACE_FLOATS = INPUT_HW * INPUT_HW * INPUT_C
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+REPO_ROOT = os.path.dirname(_HERE)
+OPSC_PATH = os.path.join(REPO_ROOT, "models", "op_scales.bin")
+OPSC2_PATH = os.path.join(REPO_ROOT, "models", "op_scales_v2.bin")
+
+
+def iresnet_schedule(stages=STAGES):
+    """List of op dicts in FFW4 order (types and conv geometry only)."""
+    ops = [dict(type=OP_CONV, Cin=3, Cout=64, k=3, s=1, p=1), dict(type=OP_PRELU, C=64)]
+    cin = 64
+    for nblocks, c in stages:
+        for bi in range(nblocks):
+            ops.append(dict(type=OP_BLOCK_START))
+            ops.append(dict(type=OP_BN, C=cin))
+            ops.append(dict(type=OP_CONV, Cin=cin, Cout=c, k=3, s=1, p=1))
+            ops.append(dict(type=OP_PRELU, C=c))
+            if bi == 0:
+                ops.append(dict(type=OP_CONV, Cin=c, Cout=c, k=3, s=2, p=1))
+                ops.append(dict(type=OP_SAVE_ID))
+                ops.append(dict(type=OP_CONV, Cin=cin, Cout=c, k=1, s=2, p=0))
+                ops.append(dict(type=OP_ADD))
+            else:
+                ops.append(dict(type=OP_CONV, Cin=c, Cout=c, k=3, s=1, p=1))
+                ops.append(dict(type=OP_ADD))
+            if bi != nblocks - 1:
+                ops.append(dict(type=OP_SAVE_ID))
+            cin = c
+    ops.append(dict(type=OP_BN, C=cin))
+    ops.append(dict(type=OP_FLATTEN))
+    ops.append(dict(type=OP_GEMM, N=EMB_N, K=cin * 7 * 7))
+    return ops
+
+
+def read_opsc2(path=OPSC2_PATH):
+    """(input_scales, [per-op forward scale arrays or None])."""
+    with open(path, "rb") as f:
+        d = f.read()
+    assert d[:5] == b"OPSC2"
+    off = 5
+    n_ops, n_in = struct.unpack_from("<II", d, off)
+    off += 8
+    in_s = np.frombuffer(d, np.float32, n_in, off).copy()
+    off += 4 * n_in
+    per_op = []
+    for _ in range(n_ops):
+        (c,) = struct.unpack_from("<I", d, off)
+        off += 4
+        per_op.append(np.frombuffer(d, np.float32, c, off).copy() if c else None)
+        off += 4 * c
+    return in_s, per_op
+
+
+def _fill_scales(ops, opsc2):
+    """Per-op forward activation scales the interpreter tracks (the producer's
+    OPSC2 entry, libfastface.c:395-396,410-411)."""
+    in_s, per_op = opsc2
+    cur = in_s
+    out = []
+    for i, op in enumerate(ops):
+        out.append(cur)
+        if per_op[i] is not None and op["type"] in (OP_CONV, OP_PRELU, OP_ADD, OP_BN):
+            cur = per_op[i]
+    return out
+
+
+def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPSC2_PATH):
+    """Write a synthetic FFW4 file (about 43.7 MB) and return its path."""
+    rng = np.random.default_rng(seed)
+    ops = iresnet_schedule()
+    opsc2 = read_opsc2(opsc2_path)
+    _, per_op = opsc2
+    track = _fill_scales(ops, opsc2)
+    n = len(ops)
+    tmp = path + ".tmp%d" % os.getpid()
+    with open(tmp, "wb") as f:
+        f.write(b"FFW4")
+        f.write(struct.pack("<I", n))
+        for i, op in enumerate(ops):
+            t = op["type"]
+            f.write(struct.pack("<B", t))
+            if t == OP_CONV:
+                cin, cout, k = op["Cin"], op["Cout"], op["k"]
+                w = rng.integers(-127, 128, size=(cout, cin, k, k), dtype=np.int8)
+                # requant target of this conv: the fused PReLU/Add's scale if any
+                eff = i + 1 if ops[i + 1]["type"] in (OP_PRELU, OP_ADD) else i
+                s_out = per_op[eff] if per_op[eff] is not None else np.full(cout, 0.02, np.float32)
+                kreal = cin * k * k
+                # keeps the int8 output spread close to the input's
+                base = s_out.astype(np.float64) * gain / (np.sqrt(kreal) * 73.6)
+                jitter = rng.uniform(0.5, 1.5, size=cout)
+                scales = (base * jitter).astype(np.float32)
+                bias = rng.normal(0.0, 0.05, size=cout).astype(np.float32)
+                f.write(struct.pack("<6H", cin, cout, k, k, op["s"], op["p"]))
+                f.write(w.tobytes())
+                f.write(scales.tobytes())
+                f.write(bias.tobytes())
+            elif t == OP_BN:
+                c = op["C"]
+                s_in = track[i].astype(np.float64)
+                s_bn = per_op[i].astype(np.float64) if per_op[i] is not None else s_in
+                ratio = np.clip(s_bn / np.maximum(s_in, 1e-30), 1e-3, 1e3)
+                scale = (ratio * rng.uniform(0.5, 1.5, size=c)).astype(np.float32)
+                offset = rng.normal(0.0, 0.05, size=c).astype(np.float32)
+                f.write(struct.pack("<H", c))
+                f.write(scale.tobytes())
+                f.write(offset.tobytes())
+            elif t == OP_PRELU:
+                c = op["C"]
+                slope = rng.uniform(0.0, 0.3, size=c).astype(np.float32)
+                f.write(struct.pack("<H", c))
+                f.write(slope.tobytes())
+            elif t == OP_GEMM:
+                nn, kk = op["N"], op["K"]
+                w = rng.integers(-127, 128, size=(nn, kk), dtype=np.int8)
+                scales = (rng.uniform(0.5, 1.5, size=nn) /
+                          (np.sqrt(kk) * 73.6 * act_sigma)).astype(np.float32)
+                bias = rng.normal(0.0, 0.05, size=nn).astype(np.float32)
+                f.write(struct.pack("<II", nn, kk))
+                f.write(w.tobytes())
+                f.write(scales.tobytes())
+                f.write(bias.tobytes())
+    os.replace(tmp, path)
+    return path
+
+
+def synthetic_ffw4_path(seed=3, cache_dir=None):
+    """Path of the cached synthetic FFW4 for `seed`, generated on first use."""
+    cache_dir = cache_dir or os.environ.get("FASTFACE_CACHE", "/tmp/fastface_cache")
+    os.makedirs(cache_dir, exist_ok=True)
+    path = os.path.join(cache_dir, "synthetic_r50_seed%d.ffw4" % seed)
+    if not os.path.exists(path):
+        write_synthetic_ffw4(path, seed=seed)
+    return path
+
+
+def faces_uniform(batch, seed):
+    """`batch` faces [B,112,112,3] fp32, uniform in [-1, 1]."""
+    rng = np.random.default_rng(seed)
+    return rng.uniform(-1.0, 1.0, size=(batch, INPUT_HW, INPUT_HW, INPUT_C)).astype(np.float32)
+
+
+def faces_normal_clipped(batch, seed, sigma=0.5):
+    """`batch` faces, N(0, sigma) clipped to [-1, 1]."""
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0.0, sigma, size=(batch, INPUT_HW, INPUT_HW, INPUT_C))
+    return np.clip(x, -1.0, 1.0).astype(np.float32)

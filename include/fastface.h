@@ -1,0 +1,98 @@
+/* fastface.h -- C API of the MI355X-native FastFace INT8 engine.
+ *
+ * Drop-in for the reference's fastface.h (bauratynov/fastface fastface.h:27-42):
+ * same three entry points, same types, same constants, same conventions --
+ * create returns NULL on any failure, embed returns 0 on success and non-zero
+ * on error, results are bit-identical to the reference's int8 CPU path.
+ *
+ *     FastFace* ff = fastface_create("models/w600k_r50_ffw4.bin");
+ *     float input[FASTFACE_INPUT_N];     // HWC fp32 face, [-1, 1]
+ *     float embedding[FASTFACE_OUTPUT_N];
+ *     fastface_embed(ff, input, embedding);
+ *     fastface_destroy(ff);
+ *
+ * Side inputs, as in the reference (libfastface.c:236-240): per-op scales are
+ * read from "models/op_scales.bin" relative to the working directory
+ * (mandatory) and per-channel scales from $OPSC2_PATH or
+ * "models/op_scales_v2.bin" (optional).
+ *
+ * Input layout:  HWC contiguous float32, 3*112*112 = 37632 floats per face.
+ * Output layout: raw (not L2-normalized) float32 embedding, 512 per face.
+ * Thread-safety: one context per thread (a context owns one HIP stream,
+ * device buffers and captured graphs); contexts may run concurrently.
+ */
+#ifndef FASTFACE_H
+#define FASTFACE_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct FastFace FastFace;
+
+/* Reference fastface.h:31.  Loads FFW4 (also FFW3/FFW2) weights, builds the
+ * fused launch plan, packs and uploads the weights once. */
+FastFace* fastface_create(const char* ffw4_path);
+
+/* Reference fastface.h:35.  One face: 37632 fp32 in, 512 fp32 out. */
+int fastface_embed(FastFace* ff, const float* input_hwc, float* out_emb);
+
+/* Reference fastface.h:38. */
+void fastface_destroy(FastFace* ff);
+
+#define FASTFACE_INPUT_N  37632   /* 3 * 112 * 112 */
+#define FASTFACE_OUTPUT_N 512
+
+/* ---------------- additive extensions (no reference counterpart) --------
+ * Batched embedding.  Face i of the batch gives exactly the embedding that
+ * fastface_embed gives for face i alone (the reference's own invariant: its
+ * batched driver, arcface_forward_int8_batched.c, is bit-identical per face).
+ * Host buffers: batch*37632 floats in, batch*512 floats out. */
+int fastface_embed_batch(FastFace* ff, const float* in_bhwc, int batch, float* out_b512);
+
+/* Device-resident variant: d_in / d_out are device pointers (HBM), the work
+ * is enqueued on `stream` (NULL: the context's stream) and not waited for. */
+int fastface_embed_batch_device(FastFace* ff, const float* d_in, int batch, float* d_out,
+                                void* stream);
+
+/* Pre-allocate device buffers for batches up to max_batch (default: grown on
+ * demand; env FASTFACE_MAX_BATCH sets the initial reservation). */
+int fastface_reserve(FastFace* ff, int max_batch);
+
+/* The context's HIP stream (hipStream_t). */
+void* fastface_stream(FastFace* ff);
+
+/* ---------------- introspection (tests, bench) ---------------------------- */
+typedef struct {
+    int kind;                 /* 1 conv, 2 FC                                   */
+    int op_first, op_last;    /* reference op indices this launch covers        */
+    int cin, cout, kh, kw, stride, pad, hin, win, hout, wout;
+    int flags;                /* FFK_EPI_* of fastface_kernels.h                */
+    int stores_x;             /* writes the pre-BN tensor                       */
+    double ops_per_face;      /* 2 * multiply-accumulates                       */
+    double act_bytes_per_face;/* activation bytes read + written, algorithmic   */
+    double weight_bytes;      /* packed weight bytes read per launch            */
+} fastface_step_info;
+
+int fastface_num_steps(const FastFace* ff);
+int fastface_get_step(const FastFace* ff, int step, fastface_step_info* info);
+
+/* Runs the launch chain `reps` times step by step with HIP events between
+ * launches (no graph) on the context stream; step_ms[s] receives the mean
+ * duration of step s.  The input buffer holds whatever the last embed left. */
+int fastface_profile_steps(FastFace* ff, int batch, int reps, float* step_ms);
+
+/* Debug: keep every intermediate tensor in its own buffer (call before the
+ * first embed), then read the int8 NHWC tensor the reference interpreter
+ * holds after op `op_idx` (a fused Conv+PReLU/Add is keyed by the fused op's
+ * index).  Returns the number of bytes, or a negative error. */
+int fastface_debug_keep_tensors(FastFace* ff, int on);
+long long fastface_debug_read(FastFace* ff, int op_idx, int batch, void* host, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTFACE_H */

@@ -1,0 +1,141 @@
+/* fastface_kernels.h -- kernel-level C ABI of the MI355X (gfx950) INT8 path.
+ *
+ * This is the thin layer between the C99 host code (libfastface's create /
+ * embed, fastface.h) and the hand-written HIP kernels.  It is exported from
+ * libfastface_amd.so so that the parity tests can drive every kernel on its
+ * own, and so that a caller with its own buffers can run single layers.
+ * Plain C types only: device pointers are `void*`/typed pointers obtained from
+ * ffk_malloc, streams/events/graphs are opaque `void*` handles.
+ *
+ * All functions return FFK_OK (0) or a negative FFK_ERR_* code; the text of
+ * the last error of the calling thread is available from ffk_last_error().
+ */
+#ifndef FASTFACE_KERNELS_H
+#define FASTFACE_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FFK_OK              0
+#define FFK_ERR_ARG        (-1)
+#define FFK_ERR_UNSUPPORTED (-2)
+#define FFK_ERR_HIP        (-3)
+#define FFK_ERR_NOMEM      (-4)
+
+const char* ffk_last_error(void);
+
+/* ---- device memory, streams, events, graphs ------------------------- */
+int   ffk_device_count(void);
+void* ffk_malloc(size_t bytes);                 /* NULL on failure */
+int   ffk_free(void* dptr);
+void* ffk_host_alloc(size_t bytes);             /* pinned host memory */
+int   ffk_host_free(void* hptr);
+int   ffk_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int   ffk_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int   ffk_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int   ffk_stream_create(void** stream);
+int   ffk_stream_destroy(void* stream);
+int   ffk_stream_sync(void* stream);            /* NULL: device-wide sync */
+int   ffk_event_create(void** event);
+int   ffk_event_destroy(void* event);
+int   ffk_event_record(void* event, void* stream);
+int   ffk_event_elapsed_ms(void* start, void* stop, float* ms);
+int   ffk_graph_begin(void* stream);            /* start stream capture */
+int   ffk_graph_end(void* stream, void** graph_exec);
+int   ffk_graph_launch(void* graph_exec, void* stream);
+int   ffk_graph_destroy(void* graph_exec);
+
+/* ---- I/O descriptor ---------------------------------------------------
+ * A captured launch chain reads its fp32 input faces and writes its fp32
+ * embeddings through this device-resident pair of pointers, so the same
+ * graph serves any caller buffers: update it (ffk_memcpy_h2d, same stream)
+ * before the launch. */
+typedef struct { const float* in; float* out; } ffk_io;
+
+/* ---- convolution (implicit GEMM on i8 MFMA, fused requant epilogue) ----
+ * Replaces, per layer, im2col_nhwc_u8 + fastface_gemm_i8_fused +
+ * fused_epilogue_int8 (+ the following in-place bn_prelu_requant_int8 as a
+ * second output) of the reference: kernels/conv2d_nhwc.c:150-220,
+ * kernels/gemm_int8_v2.c:86-110, kernels/int8_epilogue.c:25-112,253-318.
+ */
+#define FFK_EPI_PRELU    0x01   /* f = f < 0 ? f*slope : f                   */
+#define FFK_EPI_ADD      0x02   /* f = fma(add_src, add_scale, f)            */
+#define FFK_EPI_BN       0x04   /* out_bn = BN-requant of the int8 output    */
+#define FFK_EPI_BIAS     0x08   /* f = f + bias (FFW3/FFW4 always)           */
+#define FFK_EPI_INSCALE  0x10   /* f = f * in_scale before ws (FFW2/FFW3)    */
+
+/* rows of the per-layer parameter block, each `cout` floats (device) */
+enum {
+    FFK_P_WS = 0,      /* weight scale                                  */
+    FFK_P_BIAS,        /* conv bias                                     */
+    FFK_P_SLOPE,       /* PReLU slope                                   */
+    FFK_P_ADDSCALE,    /* residual per-channel scale                    */
+    FFK_P_INV,         /* 1/(out_scale + 1e-9f)                         */
+    FFK_P_BN_SIN,      /* BN input scale (forward scale of the output)  */
+    FFK_P_BN_S,        /* BN scale                                      */
+    FFK_P_BN_O,        /* BN offset                                     */
+    FFK_P_BN_INV,      /* BN 1/(out_scale + 1e-9f)                      */
+    FFK_NPARAM
+};
+
+typedef struct {
+    int batch, cin, cout, kh, kw, stride, pad, hin, win;
+    const void*    in;       /* int8 NHWC [batch,hin,win,cin]; cin == 3: fp32
+                                faces [batch,112,112,3] quantized on load     */
+    const float*   in_inv;   /* cin == 3: 3 per-channel inverse input scales  */
+    const ffk_io*  io;       /* cin == 3 and in == NULL: read io->in          */
+    const int8_t*  w;        /* packed by ffk_pack_conv_weights               */
+    const float*   params;   /* [FFK_NPARAM][cout]                            */
+    const int8_t*  add_src;  /* FFK_EPI_ADD: int8 [batch,hout,wout,cout]      */
+    int8_t*        out;      /* int8 output X, or NULL                        */
+    int8_t*        out_bn;   /* FFK_EPI_BN: BN(X), or NULL                    */
+    int32_t*       out_i32;  /* non-NULL: store raw int32 accumulators only   */
+    int            flags;
+    float          in_scale;
+} ffk_conv_desc;
+
+/* 1 if a kernel is compiled for this layer geometry, else 0. */
+int    ffk_conv_supported(int cin, int cout, int kh, int kw, int stride, int pad,
+                          int hin, int win);
+/* Bytes of the packed weights and the packing itself (host memory). */
+size_t ffk_conv_packed_bytes(int cin, int cout, int kh, int kw);
+int    ffk_pack_conv_weights(const int8_t* w_oihw, int cout, int cin, int kh, int kw,
+                             int8_t* packed);
+int    ffk_conv(const ffk_conv_desc* d, void* stream);
+
+/* ---- FC head ----------------------------------------------------------
+ * Replaces the XOR-0x80 shift + fastface_gemm_i8_matvec_vnni of the reference
+ * (libfastface.c:441-455, kernels/gemm_int8_matvec.c:33-81), batched:
+ *   out[b][n] = fma(RN((float)dot(a[b], W[n]) * a_scale), ws[n], bias[n]).
+ * a is the activation in the order W's columns are given in (the host permutes
+ * the NCHW-flatten order of the reference to NHWC once, at create time). */
+typedef struct {
+    int batch, n, k;
+    const int8_t*  a;        /* [batch][k] int8                               */
+    const int8_t*  w;        /* packed by ffk_pack_fc_weights                 */
+    const float*   ws;       /* [n] */
+    const float*   bias;     /* [n] */
+    float          a_scale;
+    float*         out;      /* [batch][n] fp32, or NULL: io->out             */
+    const ffk_io*  io;
+    int            path;     /* 0 auto, 1 matvec, 2 MFMA GEMM                 */
+} ffk_fc_desc;
+
+size_t ffk_fc_packed_bytes(int n, int k);
+int    ffk_pack_fc_weights(const int8_t* w_nk, int n, int k, int8_t* packed);
+int    ffk_fc(const ffk_fc_desc* d, void* stream);
+
+/* ---- self checks -------------------------------------------------------
+ * Runs one 32x32x32 i8 MFMA on the device with the operand / result lane
+ * layouts the conv kernels assume and compares with a host product.
+ * Returns FFK_OK when they agree, FFK_ERR_UNSUPPORTED when they differ. */
+int ffk_selftest_mfma(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FASTFACE_KERNELS_H */

@@ -1,0 +1,134 @@
+"""Device-buffer helpers over the library's own C ABI (fastface_kernels.h).
+torch is not used: it ships its own HIP runtime, and one process must not
+load two."""
+import ctypes as C
+
+import numpy as np
+
+import fastface_amd as fa
+
+
+class Dev:
+    """A device allocation; from numpy (upload) or empty."""
+
+    def __init__(self, lib, nbytes=None, host=None):
+        self.lib = lib
+        if host is not None:
+            host = np.ascontiguousarray(host)
+            nbytes = host.nbytes
+        self.nbytes = int(nbytes)
+        self.ptr = lib.ffk_malloc(max(self.nbytes, 1))
+        if not self.ptr:
+            raise MemoryError(fa.last_error())
+        if host is not None and self.nbytes:
+            check(lib, lib.ffk_memcpy_h2d(self.ptr, host.ctypes.data, self.nbytes, None))
+            check(lib, lib.ffk_stream_sync(None))
+
+    def get(self, dtype, shape):
+        out = np.empty(shape, dtype)
+        assert out.nbytes <= self.nbytes
+        check(self.lib, self.lib.ffk_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes, None))
+        check(self.lib, self.lib.ffk_stream_sync(None))
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.lib.ffk_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def check(lib, rc):
+    if rc != 0:
+        raise RuntimeError("ffk call failed (%d): %s" % (rc, fa.last_error()))
+
+
+def pack_conv(lib, w_oihw):
+    w = np.ascontiguousarray(w_oihw, np.int8)
+    cout, cin, kh, kw = w.shape
+    n = lib.ffk_conv_packed_bytes(cin, cout, kh, kw)
+    out = np.empty(n, np.int8)
+    check(lib, lib.ffk_pack_conv_weights(w.ctypes.data, cout, cin, kh, kw, out.ctypes.data))
+    return out
+
+
+def params_block(cout, **rows):
+    """[FFK_NPARAM][cout] fp32 block; rows by name (ws, bias, slope, adds, inv,
+    bn_sin, bn_s, bn_o, bn_inv)."""
+    names = ["ws", "bias", "slope", "adds", "inv", "bn_sin", "bn_s", "bn_o", "bn_inv"]
+    P = np.zeros((fa.FFK_NPARAM, cout), np.float32)
+    for k, v in rows.items():
+        P[names.index(k)] = v
+    return P
+
+
+def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=False,
+             want_x=True, want_bn=False, in_inv=None, in_scale=1.0):
+    """One ffk_conv call; returns int32 acc (raw) or (X, BN(X)) int8 arrays."""
+    B, H, W, cin = x.shape
+    cout, _, kh, kw = w_oihw.shape
+    ho = (H + 2 * pad - kh) // stride + 1
+    wo = (W + 2 * pad - kw) // stride + 1
+    keep = []
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, kh, kw
+    d.stride, d.pad, d.hin, d.win = stride, pad, H, W
+    dx = Dev(lib, host=x); keep.append(dx)
+    d.in_ = dx.ptr
+    dw = Dev(lib, host=pack_conv(lib, w_oihw)); keep.append(dw)
+    d.w = dw.ptr
+    if in_inv is not None:
+        di = Dev(lib, host=np.asarray(list(in_inv) + [0.0], np.float32)); keep.append(di)
+        d.in_inv = di.ptr
+    if params is not None:
+        dp = Dev(lib, host=params); keep.append(dp)
+        d.params = dp.ptr
+    if add is not None:
+        da = Dev(lib, host=add); keep.append(da)
+        d.add_src = da.ptr
+    n_out = B * ho * wo * cout
+    res = {}
+    if raw:
+        do = Dev(lib, nbytes=n_out * 4); keep.append(do)
+        d.out_i32 = do.ptr
+    else:
+        if want_x:
+            dox = Dev(lib, nbytes=n_out); keep.append(dox)
+            d.out = dox.ptr
+        if want_bn:
+            dob = Dev(lib, nbytes=n_out); keep.append(dob)
+            d.out_bn = dob.ptr
+    d.flags = flags
+    d.in_scale = in_scale
+    check(lib, lib.ffk_conv(C.byref(d), None))
+    check(lib, lib.ffk_stream_sync(None))
+    if raw:
+        return do.get(np.int32, (B, ho, wo, cout))
+    x_out = dox.get(np.int8, (B, ho, wo, cout)) if want_x else None
+    bn_out = dob.get(np.int8, (B, ho, wo, cout)) if want_bn else None
+    return x_out, bn_out
+
+
+def run_fc(lib, a, W_nk, ws, bias, a_scale=1.0, path=0):
+    a = np.ascontiguousarray(a, np.int8)
+    B, K = a.shape
+    N = W_nk.shape[0]
+    packed = np.empty(lib.ffk_fc_packed_bytes(N, K), np.int8)
+    check(lib, lib.ffk_pack_fc_weights(np.ascontiguousarray(W_nk, np.int8).ctypes.data, N, K,
+                                       packed.ctypes.data))
+    da, dw = Dev(lib, host=a), Dev(lib, host=packed)
+    dws, db = Dev(lib, host=np.asarray(ws, np.float32)), Dev(lib, host=np.asarray(bias, np.float32))
+    do = Dev(lib, nbytes=B * N * 4)
+    d = fa.ffk_fc_desc()
+    d.batch, d.n, d.k = B, N, K
+    d.a, d.w, d.ws, d.bias, d.out = da.ptr, dw.ptr, dws.ptr, db.ptr, do.ptr
+    d.a_scale = a_scale
+    d.path = path
+    check(lib, lib.ffk_fc(C.byref(d), None))
+    check(lib, lib.ffk_stream_sync(None))
+    return do.get(np.float32, (B, N))

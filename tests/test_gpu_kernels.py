@@ -1,0 +1,168 @@
+"""Per-kernel parity on the GPU, through the C ABI, against the pinned oracle.
+
+Bar: bit-exact int32 accumulators and bit-exact int8 / fp32 outputs.
+"""
+import numpy as np
+import pytest
+
+import fastface_amd as fa
+from conftest import rng
+from gpu_util import params_block, run_conv, run_fc
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+# every conv geometry of IResNet-50 at 112x112 (Cin, Cout, k, stride, Hin)
+SHAPES = [
+    (64, 64, 3, 1, 112), (64, 64, 3, 2, 112), (64, 64, 1, 2, 112), (64, 64, 3, 1, 56),
+    (64, 128, 3, 1, 56), (128, 128, 3, 2, 56), (64, 128, 1, 2, 56), (128, 128, 3, 1, 28),
+    (128, 256, 3, 1, 28), (256, 256, 3, 2, 28), (128, 256, 1, 2, 28), (256, 256, 3, 1, 14),
+    (256, 512, 3, 1, 14), (512, 512, 3, 2, 14), (256, 512, 1, 2, 14), (512, 512, 3, 1, 7),
+]
+
+
+def _batch_for(H):
+    return 1 if H >= 112 else (3 if H >= 28 else 5)    # odd batches: ragged last tile
+
+
+def test_mfma_lane_layout(gpu_lib):
+    assert gpu_lib.ffk_selftest_mfma() == 0, fa.last_error()
+
+
+@pytest.mark.parametrize("cin,cout,k,s,H", SHAPES)
+def test_conv_int32_accumulators(gpu_lib, oracle, cin, cout, k, s, H):
+    r = rng(100 + cin + cout + k * 7 + s * 3 + H)
+    B = _batch_for(H)
+    x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
+    x[0, 0, :, :] = -128                      # extreme products
+    w[0] = -128
+    got = run_conv(gpu_lib, x, w, s, k // 2, raw=True)
+    assert np.array_equal(got, oracle.conv_i32(x, w, s, k // 2))
+
+
+def test_stem_int32_with_fused_input_quant(gpu_lib, oracle):
+    r = rng(7)
+    B = 2
+    x = r.uniform(-1, 1, size=(B, 112, 112, 3)).astype(F32)
+    x[0, 0, :4, 0] = [0.5 / 127, -2.5 / 127, 1e10, -1e10]
+    x[0, 1, :3, 1] = [np.inf, -np.inf, np.nan]
+    x[1, 5, 5, :] = [3e9, -3e9, 2.5 / 127]
+    inv = np.array([127.0, 127.00001, 126.5], F32)
+    w = r.integers(-128, 128, size=(64, 3, 3, 3), dtype=np.int8)
+    got = run_conv(gpu_lib, x, w, 1, 1, raw=True, in_inv=inv)
+    q = oracle.quant_input(x, inv)
+    assert np.array_equal(got, oracle.conv_i32(q, w, 1, 1))
+
+
+def _special_params(r, C):
+    ws = r.uniform(1e-3, 1e-2, C).astype(F32)
+    bias = r.normal(0, 0.1, C).astype(F32)
+    inv = (1.0 / r.uniform(0.5, 5.0, C)).astype(F32)
+    ws[0], bias[0], inv[0] = 0.5, 0.0, 1.0 / 64        # exact .5 ties after scaling
+    ws[1], inv[1] = 1e-3, 3.0e38                        # overflow -> -128
+    ws[2] = np.float32(1.4e-44)                         # denormal
+    inv[2] = 1e30
+    ws[3] = np.nan
+    ws[4], bias[4] = -1e-3, -0.0
+    inv[5] = 1e9
+    return ws, bias, inv
+
+
+EPI_MODES = ["none", "prelu", "add", "add_bn", "prelu_bn", "bn_only"]
+EPI_SHAPES = [(64, 64, 3, 1, 56), (64, 64, 1, 2, 112), (128, 256, 1, 2, 28),
+              (256, 256, 3, 1, 14), (512, 512, 3, 1, 7)]
+
+
+@pytest.mark.parametrize("mode", EPI_MODES)
+@pytest.mark.parametrize("cin,cout,k,s,H", EPI_SHAPES)
+def test_conv_fused_epilogue(gpu_lib, oracle, mode, cin, cout, k, s, H):
+    r = rng(300 + cin + cout + H + EPI_MODES.index(mode))
+    B = 2
+    x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
+    Ho = (H + 2 * (k // 2) - k) // s + 1
+    ws, bias, inv = _special_params(r, cout)
+    rows = dict(ws=ws, bias=bias, inv=inv)
+    flags = fa.FFK_EPI_BIAS
+    ekw = dict(ws=ws, bias=bias, inv_pc=inv)
+    add = None
+    if "prelu" in mode:
+        slope = r.uniform(0, 0.3, cout).astype(F32)
+        rows["slope"] = slope; ekw["prelu"] = slope; flags |= fa.FFK_EPI_PRELU
+    if "add" in mode:
+        add = r.integers(-128, 128, size=(B, Ho, Ho, cout), dtype=np.int8)
+        adds = r.uniform(1e-3, 5e-2, cout).astype(F32)
+        rows["adds"] = adds; ekw.update(add_src=add, add_scale_pc=adds); flags |= fa.FFK_EPI_ADD
+    want_bn = mode.endswith("bn") or mode == "bn_only"
+    if want_bn:
+        bsin = r.uniform(1e-3, 5e-2, cout).astype(F32)
+        bsin[6] = np.float32(3e-45)
+        bns = r.uniform(0.5, 1.5, cout).astype(F32)
+        bno = r.normal(0, 0.05, cout).astype(F32)
+        binv = (1.0 / r.uniform(0.01, 0.1, cout)).astype(F32)
+        rows.update(bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
+        flags |= fa.FFK_EPI_BN
+    acc = oracle.conv_i32(x, w, s, k // 2)
+    exp_x = oracle.fused_epilogue(acc, **ekw)
+    got_x, got_bn = run_conv(gpu_lib, x, w, s, k // 2, params=params_block(cout, **rows),
+                             flags=flags, add=add, want_x=(mode != "bn_only"), want_bn=want_bn)
+    if mode != "bn_only":
+        assert np.array_equal(got_x, exp_x)
+    if want_bn:
+        exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno,
+                                         inv_pc=binv)
+        assert np.array_equal(got_bn, exp_bn)
+
+
+def test_inscale_path(gpu_lib, oracle):
+    """FFW2/FFW3 models dequantize with a runtime input scale first."""
+    r = rng(9)
+    x = r.integers(-128, 128, size=(3, 14, 14, 256), dtype=np.int8)
+    w = r.integers(-128, 128, size=(256, 256, 3, 3), dtype=np.int8)
+    ws = r.uniform(1e-3, 1e-2, 256).astype(F32)
+    bias = r.normal(0, 0.1, 256).astype(F32)
+    inv = (1.0 / r.uniform(0.5, 5, 256)).astype(F32)
+    acc = oracle.conv_i32(x, w, 1, 1)
+    exp = oracle.fused_epilogue(acc, ws=ws, bias=bias, in_scale=0.0173, inv_pc=inv)
+    got, _ = run_conv(gpu_lib, x, w, 1, 1, params=params_block(256, ws=ws, bias=bias, inv=inv),
+                      flags=fa.FFK_EPI_BIAS | fa.FFK_EPI_INSCALE, in_scale=0.0173)
+    assert np.array_equal(got, exp)
+
+
+def test_config2_microbench_layer(gpu_lib, oracle):
+    """N=64, 14x14, 256->256 3x3 s1 p1; act/weights int8
+    U[-127,127]; ws U[1e-3,1e-2]; bias N(0,0.1); PReLU 0.25; seed 1.  The
+    output scale (unspecified) is the per-channel absmax/127 of the fp32
+    pre-requant tensor."""
+    r = rng(1)
+    x = r.integers(-127, 128, size=(64, 14, 14, 256), dtype=np.int8)
+    w = r.integers(-127, 128, size=(256, 256, 3, 3), dtype=np.int8)
+    ws = r.uniform(1e-3, 1e-2, 256).astype(F32)
+    bias = r.normal(0, 0.1, 256).astype(F32)
+    slope = np.full(256, 0.25, F32)
+    acc = oracle.conv_i32(x, w, 1, 1)
+    assert np.array_equal(run_conv(gpu_lib, x, w, 1, 1, raw=True), acc)
+    f = acc.astype(F32) * ws + bias
+    f = np.where(f < 0, f * slope, f)
+    s_out = (np.abs(f).reshape(-1, 256).max(axis=0) / 127).astype(F32)
+    inv = (F32(1.0) / (s_out + F32(1e-9))).astype(F32)
+    exp = oracle.fused_epilogue(acc, ws=ws, bias=bias, prelu=slope, inv_pc=inv)
+    got, _ = run_conv(gpu_lib, x, w, 1, 1,
+                      params=params_block(256, ws=ws, bias=bias, slope=slope, inv=inv),
+                      flags=fa.FFK_EPI_BIAS | fa.FFK_EPI_PRELU)
+    assert np.array_equal(got, exp)
+    assert np.abs(exp.astype(np.int32)).max() == 127       # the scale reaches full range
+
+
+@pytest.mark.parametrize("B,path", [(1, 0), (3, 1), (16, 0), (17, 0), (40, 2), (5, 2), (130, 0)])
+def test_fc_head(gpu_lib, oracle, B, path):
+    r = rng(500 + B + path)
+    K, N = 25088, 512
+    a = r.integers(-128, 128, size=(B, K), dtype=np.int8)
+    W = r.integers(-127, 128, size=(N, K), dtype=np.int8)
+    ws = r.uniform(1e-7, 1e-5, N).astype(F32)
+    bias = r.normal(0, 0.05, N).astype(F32)
+    got = run_fc(gpu_lib, a, W, ws, bias, path=path)
+    for b in range(B):
+        assert np.array_equal(got[b], oracle.fc(a[b], W, ws, bias)), "face %d" % b

@@ -1,0 +1,134 @@
+"""End-to-end parity of the fastface.h API on the GPU against the oracle
+interpreter (itself bit-exact with the reference's fastface_embed).
+
+Weights: the synthetic FFW4 (the reference's real w600k_r50_ffw4.bin is not
+distributed); scales: the committed OPSC / OPSC2.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import fastface_amd as fa
+from fastface_amd import synth
+from gpu_util import Dev, check
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def ff(gpu_lib, synth_ffw4):
+    f = fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT)
+    yield f
+    f.close()
+
+
+def _cos(a, b):
+    return float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def test_b1_config1(ff, oracle, oracle_model):
+    x = synth.faces_uniform(1, 0)
+    got = ff.embed(x[0])
+    exp, _ = oracle.forward(oracle_model, x)
+    assert np.array_equal(got, exp[0])
+
+
+def test_reference_golden_input_face(ff, oracle, oracle_model):
+    x = np.fromfile(os.path.join(GOLDEN, "golden_input.bin"), np.float32).reshape(1, 112, 112, 3)
+    exp, _ = oracle.forward(oracle_model, x)
+    assert np.array_equal(ff.embed(x[0]), exp[0])
+
+
+def test_b8_config3(ff, oracle, oracle_model):
+    x = synth.faces_normal_clipped(8, 2)
+    got = ff.embed_batch(x)
+    exp, _ = oracle.forward(oracle_model, x)
+    for i in range(8):
+        assert _cos(got[i], exp[i]) >= 0.9999
+        assert np.abs(got[i] - exp[i]).max() <= 1e-3
+    assert np.array_equal(got, exp)
+
+
+def test_batch_equals_single(ff):
+    x = synth.faces_uniform(6, 21)
+    batch = ff.embed_batch(x)
+    for i in range(6):
+        assert np.array_equal(batch[i], ff.embed(x[i]))
+
+
+def test_graph_replays_and_batch_switching(ff):
+    x = synth.faces_uniform(5, 22)
+    first = ff.embed_batch(x)
+    for b in (1, 5, 2, 5, 3):
+        out = ff.embed_batch(x[:b])
+        assert np.array_equal(out, first[:b])
+
+
+def test_per_layer_int8_activations(gpu_lib, synth_ffw4, oracle, oracle_model):
+    """Every intermediate int8 tensor (after each fused Conv and each BN) is
+    bit-exact with the reference interpreter's activation at that op."""
+    f = fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT)
+    try:
+        assert gpu_lib.fastface_debug_keep_tensors(f.ff, 1) == 0
+        x = synth.faces_uniform(2, 23)
+        got_emb = f.embed_batch(x)
+        exp_emb, dumps = oracle.forward(oracle_model, x, dump_ops=set(range(177)))
+        assert len(dumps) >= 70
+        for op, t in sorted(dumps.items()):
+            buf = np.empty(t.size, np.int8)
+            n = gpu_lib.fastface_debug_read(f.ff, op, 2, buf.ctypes.data, buf.nbytes)
+            assert n == t.size, "op %d: read %d" % (op, n)
+            assert np.array_equal(buf.reshape(t.shape), t), "op %d differs" % op
+        assert np.array_equal(got_emb, exp_emb)
+    finally:
+        f.close()
+
+
+def test_device_resident_api(ff, gpu_lib):
+    x = synth.faces_uniform(4, 24)
+    exp = ff.embed_batch(x)
+    din = Dev(gpu_lib, host=x)
+    dout = Dev(gpu_lib, nbytes=4 * 512 * 4)
+    assert gpu_lib.fastface_embed_batch_device(ff.ff, din.ptr, 4, dout.ptr, None) == 0
+    check(gpu_lib, gpu_lib.ffk_stream_sync(gpu_lib.fastface_stream(ff.ff)))
+    assert np.array_equal(dout.get(np.float32, (4, 512)), exp)
+
+
+def test_api_errors(ff, gpu_lib):
+    out = np.empty(512, np.float32)
+    x = np.zeros(37632, np.float32)
+    assert gpu_lib.fastface_embed(None, x.ctypes.data, out.ctypes.data) != 0
+    assert gpu_lib.fastface_embed(ff.ff, None, out.ctypes.data) != 0
+    assert gpu_lib.fastface_embed(ff.ff, x.ctypes.data, None) != 0
+    assert gpu_lib.fastface_embed_batch(ff.ff, x.ctypes.data, -1, out.ctypes.data) != 0
+    assert gpu_lib.fastface_create(b"/nonexistent.ffw4") is None
+
+
+@pytest.mark.parametrize("B", [256, 1024])
+def test_large_batch_properties(ff, oracle, oracle_model, B):
+    """BASELINE configs 4/5 sizes: batch rows equal single-face results and the
+    oracle on sampled faces (the reference is batch-invariant)."""
+    x = synth.faces_uniform(B, 30 + B)
+    got = ff.embed_batch(x)
+    assert np.isfinite(got).all()
+    idx = [0, B // 3, B - 1]
+    exp, _ = oracle.forward(oracle_model, x[idx])
+    for j, i in enumerate(idx):
+        assert np.array_equal(got[i], exp[j]), "face %d" % i
+        assert np.array_equal(got[i], ff.embed(x[i]))
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(synth.REPO_ROOT, "models", "w600k_r50_ffw4.bin")),
+                    reason="the reference's real weights blob is not distributed")
+def test_reference_regression_with_real_weights(gpu_lib):
+    """tests/run_regression.py of the reference: bit-exact vs golden_int8_emb.bin,
+    cos >= 0.98 vs the ORT fp32 embedding."""
+    f = fa.FastFace(os.path.join(synth.REPO_ROOT, "models", "w600k_r50_ffw4.bin"), cwd=synth.REPO_ROOT)
+    x = np.fromfile(os.path.join(GOLDEN, "golden_input.bin"), np.float32)
+    got = f.embed(x)
+    f.close()
+    assert np.array_equal(got, np.fromfile(os.path.join(GOLDEN, "golden_int8_emb.bin"), np.float32))
+    assert _cos(got, np.fromfile(os.path.join(GOLDEN, "golden_ort_fp32_emb.bin"), np.float32)) >= 0.98

@@ -1,0 +1,95 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports
+every entry point the headers declare, weight packing, plan coverage."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import fastface_amd as fa
+from fastface_amd import synth
+
+INCLUDE = os.path.join(fa.REPO_ROOT, "include")
+
+
+def _declared_functions():
+    names = set()
+    for h in os.listdir(INCLUDE):
+        if not h.endswith(".h"):
+            continue
+        src = open(os.path.join(INCLUDE, h)).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        for m in re.finditer(r"\b((?:fastface|ffk)_[a-z0-9_]+)\s*\(", src):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = fa.load()
+    declared = _declared_functions()
+    assert len(declared) >= 35
+    missing = [n for n in declared if not hasattr(lib, n)]
+    assert not missing, missing
+    bound = {n for n, _, _ in fa.EXPORTS}
+    assert declared == bound, declared ^ bound
+
+
+def test_conv_weight_packing_layout():
+    lib = fa.load()
+    r = np.random.default_rng(0)
+    for cout, cin, k in [(64, 3, 3), (128, 64, 3), (256, 128, 1)]:
+        w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
+        n = lib.ffk_conv_packed_bytes(cin, cout, k, k)
+        packed = np.empty(n, np.int8)
+        assert lib.ffk_pack_conv_weights(w.ctypes.data, cout, cin, k, k, packed.ctypes.data) == 0
+        ktot = k * k * cin
+        steps = -(-ktot // 64)
+        assert n == steps * cout * 64
+        # reduction index k = (kh*KW + kw)*Cin + ci, zero padded to 64-steps
+        wk = np.zeros((cout, steps * 64), np.int8)
+        wk[:, :ktot] = w.transpose(0, 2, 3, 1).reshape(cout, ktot)
+        exp = wk.reshape(cout, steps, 64).transpose(1, 0, 2).reshape(-1)
+        assert np.array_equal(packed, exp)
+
+
+def test_fc_weight_packing_layout():
+    lib = fa.load()
+    r = np.random.default_rng(1)
+    W = r.integers(-128, 128, size=(8, 256), dtype=np.int8)
+    packed = np.empty(lib.ffk_fc_packed_bytes(8, 256), np.int8)
+    assert lib.ffk_pack_fc_weights(W.ctypes.data, 8, 256, packed.ctypes.data) == 0
+    assert np.array_equal(packed, W.reshape(8, 4, 64).transpose(1, 0, 2).reshape(-1))
+    assert lib.ffk_pack_fc_weights(W.ctypes.data, 8, 100, packed.ctypes.data) != 0
+
+
+def test_every_iresnet_conv_has_a_kernel():
+    lib = fa.load()
+    H = 112
+    seen = 0
+    cur = (3, 112)
+    blk = cur
+    ops = synth.iresnet_schedule()
+    for i, op in enumerate(ops):
+        if op["type"] == synth.OP_CONV:
+            src = blk if (i > 0 and ops[i - 1]["type"] == synth.OP_SAVE_ID) else cur
+            assert lib.ffk_conv_supported(op["Cin"], op["Cout"], op["k"], op["k"], op["s"],
+                                          op["p"], src[1], src[1]) == 1, op
+            cur = (op["Cout"], (src[1] + 2 * op["p"] - op["k"]) // op["s"] + 1)
+            seen += 1
+        elif op["type"] == synth.OP_BLOCK_START:
+            blk = cur
+    assert seen == 53
+    assert lib.ffk_conv_supported(64, 64, 3, 3, 1, 0, H, H) == 0      # pad must be k/2
+    assert lib.ffk_conv_supported(96, 64, 3, 3, 1, 1, H, H) == 0
+
+
+def test_create_without_gpu_returns_null(synth_ffw4):
+    lib = fa.load()
+    if lib.ffk_device_count() > 0:
+        pytest.skip("a GPU is visible")
+    old = os.getcwd()
+    os.chdir(fa.REPO_ROOT)
+    try:
+        assert lib.fastface_create(synth_ffw4.encode()) is None
+    finally:
+        os.chdir(old)

@@ -1,0 +1,219 @@
+"""Pins the CPU oracle (oracle/ff_oracle.c) before anything is compared with it.
+
+Each oracle function is checked against (a) the reference's own function
+compiled from its sources (oracle/_ref, AVX-VNNI host), on seeded inputs and
+on special cases chosen so that a plausible slip -- a dropped FMA, RNE
+instead of half-away rounding, a saturating float->int conversion, flushed
+denormals, a transposed weight index -- changes the output, and (b) closed
+forms / brute force where the mathematics fixes the answer.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import rng
+
+F32 = np.float32
+
+
+def _specials_epilogue(C, r):
+    """Per-channel parameter sets that land on the delicate cases."""
+    ws = r.uniform(1e-3, 1e-2, C).astype(F32)
+    bias = r.normal(0, 0.1, C).astype(F32)
+    inv = (1.0 / r.uniform(0.01, 0.1, C)).astype(F32)
+    ws[0], bias[0], inv[0] = 0.5, 0.0, 1.0          # acc odd -> exact .5 ties
+    ws[1], bias[1], inv[1] = 1.0, 0.0, 0.5          # ties through inv
+    ws[2], inv[2] = 1e-3, 3.0e38                    # |t| >= 2^31 and inf -> INT32_MIN -> -128
+    ws[3] = np.float32(1.4e-44)                     # denormal weight scale
+    inv[3] = np.float32(1e30)
+    ws[4] = np.nan                                  # NaN -> -128
+    ws[5], bias[5] = -1.0, -0.0                     # -0 handling
+    inv[6] = 1e9                                    # 1/(denormal + 1e-9): real OPSC2 case
+    ws[7], bias[7], inv[7] = 2.0 ** -20, 0.0, 2.0 ** 20   # exact products, sign of zero
+    return ws, bias, inv
+
+
+@pytest.mark.parametrize("prelu,add,add_pc,inv_pc,bn", [
+    (False, False, False, True, False),
+    (True, False, False, True, False),
+    (False, True, True, True, False),
+    (False, True, False, True, False),
+    (True, False, False, False, False),
+    (False, False, False, True, True),
+])
+def test_epilogue_vs_reference(oracle, ref, prelu, add, add_pc, inv_pc, bn):
+    r = rng(11)
+    C, P = 64, 3000
+    acc = r.integers(-2_000_000, 2_000_000, size=(P, C), dtype=np.int32)
+    acc[:, 0] = r.integers(-600, 600, size=P) | 1     # odd
+    acc[::7] = 0
+    ws, bias, inv = _specials_epilogue(C, r)
+    kw = dict(ws=ws, bias=bias, inv_pc=inv if inv_pc else None, out_scale=0.037)
+    if prelu:
+        slope = r.uniform(0, 0.3, C).astype(F32)
+        slope[8] = -1.0
+        kw["prelu"] = slope
+    if add:
+        kw["add_src"] = r.integers(-128, 128, size=(P, C), dtype=np.int8)
+        kw["add_scale"] = 0.021
+        if add_pc:
+            kw["add_scale_pc"] = r.uniform(1e-3, 5e-2, C).astype(F32)
+    if bn:
+        kw["bn_scale"] = r.uniform(0.5, 1.5, C).astype(F32)
+        kw["bn_offset"] = r.normal(0, 0.05, C).astype(F32)
+    got = oracle.fused_epilogue(acc, **kw)
+    exp = ref.fused_epilogue(acc, **kw)
+    assert np.array_equal(got, exp)
+    # the special channels really hit their cases
+    assert (exp[:, 2] == -128).any() and (exp[:, 4] == -128).all()
+
+
+def test_epilogue_rounding_is_half_away_in_fp32(oracle):
+    """t + copysign(0.5, t) is rounded to fp32 before truncation, so the fp32
+    just below 0.5 rounds up to 1 (an exact round-half-away would give 0)."""
+    below_half = np.nextafter(F32(0.5), F32(0))
+    acc = np.array([[1], [3], [-3], [5], [-1], [0]], np.int32).repeat(8, axis=1)
+    ws = np.full(8, 0.5, F32)
+    inv = np.full(8, 1.0, F32)
+    q = oracle.fused_epilogue(acc, ws=ws, bias=np.zeros(8, F32), inv_pc=inv)[:, 0]
+    assert list(q) == [1, 2, -2, 3, -1, 0]
+    acc1 = np.ones((1, 8), np.int32)
+    q = oracle.fused_epilogue(acc1, ws=np.full(8, below_half, F32), bias=np.zeros(8, F32),
+                              inv_pc=inv)
+    assert q[0, 0] == 1
+
+
+def test_cvtt_matches_x86_integer_indefinite(oracle):
+    assert oracle.cvtt(2147483520.0) == 2147483520
+    assert oracle.cvtt(2147483648.0) == -2147483648
+    assert oracle.cvtt(-2147483648.0) == -2147483648
+    assert oracle.cvtt(float("nan")) == -2147483648
+    assert oracle.cvtt(-7.9) == -7
+
+
+@pytest.mark.parametrize("use_pc,prelu", [(True, False), (False, False), (True, True)])
+def test_bn_requant_vs_reference(oracle, ref, use_pc, prelu):
+    r = rng(12)
+    C, P = 128, 2000
+    x = r.integers(-128, 128, size=(P, C), dtype=np.int8)
+    s_in = r.uniform(1e-3, 5e-2, C).astype(F32)
+    s_in[0] = np.float32(3e-45)            # denormal forward scale (present in OPSC2)
+    bns = r.uniform(0.5, 1.5, C).astype(F32)
+    bno = r.normal(0, 0.05, C).astype(F32)
+    inv = (1.0 / r.uniform(0.01, 0.1, C)).astype(F32)
+    inv[1] = 1e9
+    kw = dict(in_scale=0.02, in_scale_pc=s_in if use_pc else None, bn_scale=bns, bn_offset=bno,
+              inv_pc=inv, out_scale=0.05)
+    if prelu:
+        kw["prelu"] = r.uniform(0, 0.3, C).astype(F32)
+    assert np.array_equal(oracle.bn_prelu_requant(x, **kw), ref.bn_prelu_requant(x, **kw))
+
+
+def test_input_quant_vs_reference(oracle, ref):
+    r = rng(13)
+    x = r.uniform(-1, 1, size=(4096, 3)).astype(F32)
+    x[:8, 0] = [0.5 / 127, 1.5 / 127, -2.5 / 127, 1e10, -1e10, np.inf, -np.inf, np.nan]
+    x[8:12, 1] = [3e9, -3e9, 2.5, -2.5]
+    inv = np.array([127.0, 127.00001, 1.0], F32)
+    assert np.array_equal(oracle.quant_input(x, inv), ref.quant_input(x, inv))
+
+
+def test_add_requant_vs_reference(oracle, ref):
+    r = rng(14)
+    a = r.integers(-128, 128, 5000, dtype=np.int8)
+    b = r.integers(-128, 128, 5000, dtype=np.int8)
+    assert np.array_equal(oracle.add_requant(a, 0.013, b, 0.021, 0.03),
+                          ref.add_requant(a, 0.013, b, 0.021, 0.03))
+
+
+CONV_SHAPES = [  # (Cin, Cout, k, stride, H)
+    (3, 64, 3, 1, 20), (64, 64, 3, 1, 9), (64, 64, 3, 2, 10), (64, 64, 1, 2, 10),
+    (64, 128, 3, 1, 7), (128, 128, 3, 2, 8), (256, 256, 3, 1, 5), (256, 512, 1, 2, 6),
+]
+
+
+@pytest.mark.parametrize("cin,cout,k,s,H", CONV_SHAPES)
+def test_conv_i32_vs_reference(oracle, ref, cin, cout, k, s, H):
+    r = rng(15 + cin + cout + k + s)
+    x = r.integers(-128, 128, size=(2, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
+    pad = k // 2
+    assert np.array_equal(oracle.conv_i32(x, w, s, pad), ref.conv_i32(x, w, s, pad))
+
+
+def test_conv_i32_brute_force(oracle):
+    """Definition of convolution on a tiny case, including extreme values."""
+    r = rng(16)
+    x = r.integers(-128, 128, size=(2, 5, 4, 64), dtype=np.int8)
+    x[0, 0, 0, :] = -128
+    w = r.integers(-128, 128, size=(3, 64, 3, 3), dtype=np.int8)
+    w[0] = -128
+    for s in (1, 2):
+        got = oracle.conv_i32(x, w, s, 1)
+        xp = np.pad(x.astype(np.int64), ((0, 0), (1, 1), (1, 1), (0, 0)))
+        Ho, Wo = (5 + 2 - 3) // s + 1, (4 + 2 - 3) // s + 1
+        exp = np.zeros((2, Ho, Wo, 3), np.int64)
+        for oh in range(Ho):
+            for ow in range(Wo):
+                patch = xp[:, oh * s:oh * s + 3, ow * s:ow * s + 3, :]      # [B,3,3,Cin]
+                exp[:, oh, ow, :] = np.einsum("bhwc,ochw->bo", patch, w.astype(np.int64))
+        assert np.array_equal(got, exp)
+
+
+def test_fc_vs_reference_and_closed_form(oracle, ref):
+    r = rng(17)
+    K, N = 25088, 64
+    a = r.integers(-128, 128, K, dtype=np.int8)
+    W = r.integers(-127, 128, size=(N, K), dtype=np.int8)
+    ws = r.uniform(1e-7, 1e-5, N).astype(F32)
+    bias = r.normal(0, 0.05, N).astype(F32)
+    got = oracle.fc(a, W, ws, bias)
+    assert np.array_equal(got, ref.fc(a, W, ws, bias))
+    dot = W.astype(np.int64) @ a.astype(np.int64)
+    exp = (dot.astype(np.float32).astype(np.float64) * ws.astype(np.float64) +
+           bias.astype(np.float64)).astype(np.float32)     # fma: one rounding of the exact value
+    assert np.array_equal(got, exp)
+
+
+def test_schedule_matches_committed_opsc2():
+    """The synthetic FFW4's op list has the channel pattern the committed
+    OPSC2 records for the real w600k_r50 model (0 for marker ops)."""
+    from fastface_amd import synth
+    ops = synth.iresnet_schedule()
+    _, per_op = synth.read_opsc2()
+    assert len(ops) == len(per_op) == 177
+    for op, sc in zip(ops, per_op):
+        n = 0 if sc is None else len(sc)
+        t = op["type"]
+        if t == synth.OP_CONV:
+            assert n == op["Cout"]
+        elif t in (synth.OP_BN, synth.OP_PRELU):
+            assert n == op["C"]
+        elif t in (synth.OP_SAVE_ID, synth.OP_BLOCK_START):
+            assert n == 0
+        elif t == synth.OP_FLATTEN:
+            assert n == 25088
+        elif t == synth.OP_GEMM:
+            assert n == 512
+
+
+def test_forward_vs_reference_embed(oracle, ref, oracle_model, synth_ffw4):
+    """Whole network: oracle interpreter == reference fastface_embed, bit-exact,
+    on the reference's own real-face input fixture and a synthetic face."""
+    from fastface_amd import synth
+    gold_in = np.fromfile(os.path.join(os.path.dirname(__file__), "golden", "golden_input.bin"),
+                          dtype=np.float32).reshape(1, 112, 112, 3)
+    faces = np.concatenate([gold_in, synth.faces_uniform(1, 0)])
+    emb, _ = oracle.forward(oracle_model, faces)
+    emb_ref = ref.embed(synth_ffw4, faces, cwd=synth.REPO_ROOT)
+    assert np.array_equal(emb, emb_ref)
+
+
+def test_forward_batch_invariance(oracle, oracle_model):
+    from fastface_amd import synth
+    faces = synth.faces_normal_clipped(3, 2)
+    emb3, _ = oracle.forward(oracle_model, faces)
+    for i in range(3):
+        e1, _ = oracle.forward(oracle_model, faces[i:i + 1])
+        assert np.array_equal(e1[0], emb3[i])

@@ -196,6 +196,13 @@ def main():
     check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
     b1_dev_ms = ms.value / 50
     log("b=1: %.3f ms host-to-host median, %.3f ms device chain" % (b1_ms, b1_dev_ms))
+    b1_steps = np.zeros(n_steps, np.float32)
+    if lib.fastface_profile_steps(ff.ff, 1, 20, b1_steps.ctypes.data) == n_steps:
+        for s in np.argsort(-b1_steps)[:8]:
+            st = steps[s]
+            log("b=1 step %2d: %.4f ms  conv %d->%d k%d s%d @%d" % (s, b1_steps[s], st["cin"],
+                st["cout"], st["k"], st["s"], st["hin"]))
+        log("b=1 sum of step times %.4f ms" % float(b1_steps.sum()))
 
     cpu = None
     if not args.no_cpu_baseline:

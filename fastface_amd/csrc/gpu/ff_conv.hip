@@ -23,6 +23,11 @@
 
 #define EPI_FC 0x100  // internal: FC head, fp32 output via ff::fc_out
 
+// K steps of global loads kept in flight per thread
+#ifndef FF_PF
+#define FF_PF 4
+#endif
+
 struct ConvArgs {
     const int8_t* in;
     const float* in_f32;
@@ -190,7 +195,7 @@ __device__ __forceinline__ int xcd_tile(int bid, int nb) {
 // ---------------------------------------------------------------------------
 // Main conv kernel (Cin multiple of 64).
 // ---------------------------------------------------------------------------
-template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN>
+template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN, int PF>
 __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
     constexpr int PAD = KS / 2;
     constexpr int HOUT = (HIN + 2 * PAD - KS) / STRIDE + 1;
@@ -240,8 +245,12 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
     }
     const int8_t* wbase = a.w + (size_t)tn * BN * FF_KSTEP + tid * 16;
 
-    v4i ra[A_LD], rb[B_LD];
-    auto gload = [&](int s) {
+    // Prefetch queue: PF register sets, each holding one K step's global
+    // loads, so PF steps of loads are in flight while the MFMAs of the
+    // current step run out of LDS (memory latency is several times one
+    // step's MFMA time).
+    v4i ra[PF][A_LD], rb[PF][B_LD];
+    auto gload = [&](int s, v4i (&qa)[A_LD], v4i (&qb)[B_LD]) {
         const int tap = s / CSTEPS;
         const int cs = s - tap * CSTEPS;
         const int kh = tap / KS;
@@ -251,24 +260,24 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
             const int ih = a_ih0[j] + kh;
             const int iw = a_iw0[j] + kw;
             if (a_ok[j] && (unsigned)ih < (unsigned)HIN && (unsigned)iw < (unsigned)WIN)
-                ra[j] = *reinterpret_cast<const v4i*>(a_img[j] + (ih * WIN + iw) * CIN + cs * FF_KSTEP);
+                qa[j] = *reinterpret_cast<const v4i*>(a_img[j] + (ih * WIN + iw) * CIN + cs * FF_KSTEP);
             else
-                ra[j] = v4i{0, 0, 0, 0};
+                qa[j] = v4i{0, 0, 0, 0};
         }
 #pragma unroll
         for (int j = 0; j < B_LD; j++)
-            rb[j] = *reinterpret_cast<const v4i*>(wbase + (size_t)s * COUT * FF_KSTEP + j * 4096);
+            qb[j] = *reinterpret_cast<const v4i*>(wbase + (size_t)s * COUT * FF_KSTEP + j * 4096);
     };
-    auto sstore = [&](int buf) {
+    auto sstore = [&](int buf, const v4i (&qa)[A_LD], const v4i (&qb)[B_LD]) {
 #pragma unroll
         for (int j = 0; j < A_LD; j++) {
             const int idx = tid + j * 256;
-            *reinterpret_cast<v4i*>(As + buf * BM * ROWB + (idx >> 2) * ROWB + (idx & 3) * 16) = ra[j];
+            *reinterpret_cast<v4i*>(As + buf * BM * ROWB + (idx >> 2) * ROWB + (idx & 3) * 16) = qa[j];
         }
 #pragma unroll
         for (int j = 0; j < B_LD; j++) {
             const int idx = tid + j * 256;
-            *reinterpret_cast<v4i*>(Bs + buf * BN * ROWB + (idx >> 2) * ROWB + (idx & 3) * 16) = rb[j];
+            *reinterpret_cast<v4i*>(Bs + buf * BN * ROWB + (idx >> 2) * ROWB + (idx & 3) * 16) = qb[j];
         }
     };
 
@@ -287,25 +296,36 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int s = 0; s < KSTEPS; s++) {
-        const int buf = s & 1;
-        if (s + 1 < KSTEPS) gload(s + 1);
+    // prologue: steps 0 .. PF-1 in flight, step 0 staged in LDS
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            const v4i a0 = *reinterpret_cast<const v4i*>(a_rd + buf * BM * ROWB + ks * 32);
-            const v4i a1 = *reinterpret_cast<const v4i*>(a_rd + buf * BM * ROWB + 32 * ROWB + ks * 32);
-            const v4i b0 = *reinterpret_cast<const v4i*>(b_rd + buf * BN * ROWB + ks * 32);
-            const v4i b1 = *reinterpret_cast<const v4i*>(b_rd + buf * BN * ROWB + 32 * ROWB + ks * 32);
-            acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc[1][1], 0, 0, 0);
+    for (int u = 0; u < PF; u++)
+        if (u < KSTEPS) gload(u, ra[u], rb[u]);
+    sstore(0, ra[0], rb[0]);
+    __syncthreads();
+    // Step s lives in register set s % PF until it is staged into LDS buffer
+    // s & 1; right after that the set is refilled with step s + PF.
+    for (int s0 = 0; s0 < KSTEPS; s0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; u++) {
+            const int s = s0 + u;
+            if (s < KSTEPS) {
+                const int buf = s & 1;
+                if (s + PF < KSTEPS) gload(s + PF, ra[u], rb[u]);
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+                    const v4i a0 = *reinterpret_cast<const v4i*>(a_rd + buf * BM * ROWB + ks * 32);
+                    const v4i a1 = *reinterpret_cast<const v4i*>(a_rd + buf * BM * ROWB + 32 * ROWB + ks * 32);
+                    const v4i b0 = *reinterpret_cast<const v4i*>(b_rd + buf * BN * ROWB + ks * 32);
+                    const v4i b1 = *reinterpret_cast<const v4i*>(b_rd + buf * BN * ROWB + 32 * ROWB + ks * 32);
+                    acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc[0][0], 0, 0, 0);
+                    acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc[0][1], 0, 0, 0);
+                    acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc[1][0], 0, 0, 0);
+                    acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc[1][1], 0, 0, 0);
+                }
+                if (s + 1 < KSTEPS) sstore(buf ^ 1, ra[(u + 1) % PF], rb[(u + 1) % PF]);
+                __syncthreads();
+            }
         }
-        if (s + 1 < KSTEPS) sstore(buf ^ 1);
-        __syncthreads();
     }
 
     // accumulators -> LDS tile (the loop's last barrier freed the K buffers)
@@ -395,9 +415,9 @@ namespace {
 
 typedef void (*launch_fn)(const ConvArgs&, int grid, hipStream_t);
 
-template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN>
+template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN, int PF>
 void launch_conv(const ConvArgs& a, int grid, hipStream_t s) {
-    hipLaunchKernelGGL((conv_i8_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, BM, BN>), dim3(grid),
+    hipLaunchKernelGGL((conv_i8_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, BM, BN, PF>), dim3(grid),
                        dim3(256), 0, s, a);
 }
 
@@ -411,7 +431,7 @@ struct ConvEntry {
 };
 
 #define FF_CONV(CIN, COUT, KS, S, H, BM, BN) \
-    {CIN, COUT, KS, S, H, H, BM, BN, &launch_conv<CIN, COUT, KS, S, H, H, BM, BN>}
+    {CIN, COUT, KS, S, H, H, BM, BN, &launch_conv<CIN, COUT, KS, S, H, H, BM, BN, FF_PF>}
 
 const ConvEntry kConvTable[] = {
     {3, 64, 3, 1, 112, 112, 128, 64, &launch_stem},
@@ -463,7 +483,7 @@ int ffk_fc_gemm_launch(const ffk_fc_desc* d, hipStream_t s) {
     a.in_scale = d->a_scale;
     a.tiles_n = 512 / 128;
     const int grid = ((d->batch + 127) / 128) * a.tiles_n;
-    hipLaunchKernelGGL((conv_i8_kernel<25088, 512, 1, 1, 1, 1, 128, 128>), dim3(grid), dim3(256),
+    hipLaunchKernelGGL((conv_i8_kernel<25088, 512, 1, 1, 1, 1, 128, 128, FF_PF>), dim3(grid), dim3(256),
                        0, s, a);
     return ffk_check_launch("fc gemm launch");
 }

@@ -1,0 +1,114 @@
+"""Single-layer microbenchmark of the int8 conv kernels through the C ABI.
+
+    python fastface_amd/layerbench.py --cin 256 --cout 256 --k 3 --stride 1 --hin 14 \
+        --batch 64 --iters 200 [--epi prelu|add_bn|none|raw]
+
+Defaults are BASELINE config 2 (N=64, 14x14, 256->256, 3x3 s1 p1, PReLU
+epilogue).  Inputs are seeded random int8; prints one JSON line with the
+mean launch time (HIP events on the launch stream) and int8 TOP/s.  Also the
+workload rocprofv3 counter runs use, since it launches only the layer asked
+for.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+
+import numpy as np
+
+sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+import fastface_amd as fa  # noqa: E402
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--cin", type=int, default=256)
+    ap.add_argument("--cout", type=int, default=256)
+    ap.add_argument("--k", type=int, default=3)
+    ap.add_argument("--stride", type=int, default=1)
+    ap.add_argument("--hin", type=int, default=14)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--iters", type=int, default=200)
+    ap.add_argument("--epi", default="prelu", choices=["prelu", "add_bn", "none", "raw"])
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="instead: device-to-device copies of this many MiB (the calibration "
+                         "workload for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    a = ap.parse_args()
+    lib = fa.load()
+    if lib.ffk_device_count() <= 0:
+        raise RuntimeError("no HIP device")
+    if a.copy_mb:
+        n = a.copy_mb << 20
+        src, dst = lib.ffk_malloc(n), lib.ffk_malloc(n)
+        for _ in range(a.iters):
+            assert lib.ffk_memcpy_d2d(dst, src, n, None) == 0, fa.last_error()
+        lib.ffk_stream_sync(None)
+        print(json.dumps({"copy_bytes": n, "iters": a.iters}), flush=True)
+        return
+    pad = a.k // 2
+    ho = (a.hin + 2 * pad - a.k) // a.stride + 1
+    if not lib.ffk_conv_supported(a.cin, a.cout, a.k, a.k, a.stride, pad, a.hin, a.hin):
+        raise SystemExit("unsupported layer geometry")
+    r = np.random.default_rng(1)
+    x = r.integers(-127, 128, size=(a.batch, a.hin, a.hin, a.cin), dtype=np.int8)
+    w = r.integers(-127, 128, size=(a.cout, a.cin, a.k, a.k), dtype=np.int8)
+    packed = np.empty(lib.ffk_conv_packed_bytes(a.cin, a.cout, a.k, a.k), np.int8)
+    lib.ffk_pack_conv_weights(w.ctypes.data, a.cout, a.cin, a.k, a.k, packed.ctypes.data)
+    P = np.zeros((fa.FFK_NPARAM, a.cout), np.float32)
+    P[fa.FFK_P_WS] = r.uniform(1e-3, 1e-2, a.cout)
+    P[fa.FFK_P_BIAS] = r.normal(0, 0.1, a.cout)
+    P[fa.FFK_P_SLOPE] = 0.25
+    P[fa.FFK_P_ADDSCALE] = 0.02
+    P[fa.FFK_P_INV] = 1.0 / 40.0
+    P[fa.FFK_P_BN_SIN] = 0.02
+    P[fa.FFK_P_BN_S] = 1.0
+    P[fa.FFK_P_BN_INV] = 50.0
+
+    def dev(arr=None, nbytes=None):
+        n = arr.nbytes if arr is not None else nbytes
+        p = lib.ffk_malloc(n)
+        if arr is not None:
+            lib.ffk_memcpy_h2d(p, arr.ctypes.data, n, None)
+        return p
+    n_out = a.batch * ho * ho * a.cout
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw = a.batch, a.cin, a.cout, a.k, a.k
+    d.stride, d.pad, d.hin, d.win = a.stride, pad, a.hin, a.hin
+    d.in_ = dev(x)
+    d.w = dev(packed)
+    d.params = dev(P)
+    d.flags = fa.FFK_EPI_BIAS
+    if a.epi == "raw":
+        d.out_i32 = dev(nbytes=n_out * 4)
+    else:
+        d.out = dev(nbytes=n_out)
+    if a.epi == "prelu":
+        d.flags |= fa.FFK_EPI_PRELU
+    if a.epi == "add_bn":
+        d.flags |= fa.FFK_EPI_ADD | fa.FFK_EPI_BN
+        d.add_src = dev(r.integers(-127, 128, size=n_out, dtype=np.int8))
+        d.out_bn = dev(nbytes=n_out)
+    stream = C.c_void_p()
+    lib.ffk_stream_create(C.byref(stream))
+    for _ in range(3):
+        assert lib.ffk_conv(C.byref(d), stream) == 0, fa.last_error()
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    lib.ffk_event_create(C.byref(e0))
+    lib.ffk_event_create(C.byref(e1))
+    lib.ffk_event_record(e0, stream)
+    for _ in range(a.iters):
+        lib.ffk_conv(C.byref(d), stream)
+    lib.ffk_event_record(e1, stream)
+    ms = C.c_float()
+    assert lib.ffk_event_elapsed_ms(e0, e1, C.byref(ms)) == 0, fa.last_error()
+    per = ms.value / a.iters
+    ops = 2.0 * a.batch * ho * ho * a.cout * a.k * a.k * a.cin
+    print(json.dumps({"layer": "%d->%d k%d s%d @%d" % (a.cin, a.cout, a.k, a.stride, a.hin),
+                      "batch": a.batch, "epi": a.epi, "ms_per_launch": round(per, 5),
+                      "int8_tops": round(ops / (per * 1e-3) / 1e12, 2),
+                      "frac_of_peak": round(ops / (per * 1e-3) / 5e15, 4)}), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -35,7 +35,8 @@ class ffk_conv_desc(C.Structure):
     _fields_ = [("batch", C.c_int), ("cin", C.c_int), ("cout", C.c_int), ("kh", C.c_int),
                 ("kw", C.c_int), ("stride", C.c_int), ("pad", C.c_int), ("hin", C.c_int),
                 ("win", C.c_int), ("in_", _p), ("in_inv", _p), ("io", _p), ("w", _p),
-                ("params", _p), ("add_src", _p), ("out", _p), ("out_bn", _p), ("out_i32", _p),
+                ("params", _p), ("add_src", _p), ("bn_lut", _p), ("out", _p), ("out_bn", _p),
+                ("out_i32", _p),
                 ("flags", C.c_int), ("in_scale", C.c_float)]
 
 
@@ -94,6 +95,7 @@ EXPORTS = [
     ("ffk_conv_packed_bytes", C.c_size_t, [C.c_int] * 4),
     ("ffk_pack_conv_weights", C.c_int, [_p, C.c_int, C.c_int, C.c_int, C.c_int, _p]),
     ("ffk_conv", C.c_int, [C.POINTER(ffk_conv_desc), _p]),
+    ("ffk_make_bn_lut", C.c_int, [_p, _p, _p, _p, C.c_int, _p]),
     ("ffk_fc_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("ffk_pack_fc_weights", C.c_int, [_p, C.c_int, C.c_int, _p]),
     ("ffk_fc", C.c_int, [C.POINTER(ffk_fc_desc), _p]),

@@ -9,15 +9,21 @@
 // MFMA needs no correction, and integer sums do not depend on their order,
 // so the accumulators are bit-identical.
 //
-// Workgroup = 4 wave64s computing a BM x BN tile (each wave a 64x64 block of
-// 2x2 MFMA 32x32 tiles).  Per K step of 64 bytes each thread fetches 16-byte
-// pieces of the implicit im2col rows (one input pixel's channel run, zero for
-// padding) and of the packed weights, stages them through a double-buffered
-// LDS tile (80-byte row pitch: conflict-free ds_read_b128 of MFMA operands),
-// and the next step's global loads are in flight while MFMAs run.  After the
-// K loop the int32 tile goes through LDS once more so that every thread
-// requantizes 16 consecutive channels of one pixel and writes them with one
-// 16-byte store (plus one for the BN second output).
+// K loop: workgroup = 4 wave64s computing a BM x BN tile (each wave a 64x64
+// block of 2x2 MFMA 32x32 tiles).  Per K step of 64 bytes each thread fetches
+// 16-byte pieces of the implicit im2col rows (one input pixel's channel run;
+// padding taps read a zero page, so there are no branches) and of the packed
+// weights.  PF steps of loads are in flight in registers; each step is staged
+// through a double-buffered LDS tile whose 80-byte row pitch makes the
+// ds_read_b128 MFMA operand reads conflict-free.
+//
+// Epilogue straight from the accumulator registers: in the 32x32 MFMA result
+// every lane owns one output channel (column) and 16 pixels (rows), so each
+// lane needs the per-channel parameters of only NJ = 2 channels.  The int8
+// results go through a small per-wave LDS byte tile only to leave as
+// coalesced 16-byte stores.  The BN second output is a per-channel 256-entry
+// table lookup (BN is a fixed function of the int8 value; the table is built
+// bit-exactly on the host, ffk_make_bn_lut).
 #include "ff_internal.h"
 #include "ff_numerics.h"
 
@@ -28,6 +34,11 @@
 #define FF_PF 4
 #endif
 
+constexpr int FF_LUT_PITCH = 272;   // LDS row pitch of a 256-entry table
+
+// 64 zero bytes: the source of every padding tap / out-of-range row load
+__device__ __align__(64) int8_t ff_zero_page[64];
+
 struct ConvArgs {
     const int8_t* in;
     const float* in_f32;
@@ -36,6 +47,7 @@ struct ConvArgs {
     const int8_t* w;
     const float* params;
     const int8_t* add_src;
+    const int8_t* bn_lut;
     int8_t* out;
     int8_t* out_bn;
     int32_t* out_i32;
@@ -49,138 +61,164 @@ struct ConvArgs {
 };
 
 // ---------------------------------------------------------------------------
-// Epilogue: C tile (int32, LDS, row pitch BN+8) -> int8 / fp32 / int32 HBM.
+// Epilogue of one wave's MI x NJ block of 32x32 MFMA tiles.
+//   mrow0: global pixel index of the block's first row
+//   ncol0: global output channel of the block's first column
+//   Ws:    wave-private LDS byte tile [MI*32][80]
+//   Lw:    BN table of channel ncol0 (row pitch FF_LUT_PITCH) or null
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void load16f(float (&d)[16], const float* p) {
-    const float4* q = reinterpret_cast<const float4*>(p);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float4 v = q[i];
-        d[4 * i + 0] = v.x; d[4 * i + 1] = v.y; d[4 * i + 2] = v.z; d[4 * i + 3] = v.w;
-    }
-}
-
-template <int BM, int BN, int COUT, bool PRELU, bool ADD, bool BN2>
-__device__ __forceinline__ void epi_requant(const int32_t* Cs, const ConvArgs& a, int m0, int nt0) {
-    constexpr int CST = BN + 8;
-    constexpr int GROUPS = BN / 16;
-    constexpr int RSTEP = 256 / GROUPS;
-    const int tid = threadIdx.x;
-    const int cg = tid % GROUPS;
-    const int n0 = nt0 + cg * 16;
+template <int COUT, int MI, int NJ, bool PRELU, bool ADD, bool BN2>
+__device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a, int mrow0,
+                                            int ncol0, int8_t* Ws, const int8_t* Lw) {
+    constexpr int P = 80;
+    constexpr int ROWS = MI * 32;
+    constexpr int CH = NJ * 2;          // 16-byte chunks per tile row
+    constexpr int RPI = 64 / CH;        // tile rows per copy instruction
+    static_assert(NJ * 32 <= 64, "tile row must fit the 80-byte pitch");
+    const int lane = threadIdx.x & 63;
+    const int lc = lane & 31;
+    const int lh = lane >> 5;
     const bool inscale = (a.flags & FFK_EPI_INSCALE) != 0;
-    const float in_scale = a.in_scale;
-    float ws[16], bias[16], p2[16], inv[16];
-    float bsin[16], bs[16], bo[16], binv[16];
-    load16f(ws, a.params + FFK_P_WS * COUT + n0);
-    load16f(bias, a.params + FFK_P_BIAS * COUT + n0);
-    load16f(inv, a.params + FFK_P_INV * COUT + n0);
-    if (PRELU) load16f(p2, a.params + FFK_P_SLOPE * COUT + n0);
-    float adds[16];
-    if (ADD) load16f(adds, a.params + FFK_P_ADDSCALE * COUT + n0);
-    if (BN2) {
-        load16f(bsin, a.params + FFK_P_BN_SIN * COUT + n0);
-        load16f(bs, a.params + FFK_P_BN_S * COUT + n0);
-        load16f(bo, a.params + FFK_P_BN_O * COUT + n0);
-        load16f(binv, a.params + FFK_P_BN_INV * COUT + n0);
+    float ws[NJ], bias[NJ], p2[NJ], adds[NJ], inv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int c = ncol0 + j * 32 + lc;
+        ws[j] = a.params[FFK_P_WS * COUT + c];
+        bias[j] = a.params[FFK_P_BIAS * COUT + c];
+        inv[j] = a.params[FFK_P_INV * COUT + c];
+        p2[j] = PRELU ? a.params[FFK_P_SLOPE * COUT + c] : 0.0f;
+        adds[j] = ADD ? a.params[FFK_P_ADDSCALE * COUT + c] : 0.0f;
     }
-    for (int row = tid / GROUPS; row < BM; row += RSTEP) {
-        const int m = m0 + row;
-        if (m >= a.M) break;
-        int32_t acc[16];
-        {
-            const v4i* src = reinterpret_cast<const v4i*>(Cs + row * CST + cg * 16);
+    if (ADD) {      // residual tile -> LDS (coalesced 16-byte loads)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v4i v = src[i];
-                acc[4 * i] = v.x; acc[4 * i + 1] = v.y; acc[4 * i + 2] = v.z; acc[4 * i + 3] = v.w;
-            }
+        for (int k = 0; k < ROWS / RPI; k++) {
+            const int row = lane / CH + k * RPI;
+            const int ch = lane % CH;
+            const int m = mrow0 + row;
+            const int8_t* src = m < a.M ? a.add_src + (size_t)m * COUT + ncol0 + ch * 16 : ff_zero_page;
+            *reinterpret_cast<v4i*>(Ws + row * P + ch * 16) = *reinterpret_cast<const v4i*>(src);
         }
-        const size_t off = (size_t)m * COUT + n0;
-        v4i addv = {0, 0, 0, 0};
-        if (ADD) addv = *reinterpret_cast<const v4i*>(a.add_src + off);
-        uint32_t qw[4] = {0, 0, 0, 0}, bw[4] = {0, 0, 0, 0};
+        __syncthreads();
+    }
+    uint32_t bnw[MI][NJ][4];
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            float f = (float)acc[e];
-            if (inscale) f = f * in_scale;
-            f = f * ws[e];
-            f = f + bias[e];
-            if (ADD) {
-                int32_t ai = (int32_t)(int8_t)((uint32_t)addv[e >> 2] >> ((e & 3) * 8));
-                f = ff::add_residual(f, ai, adds[e]);
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+                const int col = j * 32 + lc;
+                float f = (float)acc[i][j][r];
+                if (inscale) f = f * a.in_scale;
+                f = f * ws[j];
+                f = f + bias[j];
+                if (ADD) f = ff::add_residual(f, (int32_t)Ws[row * P + col], adds[j]);
+                if (PRELU) f = ff::prelu(f, p2[j]);
+                const int32_t q = ff::requant_haz(f * inv[j]);
+                Ws[row * P + col] = (int8_t)q;
+                if (BN2) {
+                    if ((r & 3) == 0) bnw[i][j][r >> 2] = 0;
+                    const uint32_t q2 = (uint8_t)Lw[col * FF_LUT_PITCH + q + 128];
+                    bnw[i][j][r >> 2] |= q2 << ((r & 3) * 8);
+                }
             }
-            if (PRELU) f = ff::prelu(f, p2[e]);
-            const int32_t q = ff::requant_haz(f * inv[e]);
-            qw[e >> 2] |= ((uint32_t)q & 0xffu) << ((e & 3) * 8);
-            if (BN2) {
-                const int32_t q2 = ff::bn_requant(q, bsin[e], bs[e], bo[e], binv[e]);
-                bw[e >> 2] |= ((uint32_t)q2 & 0xffu) << ((e & 3) * 8);
-            }
-        }
-        if (a.out) {
-            v4i o = {(int)qw[0], (int)qw[1], (int)qw[2], (int)qw[3]};
-            *reinterpret_cast<v4i*>(a.out + off) = o;
-        }
-        if (BN2) {
-            v4i o = {(int)bw[0], (int)bw[1], (int)bw[2], (int)bw[3]};
-            *reinterpret_cast<v4i*>(a.out_bn + off) = o;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < ROWS / RPI; k++) {
+        const int row = lane / CH + k * RPI;
+        const int ch = lane % CH;
+        const int m = mrow0 + row;
+        const v4i v = *reinterpret_cast<const v4i*>(Ws + row * P + ch * 16);
+        if (a.out && m < a.M) *reinterpret_cast<v4i*>(a.out + (size_t)m * COUT + ncol0 + ch * 16) = v;
+    }
+    if (BN2) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+                    Ws[row * P + j * 32 + lc] = (int8_t)(bnw[i][j][r >> 2] >> ((r & 3) * 8));
+                }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < ROWS / RPI; k++) {
+            const int row = lane / CH + k * RPI;
+            const int ch = lane % CH;
+            const int m = mrow0 + row;
+            const v4i v = *reinterpret_cast<const v4i*>(Ws + row * P + ch * 16);
+            if (m < a.M) *reinterpret_cast<v4i*>(a.out_bn + (size_t)m * COUT + ncol0 + ch * 16) = v;
         }
     }
 }
 
-template <int BM, int BN, int COUT>
-__device__ __forceinline__ void epi_raw_or_fc(const int32_t* Cs, const ConvArgs& a, int m0, int nt0) {
-    constexpr int CST = BN + 8;
-    constexpr int GROUPS = BN / 16;
-    constexpr int RSTEP = 256 / GROUPS;
-    const int tid = threadIdx.x;
-    const int cg = tid % GROUPS;
-    const int n0 = nt0 + cg * 16;
+// raw int32 accumulators or the FC head's fp32 output: 4-byte elements are
+// stored straight from registers (a half-wave writes 128 contiguous bytes)
+template <int COUT, int MI, int NJ>
+__device__ __forceinline__ void wave_epi_wide(const v16i (&acc)[MI][NJ], const ConvArgs& a, int mrow0,
+                                              int ncol0) {
+    const int lane = threadIdx.x & 63;
+    const int lc = lane & 31;
+    const int lh = lane >> 5;
     if (a.out_i32) {
-        for (int row = tid / GROUPS; row < BM; row += RSTEP) {
-            const int m = m0 + row;
-            if (m >= a.M) break;
-            const v4i* src = reinterpret_cast<const v4i*>(Cs + row * CST + cg * 16);
-            v4i* dst = reinterpret_cast<v4i*>(a.out_i32 + (size_t)m * COUT + n0);
 #pragma unroll
-            for (int i = 0; i < 4; i++) dst[i] = src[i];
-        }
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int m = mrow0 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+                    if (m < a.M) a.out_i32[(size_t)m * COUT + ncol0 + j * 32 + lc] = acc[i][j][r];
+                }
         return;
     }
-    // FC head: out = fma(RN(dot * a_scale), ws, bias), fp32
-    float ws[16], bias[16];
-    load16f(ws, a.fc_ws + n0);
-    load16f(bias, a.fc_bias + n0);
     float* out = a.out_f32 ? a.out_f32 : a.io->out;
-    for (int row = tid / GROUPS; row < BM; row += RSTEP) {
-        const int m = m0 + row;
-        if (m >= a.M) break;
-        const int32_t* src = Cs + row * CST + cg * 16;
-        float r[16];
 #pragma unroll
-        for (int e = 0; e < 16; e++) r[e] = ff::fc_out(src[e], a.in_scale, ws[e], bias[e]);
-        float4* dst = reinterpret_cast<float4*>(out + (size_t)m * COUT + n0);
+    for (int j = 0; j < NJ; j++) {
+        const int c = ncol0 + j * 32 + lc;
+        const float ws = a.fc_ws[c], bias = a.fc_bias[c];
 #pragma unroll
-        for (int i = 0; i < 4; i++) dst[i] = make_float4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = mrow0 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+                if (m < a.M) out[(size_t)m * COUT + c] = ff::fc_out(acc[i][j][r], a.in_scale, ws, bias);
+            }
     }
 }
 
-template <int BM, int BN, int COUT>
-__device__ __forceinline__ void tile_epilogue(const int32_t* Cs, const ConvArgs& a, int m0, int nt0) {
+template <int COUT, int MI, int NJ>
+__device__ __forceinline__ void wave_epilogue(const v16i (&acc)[MI][NJ], const ConvArgs& a, int mrow0,
+                                              int ncol0, int8_t* Ws, const int8_t* Lw) {
     if (a.out_i32 || (a.flags & EPI_FC)) {
-        epi_raw_or_fc<BM, BN, COUT>(Cs, a, m0, nt0);
+        wave_epi_wide<COUT, MI, NJ>(acc, a, mrow0, ncol0);
         return;
     }
     switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN)) {
-    case 0: epi_requant<BM, BN, COUT, false, false, false>(Cs, a, m0, nt0); break;
-    case FFK_EPI_PRELU: epi_requant<BM, BN, COUT, true, false, false>(Cs, a, m0, nt0); break;
-    case FFK_EPI_ADD: epi_requant<BM, BN, COUT, false, true, false>(Cs, a, m0, nt0); break;
-    case FFK_EPI_BN: epi_requant<BM, BN, COUT, false, false, true>(Cs, a, m0, nt0); break;
-    case FFK_EPI_PRELU | FFK_EPI_BN: epi_requant<BM, BN, COUT, true, false, true>(Cs, a, m0, nt0); break;
-    case FFK_EPI_ADD | FFK_EPI_BN: epi_requant<BM, BN, COUT, false, true, true>(Cs, a, m0, nt0); break;
-    case FFK_EPI_PRELU | FFK_EPI_ADD: epi_requant<BM, BN, COUT, true, true, false>(Cs, a, m0, nt0); break;
-    default: epi_requant<BM, BN, COUT, true, true, true>(Cs, a, m0, nt0); break;
+    case 0: wave_epi_i8<COUT, MI, NJ, false, false, false>(acc, a, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_PRELU: wave_epi_i8<COUT, MI, NJ, true, false, false>(acc, a, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_ADD: wave_epi_i8<COUT, MI, NJ, false, true, false>(acc, a, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_BN: wave_epi_i8<COUT, MI, NJ, false, false, true>(acc, a, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_PRELU | FFK_EPI_BN:
+        wave_epi_i8<COUT, MI, NJ, true, false, true>(acc, a, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_ADD | FFK_EPI_BN:
+        wave_epi_i8<COUT, MI, NJ, false, true, true>(acc, a, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_PRELU | FFK_EPI_ADD:
+        wave_epi_i8<COUT, MI, NJ, true, true, false>(acc, a, mrow0, ncol0, Ws, Lw); break;
+    default: wave_epi_i8<COUT, MI, NJ, true, true, true>(acc, a, mrow0, ncol0, Ws, Lw); break;
+    }
+}
+
+// BN tables of channels [c0, c0 + nch) -> LDS (pitch FF_LUT_PITCH)
+template <int NT>
+__device__ __forceinline__ void load_bn_lut(int8_t* Ls, const int8_t* lut, int c0, int nch) {
+    for (int idx = threadIdx.x; idx < nch * 16; idx += NT) {
+        const int c = idx >> 4, piece = idx & 15;
+        *reinterpret_cast<v4i*>(Ls + c * FF_LUT_PITCH + piece * 16) =
+            *reinterpret_cast<const v4i*>(lut + (size_t)(c0 + c) * 256 + piece * 16);
     }
 }
 
@@ -208,8 +246,8 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
     constexpr int B_LD = BN * 4 / 256;
     constexpr int WN = BN / 64;
     constexpr int LDS_K = 2 * (BM + BN) * ROWB;
-    constexpr int LDS_C = BM * (BN + 8) * 4;
-    constexpr int LDS = LDS_K > LDS_C ? LDS_K : LDS_C;
+    constexpr int LDS_E = 4 * 64 * 80 + BN * FF_LUT_PITCH;
+    constexpr int LDS = LDS_K > LDS_E ? LDS_K : LDS_E;
     static_assert(CIN % FF_KSTEP == 0, "Cin must be a multiple of 64");
     static_assert((BM / 64) * (BN / 64) == 4, "4 waves of 64x64");
     static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
@@ -259,10 +297,9 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
         for (int j = 0; j < A_LD; j++) {
             const int ih = a_ih0[j] + kh;
             const int iw = a_iw0[j] + kw;
-            if (a_ok[j] && (unsigned)ih < (unsigned)HIN && (unsigned)iw < (unsigned)WIN)
-                qa[j] = *reinterpret_cast<const v4i*>(a_img[j] + (ih * WIN + iw) * CIN + cs * FF_KSTEP);
-            else
-                qa[j] = v4i{0, 0, 0, 0};
+            const bool v = a_ok[j] && (unsigned)ih < (unsigned)HIN && (unsigned)iw < (unsigned)WIN;
+            const int8_t* src = v ? a_img[j] + (ih * WIN + iw) * CIN + cs * FF_KSTEP : ff_zero_page;
+            qa[j] = *reinterpret_cast<const v4i*>(src);
         }
 #pragma unroll
         for (int j = 0; j < B_LD; j++)
@@ -328,50 +365,70 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
         }
     }
 
-    // accumulators -> LDS tile (the loop's last barrier freed the K buffers)
-    int32_t* Cs = reinterpret_cast<int32_t*>(smem);
-    constexpr int CST = BN + 8;
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                const int col = wn * 64 + j * 32 + (lane & 31);
-                Cs[row * CST + col] = acc[i][j][r];
-            }
-    __syncthreads();
-    tile_epilogue<BM, BN, COUT>(Cs, a, m0, tn * BN);
+    // epilogue (the loop's last barrier freed the K buffers)
+    int8_t* Ws = smem + wave * (64 * 80);
+    int8_t* Ls = smem + 4 * 64 * 80;
+    if (a.flags & FFK_EPI_BN && !a.out_i32) {
+        load_bn_lut<256>(Ls, a.bn_lut, tn * BN, BN);
+        __syncthreads();
+    }
+    wave_epilogue<COUT, 2, 2>(acc, a, m0 + wm * 64, tn * BN + wn * 64, Ws,
+                              Ls + (wn * 64) * FF_LUT_PITCH);
 }
 
 // ---------------------------------------------------------------------------
-// Stem: 3 -> 64, 3x3, s1, p1 at 112x112 reading the fp32 faces directly and
-// quantizing each tap on load (quantize_fp32_nhwc_to_int8_per_channel fused
-// into the conv, int8_epilogue.c:231-247).  K = 27 is padded to one 32-deep
-// MFMA; each lane gathers the 16 taps of its K half for its output pixel.
+// Stem: 3 -> 64, 3x3, s1, p1 at 112x112, reading the fp32 faces.  One
+// workgroup = two output rows of one face (224 pixels = 7 waves x 32 rows,
+// all 64 channels).  The four input rows it needs are quantized once into
+// LDS (quantize_fp32_nhwc_to_int8_per_channel fused into the conv,
+// int8_epilogue.c:231-247); K = 27 is zero-padded to one 32-deep MFMA whose
+// operands are gathered from that LDS patch.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 2) void stem_kernel(ConvArgs a) {
-    constexpr int BM = 128, BN = 64, COUT = 64, H = 112, W = 112, HW = H * W;
-    constexpr int CST = BN + 8;
-    __shared__ __align__(16) int32_t Cs[BM * CST];
+constexpr int STEM_WAVES = 7;
+constexpr int STEM_NT = STEM_WAVES * 64;
+
+__global__ __launch_bounds__(STEM_NT, 1) void stem_kernel(ConvArgs a) {
+    constexpr int COUT = 64, H = 112, W = 112, HW = H * W;
+    constexpr int PW = W + 2;                       // patch row: 114 pixels x 4 bytes
+    constexpr int PATCH = 4 * PW * 4;
+    __shared__ __align__(16) int8_t Ps[PATCH];
+    __shared__ __align__(16) int8_t Es[STEM_WAVES * 32 * 80 + COUT * FF_LUT_PITCH];
+    int8_t* Ls = Es + STEM_WAVES * 32 * 80;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int m0 = xcd_tile(blockIdx.x, gridDim.x) * BM;
-    const int m = m0 + wave * 32 + (lane & 31);
-    const bool ok = m < a.M;
-    const int mm = ok ? m : 0;
-    const int b = mm / HW;
-    const int r = mm - b * HW;
-    const int oh = r / W;
-    const int ow = r - oh * W;
+    const int t = xcd_tile(blockIdx.x, gridDim.x);   // one tile = 2 output rows
+    const int b = t / (H / 2);
+    const int oh0 = (t - b * (H / 2)) * 2;
+    const int m0 = b * HW + oh0 * W;
     const float* x = a.in_f32 ? a.in_f32 : a.io->in;
     const float* img = x + (size_t)b * HW * 3;
-    const float inv[3] = {a.in_inv[0], a.in_inv[1], a.in_inv[2]};
-    const int g = lane >> 5;
+    const float inv0 = a.in_inv[0], inv1 = a.in_inv[1], inv2 = a.in_inv[2];
 
+    // input rows oh0-1 .. oh0+2, columns -1 .. 112, channels 0..2 (+1 zero)
+    for (int e = tid; e < PATCH; e += STEM_NT) {
+        const int pr = e / (PW * 4);
+        const int rem = e - pr * (PW * 4);
+        const int pc = rem >> 2;
+        const int ci = rem & 3;
+        const int ih = oh0 - 1 + pr;
+        const int iw = pc - 1;
+        int8_t q = 0;
+        if (ci < 3 && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W && b * HW < a.M) {
+            const float v = img[(ih * W + iw) * 3 + ci];
+            q = (int8_t)ff::quant_input(v, ci == 0 ? inv0 : (ci == 1 ? inv1 : inv2));
+        }
+        Ps[e] = q;
+    }
+    if (a.flags & FFK_EPI_BN && !a.out_i32) load_bn_lut<STEM_NT>(Ls, a.bn_lut, 0, COUT);
+    __syncthreads();
+
+    // A operand: lane -> pixel (row of the MFMA tile) and K half g
+    const int p = wave * 32 + (lane & 31);           // 0..223
+    const int orow = p / W;
+    const int ow = p - orow * W;
+    const int g = lane >> 5;
     uint32_t aw[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int e = 0; e < 16; e++) {
@@ -379,32 +436,21 @@ __global__ __launch_bounds__(256, 2) void stem_kernel(ConvArgs a) {
         if (k < 27) {
             const int tap = k / 3;
             const int ci = k - tap * 3;
-            const int ih = oh - 1 + tap / 3;
-            const int iw = ow - 1 + (tap - (tap / 3) * 3);
-            if (ok && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) {
-                const float v = img[(ih * W + iw) * 3 + ci];
-                const float s = ci == 0 ? inv[0] : (ci == 1 ? inv[1] : inv[2]);
-                const int32_t q = ff::quant_input(v, s);
-                aw[e >> 2] |= ((uint32_t)q & 0xffu) << ((e & 3) * 8);
-            }
+            const int kh = tap / 3;
+            const int kw = tap - kh * 3;
+            const uint32_t q = (uint8_t)Ps[((orow + kh) * PW + ow + kw) * 4 + ci];
+            aw[e >> 2] |= q << ((e & 3) * 8);
         }
     }
     const v4i av = {(int)aw[0], (int)aw[1], (int)aw[2], (int)aw[3]};
     const v4i b0 = *reinterpret_cast<const v4i*>(a.w + (lane & 31) * FF_KSTEP + g * 16);
     const v4i b1 = *reinterpret_cast<const v4i*>(a.w + (32 + (lane & 31)) * FF_KSTEP + g * 16);
-    v16i zero;
+    v16i acc[1][2];
 #pragma unroll
-    for (int i = 0; i < 16; i++) zero[i] = 0;
-    const v16i c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, zero, 0, 0, 0);
-    const v16i c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, zero, 0, 0, 0);
-#pragma unroll
-    for (int rr = 0; rr < 16; rr++) {
-        const int row = wave * 32 + (rr >> 2) * 8 + (lane >> 5) * 4 + (rr & 3);
-        Cs[row * CST + (lane & 31)] = c0[rr];
-        Cs[row * CST + 32 + (lane & 31)] = c1[rr];
-    }
-    __syncthreads();
-    tile_epilogue<BM, BN, COUT>(Cs, a, m0, 0);
+    for (int r = 0; r < 16; r++) { acc[0][0][r] = 0; acc[0][1][r] = 0; }
+    acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, acc[0][0], 0, 0, 0);
+    acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, acc[0][1], 0, 0, 0);
+    wave_epilogue<COUT, 1, 2>(acc, a, m0 + wave * 32, 0, Es + wave * (32 * 80), Ls);
 }
 
 // ---------------------------------------------------------------------------
@@ -422,7 +468,9 @@ void launch_conv(const ConvArgs& a, int grid, hipStream_t s) {
 }
 
 void launch_stem(const ConvArgs& a, int grid, hipStream_t s) {
-    hipLaunchKernelGGL(stem_kernel, dim3(grid), dim3(256), 0, s, a);
+    (void)grid;
+    const int tiles = a.M / (112 * 2);
+    hipLaunchKernelGGL(stem_kernel, dim3(tiles), dim3(STEM_NT), 0, s, a);
 }
 
 struct ConvEntry {
@@ -434,7 +482,7 @@ struct ConvEntry {
     {CIN, COUT, KS, S, H, H, BM, BN, &launch_conv<CIN, COUT, KS, S, H, H, BM, BN, FF_PF>}
 
 const ConvEntry kConvTable[] = {
-    {3, 64, 3, 1, 112, 112, 128, 64, &launch_stem},
+    {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem},
     FF_CONV(64, 64, 3, 1, 112, 256, 64),
     FF_CONV(64, 64, 3, 2, 112, 256, 64),
     FF_CONV(64, 64, 1, 2, 112, 256, 64),
@@ -468,7 +516,7 @@ const ConvEntry* find_conv(int cin, int cout, int kh, int kw, int stride, int pa
 // Cin = K): M = batch faces, N = 512, K = 25088.
 int ffk_fc_gemm_launch(const ffk_fc_desc* d, hipStream_t s) {
     if (d->n != 512 || d->k != 25088) {
-        ffk_set_error("fc gemm: unsupported shape n=%s k=%s", "?", "?");
+        ffk_set_error("fc gemm: unsupported shape (n must be 512, k 25088)%s%s", nullptr, nullptr);
         return FFK_ERR_UNSUPPORTED;
     }
     ConvArgs a = {};
@@ -545,7 +593,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
                (!stem && !d->in);
     if (!raw) {
         if ((d->flags & FFK_EPI_ADD) && !d->add_src) bad = true;
-        if ((d->flags & FFK_EPI_BN) && !d->out_bn) bad = true;
+        if ((d->flags & FFK_EPI_BN) && (!d->out_bn || !d->bn_lut)) bad = true;
         if (!(d->flags & FFK_EPI_BN) && !d->out) bad = true;
     }
     if (bad) {
@@ -561,6 +609,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     a.w = d->w;
     a.params = d->params;
     a.add_src = d->add_src;
+    a.bn_lut = d->bn_lut;
     a.out = d->out;
     a.out_bn = d->out_bn;
     a.out_i32 = d->out_i32;
@@ -571,6 +620,32 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     const int tiles_m = (int)((M + e->bm - 1) / e->bm);
     e->fn(a, tiles_m * a.tiles_n, (hipStream_t)stream);
     return ffk_check_launch("conv launch");
+}
+
+// BN second output as a table: lut[c][q + 128] = BN-requant of the int8
+// value q for channel c, computed with the reference's fp32 sequence
+// (bn_prelu_requant_int8 with bn != NULL, int8_epilogue.c:273-303):
+//   f = fma(RN(q * s_in), bn_s, bn_o); round half away of RN(f * inv);
+//   x86 cvttps2dq semantics; clamp to int8.
+int ffk_make_bn_lut(const float* s_in, const float* bn_s, const float* bn_o, const float* bn_inv,
+                    int cout, int8_t* lut) {
+    if (!s_in || !bn_s || !bn_o || !bn_inv || !lut || cout <= 0) {
+        ffk_set_error("make_bn_lut: bad arguments%s%s", nullptr, nullptr);
+        return FFK_ERR_ARG;
+    }
+    for (int c = 0; c < cout; c++)
+        for (int q = -128; q < 128; q++) {
+            volatile float f = (float)q * s_in[c];
+            f = __builtin_fmaf(f, bn_s[c], bn_o[c]);
+            volatile float t = f * bn_inv[c];
+            volatile float r = t + __builtin_copysignf(0.5f, t);
+            int32_t v;
+            if (r >= -2147483648.0f && r < 2147483648.0f) v = (int32_t)r;
+            else v = INT32_MIN;
+            v = v < -128 ? -128 : (v > 127 ? 127 : v);
+            lut[(size_t)c * 256 + (q + 128)] = (int8_t)v;
+        }
+    return FFK_OK;
 }
 
 }  // extern "C"

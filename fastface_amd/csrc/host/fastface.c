@@ -131,6 +131,7 @@ static int launch_step(FastFace* ff, int s, int batch, void* stream)
         d.add_src = tensor_ptr(ff, st->t_add);
         d.out = tensor_ptr(ff, st->t_out);
         d.out_bn = tensor_ptr(ff, st->t_bn);
+        if (st->flags & FFK_EPI_BN) d.bn_lut = ff->d_weights + st->lut_off;
         d.flags = st->flags;
         d.in_scale = st->in_scale;
         return ffk_conv(&d, stream);

@@ -56,6 +56,7 @@ typedef struct {
     int flags; float in_scale;
     size_t w_off;               /* bytes into the weight arena */
     size_t p_off;               /* floats into the parameter arena */
+    size_t lut_off;             /* bytes into the weight arena: BN table */
     /* fc */
     int fc_n, fc_k; float a_scale; size_t ws_off, bias_off;
 } FfStep;

@@ -252,6 +252,10 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
             fill_row(P + FFK_P_BN_O * C, C, op->bn_offset, 0.0f);
             fill_rowf(P + FFK_P_BN_INV * C, C, bn_inv, inv_of(next_scale));
             s->flags |= FFK_EPI_BN;
+            s->lut_off = alloc_weights(&B, (size_t)C * 256);
+            P = p->p_host + s->p_off;
+            ffk_make_bn_lut(P + FFK_P_BN_SIN * C, P + FFK_P_BN_S * C, P + FFK_P_BN_O * C,
+                            P + FFK_P_BN_INV * C, C, p->w_host + s->lut_off);
             const int Y = new_tensor(&B, C, si.H, si.W, i);
             p->tensors[Y].def_step = last_conv;
             s->t_bn = Y;

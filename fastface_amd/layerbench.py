@@ -89,6 +89,12 @@ def main():
         d.flags |= fa.FFK_EPI_ADD | fa.FFK_EPI_BN
         d.add_src = dev(r.integers(-127, 128, size=n_out, dtype=np.int8))
         d.out_bn = dev(nbytes=n_out)
+        lut = np.empty((a.cout, 256), np.int8)
+        rows = [np.ascontiguousarray(P[i]) for i in (fa.FFK_P_BN_SIN, fa.FFK_P_BN_S,
+                                                       fa.FFK_P_BN_O, fa.FFK_P_BN_INV)]
+        lib.ffk_make_bn_lut(rows[0].ctypes.data, rows[1].ctypes.data, rows[2].ctypes.data,
+                            rows[3].ctypes.data, a.cout, lut.ctypes.data)
+        d.bn_lut = dev(lut)
     stream = C.c_void_p()
     lib.ffk_stream_create(C.byref(stream))
     for _ in range(3):

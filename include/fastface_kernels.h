@@ -91,6 +91,7 @@ typedef struct {
     const int8_t*  w;        /* packed by ffk_pack_conv_weights               */
     const float*   params;   /* [FFK_NPARAM][cout]                            */
     const int8_t*  add_src;  /* FFK_EPI_ADD: int8 [batch,hout,wout,cout]      */
+    const int8_t*  bn_lut;   /* FFK_EPI_BN: [cout][256] from ffk_make_bn_lut  */
     int8_t*        out;      /* int8 output X, or NULL                        */
     int8_t*        out_bn;   /* FFK_EPI_BN: BN(X), or NULL                    */
     int32_t*       out_i32;  /* non-NULL: store raw int32 accumulators only   */
@@ -106,6 +107,12 @@ size_t ffk_conv_packed_bytes(int cin, int cout, int kh, int kw);
 int    ffk_pack_conv_weights(const int8_t* w_oihw, int cout, int cin, int kh, int kw,
                              int8_t* packed);
 int    ffk_conv(const ffk_conv_desc* d, void* stream);
+
+/* The BN second output as a table: lut[c*256 + q + 128] is the reference's
+ * BN requant (kernels/int8_epilogue.c:273-303 with bn != NULL) of the int8
+ * value q for channel c, from the FFK_P_BN_* rows (host function). */
+int    ffk_make_bn_lut(const float* s_in, const float* bn_s, const float* bn_o,
+                       const float* bn_inv, int cout, int8_t* lut);
 
 /* ---- FC head ----------------------------------------------------------
  * Replaces the XOR-0x80 shift + fastface_gemm_i8_matvec_vnni of the reference

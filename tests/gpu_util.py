@@ -57,6 +57,18 @@ def pack_conv(lib, w_oihw):
     return out
 
 
+def make_bn_lut(lib, params):
+    """[cout][256] BN table from the FFK_P_BN_* rows of a parameter block."""
+    P = np.ascontiguousarray(params, np.float32)
+    cout = P.shape[1]
+    lut = np.empty((cout, 256), np.int8)
+    rows = [np.ascontiguousarray(P[i]) for i in (fa.FFK_P_BN_SIN, fa.FFK_P_BN_S, fa.FFK_P_BN_O,
+                                                   fa.FFK_P_BN_INV)]
+    check(lib, lib.ffk_make_bn_lut(rows[0].ctypes.data, rows[1].ctypes.data, rows[2].ctypes.data,
+                                   rows[3].ctypes.data, cout, lut.ctypes.data))
+    return lut
+
+
 def params_block(cout, **rows):
     """[FFK_NPARAM][cout] fp32 block; rows by name (ws, bias, slope, adds, inv,
     bn_sin, bn_s, bn_o, bn_inv)."""
@@ -88,6 +100,10 @@ def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=Fa
     if params is not None:
         dp = Dev(lib, host=params); keep.append(dp)
         d.params = dp.ptr
+        if flags & fa.FFK_EPI_BN:
+            lut = make_bn_lut(lib, params)
+            dl = Dev(lib, host=lut); keep.append(dl)
+            d.bn_lut = dl.ptr
     if add is not None:
         da = Dev(lib, host=add); keep.append(da)
         d.add_src = da.ptr

@@ -62,6 +62,28 @@ def test_fc_weight_packing_layout():
     assert lib.ffk_pack_fc_weights(W.ctypes.data, 8, 100, packed.ctypes.data) != 0
 
 
+def test_bn_table_matches_oracle_bn_requant(oracle):
+    """The BN second output is a table over the 256 int8 values; every entry
+    equals the (reference-pinned) BN requant of that value."""
+    lib = fa.load()
+    r = np.random.default_rng(3)
+    C_ = 96
+    s_in = r.uniform(1e-3, 5e-2, C_).astype(np.float32)
+    s_in[0], s_in[1] = np.float32(3e-45), np.float32(1.2e-38)      # denormal / tiny
+    bns = r.uniform(0.5, 1.5, C_).astype(np.float32)
+    bns[2] = np.nan
+    bno = r.normal(0, 0.05, C_).astype(np.float32)
+    bno[3] = -0.0
+    inv = (1.0 / r.uniform(0.01, 0.1, C_)).astype(np.float32)
+    inv[4], inv[5] = 1e9, 3e38
+    lut = np.empty((C_, 256), np.int8)
+    assert lib.ffk_make_bn_lut(s_in.ctypes.data, bns.ctypes.data, bno.ctypes.data,
+                               inv.ctypes.data, C_, lut.ctypes.data) == 0
+    q = np.arange(-128, 128, dtype=np.int8).reshape(256, 1).repeat(C_, axis=1)
+    exp = oracle.bn_prelu_requant(q, in_scale_pc=s_in, bn_scale=bns, bn_offset=bno, inv_pc=inv)
+    assert np.array_equal(lut.T, exp)
+
+
 def test_every_iresnet_conv_has_a_kernel():
     lib = fa.load()
     H = 112

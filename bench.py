@@ -152,6 +152,16 @@ def main():
                           hin=info.hin, hout=info.hout, ops=info.ops_per_face,
                           act=info.act_bytes_per_face, wbytes=info.weight_bytes,
                           ms=float(step_ms[s])))
+    by_shape = {}
+    for st in steps:
+        key = "fc" if st["kind"] == 2 else "%d->%d k%d s%d @%d" % (st["cin"], st["cout"], st["k"],
+                                                                    st["s"], st["hin"])
+        e = by_shape.setdefault(key, [0, 0.0, st["ops"] * B])
+        e[0] += 1
+        e[1] += st["ms"]
+    for key, (n, tms, ops) in sorted(by_shape.items(), key=lambda kv: -kv[1][1]):
+        log("B=%d %-22s x%-2d %8.3f ms total  %7.4f ms each  %6.1f TOP/s" %
+            (B, key, n, tms, tms / n, ops / (tms / n * 1e-3) / 1e12))
     dom = [st for st in steps if st["kind"] == 1 and st["cin"] == 256 and st["cout"] == 256
            and st["k"] == 3 and st["s"] == 1]
     dom_ms = statistics.mean(st["ms"] for st in dom)

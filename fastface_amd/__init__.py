@@ -13,7 +13,7 @@ import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO_ROOT = os.path.dirname(HERE)
-LIB_PATH = os.path.join(HERE, "lib", "libfastface_amd.so")
+LIB_PATH = os.environ.get("FASTFACE_LIB") or os.path.join(HERE, "lib", "libfastface_amd.so")
 CSRC = os.path.join(HERE, "csrc")
 
 FASTFACE_INPUT_N = 37632

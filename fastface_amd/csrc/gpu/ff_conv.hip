@@ -29,9 +29,12 @@
 
 #define EPI_FC 0x100  // internal: FC head, fp32 output via ff::fc_out
 
-// K steps of global loads kept in flight per thread
+// stages of global loads kept in flight per thread (64- and 128-byte stages)
 #ifndef FF_PF
 #define FF_PF 4
+#endif
+#ifndef FF_PF128
+#define FF_PF128 2
 #endif
 
 constexpr int FF_LUT_PITCH = 272;   // LDS row pitch of a 256-entry table
@@ -64,17 +67,19 @@ struct ConvArgs {
 // Epilogue of one wave's MI x NJ block of 32x32 MFMA tiles.
 //   mrow0: global pixel index of the block's first row
 //   ncol0: global output channel of the block's first column
-//   Ws:    wave-private LDS byte tile [MI*32][80]
+//   Ws:    wave-private LDS byte tile [MI*32][NJ*32 + 16]
 //   Lw:    BN table of channel ncol0 (row pitch FF_LUT_PITCH) or null
 // ---------------------------------------------------------------------------
+template <int MI, int NJ>
+constexpr int wave_tile_bytes() { return MI * 32 * (NJ * 32 + 16); }
+
 template <int COUT, int MI, int NJ, bool PRELU, bool ADD, bool BN2>
 __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a, int mrow0,
                                             int ncol0, int8_t* Ws, const int8_t* Lw) {
-    constexpr int P = 80;
+    constexpr int P = NJ * 32 + 16;
     constexpr int ROWS = MI * 32;
     constexpr int CH = NJ * 2;          // 16-byte chunks per tile row
     constexpr int RPI = 64 / CH;        // tile rows per copy instruction
-    static_assert(NJ * 32 <= 64, "tile row must fit the 80-byte pitch");
     const int lane = threadIdx.x & 63;
     const int lc = lane & 31;
     const int lh = lane >> 5;
@@ -233,23 +238,31 @@ __device__ __forceinline__ int xcd_tile(int bid, int nb) {
 // ---------------------------------------------------------------------------
 // Main conv kernel (Cin multiple of 64).
 // ---------------------------------------------------------------------------
-template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN, int PF>
-__global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
+// KB: bytes of K per LDS stage (64 or 128: one or two 64-channel runs of one
+// tap).  PF: stages of global loads kept in flight.  Each of the 4 waves
+// computes MI x NJ MFMA tiles (MI*32 pixels x NJ*32 channels): bigger wave
+// tiles read fewer LDS operand bytes per MFMA (MI+NJ reads per MI*NJ MFMAs).
+// OCC: workgroups per CU the register/LDS budget is sized for.
+template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN, int KB, int PF,
+          int MI, int NJ, int OCC>
+__global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
     constexpr int PAD = KS / 2;
     constexpr int HOUT = (HIN + 2 * PAD - KS) / STRIDE + 1;
     constexpr int WOUT = (WIN + 2 * PAD - KS) / STRIDE + 1;
     constexpr int HWO = HOUT * WOUT;
-    constexpr int CSTEPS = CIN / FF_KSTEP;
-    constexpr int KSTEPS = KS * KS * CSTEPS;
-    constexpr int ROWB = 80;
-    constexpr int A_LD = BM * 4 / 256;
-    constexpr int B_LD = BN * 4 / 256;
-    constexpr int WN = BN / 64;
+    constexpr int CSTEPS = CIN / KB;               // stages per tap
+    constexpr int KSTEPS = KS * KS * CSTEPS;       // stages
+    constexpr int ROWB = KB + 16;                  // LDS row pitch (conflict-free b128 reads)
+    constexpr int PPR = KB / 16;                   // 16-byte pieces per row and stage
+    constexpr int A_LD = BM * PPR / 256;
+    constexpr int B_LD = BN * PPR / 256;
+    constexpr int WTM = MI * 32, WTN = NJ * 32;    // wave tile
+    constexpr int WN = BN / WTN;                   // waves along N
     constexpr int LDS_K = 2 * (BM + BN) * ROWB;
-    constexpr int LDS_E = 4 * 64 * 80 + BN * FF_LUT_PITCH;
+    constexpr int LDS_E = 4 * wave_tile_bytes<MI, NJ>() + BN * FF_LUT_PITCH;
     constexpr int LDS = LDS_K > LDS_E ? LDS_K : LDS_E;
-    static_assert(CIN % FF_KSTEP == 0, "Cin must be a multiple of 64");
-    static_assert((BM / 64) * (BN / 64) == 4, "4 waves of 64x64");
+    static_assert(CIN % KB == 0 && KB % FF_KSTEP == 0, "Cin must be a multiple of the stage");
+    static_assert((BM / WTM) * (BN / WTN) == 4, "4 waves");
     static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
 
     __shared__ __align__(16) int8_t smem[LDS];
@@ -269,19 +282,27 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
 #pragma unroll
     for (int j = 0; j < A_LD; j++) {
         const int idx = tid + j * 256;
-        const int m = m0 + (idx >> 2);
+        const int m = m0 + idx / PPR;
         const bool ok = m < a.M;
         const int mm = ok ? m : 0;
         const int b = mm / HWO;
         const int r = mm - b * HWO;
         const int oh = r / WOUT;
         const int ow = r - oh * WOUT;
-        a_img[j] = a.in + (size_t)b * (HIN * WIN * CIN) + (idx & 3) * 16;
+        a_img[j] = a.in + (size_t)b * (HIN * WIN * CIN) + (idx % PPR) * 16;
         a_ih0[j] = oh * STRIDE - PAD;
         a_iw0[j] = ow * STRIDE - PAD;
         a_ok[j] = ok;
     }
-    const int8_t* wbase = a.w + (size_t)tn * BN * FF_KSTEP + tid * 16;
+    // packed weights are [K/64][Cout][64]: piece p of a stage row n lies in
+    // 64-byte K step (stage*KB/64 + p/4) at byte (p%4)*16
+    int b_off[B_LD];
+#pragma unroll
+    for (int j = 0; j < B_LD; j++) {
+        const int idx = tid + j * 256;
+        const int n = idx / PPR, p = idx % PPR;
+        b_off[j] = ((p / 4) * COUT + tn * BN + n) * FF_KSTEP + (p % 4) * 16;
+    }
 
     // Prefetch queue: PF register sets, each holding one K step's global
     // loads, so PF steps of loads are in flight while the MFMAs of the
@@ -298,23 +319,23 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
             const int ih = a_ih0[j] + kh;
             const int iw = a_iw0[j] + kw;
             const bool v = a_ok[j] && (unsigned)ih < (unsigned)HIN && (unsigned)iw < (unsigned)WIN;
-            const int8_t* src = v ? a_img[j] + (ih * WIN + iw) * CIN + cs * FF_KSTEP : ff_zero_page;
+            const int8_t* src = v ? a_img[j] + (ih * WIN + iw) * CIN + cs * KB : ff_zero_page;
             qa[j] = *reinterpret_cast<const v4i*>(src);
         }
+        const int8_t* wst = a.w + (size_t)s * (KB / FF_KSTEP) * COUT * FF_KSTEP;
 #pragma unroll
-        for (int j = 0; j < B_LD; j++)
-            qb[j] = *reinterpret_cast<const v4i*>(wbase + (size_t)s * COUT * FF_KSTEP + j * 4096);
+        for (int j = 0; j < B_LD; j++) qb[j] = *reinterpret_cast<const v4i*>(wst + b_off[j]);
     };
     auto sstore = [&](int buf, const v4i (&qa)[A_LD], const v4i (&qb)[B_LD]) {
 #pragma unroll
         for (int j = 0; j < A_LD; j++) {
             const int idx = tid + j * 256;
-            *reinterpret_cast<v4i*>(As + buf * BM * ROWB + (idx >> 2) * ROWB + (idx & 3) * 16) = qa[j];
+            *reinterpret_cast<v4i*>(As + buf * BM * ROWB + (idx / PPR) * ROWB + (idx % PPR) * 16) = qa[j];
         }
 #pragma unroll
         for (int j = 0; j < B_LD; j++) {
             const int idx = tid + j * 256;
-            *reinterpret_cast<v4i*>(Bs + buf * BN * ROWB + (idx >> 2) * ROWB + (idx & 3) * 16) = qb[j];
+            *reinterpret_cast<v4i*>(Bs + buf * BN * ROWB + (idx / PPR) * ROWB + (idx % PPR) * 16) = qb[j];
         }
     };
 
@@ -322,14 +343,14 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
     const int lane = tid & 63;
     const int wm = wave / WN;
     const int wn = wave % WN;
-    const int8_t* a_rd = As + (wm * 64 + (lane & 31)) * ROWB + (lane >> 5) * 16;
-    const int8_t* b_rd = Bs + (wn * 64 + (lane & 31)) * ROWB + (lane >> 5) * 16;
+    const int8_t* a_rd = As + (wm * WTM + (lane & 31)) * ROWB + (lane >> 5) * 16;
+    const int8_t* b_rd = Bs + (wn * WTN + (lane & 31)) * ROWB + (lane >> 5) * 16;
 
-    v16i acc[2][2];
+    v16i acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < NJ; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
@@ -349,15 +370,19 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
                 const int buf = s & 1;
                 if (s + PF < KSTEPS) gload(s + PF, ra[u], rb[u]);
 #pragma unroll
-                for (int ks = 0; ks < 2; ks++) {
-                    const v4i a0 = *reinterpret_cast<const v4i*>(a_rd + buf * BM * ROWB + ks * 32);
-                    const v4i a1 = *reinterpret_cast<const v4i*>(a_rd + buf * BM * ROWB + 32 * ROWB + ks * 32);
-                    const v4i b0 = *reinterpret_cast<const v4i*>(b_rd + buf * BN * ROWB + ks * 32);
-                    const v4i b1 = *reinterpret_cast<const v4i*>(b_rd + buf * BN * ROWB + 32 * ROWB + ks * 32);
-                    acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc[0][0], 0, 0, 0);
-                    acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc[0][1], 0, 0, 0);
-                    acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc[1][0], 0, 0, 0);
-                    acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc[1][1], 0, 0, 0);
+                for (int ks = 0; ks < KB / 32; ks++) {
+                    v4i af[MI], bf[NJ];
+#pragma unroll
+                    for (int i = 0; i < MI; i++)
+                        af[i] = *reinterpret_cast<const v4i*>(a_rd + buf * BM * ROWB + i * 32 * ROWB + ks * 32);
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+                        bf[j] = *reinterpret_cast<const v4i*>(b_rd + buf * BN * ROWB + j * 32 * ROWB + ks * 32);
+#pragma unroll
+                    for (int i = 0; i < MI; i++)
+#pragma unroll
+                        for (int j = 0; j < NJ; j++)
+                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
                 }
                 if (s + 1 < KSTEPS) sstore(buf ^ 1, ra[(u + 1) % PF], rb[(u + 1) % PF]);
                 __syncthreads();
@@ -366,14 +391,14 @@ __global__ __launch_bounds__(256, 2) void conv_i8_kernel(ConvArgs a) {
     }
 
     // epilogue (the loop's last barrier freed the K buffers)
-    int8_t* Ws = smem + wave * (64 * 80);
-    int8_t* Ls = smem + 4 * 64 * 80;
+    int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
+    int8_t* Ls = smem + 4 * wave_tile_bytes<MI, NJ>();
     if (a.flags & FFK_EPI_BN && !a.out_i32) {
         load_bn_lut<256>(Ls, a.bn_lut, tn * BN, BN);
         __syncthreads();
     }
-    wave_epilogue<COUT, 2, 2>(acc, a, m0 + wm * 64, tn * BN + wn * 64, Ws,
-                              Ls + (wn * 64) * FF_LUT_PITCH);
+    wave_epilogue<COUT, MI, NJ>(acc, a, m0 + wm * WTM, tn * BN + wn * WTN, Ws,
+                                Ls + (wn * WTN) * FF_LUT_PITCH);
 }
 
 // ---------------------------------------------------------------------------
@@ -461,10 +486,11 @@ namespace {
 
 typedef void (*launch_fn)(const ConvArgs&, int grid, hipStream_t);
 
-template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN, int PF>
+template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN, int KB, int PF,
+          int MI, int NJ, int OCC>
 void launch_conv(const ConvArgs& a, int grid, hipStream_t s) {
-    hipLaunchKernelGGL((conv_i8_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, BM, BN, PF>), dim3(grid),
-                       dim3(256), 0, s, a);
+    hipLaunchKernelGGL((conv_i8_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, BM, BN, KB, PF, MI, NJ, OCC>),
+                       dim3(grid), dim3(256), 0, s, a);
 }
 
 void launch_stem(const ConvArgs& a, int grid, hipStream_t s) {
@@ -478,27 +504,53 @@ struct ConvEntry {
     launch_fn fn;
 };
 
-#define FF_CONV(CIN, COUT, KS, S, H, BM, BN) \
-    {CIN, COUT, KS, S, H, H, BM, BN, &launch_conv<CIN, COUT, KS, S, H, H, BM, BN, FF_PF>}
+// Tile configurations: (BM, BN, MI, NJ, OCC) -- workgroup tile, wave tile in
+// 32x32 MFMA blocks, workgroups per CU.
+//   T64:  Cout = 64, 256x64 tiles of 64x64 waves
+//   T128: 128x128 tiles of 64x64 waves
+//   TBIG: the Cout >= 256 layers (stages 3-4)
+#define FF_T64 256, 64, 2, 2, 2
+#define FF_T128 128, 128, 2, 2, 2
+#ifndef FF_TBIG
+#define FF_TBIG 128, 128, 2, 2, 2
+#endif
+// 128-byte stages wherever Cin allows (twice the MFMA work per barrier)
+#define FF_KB(CIN) ((CIN) % 128 == 0 ? 128 : 64)
+#define FF_PFS(CIN) (FF_KB(CIN) == 128 ? FF_PF128 : FF_PF)
+#ifdef FF_KB_BIG_V
+#define FF_KB_BIG(CIN) FF_KB_BIG_V
+#define FF_PF_BIG(CIN) FF_PF_BIG_V
+#else
+#define FF_KB_BIG(CIN) FF_KB(CIN)
+#define FF_PF_BIG(CIN) FF_PFS(CIN)
+#endif
+#define FF_ENTRY(CIN, COUT, KS, S, H, KB, PF, BM, BN, MI, NJ, OCC) \
+    {CIN, COUT, KS, S, H, H, BM, BN,                                \
+     &launch_conv<CIN, COUT, KS, S, H, H, BM, BN, KB, PF, MI, NJ, OCC>}
+#define FF_CONV(CIN, COUT, KS, S, H, TILE) \
+    FF_ENTRY(CIN, COUT, KS, S, H, FF_KB(CIN), FF_PFS(CIN), TILE)
+#define FF_CONV_K(CIN, COUT, KS, S, H, KB, PF, TILE) FF_ENTRY(CIN, COUT, KS, S, H, KB, PF, TILE)
+#define FF_CONVB(CIN, COUT, KS, S, H) \
+    FF_CONV_K(CIN, COUT, KS, S, H, FF_KB_BIG(CIN), FF_PF_BIG(CIN), FF_TBIG)
 
 const ConvEntry kConvTable[] = {
     {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem},
-    FF_CONV(64, 64, 3, 1, 112, 256, 64),
-    FF_CONV(64, 64, 3, 2, 112, 256, 64),
-    FF_CONV(64, 64, 1, 2, 112, 256, 64),
-    FF_CONV(64, 64, 3, 1, 56, 256, 64),
-    FF_CONV(64, 128, 3, 1, 56, 128, 128),
-    FF_CONV(128, 128, 3, 2, 56, 128, 128),
-    FF_CONV(64, 128, 1, 2, 56, 128, 128),
-    FF_CONV(128, 128, 3, 1, 28, 128, 128),
-    FF_CONV(128, 256, 3, 1, 28, 128, 128),
-    FF_CONV(256, 256, 3, 2, 28, 128, 128),
-    FF_CONV(128, 256, 1, 2, 28, 128, 128),
-    FF_CONV(256, 256, 3, 1, 14, 128, 128),
-    FF_CONV(256, 512, 3, 1, 14, 128, 128),
-    FF_CONV(512, 512, 3, 2, 14, 128, 128),
-    FF_CONV(256, 512, 1, 2, 14, 128, 128),
-    FF_CONV(512, 512, 3, 1, 7, 128, 128),
+    FF_CONV(64, 64, 3, 1, 112, FF_T64),
+    FF_CONV(64, 64, 3, 2, 112, FF_T64),
+    FF_CONV(64, 64, 1, 2, 112, FF_T64),
+    FF_CONV(64, 64, 3, 1, 56, FF_T64),
+    FF_CONV(64, 128, 3, 1, 56, FF_T128),
+    FF_CONV(128, 128, 3, 2, 56, FF_T128),
+    FF_CONV(64, 128, 1, 2, 56, FF_T128),
+    FF_CONV(128, 128, 3, 1, 28, FF_T128),
+    FF_CONVB(128, 256, 3, 1, 28),
+    FF_CONVB(256, 256, 3, 2, 28),
+    FF_CONVB(128, 256, 1, 2, 28),
+    FF_CONVB(256, 256, 3, 1, 14),
+    FF_CONVB(256, 512, 3, 1, 14),
+    FF_CONVB(512, 512, 3, 2, 14),
+    FF_CONVB(256, 512, 1, 2, 14),
+    FF_CONVB(512, 512, 3, 1, 7),
 };
 
 const ConvEntry* find_conv(int cin, int cout, int kh, int kw, int stride, int pad, int hin, int win) {
@@ -531,8 +583,8 @@ int ffk_fc_gemm_launch(const ffk_fc_desc* d, hipStream_t s) {
     a.in_scale = d->a_scale;
     a.tiles_n = 512 / 128;
     const int grid = ((d->batch + 127) / 128) * a.tiles_n;
-    hipLaunchKernelGGL((conv_i8_kernel<25088, 512, 1, 1, 1, 1, 128, 128, FF_PF>), dim3(grid), dim3(256),
-                       0, s, a);
+    hipLaunchKernelGGL((conv_i8_kernel<25088, 512, 1, 1, 1, 1, 128, 128, 128, FF_PF128, 2, 2, 2>),
+                       dim3(grid), dim3(256), 0, s, a);
     return ffk_check_launch("fc gemm launch");
 }
 

@@ -37,7 +37,8 @@ class ffk_conv_desc(C.Structure):
                 ("win", C.c_int), ("in_", _p), ("in_inv", _p), ("io", _p), ("w", _p),
                 ("params", _p), ("add_src", _p), ("bn_lut", _p), ("out", _p), ("out_bn", _p),
                 ("out_i32", _p),
-                ("flags", C.c_int), ("in_scale", C.c_float)]
+                ("flags", C.c_int), ("in_scale", C.c_float),
+                ("workspace", _p), ("workspace_bytes", C.c_size_t)]
 
 
 class ffk_fc_desc(C.Structure):
@@ -80,6 +81,7 @@ EXPORTS = [
     ("ffk_memcpy_h2d", C.c_int, [_p, _p, C.c_size_t, _p]),
     ("ffk_memcpy_d2h", C.c_int, [_p, _p, C.c_size_t, _p]),
     ("ffk_memcpy_d2d", C.c_int, [_p, _p, C.c_size_t, _p]),
+    ("ffk_zero", C.c_int, [_p, C.c_size_t, _p]),
     ("ffk_stream_create", C.c_int, [C.POINTER(_p)]),
     ("ffk_stream_destroy", C.c_int, [_p]),
     ("ffk_stream_sync", C.c_int, [_p]),
@@ -94,6 +96,7 @@ EXPORTS = [
     ("ffk_conv_supported", C.c_int, [C.c_int] * 8),
     ("ffk_conv_packed_bytes", C.c_size_t, [C.c_int] * 4),
     ("ffk_pack_conv_weights", C.c_int, [_p, C.c_int, C.c_int, C.c_int, C.c_int, _p]),
+    ("ffk_conv_workspace_bytes", C.c_size_t, [C.POINTER(ffk_conv_desc)]),
     ("ffk_conv", C.c_int, [C.POINTER(ffk_conv_desc), _p]),
     ("ffk_make_bn_lut", C.c_int, [_p, _p, _p, _p, C.c_int, _p]),
     ("ffk_fc_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),

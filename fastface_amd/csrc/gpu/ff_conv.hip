@@ -9,13 +9,15 @@
 // MFMA needs no correction, and integer sums do not depend on their order,
 // so the accumulators are bit-identical.
 //
-// K loop: workgroup = 4 wave64s computing a BM x BN tile (each wave a 64x64
-// block of 2x2 MFMA 32x32 tiles).  Per K step of 64 bytes each thread fetches
+// K loop: workgroup = 4 wave64s computing a BM x BN tile (each wave MI x NJ
+// MFMA 32x32 tiles).  Per K stage of KB = 64 or 128 bytes each thread fetches
 // 16-byte pieces of the implicit im2col rows (one input pixel's channel run;
 // padding taps read a zero page, so there are no branches) and of the packed
-// weights.  PF steps of loads are in flight in registers; each step is staged
-// through a double-buffered LDS tile whose 80-byte row pitch makes the
-// ds_read_b128 MFMA operand reads conflict-free.
+// weights.  PF stages of loads are in flight in registers; each stage goes
+// through a double-buffered LDS tile whose KB+16-byte row pitch makes the
+// ds_read_b128 MFMA operand reads conflict-free.  Small batches of the layers
+// with long K chains split the stages of a tile over several workgroups
+// (split-K, int32 partial tiles in a caller workspace).
 //
 // Epilogue straight from the accumulator registers: in the 32x32 MFMA result
 // every lane owns one output channel (column) and 16 pixels (rows), so each
@@ -57,6 +59,8 @@ struct ConvArgs {
     float* out_f32;
     const float* fc_ws;
     const float* fc_bias;
+    int32_t* ws;            // split-K partial tiles
+    unsigned* counters;     // split-K arrival counters, one per tile (zero between launches)
     int M;
     int flags;
     float in_scale;
@@ -243,15 +247,22 @@ __device__ __forceinline__ int xcd_tile(int bid, int nb) {
 // computes MI x NJ MFMA tiles (MI*32 pixels x NJ*32 channels): bigger wave
 // tiles read fewer LDS operand bytes per MFMA (MI+NJ reads per MI*NJ MFMAs).
 // OCC: workgroups per CU the register/LDS budget is sized for.
+// SPLIT > 1 (small batches): the K stages are cut into SPLIT ranges, one
+// workgroup each; every workgroup stores its int32 partial tile and the last
+// one to arrive at the tile (agent-scope counter) sums them and runs the
+// epilogue.  Integer sums are exact, so the result does not depend on the
+// order in which the partial tiles arrive.
 template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN, int KB, int PF,
-          int MI, int NJ, int OCC>
+          int MI, int NJ, int OCC, int SPLIT>
 __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
     constexpr int PAD = KS / 2;
     constexpr int HOUT = (HIN + 2 * PAD - KS) / STRIDE + 1;
     constexpr int WOUT = (WIN + 2 * PAD - KS) / STRIDE + 1;
     constexpr int HWO = HOUT * WOUT;
     constexpr int CSTEPS = CIN / KB;               // stages per tap
-    constexpr int KSTEPS = KS * KS * CSTEPS;       // stages
+    constexpr int KALL = KS * KS * CSTEPS;         // stages of the whole reduction
+    constexpr int KSTEPS = KALL / SPLIT;           // stages of this workgroup
+    static_assert(KALL % SPLIT == 0, "split must divide the stages");
     constexpr int ROWB = KB + 16;                  // LDS row pitch (conflict-free b128 reads)
     constexpr int PPR = KB / 16;                   // 16-byte pieces per row and stage
     constexpr int A_LD = BM * PPR / 256;
@@ -270,7 +281,10 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
     int8_t* Bs = smem + 2 * BM * ROWB;
 
     const int tid = threadIdx.x;
-    const int bid = xcd_tile(blockIdx.x, gridDim.x);
+    const int xbid = xcd_tile(blockIdx.x, gridDim.x);
+    const int bid = xbid / SPLIT;                  // the splits of a tile are consecutive
+    const int sp = xbid - bid * SPLIT;
+    const int s_beg = sp * KSTEPS;
     const int tn = bid % a.tiles_n;
     const int tm = bid / a.tiles_n;
     const int m0 = tm * BM;
@@ -357,7 +371,7 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
     // prologue: steps 0 .. PF-1 in flight, step 0 staged in LDS
 #pragma unroll
     for (int u = 0; u < PF; u++)
-        if (u < KSTEPS) gload(u, ra[u], rb[u]);
+        if (u < KSTEPS) gload(s_beg + u, ra[u], rb[u]);
     sstore(0, ra[0], rb[0]);
     __syncthreads();
     // Step s lives in register set s % PF until it is staged into LDS buffer
@@ -368,7 +382,7 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
             const int s = s0 + u;
             if (s < KSTEPS) {
                 const int buf = s & 1;
-                if (s + PF < KSTEPS) gload(s + PF, ra[u], rb[u]);
+                if (s + PF < KSTEPS) gload(s_beg + s + PF, ra[u], rb[u]);
 #pragma unroll
                 for (int ks = 0; ks < KB / 32; ks++) {
                     v4i af[MI], bf[NJ];
@@ -388,6 +402,66 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
                 __syncthreads();
             }
         }
+    }
+
+    if (SPLIT > 1) {
+        // Partial tiles are exchanged with the documented agent-scope
+        // release / acquire pattern, paid once per workgroup (the XCDs' L2s
+        // are not coherent with each other): every thread stores its part
+        // and waits for the stores; after the barrier one thread releases
+        // (L2 write-back) and bumps the tile's arrival count; the workgroup
+        // that arrives last acquires (L2 invalidate) and sums the partials.
+        constexpr int NCH = MI * NJ * 4;            // 16-byte chunks per thread
+        constexpr int PART = BM * BN * 4;           // bytes of one partial tile
+        int8_t* part = reinterpret_cast<int8_t*>(a.ws + (size_t)bid * SPLIT * (BM * BN));
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {             // chunk-major: a wave stores 1 KB runs
+            const v16i& t = acc[c / (NJ * 4)][(c / 4) % NJ];
+            const v4i v = {t[(c % 4) * 4], t[(c % 4) * 4 + 1], t[(c % 4) * 4 + 2], t[(c % 4) * 4 + 3]};
+            *reinterpret_cast<v4i*>(part + sp * PART + (c * 256 + tid) * 16) = v;
+        }
+        __builtin_amdgcn_s_waitcnt(0);              // this wave's stores have reached L2
+        __syncthreads();
+        int* last = reinterpret_cast<int*>(smem);
+        if (tid == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            __builtin_amdgcn_s_waitcnt(0);          // write-back complete before the count moves
+            const bool is_last = __hip_atomic_fetch_add(&a.counters[bid], 1u, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(SPLIT - 1);
+            if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __builtin_amdgcn_s_waitcnt(0);
+            last[0] = is_last;
+        }
+        __syncthreads();
+        if (!last[0]) return;                       // another workgroup finishes this tile
+        // G partial tiles per round (NCH * G loads in flight) keep the
+        // registers within the occupancy budget
+        constexpr int G = SPLIT % 4 == 0 ? 4 : (SPLIT % 3 == 0 ? 3 : (SPLIT % 2 == 0 ? 2 : 1));
+        v4i s[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; c++) s[c] = v4i{0, 0, 0, 0};
+#pragma unroll 1
+        for (int q0 = 0; q0 < SPLIT; q0 += G) {
+            v4i t[NCH][G];
+#pragma unroll
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int c = 0; c < NCH; c++)
+                    t[c][g] = *reinterpret_cast<const v4i*>(part + (q0 + g) * PART + (c * 256 + tid) * 16);
+#pragma unroll
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int c = 0; c < NCH; c++) s[c] += t[c][g];
+        }
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            v16i& t = acc[c / (NJ * 4)][(c / 4) % NJ];
+#pragma unroll
+            for (int e = 0; e < 4; e++) t[(c % 4) * 4 + e] = s[c][e];
+        }
+        if (tid == 0)                               // ready for the next launch
+            __hip_atomic_store(&a.counters[bid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
     }
 
     // epilogue (the loop's last barrier freed the K buffers)
@@ -487,9 +561,9 @@ namespace {
 typedef void (*launch_fn)(const ConvArgs&, int grid, hipStream_t);
 
 template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN, int KB, int PF,
-          int MI, int NJ, int OCC>
+          int MI, int NJ, int OCC, int SPLIT>
 void launch_conv(const ConvArgs& a, int grid, hipStream_t s) {
-    hipLaunchKernelGGL((conv_i8_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, BM, BN, KB, PF, MI, NJ, OCC>),
+    hipLaunchKernelGGL((conv_i8_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, BM, BN, KB, PF, MI, NJ, OCC, SPLIT>),
                        dim3(grid), dim3(256), 0, s, a);
 }
 
@@ -499,9 +573,23 @@ void launch_stem(const ConvArgs& a, int grid, hipStream_t s) {
     hipLaunchKernelGGL(stem_kernel, dim3(tiles), dim3(STEM_NT), 0, s, a);
 }
 
+// Small-batch split-K tiling: 64x64 workgroup tiles (one 32x32 MFMA tile per
+// wave), the K stages of a tile shared by `split` workgroups.
+constexpr int FF_SM_BM = 64, FF_SM_BN = 64;
+// The split path is taken when the whole-K tiling leaves most CUs idle and the
+// split grid stays small: every split workgroup pays one agent-scope L2
+// write-back (~0.4 us, serialized per XCD), so a split grid much beyond ~20
+// workgroups per XCD costs more than the shorter K chain saves.
+constexpr int FF_SPLIT_MIN_WG = 256;
+constexpr int FF_SPLIT_MAX_WG = 160;
+// split-K workspace: [counter per tile, fixed size][int32 partial tiles]
+constexpr size_t FF_SPLIT_COUNTER_BYTES = FF_SPLIT_MAX_WG * sizeof(unsigned);
+
 struct ConvEntry {
     int cin, cout, ks, stride, hin, win, bm, bn;
     launch_fn fn;
+    int split;          // K split of the small-batch variant (1: no partial tiles)
+    launch_fn small;    // 64x64-tile variant (stem: none)
 };
 
 // Tile configurations: (BM, BN, MI, NJ, OCC) -- workgroup tile, wave tile in
@@ -524,33 +612,46 @@ struct ConvEntry {
 #define FF_KB_BIG(CIN) FF_KB(CIN)
 #define FF_PF_BIG(CIN) FF_PFS(CIN)
 #endif
-#define FF_ENTRY(CIN, COUT, KS, S, H, KB, PF, BM, BN, MI, NJ, OCC) \
-    {CIN, COUT, KS, S, H, H, BM, BN,                                \
-     &launch_conv<CIN, COUT, KS, S, H, H, BM, BN, KB, PF, MI, NJ, OCC>}
-#define FF_CONV(CIN, COUT, KS, S, H, TILE) \
-    FF_ENTRY(CIN, COUT, KS, S, H, FF_KB(CIN), FF_PFS(CIN), TILE)
-#define FF_CONV_K(CIN, COUT, KS, S, H, KB, PF, TILE) FF_ENTRY(CIN, COUT, KS, S, H, KB, PF, TILE)
-#define FF_CONVB(CIN, COUT, KS, S, H) \
-    FF_CONV_K(CIN, COUT, KS, S, H, FF_KB_BIG(CIN), FF_PF_BIG(CIN), FF_TBIG)
+template <int CIN, int COUT, int KS, int S, int H, int SPLIT>
+constexpr launch_fn split_launch() {
+    if constexpr (SPLIT > 1)
+        return &launch_conv<CIN, COUT, KS, S, H, H, FF_SM_BM, FF_SM_BN, FF_KB(CIN), 2, 1, 1, 4, SPLIT>;
+    else
+        return nullptr;
+}
+#define FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, KB, PF, BM, BN, MI, NJ, OCC)       \
+    {CIN, COUT, KS, S, H, H, BM, BN,                                             \
+     &launch_conv<CIN, COUT, KS, S, H, H, BM, BN, KB, PF, MI, NJ, OCC, 1>, SPLIT, \
+     split_launch<CIN, COUT, KS, S, H, SPLIT>()}
+#define FF_CONV(CIN, COUT, KS, S, H, SPLIT, TILE) \
+    FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, FF_KB(CIN), FF_PFS(CIN), TILE)
+#define FF_CONV_K(CIN, COUT, KS, S, H, SPLIT, KB, PF, TILE) \
+    FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, KB, PF, TILE)
+#define FF_CONVB(CIN, COUT, KS, S, H, SPLIT) \
+    FF_CONV_K(CIN, COUT, KS, S, H, SPLIT, FF_KB_BIG(CIN), FF_PF_BIG(CIN), FF_TBIG)
 
+// split: how many workgroups share the K stages of one small-batch tile (1:
+// never split).  Only the long K chains of stages 3-4 (18 or 36 stages of
+// 128 bytes) gain from it; the split is sized so that one face gives 72-144
+// workgroups.
 const ConvEntry kConvTable[] = {
-    {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem},
-    FF_CONV(64, 64, 3, 1, 112, FF_T64),
-    FF_CONV(64, 64, 3, 2, 112, FF_T64),
-    FF_CONV(64, 64, 1, 2, 112, FF_T64),
-    FF_CONV(64, 64, 3, 1, 56, FF_T64),
-    FF_CONV(64, 128, 3, 1, 56, FF_T128),
-    FF_CONV(128, 128, 3, 2, 56, FF_T128),
-    FF_CONV(64, 128, 1, 2, 56, FF_T128),
-    FF_CONV(128, 128, 3, 1, 28, FF_T128),
-    FF_CONVB(128, 256, 3, 1, 28),
-    FF_CONVB(256, 256, 3, 2, 28),
-    FF_CONVB(128, 256, 1, 2, 28),
-    FF_CONVB(256, 256, 3, 1, 14),
-    FF_CONVB(256, 512, 3, 1, 14),
-    FF_CONVB(512, 512, 3, 2, 14),
-    FF_CONVB(256, 512, 1, 2, 14),
-    FF_CONVB(512, 512, 3, 1, 7),
+    {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem, 1, nullptr},
+    FF_CONV(64, 64, 3, 1, 112, 1, FF_T64),
+    FF_CONV(64, 64, 3, 2, 112, 1, FF_T64),
+    FF_CONV(64, 64, 1, 2, 112, 1, FF_T64),
+    FF_CONV(64, 64, 3, 1, 56, 1, FF_T64),
+    FF_CONV(64, 128, 3, 1, 56, 1, FF_T128),
+    FF_CONV(128, 128, 3, 2, 56, 1, FF_T128),
+    FF_CONV(64, 128, 1, 2, 56, 1, FF_T128),
+    FF_CONV(128, 128, 3, 1, 28, 1, FF_T128),
+    FF_CONVB(128, 256, 3, 1, 28, 1),
+    FF_CONVB(256, 256, 3, 2, 28, 6),
+    FF_CONVB(128, 256, 1, 2, 28, 1),
+    FF_CONVB(256, 256, 3, 1, 14, 9),
+    FF_CONVB(256, 512, 3, 1, 14, 3),
+    FF_CONVB(512, 512, 3, 2, 14, 9),
+    FF_CONVB(256, 512, 1, 2, 14, 1),
+    FF_CONVB(512, 512, 3, 1, 7, 9),
 };
 
 const ConvEntry* find_conv(int cin, int cout, int kh, int kw, int stride, int pad, int hin, int win) {
@@ -560,6 +661,47 @@ const ConvEntry* find_conv(int cin, int cout, int kh, int kw, int stride, int pa
             e.win == win)
             return &e;
     return nullptr;
+}
+
+// Launch choice for one layer at M output pixels.
+struct ConvLaunch {
+    launch_fn fn;
+    int bn;             // workgroup tile width (tiles_n = cout / bn)
+    int grid;
+    int split;
+    size_t counter_bytes, ws_bytes;   // split > 1: workspace layout
+};
+
+// ws_avail: workspace bytes the caller provides (a split > 1 variant that
+// needs more falls back to the whole-K tiling).
+ConvLaunch choose_launch(const ConvEntry* e, long long M, size_t ws_avail) {
+    const long long big = ((M + e->bm - 1) / e->bm) * (e->cout / e->bn);
+    ConvLaunch l = {e->fn, e->bn, (int)big, 1, 0, 0};
+    if (!e->small || big >= FF_SPLIT_MIN_WG) return l;
+    const long long tiles = ((M + FF_SM_BM - 1) / FF_SM_BM) * (e->cout / FF_SM_BN);
+    const long long wgs = tiles * e->split;
+    if (wgs > FF_SPLIT_MAX_WG || wgs <= big) return l;
+    if (e->split > 1) {
+        // the counter area has the same size at every batch (tiles <= wgs), so
+        // launches of different sizes never see each other's partial tiles
+        // in their counters
+        const size_t cnt = FF_SPLIT_COUNTER_BYTES;
+        const size_t need = cnt + (size_t)wgs * FF_SM_BM * FF_SM_BN * sizeof(int32_t);
+        if (need > ws_avail) return l;
+        l.counter_bytes = cnt;
+        l.ws_bytes = need;
+    }
+    l.fn = e->small;
+    l.bn = FF_SM_BN;
+    l.grid = (int)wgs;
+    l.split = e->split;
+    return l;
+}
+
+long long conv_pixels(const ffk_conv_desc* d) {
+    const int hout = (d->hin + 2 * d->pad - d->kh) / d->stride + 1;
+    const int wout = (d->win + 2 * d->pad - d->kw) / d->stride + 1;
+    return (long long)d->batch * hout * wout;
 }
 
 }  // namespace
@@ -583,7 +725,7 @@ int ffk_fc_gemm_launch(const ffk_fc_desc* d, hipStream_t s) {
     a.in_scale = d->a_scale;
     a.tiles_n = 512 / 128;
     const int grid = ((d->batch + 127) / 128) * a.tiles_n;
-    hipLaunchKernelGGL((conv_i8_kernel<25088, 512, 1, 1, 1, 1, 128, 128, 128, FF_PF128, 2, 2, 2>),
+    hipLaunchKernelGGL((conv_i8_kernel<25088, 512, 1, 1, 1, 1, 128, 128, 128, FF_PF128, 2, 2, 2, 1>),
                        dim3(grid), dim3(256), 0, s, a);
     return ffk_check_launch("fc gemm launch");
 }
@@ -632,9 +774,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
         ffk_set_error("conv: no kernel for this layer geometry%s%s", nullptr, nullptr);
         return FFK_ERR_UNSUPPORTED;
     }
-    const int hout = (d->hin + 2 * d->pad - d->kh) / d->stride + 1;
-    const int wout = (d->win + 2 * d->pad - d->kw) / d->stride + 1;
-    const long long M = (long long)d->batch * hout * wout;
+    const long long M = conv_pixels(d);
     if (M > 0x7fffffffLL) {
         ffk_set_error("conv: batch too large%s%s", nullptr, nullptr);
         return FFK_ERR_ARG;
@@ -668,10 +808,23 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     a.M = (int)M;
     a.flags = d->flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_BIAS | FFK_EPI_INSCALE);
     a.in_scale = d->in_scale;
-    a.tiles_n = d->cout / e->bn;
-    const int tiles_m = (int)((M + e->bm - 1) / e->bm);
-    e->fn(a, tiles_m * a.tiles_n, (hipStream_t)stream);
+    const ConvLaunch l = choose_launch(e, M, d->workspace ? d->workspace_bytes : 0);
+    if (l.split > 1) {
+        a.counters = (unsigned*)d->workspace;
+        a.ws = (int32_t*)((int8_t*)d->workspace + l.counter_bytes);
+    }
+    a.tiles_n = d->cout / l.bn;
+    l.fn(a, l.grid, (hipStream_t)stream);
     return ffk_check_launch("conv launch");
+}
+
+size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d) {
+    if (!d || d->batch <= 0) return 0;
+    const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);
+    if (!e) return 0;
+    const long long M = conv_pixels(d);
+    if (M > 0x7fffffffLL) return 0;
+    return choose_launch(e, M, (size_t)-1).ws_bytes;
 }
 
 // BN second output as a table: lut[c][q + 128] = BN-requant of the int8

@@ -20,6 +20,15 @@ int ffk_hip_fail(hipError_t e, const char* what) {
     return FFK_ERR_HIP;
 }
 
+// n bytes from a 16-byte aligned d: 16-byte vector stores, then the tail
+__global__ void zero_kernel(int8_t* d, size_t n) {
+    const size_t n16 = n / 16;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        reinterpret_cast<v4i*>(d)[i] = v4i{0, 0, 0, 0};
+    if (blockIdx.x == 0 && threadIdx.x < n - n16 * 16) d[n16 * 16 + threadIdx.x] = 0;
+}
+
 extern "C" {
 
 const char* ffk_last_error(void) { return g_err; }
@@ -71,6 +80,18 @@ int ffk_memcpy_d2h(void* h, const void* d, size_t n, void* s) {
 }
 int ffk_memcpy_d2d(void* d, const void* s2, size_t n, void* s) {
     return copy(d, s2, n, hipMemcpyDeviceToDevice, s, "memcpy d2d");
+}
+
+int ffk_zero(void* d, size_t n, void* s) {
+    if (n == 0) return FFK_OK;
+    if (!d || ((uintptr_t)d & 15)) {
+        ffk_set_error("zero: null or unaligned pointer%s%s", nullptr, nullptr);
+        return FFK_ERR_ARG;
+    }
+    const size_t n16 = n / 16;
+    const int grid = (int)(n16 / 256 + 1 < 4096 ? n16 / 256 + 1 : 4096);
+    hipLaunchKernelGGL(zero_kernel, dim3(grid), dim3(256), 0, (hipStream_t)s, (int8_t*)d, n);
+    return ffk_check_launch("zero launch");
 }
 
 int ffk_stream_create(void** s) {
@@ -130,7 +151,7 @@ int ffk_graph_end(void* s, void** exec) {
     if (e != hipSuccess) return ffk_hip_fail(e, "hipStreamEndCapture");
     hipGraphExec_t ge = nullptr;
     e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     if (e != hipSuccess) return ffk_hip_fail(e, "hipGraphInstantiate");
     *exec = ge;
     return FFK_OK;

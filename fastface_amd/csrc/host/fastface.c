@@ -33,6 +33,8 @@ struct FastFace {
     int8_t** d_bufs;            /* plan.n_buffers buffers */
     float* d_input;             /* capacity * 37632 */
     float* d_output;            /* capacity * 512 */
+    void* d_ws;                 /* split-K workspace of the small-batch convs */
+    size_t ws_bytes;
     ffk_io* d_io;               /* device I/O descriptor */
     ffk_io* h_io;               /* pinned staging */
     ffk_io io_cur;              /* what d_io holds now */
@@ -63,6 +65,8 @@ static void free_activations(FastFace* ff)
     }
     ffk_free(ff->d_input); ff->d_input = NULL;
     ffk_free(ff->d_output); ff->d_output = NULL;
+    ffk_free(ff->d_ws); ff->d_ws = NULL;
+    ff->ws_bytes = 0;
     ff->capacity = 0;
 }
 
@@ -82,6 +86,27 @@ static int set_io(FastFace* ff, const float* in, float* out, void* stream)
     return 0;
 }
 
+static void step_desc(FastFace* ff, int s, int batch, ffk_conv_desc* d);
+
+/* Largest split-K workspace any conv step asks for at 1..max_batch faces.
+ * Only small batches split (the split grid is capped at a few thousand
+ * 64x64 tiles, i.e. below ~4096 faces for every IResNet layer). */
+static size_t workspace_bytes(FastFace* ff, int max_batch)
+{
+    size_t best = 0;
+    const int top = max_batch < 4096 ? max_batch : 4096;
+    for (int s = 0; s < ff->plan.n_steps; s++) {
+        if (ff->plan.steps[s].kind != 1) continue;
+        for (int b = 1; b <= top; b++) {
+            ffk_conv_desc d;
+            step_desc(ff, s, b, &d);
+            const size_t n = ffk_conv_workspace_bytes(&d);
+            if (n > best) best = n;
+        }
+    }
+    return best;
+}
+
 static int ensure_capacity(FastFace* ff, int batch)
 {
     if (batch <= ff->capacity) return 0;
@@ -99,6 +124,15 @@ static int ensure_capacity(FastFace* ff, int batch)
     ff->d_input = (float*)ffk_malloc((size_t)batch * FASTFACE_INPUT_N * sizeof(float));
     ff->d_output = (float*)ffk_malloc((size_t)batch * FASTFACE_OUTPUT_N * sizeof(float));
     if (!ff->d_input || !ff->d_output) { free_activations(ff); return FFK_ERR_NOMEM; }
+    const size_t ws = workspace_bytes(ff, batch);
+    if (ws) {
+        ff->d_ws = ffk_malloc(ws);
+        if (!ff->d_ws) { free_activations(ff); return FFK_ERR_NOMEM; }
+        rc = ffk_zero(ff->d_ws, ws, ff->stream);
+        if (!rc) rc = ffk_stream_sync(ff->stream);
+        if (rc) { free_activations(ff); return rc; }
+        ff->ws_bytes = ws;
+    }
     ff->capacity = batch;
     ff->io_cur.in = NULL; ff->io_cur.out = NULL;
     return 0;
@@ -111,29 +145,40 @@ static int8_t* tensor_ptr(FastFace* ff, int t)
     return b >= 0 ? ff->d_bufs[b] : NULL;
 }
 
+/* conv descriptor of step s (pointers are NULL while no activations exist) */
+static void step_desc(FastFace* ff, int s, int batch, ffk_conv_desc* d)
+{
+    const FfStep* st = &ff->plan.steps[s];
+    memset(d, 0, sizeof *d);
+    d->batch = batch; d->cin = st->cin; d->cout = st->cout; d->kh = st->kh; d->kw = st->kw;
+    d->stride = st->stride; d->pad = st->pad; d->hin = st->hin; d->win = st->win;
+    if (st->t_in == FF_T_INPUT) {
+        d->in = NULL;
+        d->io = ff->d_io;
+        d->in_inv = ff->d_in_inv;
+    } else {
+        d->in = ff->d_bufs ? tensor_ptr(ff, st->t_in) : NULL;
+    }
+    d->w = ff->d_weights + st->w_off;
+    d->params = ff->d_params + st->p_off;
+    if (ff->d_bufs) {
+        d->add_src = tensor_ptr(ff, st->t_add);
+        d->out = tensor_ptr(ff, st->t_out);
+        d->out_bn = tensor_ptr(ff, st->t_bn);
+    }
+    if (st->flags & FFK_EPI_BN) d->bn_lut = ff->d_weights + st->lut_off;
+    d->flags = st->flags;
+    d->in_scale = st->in_scale;
+    d->workspace = ff->d_ws;
+    d->workspace_bytes = ff->ws_bytes;
+}
+
 static int launch_step(FastFace* ff, int s, int batch, void* stream)
 {
     const FfStep* st = &ff->plan.steps[s];
     if (st->kind == 1) {
         ffk_conv_desc d;
-        memset(&d, 0, sizeof d);
-        d.batch = batch; d.cin = st->cin; d.cout = st->cout; d.kh = st->kh; d.kw = st->kw;
-        d.stride = st->stride; d.pad = st->pad; d.hin = st->hin; d.win = st->win;
-        if (st->t_in == FF_T_INPUT) {
-            d.in = NULL;
-            d.io = ff->d_io;
-            d.in_inv = ff->d_in_inv;
-        } else {
-            d.in = tensor_ptr(ff, st->t_in);
-        }
-        d.w = ff->d_weights + st->w_off;
-        d.params = ff->d_params + st->p_off;
-        d.add_src = tensor_ptr(ff, st->t_add);
-        d.out = tensor_ptr(ff, st->t_out);
-        d.out_bn = tensor_ptr(ff, st->t_bn);
-        if (st->flags & FFK_EPI_BN) d.bn_lut = ff->d_weights + st->lut_off;
-        d.flags = st->flags;
-        d.in_scale = st->in_scale;
+        step_desc(ff, s, batch, &d);
         return ffk_conv(&d, stream);
     }
     ffk_fc_desc f;

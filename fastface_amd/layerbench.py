@@ -31,6 +31,8 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--epi", default="prelu", choices=["prelu", "add_bn", "none", "raw"])
+    ap.add_argument("--no-split", action="store_true",
+                    help="give no split-K workspace (small batches then use the whole-K tiling)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="instead: device-to-device copies of this many MiB (the calibration "
                          "workload for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -95,6 +97,10 @@ def main():
         lib.ffk_make_bn_lut(rows[0].ctypes.data, rows[1].ctypes.data, rows[2].ctypes.data,
                             rows[3].ctypes.data, a.cout, lut.ctypes.data)
         d.bn_lut = dev(lut)
+    ws_bytes = 0 if a.no_split else lib.ffk_conv_workspace_bytes(C.byref(d))
+    if ws_bytes:
+        d.workspace, d.workspace_bytes = dev(nbytes=ws_bytes), ws_bytes
+        assert lib.ffk_zero(d.workspace, ws_bytes, None) == 0, fa.last_error()
     stream = C.c_void_p()
     lib.ffk_stream_create(C.byref(stream))
     for _ in range(3):
@@ -111,7 +117,8 @@ def main():
     per = ms.value / a.iters
     ops = 2.0 * a.batch * ho * ho * a.cout * a.k * a.k * a.cin
     print(json.dumps({"layer": "%d->%d k%d s%d @%d" % (a.cin, a.cout, a.k, a.stride, a.hin),
-                      "batch": a.batch, "epi": a.epi, "ms_per_launch": round(per, 5),
+                      "batch": a.batch, "epi": a.epi, "split_ws_bytes": ws_bytes,
+                      "ms_per_launch": round(per, 5),
                       "int8_tops": round(ops / (per * 1e-3) / 1e12, 2),
                       "frac_of_peak": round(ops / (per * 1e-3) / 5e15, 4)}), flush=True)
 

@@ -37,6 +37,8 @@ int   ffk_host_free(void* hptr);
 int   ffk_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int   ffk_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int   ffk_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* zero-fill with a kernel (safe inside graph capture; 16-byte aligned dst) */
+int   ffk_zero(void* dst, size_t bytes, void* stream);
 int   ffk_stream_create(void** stream);
 int   ffk_stream_destroy(void* stream);
 int   ffk_stream_sync(void* stream);            /* NULL: device-wide sync */
@@ -97,6 +99,14 @@ typedef struct {
     int32_t*       out_i32;  /* non-NULL: store raw int32 accumulators only   */
     int            flags;
     float          in_scale;
+    /* Optional split-K workspace (device memory) for small batches, where the
+     * whole-K tiling would leave most CUs idle: the K reduction of each output
+     * tile is shared by several workgroups that exchange int32 partial tiles
+     * through it.  Zero-fill it once before its first use; every launch
+     * leaves its counter area zero again.  Launches sharing one workspace
+     * must be ordered (one stream).  NULL / too small: whole-K tiling. */
+    void*          workspace;
+    size_t         workspace_bytes;
 } ffk_conv_desc;
 
 /* 1 if a kernel is compiled for this layer geometry, else 0. */
@@ -106,6 +116,10 @@ int    ffk_conv_supported(int cin, int cout, int kh, int kw, int stride, int pad
 size_t ffk_conv_packed_bytes(int cin, int cout, int kh, int kw);
 int    ffk_pack_conv_weights(const int8_t* w_oihw, int cout, int cin, int kh, int kw,
                              int8_t* packed);
+/* Workspace bytes ffk_conv would use for this descriptor's geometry and
+ * batch (0: it takes the whole-K tiling and needs none); the workspace and
+ * workspace_bytes fields are not read. */
+size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d);
 int    ffk_conv(const ffk_conv_desc* d, void* stream);
 
 /* The BN second output as a table: lut[c*256 + q + 128] is the reference's

@@ -79,9 +79,29 @@ def params_block(cout, **rows):
     return P
 
 
+def conv_workspace(lib, d):
+    """Zero-filled split-K workspace of the size ffk_conv asks for (or None)."""
+    n = lib.ffk_conv_workspace_bytes(C.byref(d))
+    if n == 0:
+        return None
+    ws = Dev(lib, nbytes=n)
+    check(lib, lib.ffk_zero(ws.ptr, n, None))
+    return ws
+
+
+SPLIT_COUNTERS = 160      # uint32 arrival counters at the start of the workspace
+
+
+def split_counters_zero(lib, ws):
+    """The whole counter area is zero again after a launch."""
+    return not ws.get(np.uint32, (SPLIT_COUNTERS,)).any()
+
+
 def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=False,
-             want_x=True, want_bn=False, in_inv=None, in_scale=1.0):
-    """One ffk_conv call; returns int32 acc (raw) or (X, BN(X)) int8 arrays."""
+             want_x=True, want_bn=False, in_inv=None, in_scale=1.0, split=True):
+    """One ffk_conv call; returns int32 acc (raw) or (X, BN(X)) int8 arrays.
+    split: give the call the split-K workspace it asks for (small batches take
+    the split path); False: no workspace (whole-K tiling)."""
     B, H, W, cin = x.shape
     cout, _, kh, kw = w_oihw.shape
     ho = (H + 2 * pad - kh) // stride + 1
@@ -121,8 +141,14 @@ def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=Fa
             d.out_bn = dob.ptr
     d.flags = flags
     d.in_scale = in_scale
+    ws = conv_workspace(lib, d) if split else None
+    if ws is not None:
+        keep.append(ws)
+        d.workspace, d.workspace_bytes = ws.ptr, ws.nbytes
     check(lib, lib.ffk_conv(C.byref(d), None))
     check(lib, lib.ffk_stream_sync(None))
+    if ws is not None:
+        assert split_counters_zero(lib, ws)
     if raw:
         return do.get(np.int32, (B, ho, wo, cout))
     x_out = dox.get(np.int8, (B, ho, wo, cout)) if want_x else None

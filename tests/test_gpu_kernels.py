@@ -29,30 +29,68 @@ def test_mfma_lane_layout(gpu_lib):
     assert gpu_lib.ffk_selftest_mfma() == 0, fa.last_error()
 
 
+# geometries with a split-K small-batch variant (one face takes it)
+SPLIT_SHAPES = [(256, 256, 3, 2, 28), (256, 256, 3, 1, 14), (256, 512, 3, 1, 14),
+                (512, 512, 3, 2, 14), (512, 512, 3, 1, 7)]
+
+
+def _assert_split_taken(lib, cin, cout, k, s, H, B):
+    import ctypes as C
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, k, k
+    d.stride, d.pad, d.hin, d.win = s, k // 2, H, H
+    assert lib.ffk_conv_workspace_bytes(C.byref(d)) > 0
+
+
+@pytest.mark.parametrize("split", [True, False], ids=["splitk", "wholek"])
 @pytest.mark.parametrize("cin,cout,k,s,H", SHAPES)
-def test_conv_int32_accumulators(gpu_lib, oracle, cin, cout, k, s, H):
+def test_conv_int32_accumulators(gpu_lib, oracle, cin, cout, k, s, H, split):
+    if split and (cin, cout, k, s, H) not in SPLIT_SHAPES:
+        pytest.skip("no split-K variant for this geometry")
     r = rng(100 + cin + cout + k * 7 + s * 3 + H)
-    B = _batch_for(H)
+    B = 1 if split else _batch_for(H)
+    if split:
+        _assert_split_taken(gpu_lib, cin, cout, k, s, H, B)
     x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
     w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
     x[0, 0, :, :] = -128                      # extreme products
     w[0] = -128
-    got = run_conv(gpu_lib, x, w, s, k // 2, raw=True)
+    got = run_conv(gpu_lib, x, w, s, k // 2, raw=True, split=split)
     assert np.array_equal(got, oracle.conv_i32(x, w, s, k // 2))
 
 
-def test_stem_int32_with_fused_input_quant(gpu_lib, oracle):
-    r = rng(7)
-    B = 2
-    x = r.uniform(-1, 1, size=(B, 112, 112, 3)).astype(F32)
-    x[0, 0, :4, 0] = [0.5 / 127, -2.5 / 127, 1e10, -1e10]
-    x[0, 1, :3, 1] = [np.inf, -np.inf, np.nan]
-    x[1, 5, 5, :] = [3e9, -3e9, 2.5 / 127]
-    inv = np.array([127.0, 127.00001, 126.5], F32)
-    w = r.integers(-128, 128, size=(64, 3, 3, 3), dtype=np.int8)
-    got = run_conv(gpu_lib, x, w, 1, 1, raw=True, in_inv=inv)
-    q = oracle.quant_input(x, inv)
-    assert np.array_equal(got, oracle.conv_i32(q, w, 1, 1))
+@pytest.mark.parametrize("cin,cout,s,H,batches", [(512, 512, 1, 7, (2, 1, 2)),
+                                                   (512, 512, 2, 14, (1, 2))])
+def test_split_workspace_reused_across_calls(gpu_lib, oracle, cin, cout, s, H, batches):
+    """Split-K launches of different batch sizes in a row on one workspace
+    (sized for the largest): the arrival counters are back at zero after each,
+    and every result is exact."""
+    import ctypes as C
+    from gpu_util import Dev, check, pack_conv, split_counters_zero
+    lib = gpu_lib
+    r = rng(41 + cin)
+    w = r.integers(-128, 128, size=(cout, cin, 3, 3), dtype=np.int8)
+    dw = Dev(lib, host=pack_conv(lib, w))
+    d = fa.ffk_conv_desc()
+    d.cin, d.cout, d.kh, d.kw, d.stride, d.pad, d.hin, d.win = cin, cout, 3, 3, s, 1, H, H
+    Ho = (H - 1) // s + 1
+    n = 0
+    for B in batches:
+        d.batch = B
+        need = lib.ffk_conv_workspace_bytes(C.byref(d))
+        assert need > 0
+        n = max(n, need)
+    ws = Dev(lib, nbytes=n)
+    check(lib, lib.ffk_zero(ws.ptr, n, None))
+    d.w, d.workspace, d.workspace_bytes = dw.ptr, ws.ptr, n
+    for B in batches:
+        x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+        dx, do = Dev(lib, host=x), Dev(lib, nbytes=B * Ho * Ho * cout * 4)
+        d.batch, d.in_, d.out_i32 = B, dx.ptr, do.ptr
+        check(lib, lib.ffk_conv(C.byref(d), None))
+        check(lib, lib.ffk_stream_sync(None))
+        assert split_counters_zero(lib, ws)
+        assert np.array_equal(do.get(np.int32, (B, Ho, Ho, cout)), oracle.conv_i32(x, w, s, 1)), B
 
 
 def _special_params(r, C):
@@ -74,11 +112,16 @@ EPI_SHAPES = [(64, 64, 3, 1, 56), (64, 64, 1, 2, 112), (128, 256, 1, 2, 28),
               (256, 256, 3, 1, 14), (512, 512, 3, 1, 7)]
 
 
+@pytest.mark.parametrize("split", [True, False], ids=["splitk", "wholek"])
 @pytest.mark.parametrize("mode", EPI_MODES)
 @pytest.mark.parametrize("cin,cout,k,s,H", EPI_SHAPES)
-def test_conv_fused_epilogue(gpu_lib, oracle, mode, cin, cout, k, s, H):
+def test_conv_fused_epilogue(gpu_lib, oracle, mode, cin, cout, k, s, H, split):
+    if split and (cin, cout, k, s, H) not in SPLIT_SHAPES:
+        pytest.skip("no split-K variant for this geometry")
     r = rng(300 + cin + cout + H + EPI_MODES.index(mode))
-    B = 2
+    B = 1 if split else 2
+    if split:
+        _assert_split_taken(gpu_lib, cin, cout, k, s, H, B)
     x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
     w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
     Ho = (H + 2 * (k // 2) - k) // s + 1
@@ -106,7 +149,8 @@ def test_conv_fused_epilogue(gpu_lib, oracle, mode, cin, cout, k, s, H):
     acc = oracle.conv_i32(x, w, s, k // 2)
     exp_x = oracle.fused_epilogue(acc, **ekw)
     got_x, got_bn = run_conv(gpu_lib, x, w, s, k // 2, params=params_block(cout, **rows),
-                             flags=flags, add=add, want_x=(mode != "bn_only"), want_bn=want_bn)
+                             flags=flags, add=add, want_x=(mode != "bn_only"), want_bn=want_bn,
+                             split=split)
     if mode != "bn_only":
         assert np.array_equal(got_x, exp_x)
     if want_bn:

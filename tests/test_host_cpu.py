@@ -1,5 +1,6 @@
 """Host-side checks that need no GPU: the C ABI library loads and exports
 every entry point the headers declare, weight packing, plan coverage."""
+import ctypes as C
 import os
 import re
 
@@ -115,3 +116,29 @@ def test_create_without_gpu_returns_null(synth_ffw4):
         assert lib.fastface_create(synth_ffw4.encode()) is None
     finally:
         os.chdir(old)
+
+
+def test_split_workspace_only_for_small_batches():
+    """Small batches of the 3x3 layers take the split-K path (a workspace is
+    asked for); large batches and the stem never do."""
+    lib = fa.load()
+    d = fa.ffk_conv_desc()
+
+    def need(cin, cout, k, s, H, B):
+        d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, k, k
+        d.stride, d.pad, d.hin, d.win = s, k // 2, H, H
+        return lib.ffk_conv_workspace_bytes(C.byref(d))
+    for cin, cout, s, H in [(256, 256, 2, 28), (256, 256, 1, 14), (256, 512, 1, 14),
+                            (512, 512, 1, 7), (512, 512, 2, 14)]:
+        n = need(cin, cout, 3, s, H, 1)
+        ho = (H - 1) // s + 1
+        tiles = -(-ho * ho // 64) * (cout // 64)
+        assert n > tiles * 64 * 64 * 4, (cin, cout, s, H)
+        assert need(cin, cout, 3, s, H, 64) == 0
+        assert need(cin, cout, 3, s, H, 1024) == 0
+    assert need(3, 64, 3, 1, 112, 1) == 0
+    assert need(64, 64, 3, 1, 56, 1) == 0             # short K chains never split
+    assert need(128, 256, 3, 1, 28, 1) == 0
+    assert need(64, 64, 1, 2, 112, 1) == 0            # 1x1: one K stage, nothing to split
+    assert need(96, 64, 3, 1, 112, 1) == 0            # no kernel
+    assert lib.ffk_conv_workspace_bytes(None) == 0

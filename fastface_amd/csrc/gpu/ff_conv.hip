@@ -29,14 +29,12 @@
 #include "ff_internal.h"
 #include "ff_numerics.h"
 
-#define EPI_FC 0x100  // internal: FC head, fp32 output via ff::fc_out
-
 // stages of global loads kept in flight per thread (64- and 128-byte stages)
 #ifndef FF_PF
 #define FF_PF 4
 #endif
 #ifndef FF_PF128
-#define FF_PF128 2
+#define FF_PF128 3
 #endif
 
 constexpr int FF_LUT_PITCH = 272;   // LDS row pitch of a 256-entry table
@@ -109,7 +107,6 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
         }
         __syncthreads();
     }
-    uint32_t bnw[MI][NJ][4];
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
@@ -124,64 +121,64 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
                 f = f + bias[j];
                 if (ADD) f = ff::add_residual(f, (int32_t)Ws[row * P + col], adds[j]);
                 if (PRELU) f = ff::prelu(f, p2[j]);
-                const int32_t q = ff::requant_haz(f * inv[j]);
-                Ws[row * P + col] = (int8_t)q;
-                if (BN2) {
-                    if ((r & 3) == 0) bnw[i][j][r >> 2] = 0;
-                    const uint32_t q2 = (uint8_t)Lw[col * FF_LUT_PITCH + q + 128];
-                    bnw[i][j][r >> 2] |= q2 << ((r & 3) * 8);
-                }
+                Ws[row * P + col] = (int8_t)ff::requant_haz(f * inv[j]);
+                // one 32x32 tile at a time: keeps the compiler from hoisting
+                // every residual read of the wave tile into registers
+                if (r == 15) asm volatile("" ::: "memory");
             }
     __syncthreads();
+    // Flush: 16-byte chunks of the X tile go out as they are; the BN second
+    // output maps each byte through its channel's table on the way.
 #pragma unroll
     for (int k = 0; k < ROWS / RPI; k++) {
         const int row = lane / CH + k * RPI;
         const int ch = lane % CH;
         const int m = mrow0 + row;
         const v4i v = *reinterpret_cast<const v4i*>(Ws + row * P + ch * 16);
-        if (a.out && m < a.M) *reinterpret_cast<v4i*>(a.out + (size_t)m * COUT + ncol0 + ch * 16) = v;
-    }
-    if (BN2) {
-        __syncthreads();
+        if (m < a.M) {
+            if (a.out) *reinterpret_cast<v4i*>(a.out + (size_t)m * COUT + ncol0 + ch * 16) = v;
+            if (BN2) {
+                const int8_t* L = Lw + (ch * 16) * FF_LUT_PITCH + 128;
+                v4i o;
 #pragma unroll
-        for (int i = 0; i < MI; i++)
+                for (int w = 0; w < 4; w++) {
+                    uint32_t packed = 0;
 #pragma unroll
-            for (int j = 0; j < NJ; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
-                    Ws[row * P + j * 32 + lc] = (int8_t)(bnw[i][j][r >> 2] >> ((r & 3) * 8));
+                    for (int e = 0; e < 4; e++) {
+                        const int q = (int8_t)((uint32_t)v[w] >> (e * 8));
+                        packed |= (uint32_t)(uint8_t)L[(w * 4 + e) * FF_LUT_PITCH + q] << (e * 8);
+                    }
+                    o[w] = (int)packed;
                 }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < ROWS / RPI; k++) {
-            const int row = lane / CH + k * RPI;
-            const int ch = lane % CH;
-            const int m = mrow0 + row;
-            const v4i v = *reinterpret_cast<const v4i*>(Ws + row * P + ch * 16);
-            if (m < a.M) *reinterpret_cast<v4i*>(a.out_bn + (size_t)m * COUT + ncol0 + ch * 16) = v;
+                *reinterpret_cast<v4i*>(a.out_bn + (size_t)m * COUT + ncol0 + ch * 16) = o;
+            }
         }
+        if (BN2) asm volatile("" ::: "memory");
     }
 }
 
-// raw int32 accumulators or the FC head's fp32 output: 4-byte elements are
-// stored straight from registers (a half-wave writes 128 contiguous bytes)
-template <int COUT, int MI, int NJ>
+// raw int32 accumulators or the FC head's fp32 output (FC: the FC GEMM
+// instantiation only): 4-byte elements are stored straight from registers (a
+// half-wave writes 128 contiguous bytes)
+template <int COUT, int MI, int NJ, bool FC>
 __device__ __forceinline__ void wave_epi_wide(const v16i (&acc)[MI][NJ], const ConvArgs& a, int mrow0,
                                               int ncol0) {
     const int lane = threadIdx.x & 63;
     const int lc = lane & 31;
     const int lh = lane >> 5;
-    if (a.out_i32) {
+    if (!FC) {
 #pragma unroll
         for (int i = 0; i < MI; i++)
 #pragma unroll
-            for (int j = 0; j < NJ; j++)
+            for (int j = 0; j < NJ; j++) {
+                int32_t* col = a.out_i32 + ncol0 + j * 32 + lc;
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int m = mrow0 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
-                    if (m < a.M) a.out_i32[(size_t)m * COUT + ncol0 + j * 32 + lc] = acc[i][j][r];
+                    if (m < a.M) col[(size_t)m * COUT] = acc[i][j][r];
                 }
+                asm volatile("" ::: "memory");
+            }
         return;
     }
     float* out = a.out_f32 ? a.out_f32 : a.io->out;
@@ -199,11 +196,15 @@ __device__ __forceinline__ void wave_epi_wide(const v16i (&acc)[MI][NJ], const C
     }
 }
 
-template <int COUT, int MI, int NJ>
+template <int COUT, int MI, int NJ, bool FC = false>
 __device__ __forceinline__ void wave_epilogue(const v16i (&acc)[MI][NJ], const ConvArgs& a, int mrow0,
                                               int ncol0, int8_t* Ws, const int8_t* Lw) {
-    if (a.out_i32 || (a.flags & EPI_FC)) {
-        wave_epi_wide<COUT, MI, NJ>(acc, a, mrow0, ncol0);
+    if (FC) {
+        wave_epi_wide<COUT, MI, NJ, true>(acc, a, mrow0, ncol0);
+        return;
+    }
+    if (a.out_i32) {
+        wave_epi_wide<COUT, MI, NJ, false>(acc, a, mrow0, ncol0);
         return;
     }
     switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN)) {
@@ -471,8 +472,182 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
         load_bn_lut<256>(Ls, a.bn_lut, tn * BN, BN);
         __syncthreads();
     }
-    wave_epilogue<COUT, MI, NJ>(acc, a, m0 + wm * WTM, tn * BN + wn * WTN, Ws,
+    // the FC head runs this kernel as a 1x1 "conv" over a 1x1 image
+    wave_epilogue<COUT, MI, NJ, HIN == 1 && WIN == 1>(acc, a, m0 + wm * WTM, tn * BN + wn * WTN, Ws,
                                 Ls + (wn * WTN) * FF_LUT_PITCH);
+}
+
+// ---------------------------------------------------------------------------
+// Conv kernel with direct-to-LDS operand loads (global_load_lds_dwordx4).
+// ---------------------------------------------------------------------------
+// WM x WN waves, each an MI x NJ block of 32x32 MFMA tiles: BM = WM*MI*32,
+// BN = WN*NJ*32.  The K loop runs over 64-byte stages (one tap's 64-channel
+// run).  Global loads go straight into an NST-deep LDS ring -- no register
+// staging and no LDS store instructions, so the registers go to occupancy
+// (WPE waves per SIMD) instead.  One wave load instruction writes 1 KB of LDS,
+// lane L at byte 16*L.  A stage tile is a run of 128-byte lines of two 64-byte
+// rows; the 16-byte slot of (row r, piece p) in line r/2 is
+// ((r%2)*4 + p) XOR (r/2 % 8), which keeps the ds_read_b128 operand reads
+// conflict-free.  The swizzle is realised by choosing which global piece each
+// lane fetches: a line's 8 lanes still read one 128-byte window.
+// Per stage: wait for this thread's loads of the stage (vmcnt), barrier (every
+// thread's loads landed; every wave is done with the stage the next loads
+// overwrite), issue the loads of stage s+NST-1, then the MFMAs of stage s.
+constexpr int DMA_KB = 64;
+
+__device__ __forceinline__ int dma_slot(int r, int p) {
+    const int line = r >> 1;
+    return line * 128 + ((((r & 1) << 2) | p) ^ (line & 7)) * 16;
+}
+
+// Wait until at most N of this wave's global loads are in flight (and its LDS
+// reads are done), then barrier.  Written as one asm block so that neither
+// the compiler's waitcnt pass nor its scheduler moves LDS accesses across it.
+template <int N>
+__device__ __forceinline__ void dma_wait_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void dma16(const int8_t* g, int8_t* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+}
+
+template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int WM, int WN, int MI, int NJ,
+          int NST, int WPE>
+__global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a) {
+    constexpr int NW = WM * WN;
+    constexpr int NT = NW * 64;
+    constexpr int BM = WM * MI * 32, BN = WN * NJ * 32;
+    constexpr int PAD = KS / 2;
+    constexpr int HOUT = (HIN + 2 * PAD - KS) / STRIDE + 1;
+    constexpr int WOUT = (WIN + 2 * PAD - KS) / STRIDE + 1;
+    constexpr int HWO = HOUT * WOUT;
+    constexpr int CSTEPS = CIN / DMA_KB;
+    constexpr int KSTEPS = KS * KS * CSTEPS;
+    constexpr int A_BYTES = BM * DMA_KB, B_BYTES = BN * DMA_KB;
+    constexpr int STAGE = A_BYTES + B_BYTES;
+    constexpr int A_LD = A_BYTES / (NT * 16), B_LD = B_BYTES / (NT * 16);
+    constexpr int LPS = A_LD + B_LD;                        // loads per thread and stage
+    constexpr int LDS_K = NST * STAGE;
+    constexpr int LDS_E = NW * wave_tile_bytes<MI, NJ>() + BN * FF_LUT_PITCH;
+    constexpr int LDS = LDS_K > LDS_E ? LDS_K : LDS_E;
+    static_assert(CIN % DMA_KB == 0, "Cin must be a multiple of 64");
+    static_assert(A_BYTES % (NT * 16) == 0 && B_BYTES % (NT * 16) == 0, "whole wave loads");
+    static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
+    static_assert(NST >= 2 && (NST - 2) * LPS < 64, "ring depth");
+
+    __shared__ __align__(1024) int8_t smem[LDS];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int xbid = xcd_tile(blockIdx.x, gridDim.x);
+    const int tn = xbid % a.tiles_n;
+    const int tm = xbid / a.tiles_n;
+    const int m0 = tm * BM;
+
+    // This thread's pieces: wave load j of wave w fills lines (j*NW + w)*8 ..
+    // +7 of the stage tile; lane L takes line +L/8, slot L%8.  Registers are
+    // kept few (occupancy): a 32-bit image offset per piece, the piece's input
+    // origin (a row past the tile's end gets an origin that fails every bounds
+    // check), and its 16-byte slot in a 64-byte channel run.
+    int a_off[A_LD], a_ih0[A_LD], a_iw0[A_LD], a_p[A_LD];
+#pragma unroll
+    for (int j = 0; j < A_LD; j++) {
+        const int line = (j * NW + wave) * 8 + (lane >> 3);
+        const int s = (lane & 7) ^ (line & 7);
+        const int r = line * 2 + (s >> 2);
+        const int p = s & 3;
+        const int m = m0 + r;
+        const bool ok = m < a.M;
+        const int mm = ok ? m : 0;
+        const int b = mm / HWO;
+        const int rr = mm - b * HWO;
+        const int oh = rr / WOUT;
+        const int ow = rr - oh * WOUT;
+        a_off[j] = b * (HIN * WIN * CIN) + p * 16;
+        a_ih0[j] = ok ? oh * STRIDE - PAD : -4 * HIN;
+        a_iw0[j] = ow * STRIDE - PAD;
+        a_p[j] = p;
+    }
+    int b_off[B_LD];
+#pragma unroll
+    for (int j = 0; j < B_LD; j++) {
+        const int line = (j * NW + wave) * 8 + (lane >> 3);
+        const int s = (lane & 7) ^ (line & 7);
+        const int n = line * 2 + (s >> 2);
+        b_off[j] = (tn * BN + n) * FF_KSTEP + (s & 3) * 16;
+    }
+    auto issue = [&](int st, int buf) {
+        const int tap = st / CSTEPS;
+        const int cs = st - tap * CSTEPS;
+        const int kh = tap / KS;
+        const int kw = tap - kh * KS;
+        int8_t* sb = smem + buf * STAGE;
+#pragma unroll
+        for (int j = 0; j < A_LD; j++) {
+            const int ih = a_ih0[j] + kh;
+            const int iw = a_iw0[j] + kw;
+            const bool v = (unsigned)ih < (unsigned)HIN && (unsigned)iw < (unsigned)WIN;
+            const int8_t* src = v ? a.in + (a_off[j] + (ih * WIN + iw) * CIN + cs * DMA_KB)
+                                  : ff_zero_page + a_p[j] * 16;
+            dma16(src, sb + (j * NW + wave) * 1024);
+        }
+        const int8_t* wst = a.w + (size_t)st * COUT * FF_KSTEP;
+#pragma unroll
+        for (int j = 0; j < B_LD; j++) dma16(wst + b_off[j], sb + A_BYTES + (j * NW + wave) * 1024);
+    };
+
+    const int wm = wave / WN;
+    const int wn = wave % WN;
+    // Fragment (i, ks) of this lane sits at a_rd + i*2048, XOR ks*32: 32 rows
+    // are 16 lines (the swizzle key line%8 repeats), and the second 32-byte
+    // k half flips bit 1 of the slot.
+    const int a_rd = dma_slot(wm * MI * 32 + (lane & 31), lane >> 5);
+    const int b_rd = A_BYTES + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
+
+    v16i acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+#pragma unroll
+    for (int u = 0; u < NST - 1; u++)
+        if (u < KSTEPS) issue(u, u);
+    int rbuf = 0;                          // ring slot of stage s
+    for (int s = 0; s < KSTEPS; s++) {
+        if (s + NST - 2 < KSTEPS) dma_wait_barrier<(NST - 2) * LPS>();
+        else dma_wait_barrier<0>();
+        if (s + NST - 1 < KSTEPS) issue(s + NST - 1, rbuf == 0 ? NST - 1 : rbuf - 1);
+        const int8_t* sb = smem + rbuf * STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            v4i af[MI], bf[NJ];
+#pragma unroll
+            for (int i = 0; i < MI; i++) af[i] = *reinterpret_cast<const v4i*>(sb + ((a_rd + i * 2048) ^ (ks * 32)));
+#pragma unroll
+            for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(sb + ((b_rd + j * 2048) ^ (ks * 32)));
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        rbuf = rbuf == NST - 1 ? 0 : rbuf + 1;
+    }
+    __syncthreads();                       // every wave is done with the ring
+
+    int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
+    int8_t* Ls = smem + NW * wave_tile_bytes<MI, NJ>();
+    if (a.flags & FFK_EPI_BN && !a.out_i32) {
+        load_bn_lut<NT>(Ls, a.bn_lut, tn * BN, BN);
+        __syncthreads();
+    }
+    wave_epilogue<COUT, MI, NJ>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
+                                Ls + (wn * NJ * 32) * FF_LUT_PITCH);
 }
 
 // ---------------------------------------------------------------------------
@@ -567,6 +742,13 @@ void launch_conv(const ConvArgs& a, int grid, hipStream_t s) {
                        dim3(grid), dim3(256), 0, s, a);
 }
 
+template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int WM, int WN, int MI, int NJ,
+          int NST, int WPE>
+void launch_conv_dma(const ConvArgs& a, int grid, hipStream_t s) {
+    hipLaunchKernelGGL((conv_dma_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, WM, WN, MI, NJ, NST, WPE>),
+                       dim3(grid), dim3(WM * WN * 64), 0, s, a);
+}
+
 void launch_stem(const ConvArgs& a, int grid, hipStream_t s) {
     (void)grid;
     const int tiles = a.M / (112 * 2);
@@ -589,8 +771,14 @@ struct ConvEntry {
     int cin, cout, ks, stride, hin, win, bm, bn;
     launch_fn fn;
     int split;          // K split of the small-batch variant (1: no partial tiles)
-    launch_fn small;    // 64x64-tile variant (stem: none)
+    launch_fn small;    // 64x64-tile split-K variant, or none
+    launch_fn mid;      // 128x128-tile register-staged variant for grids too small
+                        // for the big direct-to-LDS tiles, or none
 };
+
+// A grid of fewer big tiles than this leaves CUs idle; the 128x128 variant
+// (four times the workgroups) is taken instead.
+constexpr int FF_MID_MAX_WG = 512;
 
 // Tile configurations: (BM, BN, MI, NJ, OCC) -- workgroup tile, wave tile in
 // 32x32 MFMA blocks, workgroups per CU.
@@ -622,7 +810,7 @@ constexpr launch_fn split_launch() {
 #define FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, KB, PF, BM, BN, MI, NJ, OCC)       \
     {CIN, COUT, KS, S, H, H, BM, BN,                                             \
      &launch_conv<CIN, COUT, KS, S, H, H, BM, BN, KB, PF, MI, NJ, OCC, 1>, SPLIT, \
-     split_launch<CIN, COUT, KS, S, H, SPLIT>()}
+     split_launch<CIN, COUT, KS, S, H, SPLIT>(), nullptr}
 #define FF_CONV(CIN, COUT, KS, S, H, SPLIT, TILE) \
     FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, FF_KB(CIN), FF_PFS(CIN), TILE)
 #define FF_CONV_K(CIN, COUT, KS, S, H, SPLIT, KB, PF, TILE) \
@@ -630,28 +818,48 @@ constexpr launch_fn split_launch() {
 #define FF_CONVB(CIN, COUT, KS, S, H, SPLIT) \
     FF_CONV_K(CIN, COUT, KS, S, H, SPLIT, FF_KB_BIG(CIN), FF_PF_BIG(CIN), FF_TBIG)
 
+// Direct-to-LDS tiles (WM, WN, MI, NJ, NST, WPE): 8 waves of 2x2 MFMA tiles
+// -> 256x128, a 3-stage ring, 4 waves per SIMD (two workgroups per CU).
+#ifndef FF_TDMA
+#define FF_TDMA 4, 2, 2, 2, 3, 4
+#endif
+#define FF_DENTRY(CIN, COUT, KS, S, H, SPLIT, WM, WN, MI, NJ, NST, WPE)              \
+    {CIN, COUT, KS, S, H, H, WM * MI * 32, WN * NJ * 32,                             \
+     &launch_conv_dma<CIN, COUT, KS, S, H, H, WM, WN, MI, NJ, NST, WPE>, SPLIT,      \
+     split_launch<CIN, COUT, KS, S, H, SPLIT>(),                                     \
+     &launch_conv<CIN, COUT, KS, S, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>}
+#define FF_CONVD_K(CIN, COUT, KS, S, H, SPLIT, TILE) FF_DENTRY(CIN, COUT, KS, S, H, SPLIT, TILE)
+#define FF_CONVD(CIN, COUT, KS, S, H, SPLIT) FF_CONVD_K(CIN, COUT, KS, S, H, SPLIT, FF_TDMA)
+#ifdef FF_NO_DMA
+#define FF_C128(CIN, COUT, KS, S, H, SPLIT) FF_CONV(CIN, COUT, KS, S, H, SPLIT, FF_T128)
+#define FF_CBIG(CIN, COUT, KS, S, H, SPLIT) FF_CONVB(CIN, COUT, KS, S, H, SPLIT)
+#else
+#define FF_C128(CIN, COUT, KS, S, H, SPLIT) FF_CONVD(CIN, COUT, KS, S, H, SPLIT)
+#define FF_CBIG(CIN, COUT, KS, S, H, SPLIT) FF_CONVD(CIN, COUT, KS, S, H, SPLIT)
+#endif
+
 // split: how many workgroups share the K stages of one small-batch tile (1:
 // never split).  Only the long K chains of stages 3-4 (18 or 36 stages of
 // 128 bytes) gain from it; the split is sized so that one face gives 72-144
 // workgroups.
 const ConvEntry kConvTable[] = {
-    {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem, 1, nullptr},
+    {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem, 1, nullptr, nullptr},
     FF_CONV(64, 64, 3, 1, 112, 1, FF_T64),
     FF_CONV(64, 64, 3, 2, 112, 1, FF_T64),
     FF_CONV(64, 64, 1, 2, 112, 1, FF_T64),
     FF_CONV(64, 64, 3, 1, 56, 1, FF_T64),
-    FF_CONV(64, 128, 3, 1, 56, 1, FF_T128),
-    FF_CONV(128, 128, 3, 2, 56, 1, FF_T128),
-    FF_CONV(64, 128, 1, 2, 56, 1, FF_T128),
-    FF_CONV(128, 128, 3, 1, 28, 1, FF_T128),
-    FF_CONVB(128, 256, 3, 1, 28, 1),
-    FF_CONVB(256, 256, 3, 2, 28, 6),
-    FF_CONVB(128, 256, 1, 2, 28, 1),
-    FF_CONVB(256, 256, 3, 1, 14, 9),
-    FF_CONVB(256, 512, 3, 1, 14, 3),
-    FF_CONVB(512, 512, 3, 2, 14, 9),
-    FF_CONVB(256, 512, 1, 2, 14, 1),
-    FF_CONVB(512, 512, 3, 1, 7, 9),
+    FF_C128(64, 128, 3, 1, 56, 1),
+    FF_C128(128, 128, 3, 2, 56, 1),
+    FF_C128(64, 128, 1, 2, 56, 1),
+    FF_C128(128, 128, 3, 1, 28, 1),
+    FF_CBIG(128, 256, 3, 1, 28, 1),
+    FF_CBIG(256, 256, 3, 2, 28, 6),
+    FF_CBIG(128, 256, 1, 2, 28, 1),
+    FF_CBIG(256, 256, 3, 1, 14, 9),
+    FF_CBIG(256, 512, 3, 1, 14, 3),
+    FF_CBIG(512, 512, 3, 2, 14, 9),
+    FF_CBIG(256, 512, 1, 2, 14, 1),
+    FF_CBIG(512, 512, 3, 1, 7, 9),
 };
 
 const ConvEntry* find_conv(int cin, int cout, int kh, int kw, int stride, int pad, int hin, int win) {
@@ -675,8 +883,12 @@ struct ConvLaunch {
 // ws_avail: workspace bytes the caller provides (a split > 1 variant that
 // needs more falls back to the whole-K tiling).
 ConvLaunch choose_launch(const ConvEntry* e, long long M, size_t ws_avail) {
-    const long long big = ((M + e->bm - 1) / e->bm) * (e->cout / e->bn);
+    long long big = ((M + e->bm - 1) / e->bm) * (e->cout / e->bn);
     ConvLaunch l = {e->fn, e->bn, (int)big, 1, 0, 0};
+    if (e->mid && big < FF_MID_MAX_WG) {
+        big = ((M + 127) / 128) * (e->cout / 128);
+        l = {e->mid, 128, (int)big, 1, 0, 0};
+    }
     if (!e->small || big >= FF_SPLIT_MIN_WG) return l;
     const long long tiles = ((M + FF_SM_BM - 1) / FF_SM_BM) * (e->cout / FF_SM_BN);
     const long long wgs = tiles * e->split;
@@ -721,7 +933,7 @@ int ffk_fc_gemm_launch(const ffk_fc_desc* d, hipStream_t s) {
     a.io = d->io;
     a.out_f32 = d->out;
     a.M = d->batch;
-    a.flags = EPI_FC;
+    a.flags = 0;
     a.in_scale = d->a_scale;
     a.tiles_n = 512 / 128;
     const int grid = ((d->batch + 127) / 128) * a.tiles_n;

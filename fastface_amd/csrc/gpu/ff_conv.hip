@@ -830,6 +830,21 @@ constexpr launch_fn split_launch() {
      &launch_conv<CIN, COUT, KS, S, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>}
 #define FF_CONVD_K(CIN, COUT, KS, S, H, SPLIT, TILE) FF_DENTRY(CIN, COUT, KS, S, H, SPLIT, TILE)
 #define FF_CONVD(CIN, COUT, KS, S, H, SPLIT) FF_CONVD_K(CIN, COUT, KS, S, H, SPLIT, FF_TDMA)
+#define FF_DENTRY_NOMID(CIN, COUT, KS, S, H, SPLIT, WM, WN, MI, NJ, NST, WPE)        \
+    {CIN, COUT, KS, S, H, H, WM * MI * 32, WN * NJ * 32,                             \
+     &launch_conv_dma<CIN, COUT, KS, S, H, H, WM, WN, MI, NJ, NST, WPE>, SPLIT,      \
+     split_launch<CIN, COUT, KS, S, H, SPLIT>(), nullptr}
+#define FF_CONVD64_K(CIN, COUT, KS, S, H, SPLIT, TILE) FF_DENTRY_NOMID(CIN, COUT, KS, S, H, SPLIT, TILE)
+// Cout = 64: 4 waves of 2x2 MFMA tiles -> 256x64, a 2-stage ring, 4 waves per
+// SIMD (four workgroups per CU)
+#ifndef FF_T64DMA
+#define FF_T64DMA 4, 1, 2, 2, 2, 4
+#endif
+#ifdef FF_NO_DMA
+#define FF_C64(CIN, COUT, KS, S, H, SPLIT) FF_CONV(CIN, COUT, KS, S, H, SPLIT, FF_T64)
+#else
+#define FF_C64(CIN, COUT, KS, S, H, SPLIT) FF_CONVD64_K(CIN, COUT, KS, S, H, SPLIT, FF_T64DMA)
+#endif
 #ifdef FF_NO_DMA
 #define FF_C128(CIN, COUT, KS, S, H, SPLIT) FF_CONV(CIN, COUT, KS, S, H, SPLIT, FF_T128)
 #define FF_CBIG(CIN, COUT, KS, S, H, SPLIT) FF_CONVB(CIN, COUT, KS, S, H, SPLIT)
@@ -844,10 +859,10 @@ constexpr launch_fn split_launch() {
 // workgroups.
 const ConvEntry kConvTable[] = {
     {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem, 1, nullptr, nullptr},
-    FF_CONV(64, 64, 3, 1, 112, 1, FF_T64),
-    FF_CONV(64, 64, 3, 2, 112, 1, FF_T64),
-    FF_CONV(64, 64, 1, 2, 112, 1, FF_T64),
-    FF_CONV(64, 64, 3, 1, 56, 1, FF_T64),
+    FF_C64(64, 64, 3, 1, 112, 1),
+    FF_C64(64, 64, 3, 2, 112, 1),
+    FF_C64(64, 64, 1, 2, 112, 1),
+    FF_C64(64, 64, 3, 1, 56, 1),
     FF_C128(64, 128, 3, 1, 56, 1),
     FF_C128(128, 128, 3, 2, 56, 1),
     FF_C128(64, 128, 1, 2, 56, 1),

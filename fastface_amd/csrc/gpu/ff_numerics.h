@@ -18,16 +18,13 @@
 namespace ff {
 
 // x86 cvttps2dq followed by the [-128, 127] clamp (int8_epilogue.c:84-87).
+// Clamping in fp32 first gives the same integers for every finite r below
+// 2^31 (the bounds are integers, so truncation commutes with the clamp, and
+// r <= -2^31 lands on -128 either way); NaN and r >= 2^31, where cvttps2dq
+// returns INT32_MIN, fail the final compare and give -128.
 __device__ __forceinline__ int32_t cvtt_clamp_i8(float r) {
-    int32_t q;
-    if (r >= -2147483648.0f && r < 2147483648.0f) {
-        q = (int32_t)r;                       // truncation toward zero
-        q = q < -128 ? -128 : q;
-        q = q > 127 ? 127 : q;
-    } else {
-        q = -128;                             // INT32_MIN, clamped
-    }
-    return q;
+    const int32_t q = (int32_t)__builtin_amdgcn_fmed3f(r, -128.0f, 127.0f);
+    return r < 2147483648.0f ? q : -128;
 }
 
 // Round half away from zero in fp32: t + copysign(0.5, t), one rounding,

@@ -218,6 +218,33 @@ def main():
                 st["cout"], st["k"], st["s"], st["hin"]))
         log("b=1 sum of step times %.4f ms" % float(b1_steps.sum()))
 
+    # Host-buffer (PCIe-inclusive) rates of the boundary: fp32 faces and the
+    # uint8 RGB entry point (a quarter of the input bytes).  Reported beside
+    # `value`, never as it.  Pageable numpy buffers, as a caller would pass.
+    imgs = np.random.default_rng(5).integers(0, 256, size=(B, 112, 112, 3), dtype=np.uint8)
+
+    def host_rate(fn, arr, reps=3):
+        fn(ff.ff, arr.ctypes.data, B, out.ctypes.data)           # capture / warm
+        t = time.perf_counter()
+        for _ in range(reps):
+            check(lib, fn(ff.ff, arr.ctypes.data, B, out.ctypes.data), "host embed")
+        return B * reps / (time.perf_counter() - t)
+    host_fp32 = host_rate(lib.fastface_embed_batch, x)
+    host_rgb8 = host_rate(lib.fastface_embed_batch_rgb8, imgs)
+    d_img = lib.ffk_malloc(imgs.nbytes)
+    check(lib, lib.ffk_memcpy_h2d(d_img, imgs.ctypes.data, imgs.nbytes, stream), "upload rgb8")
+    check(lib, lib.fastface_embed_batch_rgb8_device(ff.ff, d_img, B, d_out, stream), "rgb8 dev")
+    check(lib, lib.ffk_stream_sync(stream), "sync")
+    check(lib, lib.ffk_event_record(ev0, stream), "record")
+    for _ in range(K):
+        check(lib, lib.fastface_embed_batch_rgb8_device(ff.ff, d_img, B, d_out, stream), "rgb8 dev")
+    check(lib, lib.ffk_event_record(ev1, stream), "record")
+    check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
+    dev_rgb8 = B * K / (ms.value / 1e3)
+    lib.ffk_free(d_img)
+    log("B=%d host buffers: fp32 %.0f faces/s, uint8 RGB %.0f faces/s; uint8 RGB resident %.0f faces/s"
+        % (B, host_fp32, host_rgb8, dev_rgb8))
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(ffw)
@@ -241,6 +268,9 @@ def main():
                                "inputs resident in HBM, one hipGraph per step" % B,
                    "global_batch": B, "input": "112x112x3 fp32 NHWC", "parallelism": "single GPU"},
         "b1_latency_ms": round(b1_ms, 4),
+        "host_fp32_faces_s": round(host_fp32, 1),
+        "host_rgb8_faces_s": round(host_rgb8, 1),
+        "rgb8_resident_faces_s": round(dev_rgb8, 1),
         "b1_device_ms": round(b1_dev_ms, 4),
         "chain_int8_tops": round(chain_tops, 2),
         "chain_frac_of_int8_peak": round(chain_tops / PEAK_INT8_TOPS, 4),

@@ -21,6 +21,7 @@ FASTFACE_OUTPUT_N = 512
 
 # fastface_kernels.h
 FFK_EPI_PRELU, FFK_EPI_ADD, FFK_EPI_BN, FFK_EPI_BIAS, FFK_EPI_INSCALE = 1, 2, 4, 8, 16
+FFK_IN_RGB8 = 0x20
 (FFK_P_WS, FFK_P_BIAS, FFK_P_SLOPE, FFK_P_ADDSCALE, FFK_P_INV, FFK_P_BN_SIN, FFK_P_BN_S,
  FFK_P_BN_O, FFK_P_BN_INV, FFK_NPARAM) = range(10)
 
@@ -38,7 +39,7 @@ class ffk_conv_desc(C.Structure):
                 ("params", _p), ("add_src", _p), ("bn_lut", _p), ("out", _p), ("out_bn", _p),
                 ("out_i32", _p),
                 ("flags", C.c_int), ("in_scale", C.c_float),
-                ("workspace", _p), ("workspace_bytes", C.c_size_t)]
+                ("workspace", _p), ("workspace_bytes", C.c_size_t), ("in_lut", _p)]
 
 
 class ffk_fc_desc(C.Structure):
@@ -64,6 +65,8 @@ EXPORTS = [
     ("fastface_destroy", None, [_p]),
     ("fastface_embed_batch", C.c_int, [_p, _p, C.c_int, _p]),
     ("fastface_embed_batch_device", C.c_int, [_p, _p, C.c_int, _p, _p]),
+    ("fastface_embed_batch_rgb8", C.c_int, [_p, _p, C.c_int, _p]),
+    ("fastface_embed_batch_rgb8_device", C.c_int, [_p, _p, C.c_int, _p, _p]),
     ("fastface_reserve", C.c_int, [_p, C.c_int]),
     ("fastface_stream", _p, [_p]),
     ("fastface_num_steps", C.c_int, [_p]),
@@ -99,6 +102,7 @@ EXPORTS = [
     ("ffk_conv_workspace_bytes", C.c_size_t, [C.POINTER(ffk_conv_desc)]),
     ("ffk_conv", C.c_int, [C.POINTER(ffk_conv_desc), _p]),
     ("ffk_make_bn_lut", C.c_int, [_p, _p, _p, _p, C.c_int, _p]),
+    ("ffk_make_rgb8_lut", C.c_int, [_p, _p]),
     ("ffk_fc_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("ffk_pack_fc_weights", C.c_int, [_p, C.c_int, C.c_int, _p]),
     ("ffk_fc", C.c_int, [C.POINTER(ffk_fc_desc), _p]),

@@ -56,6 +56,19 @@ class FastFace:
             raise RuntimeError("fastface_embed_batch failed (%d)" % rc)
         return out
 
+    def embed_batch_rgb8(self, imgs: Sequence[np.ndarray] | np.ndarray) -> np.ndarray:
+        """uint8 RGB faces, HWC [112, 112, 3] each: the embeddings of the
+        fp32 faces (x - 127.5) / 127.5 that the reference SDK builds from them."""
+        a = np.ascontiguousarray(np.asarray(imgs, dtype=np.uint8))
+        b = a.size // FASTFACE_INPUT_N
+        if a.size != b * FASTFACE_INPUT_N:
+            raise ValueError("input is not a whole number of faces")
+        out = np.empty((b, FASTFACE_OUTPUT_N), np.float32)
+        rc = self.lib.fastface_embed_batch_rgb8(self.ff, a.ctypes.data, b, out.ctypes.data)
+        if rc != 0:
+            raise RuntimeError("fastface_embed_batch_rgb8 failed (%d)" % rc)
+        return out
+
     @staticmethod
     def cos_sim(a: np.ndarray, b: np.ndarray) -> float:
         return float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))

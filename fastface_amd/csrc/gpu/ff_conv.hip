@@ -57,6 +57,7 @@ struct ConvArgs {
     float* out_f32;
     const float* fc_ws;
     const float* fc_bias;
+    const int8_t* in_lut;   // FFK_IN_RGB8: [3][256] input quantization table
     int32_t* ws;            // split-K partial tiles
     unsigned* counters;     // split-K arrival counters, one per tile (zero between launches)
     int M;
@@ -676,24 +677,42 @@ __global__ __launch_bounds__(STEM_NT, 1) void stem_kernel(ConvArgs a) {
     const int b = t / (H / 2);
     const int oh0 = (t - b * (H / 2)) * 2;
     const int m0 = b * HW + oh0 * W;
-    const float* x = a.in_f32 ? a.in_f32 : a.io->in;
-    const float* img = x + (size_t)b * HW * 3;
-    const float inv0 = a.in_inv[0], inv1 = a.in_inv[1], inv2 = a.in_inv[2];
+    const void* x = a.in_f32 ? (const void*)a.in_f32 : (const void*)a.io->in;
+    const bool rgb8 = (a.flags & FFK_IN_RGB8) != 0;
 
-    // input rows oh0-1 .. oh0+2, columns -1 .. 112, channels 0..2 (+1 zero)
-    for (int e = tid; e < PATCH; e += STEM_NT) {
-        const int pr = e / (PW * 4);
-        const int rem = e - pr * (PW * 4);
-        const int pc = rem >> 2;
-        const int ci = rem & 3;
-        const int ih = oh0 - 1 + pr;
-        const int iw = pc - 1;
-        int8_t q = 0;
-        if (ci < 3 && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W && b * HW < a.M) {
-            const float v = img[(ih * W + iw) * 3 + ci];
-            q = (int8_t)ff::quant_input(v, ci == 0 ? inv0 : (ci == 1 ? inv1 : inv2));
+    // input rows oh0-1 .. oh0+2, columns -1 .. 112, channels 0..2 (+1 zero):
+    // fp32 faces quantized in place, or uint8 pixels through the table
+    if (rgb8) {
+        const uint8_t* img = (const uint8_t*)x + (size_t)b * HW * 3;
+        for (int e = tid; e < PATCH; e += STEM_NT) {
+            const int pr = e / (PW * 4);
+            const int rem = e - pr * (PW * 4);
+            const int pc = rem >> 2;
+            const int ci = rem & 3;
+            const int ih = oh0 - 1 + pr;
+            const int iw = pc - 1;
+            int8_t q = 0;
+            if (ci < 3 && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W && b * HW < a.M)
+                q = a.in_lut[ci * 256 + img[(ih * W + iw) * 3 + ci]];
+            Ps[e] = q;
         }
-        Ps[e] = q;
+    } else {
+        const float* img = (const float*)x + (size_t)b * HW * 3;
+        const float inv0 = a.in_inv[0], inv1 = a.in_inv[1], inv2 = a.in_inv[2];
+        for (int e = tid; e < PATCH; e += STEM_NT) {
+            const int pr = e / (PW * 4);
+            const int rem = e - pr * (PW * 4);
+            const int pc = rem >> 2;
+            const int ci = rem & 3;
+            const int ih = oh0 - 1 + pr;
+            const int iw = pc - 1;
+            int8_t q = 0;
+            if (ci < 3 && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W && b * HW < a.M) {
+                const float v = img[(ih * W + iw) * 3 + ci];
+                q = (int8_t)ff::quant_input(v, ci == 0 ? inv0 : (ci == 1 ? inv1 : inv2));
+            }
+            Ps[e] = q;
+        }
     }
     if (a.flags & FFK_EPI_BN && !a.out_i32) load_bn_lut<STEM_NT>(Ls, a.bn_lut, 0, COUT);
     __syncthreads();
@@ -1008,7 +1027,13 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     }
     const bool stem = d->cin == 3;
     const bool raw = d->out_i32 != nullptr;
-    bool bad = !d->w || (!raw && !d->params) || (stem && !d->in_inv) || (stem && !d->in && !d->io) ||
+    const bool rgb8 = stem && (d->flags & FFK_IN_RGB8);
+    if ((d->flags & FFK_IN_RGB8) && !stem) {
+        ffk_set_error("conv: FFK_IN_RGB8 applies to the 3-channel input layer only%s%s", nullptr, nullptr);
+        return FFK_ERR_ARG;
+    }
+    bool bad = !d->w || (!raw && !d->params) || (stem && !rgb8 && !d->in_inv) || (rgb8 && !d->in_lut) ||
+               (stem && !d->in && !d->io) ||
                (!stem && !d->in);
     if (!raw) {
         if ((d->flags & FFK_EPI_ADD) && !d->add_src) bad = true;
@@ -1024,6 +1049,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     if (stem) a.in_f32 = (const float*)d->in;
     else a.in = (const int8_t*)d->in;
     a.in_inv = d->in_inv;
+    a.in_lut = d->in_lut;
     a.io = d->io;
     a.w = d->w;
     a.params = d->params;
@@ -1033,7 +1059,8 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     a.out_bn = d->out_bn;
     a.out_i32 = d->out_i32;
     a.M = (int)M;
-    a.flags = d->flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_BIAS | FFK_EPI_INSCALE);
+    a.flags = d->flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_BIAS | FFK_EPI_INSCALE |
+                          FFK_IN_RGB8);
     a.in_scale = d->in_scale;
     const ConvLaunch l = choose_launch(e, M, d->workspace ? d->workspace_bytes : 0);
     if (l.split > 1) {
@@ -1076,6 +1103,24 @@ int ffk_make_bn_lut(const float* s_in, const float* bn_s, const float* bn_o, con
             else v = INT32_MIN;
             v = v < -128 ? -128 : (v > 127 ? 127 : v);
             lut[(size_t)c * 256 + (q + 128)] = (int8_t)v;
+        }
+    return FFK_OK;
+}
+
+int ffk_make_rgb8_lut(const float* in_inv, int8_t* lut) {
+    if (!in_inv || !lut) {
+        ffk_set_error("make_rgb8_lut: bad arguments%s%s", nullptr, nullptr);
+        return FFK_ERR_ARG;
+    }
+    for (int c = 0; c < 3; c++)
+        for (int x = 0; x < 256; x++) {
+            volatile float v = (float)x - 127.5f;      // exact
+            v = v / 127.5f;                            // one correctly rounded division
+            volatile float t = v * in_inv[c];
+            long q = lrintf(t);                        // the reference's glibc call
+            int32_t qi = (int32_t)q;
+            qi = qi < -128 ? -128 : (qi > 127 ? 127 : qi);
+            lut[c * 256 + x] = (int8_t)qi;
         }
     return FFK_OK;
 }

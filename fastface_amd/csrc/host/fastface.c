@@ -20,7 +20,8 @@
 
 #define FF_MAX_GRAPHS 16
 
-typedef struct { int batch; void* exec; } GraphEntry;
+/* one captured chain per (batch, input format: 0 fp32 faces, 1 uint8 RGB) */
+typedef struct { int batch, fmt; void* exec; } GraphEntry;
 
 struct FastFace {
     FfModel model;
@@ -32,6 +33,8 @@ struct FastFace {
     int capacity;               /* faces the activation buffers hold */
     int8_t** d_bufs;            /* plan.n_buffers buffers */
     float* d_input;             /* capacity * 37632 */
+    uint8_t* d_input_u8;        /* capacity * 37632 (uint8 RGB input) */
+    int8_t* d_in_lut;           /* [3][256] uint8 pixel -> int8 input table */
     float* d_output;            /* capacity * 512 */
     void* d_ws;                 /* split-K workspace of the small-batch convs */
     size_t ws_bytes;
@@ -64,6 +67,7 @@ static void free_activations(FastFace* ff)
         ff->d_bufs = NULL;
     }
     ffk_free(ff->d_input); ff->d_input = NULL;
+    ffk_free(ff->d_input_u8); ff->d_input_u8 = NULL;
     ffk_free(ff->d_output); ff->d_output = NULL;
     ffk_free(ff->d_ws); ff->d_ws = NULL;
     ff->ws_bytes = 0;
@@ -86,7 +90,7 @@ static int set_io(FastFace* ff, const float* in, float* out, void* stream)
     return 0;
 }
 
-static void step_desc(FastFace* ff, int s, int batch, ffk_conv_desc* d);
+static void step_desc(FastFace* ff, int s, int batch, int fmt, ffk_conv_desc* d);
 
 /* Largest split-K workspace any conv step asks for at 1..max_batch faces.
  * Only small batches split (the split grid is capped at a few thousand
@@ -99,7 +103,7 @@ static size_t workspace_bytes(FastFace* ff, int max_batch)
         if (ff->plan.steps[s].kind != 1) continue;
         for (int b = 1; b <= top; b++) {
             ffk_conv_desc d;
-            step_desc(ff, s, b, &d);
+            step_desc(ff, s, b, 0, &d);
             const size_t n = ffk_conv_workspace_bytes(&d);
             if (n > best) best = n;
         }
@@ -123,7 +127,8 @@ static int ensure_capacity(FastFace* ff, int batch)
     }
     ff->d_input = (float*)ffk_malloc((size_t)batch * FASTFACE_INPUT_N * sizeof(float));
     ff->d_output = (float*)ffk_malloc((size_t)batch * FASTFACE_OUTPUT_N * sizeof(float));
-    if (!ff->d_input || !ff->d_output) { free_activations(ff); return FFK_ERR_NOMEM; }
+    ff->d_input_u8 = (uint8_t*)ffk_malloc((size_t)batch * FASTFACE_INPUT_N);
+    if (!ff->d_input || !ff->d_output || !ff->d_input_u8) { free_activations(ff); return FFK_ERR_NOMEM; }
     const size_t ws = workspace_bytes(ff, batch);
     if (ws) {
         ff->d_ws = ffk_malloc(ws);
@@ -145,8 +150,9 @@ static int8_t* tensor_ptr(FastFace* ff, int t)
     return b >= 0 ? ff->d_bufs[b] : NULL;
 }
 
-/* conv descriptor of step s (pointers are NULL while no activations exist) */
-static void step_desc(FastFace* ff, int s, int batch, ffk_conv_desc* d)
+/* conv descriptor of step s (pointers are NULL while no activations exist);
+ * fmt 1: the input layer reads uint8 RGB pixels through the input table */
+static void step_desc(FastFace* ff, int s, int batch, int fmt, ffk_conv_desc* d)
 {
     const FfStep* st = &ff->plan.steps[s];
     memset(d, 0, sizeof *d);
@@ -156,6 +162,7 @@ static void step_desc(FastFace* ff, int s, int batch, ffk_conv_desc* d)
         d->in = NULL;
         d->io = ff->d_io;
         d->in_inv = ff->d_in_inv;
+        if (fmt) d->in_lut = ff->d_in_lut;
     } else {
         d->in = ff->d_bufs ? tensor_ptr(ff, st->t_in) : NULL;
     }
@@ -167,18 +174,18 @@ static void step_desc(FastFace* ff, int s, int batch, ffk_conv_desc* d)
         d->out_bn = tensor_ptr(ff, st->t_bn);
     }
     if (st->flags & FFK_EPI_BN) d->bn_lut = ff->d_weights + st->lut_off;
-    d->flags = st->flags;
+    d->flags = st->flags | ((fmt && st->t_in == FF_T_INPUT) ? FFK_IN_RGB8 : 0);
     d->in_scale = st->in_scale;
     d->workspace = ff->d_ws;
     d->workspace_bytes = ff->ws_bytes;
 }
 
-static int launch_step(FastFace* ff, int s, int batch, void* stream)
+static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt)
 {
     const FfStep* st = &ff->plan.steps[s];
     if (st->kind == 1) {
         ffk_conv_desc d;
-        step_desc(ff, s, batch, &d);
+        step_desc(ff, s, batch, fmt, &d);
         return ffk_conv(&d, stream);
     }
     ffk_fc_desc f;
@@ -195,21 +202,21 @@ static int launch_step(FastFace* ff, int s, int batch, void* stream)
     return ffk_fc(&f, stream);
 }
 
-static int run_direct(FastFace* ff, int batch, void* stream)
+static int run_direct(FastFace* ff, int batch, void* stream, int fmt)
 {
     for (int s = 0; s < ff->plan.n_steps; s++) {
-        int rc = launch_step(ff, s, batch, stream);
+        int rc = launch_step(ff, s, batch, stream, fmt);
         if (rc) return rc;
     }
     return 0;
 }
 
-static void* graph_for(FastFace* ff, int batch)
+static void* graph_for(FastFace* ff, int batch, int fmt)
 {
     for (int i = 0; i < ff->n_graphs; i++)
-        if (ff->graphs[i].batch == batch) return ff->graphs[i].exec;
+        if (ff->graphs[i].batch == batch && ff->graphs[i].fmt == fmt) return ff->graphs[i].exec;
     if (ffk_graph_begin(ff->stream)) return NULL;
-    int rc = run_direct(ff, batch, ff->stream);
+    int rc = run_direct(ff, batch, ff->stream, fmt);
     void* exec = NULL;
     int rc2 = ffk_graph_end(ff->stream, &exec);
     if (rc || rc2) { if (exec) ffk_graph_destroy(exec); return NULL; }
@@ -218,15 +225,16 @@ static void* graph_for(FastFace* ff, int batch)
     else { slot = ff->graph_rr; ff->graph_rr = (ff->graph_rr + 1) % FF_MAX_GRAPHS;
            ffk_graph_destroy(ff->graphs[slot].exec); }
     ff->graphs[slot].batch = batch;
+    ff->graphs[slot].fmt = fmt;
     ff->graphs[slot].exec = exec;
     return exec;
 }
 
 /* enqueue one batch whose I/O pointers are already in d_io */
-static int enqueue(FastFace* ff, int batch, void* stream)
+static int enqueue(FastFace* ff, int batch, void* stream, int fmt)
 {
-    if (ff->keep_all) return run_direct(ff, batch, stream);
-    void* g = graph_for(ff, batch);
+    if (ff->keep_all) return run_direct(ff, batch, stream, fmt);
+    void* g = graph_for(ff, batch, fmt);
     if (!g) return FFK_ERR_HIP;
     return ffk_graph_launch(g, stream);
 }
@@ -255,15 +263,19 @@ FastFace* fastface_create(const char* ffw4_path)
     ff->d_weights = (int8_t*)ffk_malloc(ff->plan.w_bytes);
     ff->d_params = (float*)ffk_malloc(ff->plan.p_floats * sizeof(float));
     ff->d_in_inv = (float*)ffk_malloc(4 * sizeof(float));
+    ff->d_in_lut = (int8_t*)ffk_malloc(3 * 256);
     ff->d_io = (ffk_io*)ffk_malloc(sizeof(ffk_io));
     ff->h_io = (ffk_io*)ffk_host_alloc(sizeof(ffk_io));
-    if (!ff->d_weights || !ff->d_params || !ff->d_in_inv || !ff->d_io || !ff->h_io) {
+    if (!ff->d_weights || !ff->d_params || !ff->d_in_inv || !ff->d_in_lut || !ff->d_io || !ff->h_io) {
         report("device allocation", FFK_ERR_NOMEM);
         goto fail;
     }
-    if (ffk_memcpy_h2d(ff->d_weights, ff->plan.w_host, ff->plan.w_bytes, ff->stream) ||
+    int8_t in_lut[3 * 256];
+    if (ffk_make_rgb8_lut(ff->plan.in_inv, in_lut) ||
+        ffk_memcpy_h2d(ff->d_weights, ff->plan.w_host, ff->plan.w_bytes, ff->stream) ||
         ffk_memcpy_h2d(ff->d_params, ff->plan.p_host, ff->plan.p_floats * sizeof(float), ff->stream) ||
         ffk_memcpy_h2d(ff->d_in_inv, ff->plan.in_inv, 4 * sizeof(float), ff->stream) ||
+        ffk_memcpy_h2d(ff->d_in_lut, in_lut, sizeof in_lut, ff->stream) ||
         ffk_stream_sync(ff->stream)) {
         report("weight upload", FFK_ERR_HIP);
         goto fail;
@@ -290,6 +302,7 @@ void fastface_destroy(FastFace* ff)
     ffk_free(ff->d_weights);
     ffk_free(ff->d_params);
     ffk_free(ff->d_in_inv);
+    ffk_free(ff->d_in_lut);
     ffk_free(ff->d_io);
     ffk_host_free(ff->h_io);
     if (ff->stream) ffk_stream_destroy(ff->stream);
@@ -314,7 +327,7 @@ int fastface_embed_batch(FastFace* ff, const float* in, int batch, float* out)
     if (rc) { report("activation allocation", rc); return -2; }
     rc = set_io(ff, ff->d_input, ff->d_output, ff->stream);
     if (!rc) rc = ffk_memcpy_h2d(ff->d_input, in, (size_t)batch * FASTFACE_INPUT_N * sizeof(float), ff->stream);
-    if (!rc) rc = enqueue(ff, batch, ff->stream);
+    if (!rc) rc = enqueue(ff, batch, ff->stream, 0);
     if (!rc) rc = ffk_memcpy_d2h(out, ff->d_output, (size_t)batch * FASTFACE_OUTPUT_N * sizeof(float), ff->stream);
     if (!rc) rc = ffk_stream_sync(ff->stream);
     if (rc) { report("embed", rc); return -3; }
@@ -335,8 +348,37 @@ int fastface_embed_batch_device(FastFace* ff, const float* d_in, int batch, floa
     int rc = ensure_capacity(ff, batch);
     if (rc) { report("activation allocation", rc); return -2; }
     rc = set_io(ff, d_in, d_out, stream);
-    if (!rc) rc = enqueue(ff, batch, stream);
+    if (!rc) rc = enqueue(ff, batch, stream, 0);
     if (rc) { report("embed_batch_device", rc); return -3; }
+    return 0;
+}
+
+int fastface_embed_batch_rgb8(FastFace* ff, const uint8_t* in, int batch, float* out)
+{
+    if (!ff || !in || !out || batch < 0) return -1;
+    if (batch == 0) return 0;
+    int rc = ensure_capacity(ff, batch);
+    if (rc) { report("activation allocation", rc); return -2; }
+    rc = set_io(ff, (const float*)ff->d_input_u8, ff->d_output, ff->stream);
+    if (!rc) rc = ffk_memcpy_h2d(ff->d_input_u8, in, (size_t)batch * FASTFACE_INPUT_N, ff->stream);
+    if (!rc) rc = enqueue(ff, batch, ff->stream, 1);
+    if (!rc) rc = ffk_memcpy_d2h(out, ff->d_output, (size_t)batch * FASTFACE_OUTPUT_N * sizeof(float), ff->stream);
+    if (!rc) rc = ffk_stream_sync(ff->stream);
+    if (rc) { report("embed_rgb8", rc); return -3; }
+    return 0;
+}
+
+int fastface_embed_batch_rgb8_device(FastFace* ff, const uint8_t* d_in, int batch, float* d_out,
+                                     void* stream)
+{
+    if (!ff || !d_in || !d_out || batch < 0) return -1;
+    if (batch == 0) return 0;
+    if (!stream) stream = ff->stream;
+    int rc = ensure_capacity(ff, batch);
+    if (rc) { report("activation allocation", rc); return -2; }
+    rc = set_io(ff, (const float*)d_in, d_out, stream);
+    if (!rc) rc = enqueue(ff, batch, stream, 1);
+    if (rc) { report("embed_batch_rgb8_device", rc); return -3; }
     return 0;
 }
 
@@ -386,7 +428,7 @@ int fastface_profile_steps(FastFace* ff, int batch, int reps, float* step_ms)
     for (int r = 0; r < reps && !rc; r++) {
         for (int s = 0; s < n && !rc; s++) {
             rc = ffk_event_record(ev[s], ff->stream);
-            if (!rc) rc = launch_step(ff, s, batch, ff->stream);
+            if (!rc) rc = launch_step(ff, s, batch, ff->stream, 0);
         }
         if (!rc) rc = ffk_event_record(ev[n], ff->stream);
         if (!rc) rc = ffk_stream_sync(ff->stream);

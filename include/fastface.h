@@ -24,6 +24,8 @@
 #ifndef FASTFACE_H
 #define FASTFACE_H
 
+#include <stdint.h>
+
 #include <stddef.h>
 
 #ifdef __cplusplus
@@ -56,6 +58,16 @@ int fastface_embed_batch(FastFace* ff, const float* in_bhwc, int batch, float* o
  * is enqueued on `stream` (NULL: the context's stream) and not waited for. */
 int fastface_embed_batch_device(FastFace* ff, const float* d_in, int batch, float* d_out,
                                 void* stream);
+
+/* uint8 RGB input, HWC [112][112][3] per face (batch*37632 bytes): gives
+ * exactly the embedding fastface_embed gives for the face its SDKs build
+ * from the same pixels, (float)x - 127.5f then / 127.5f (fastface.py:10,
+ * README.md:152).  The input layer maps each pixel through a 256-entry table
+ * per channel (normalization + the reference's input quantization), so a
+ * quarter of the fp32 input bytes cross PCIe and HBM. */
+int fastface_embed_batch_rgb8(FastFace* ff, const uint8_t* in_bhwc, int batch, float* out_b512);
+int fastface_embed_batch_rgb8_device(FastFace* ff, const uint8_t* d_in, int batch, float* d_out,
+                                     void* stream);
 
 /* Pre-allocate device buffers for batches up to max_batch (default: grown on
  * demand; env FASTFACE_MAX_BATCH sets the initial reservation). */

@@ -52,8 +52,9 @@ int   ffk_graph_launch(void* graph_exec, void* stream);
 int   ffk_graph_destroy(void* graph_exec);
 
 /* ---- I/O descriptor ---------------------------------------------------
- * A captured launch chain reads its fp32 input faces and writes its fp32
- * embeddings through this device-resident pair of pointers, so the same
+ * A captured launch chain reads its input faces (fp32, or uint8 RGB for the
+ * FFK_IN_RGB8 chain) and writes its fp32 embeddings through this
+ * device-resident pair of pointers, so the same
  * graph serves any caller buffers: update it (ffk_memcpy_h2d, same stream)
  * before the launch. */
 typedef struct { const float* in; float* out; } ffk_io;
@@ -69,6 +70,8 @@ typedef struct { const float* in; float* out; } ffk_io;
 #define FFK_EPI_BN       0x04   /* out_bn = BN-requant of the int8 output    */
 #define FFK_EPI_BIAS     0x08   /* f = f + bias (FFW3/FFW4 always)           */
 #define FFK_EPI_INSCALE  0x10   /* f = f * in_scale before ws (FFW2/FFW3)    */
+#define FFK_IN_RGB8      0x20   /* cin == 3: `in` holds uint8 RGB pixels, each
+                                   channel quantized through in_lut          */
 
 /* rows of the per-layer parameter block, each `cout` floats (device) */
 enum {
@@ -87,7 +90,8 @@ enum {
 typedef struct {
     int batch, cin, cout, kh, kw, stride, pad, hin, win;
     const void*    in;       /* int8 NHWC [batch,hin,win,cin]; cin == 3: fp32
-                                faces [batch,112,112,3] quantized on load     */
+                                faces [batch,112,112,3] quantized on load, or
+                                uint8 RGB pixels with FFK_IN_RGB8             */
     const float*   in_inv;   /* cin == 3: 3 per-channel inverse input scales  */
     const ffk_io*  io;       /* cin == 3 and in == NULL: read io->in          */
     const int8_t*  w;        /* packed by ffk_pack_conv_weights               */
@@ -107,6 +111,7 @@ typedef struct {
      * must be ordered (one stream).  NULL / too small: whole-K tiling. */
     void*          workspace;
     size_t         workspace_bytes;
+    const int8_t*  in_lut;   /* FFK_IN_RGB8: [3][256] from ffk_make_rgb8_lut */
 } ffk_conv_desc;
 
 /* 1 if a kernel is compiled for this layer geometry, else 0. */
@@ -127,6 +132,13 @@ int    ffk_conv(const ffk_conv_desc* d, void* stream);
  * value q for channel c, from the FFK_P_BN_* rows (host function). */
 int    ffk_make_bn_lut(const float* s_in, const float* bn_s, const float* bn_o,
                        const float* bn_inv, int cout, int8_t* lut);
+
+/* uint8 RGB input as a table: lut[c*256 + x] is the reference's input
+ * quantization (quantize_fp32_nhwc_to_int8_per_channel,
+ * kernels/int8_epilogue.c:231-247) of the pixel value its SDKs feed it,
+ * (float)x - 127.5f then / 127.5f in fp32 (fastface.py:10, README.md:152),
+ * with channel c's inverse scale in_inv[c] (host function). */
+int    ffk_make_rgb8_lut(const float* in_inv, int8_t* lut);
 
 /* ---- FC head ----------------------------------------------------------
  * Replaces the XOR-0x80 shift + fastface_gemm_i8_matvec_vnni of the reference

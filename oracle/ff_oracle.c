@@ -111,6 +111,101 @@ void orc_conv_i32(const int8_t* in, int B, int H, int W, int Cin,
     free(wr);
 }
 
+/* ---- kernels/winograd_int8_ref.c:36-179 -------------------------------- */
+/* F(2,3) with G' = 2G keeps every transform in integers:
+ *   B^T = [1 0 -1 0; 0 1 1 0; 0 -1 1 0; 0 1 0 -1]
+ *   G'  = [2 0 0; 1 1 1; 1 -1 1; 0 0 2]
+ *   A^T = [1 1 1 0; 0 1 -1 -1]
+ * Written as plain small matrix products (rows x cols), not as the
+ * reference's unrolled butterflies. */
+static const int WG_BT[4][4] = {{1, 0, -1, 0}, {0, 1, 1, 0}, {0, -1, 1, 0}, {0, 1, 0, -1}};
+static const int WG_G2[4][3] = {{2, 0, 0}, {1, 1, 1}, {1, -1, 1}, {0, 0, 2}};
+static const int WG_AT[2][4] = {{1, 1, 1, 0}, {0, 1, -1, -1}};
+
+void orc_winograd_f23_weights(const int8_t* w_oihw, int Cout, int Cin, int16_t* u)
+{
+    for (int co = 0; co < Cout; co++)
+        for (int ci = 0; ci < Cin; ci++) {
+            const int8_t* g = w_oihw + ((size_t)co * Cin + ci) * 9;
+            int t[4][3];                       /* G' g */
+            for (int i = 0; i < 4; i++)
+                for (int j = 0; j < 3; j++) {
+                    int acc = 0;
+                    for (int k = 0; k < 3; k++) acc += WG_G2[i][k] * g[k * 3 + j];
+                    t[i][j] = acc;
+                }
+            for (int i = 0; i < 4; i++)        /* (G' g) G'^T */
+                for (int j = 0; j < 4; j++) {
+                    int acc = 0;
+                    for (int k = 0; k < 3; k++) acc += t[i][k] * WG_G2[j][k];
+                    u[((size_t)(i * 4 + j) * Cout + co) * Cin + ci] = (int16_t)acc;
+                }
+        }
+}
+
+void orc_conv_winograd_f23(const int8_t* in, int B, int H, int W, int Cin,
+                           const int16_t* u, int Cout, int32_t* out)
+{
+    const int TH = H / 2, TW = W / 2;
+    const long n_tiles = (long)B * TH * TW;
+    #pragma omp parallel
+    {
+        int32_t* V = (int32_t*)malloc((size_t)16 * Cin * sizeof(int32_t));
+        int64_t* M = (int64_t*)malloc((size_t)16 * Cout * sizeof(int64_t));
+        #pragma omp for schedule(static)
+        for (long t = 0; t < n_tiles; t++) {
+            const int b = (int)(t / ((long)TH * TW));
+            const int r = (int)(t % ((long)TH * TW));
+            const int oh = (r / TW) * 2, ow = (r % TW) * 2;
+            /* V = B^T d B per input channel, d = the 4x4 input window at
+             * (oh-1, ow-1) with zero padding */
+            for (int ci = 0; ci < Cin; ci++) {
+                int d[4][4], e[4][4];
+                for (int i = 0; i < 4; i++)
+                    for (int j = 0; j < 4; j++) {
+                        const int ih = oh - 1 + i, iw = ow - 1 + j;
+                        d[i][j] = (ih >= 0 && ih < H && iw >= 0 && iw < W)
+                                      ? in[(((size_t)b * H + ih) * W + iw) * Cin + ci] : 0;
+                    }
+                for (int i = 0; i < 4; i++)
+                    for (int j = 0; j < 4; j++) {
+                        int acc = 0;
+                        for (int k = 0; k < 4; k++) acc += WG_BT[i][k] * d[k][j];
+                        e[i][j] = acc;
+                    }
+                for (int i = 0; i < 4; i++)
+                    for (int j = 0; j < 4; j++) {
+                        int acc = 0;
+                        for (int k = 0; k < 4; k++) acc += e[i][k] * WG_BT[j][k];
+                        V[(i * 4 + j) * Cin + ci] = acc;
+                    }
+            }
+            /* M[cell][co] = sum_ci U[cell][co][ci] * V[cell][ci] (64-bit here;
+             * the reference's int32 sums cannot overflow: |u|<=1152, |v|<=512) */
+            for (int c = 0; c < 16; c++)
+                for (int co = 0; co < Cout; co++) {
+                    const int16_t* uc = u + ((size_t)c * Cout + co) * Cin;
+                    const int32_t* vc = V + (size_t)c * Cin;
+                    int64_t acc = 0;
+                    for (int ci = 0; ci < Cin; ci++) acc += (int64_t)uc[ci] * vc[ci];
+                    M[(size_t)c * Cout + co] = acc;
+                }
+            /* Y = A^T M A per output channel */
+            for (int co = 0; co < Cout; co++)
+                for (int i = 0; i < 2; i++)
+                    for (int j = 0; j < 2; j++) {
+                        int64_t acc = 0;
+                        for (int p = 0; p < 4; p++)
+                            for (int q = 0; q < 4; q++)
+                                acc += (int64_t)WG_AT[i][p] * WG_AT[j][q] * M[(size_t)(p * 4 + q) * Cout + co];
+                        out[(((size_t)b * H + oh + i) * W + ow + j) * Cout + co] = (int32_t)acc;
+                    }
+        }
+        free(V);
+        free(M);
+    }
+}
+
 /* ---- kernels/int8_epilogue.c:25-112 ----------------------------------- */
 void orc_fused_epilogue(const int32_t* acc, int n_pos, int Cout,
                         float in_scale, const float* ws, const float* bias,

@@ -40,6 +40,15 @@ void orc_conv_i32(const int8_t* in, int B, int H, int W, int Cin,
                   const int8_t* w_oihw, int Cout, int KH, int KW,
                   int stride, int pad, int Ho, int Wo, int32_t* out);
 
+/* Integer Winograd F(2,3) for 3x3 s1 p1 convs (kernels/winograd_int8_ref.c:
+ * 36-179).  Weight transform u = G' g G'^T with G' = 2G, int16, laid out
+ * [16][Cout][Cin] (transform cell i*4+j) as the reference stores it; the conv
+ * returns A^T[(G' g G'^T) .* (B^T d B)]A summed over Cin, which is exactly 4x
+ * the direct convolution.  H and W even.  in [B,H,W,Cin], out [B,H,W,Cout]. */
+void orc_winograd_f23_weights(const int8_t* w_oihw, int Cout, int Cin, int16_t* u);
+void orc_conv_winograd_f23(const int8_t* in, int B, int H, int W, int Cin,
+                           const int16_t* u, int Cout, int32_t* out);
+
 /* kernels/int8_epilogue.c:25-112 fused_epilogue_int8 (AVX2 body; requires
  * Cout % 8 == 0, which holds for every IResNet-50 layer). */
 void orc_fused_epilogue(const int32_t* acc, int n_pos, int Cout,

@@ -47,6 +47,10 @@ class Oracle:
         L.orc_conv_i32.argtypes = [_i8p, C.c_int, C.c_int, C.c_int, C.c_int, _i8p,
                                    C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                    C.c_int, C.c_int, _i32p]
+        _i16p = np.ctypeslib.ndpointer(np.int16, flags="C_CONTIGUOUS")
+        L.orc_winograd_f23_weights.argtypes = [_i8p, C.c_int, C.c_int, _i16p]
+        L.orc_conv_winograd_f23.argtypes = [_i8p, C.c_int, C.c_int, C.c_int, C.c_int, _i16p,
+                                            C.c_int, _i32p]
         L.orc_fused_epilogue.argtypes = [_i32p, C.c_int, C.c_int, C.c_float, _p, _p, _p,
                                          _p, _p, _p, C.c_float, _p, _p, C.c_float, _i8p]
         L.orc_bn_prelu_requant.argtypes = [_i8p, C.c_float, _p, _p, _p, _p, _p,
@@ -87,6 +91,26 @@ class Oracle:
         out = np.empty((B, Ho, Wo, Cout), np.int32)
         self.lib.orc_conv_i32(x.reshape(-1), B, H, W, Cin, w.reshape(-1), Cout, KH, KW,
                               stride, pad, Ho, Wo, out.reshape(-1))
+        return out
+
+    def winograd_weights(self, w_oihw):
+        """[Cout,Cin,3,3] int8 -> u = G' g G'^T, int16 [16, Cout, Cin]."""
+        w = np.ascontiguousarray(w_oihw, np.int8)
+        Cout, Cin = w.shape[:2]
+        u = np.empty((16, Cout, Cin), np.int16)
+        self.lib.orc_winograd_f23_weights(w.reshape(-1), Cout, Cin, u.reshape(-1))
+        return u
+
+    def conv_winograd(self, x, u):
+        """x [B,H,W,Cin] int8 (H, W even), u from winograd_weights -> int32
+        [B,H,W,Cout] = 4 x the 3x3 s1 p1 convolution."""
+        x = np.ascontiguousarray(x, np.int8)
+        B, H, W, Cin = x.shape
+        Cout = u.shape[1]
+        out = np.empty((B, H, W, Cout), np.int32)
+        self.lib.orc_conv_winograd_f23(x.reshape(-1), B, H, W, Cin,
+                                       np.ascontiguousarray(u, np.int16).reshape(-1), Cout,
+                                       out.reshape(-1))
         return out
 
     def fused_epilogue(self, acc, ws, bias=None, in_scale=1.0, bn_scale=None,
@@ -202,6 +226,10 @@ class Ref:
                                                       _i32p, _u8p]
         L.fastface_gemm_i8_matvec_vnni.argtypes = [_u8p, _i8p, _i32p, _f32p, _f32p, C.c_float,
                                                    _f32p, C.c_int, C.c_int]
+        _i16p = np.ctypeslib.ndpointer(np.int16, flags="C_CONTIGUOUS")
+        L.winograd_int8_transform_weights_ref.argtypes = [_i8p, C.c_int, C.c_int, _i16p]
+        L.fastface_conv2d_i8_winograd_f23_ref.argtypes = [_i8p, C.c_int, C.c_int, C.c_int,
+                                                          C.c_int, _i16p, _i32p]
         L.fastface_create.argtypes = [C.c_char_p]
         L.fastface_create.restype = _p
         L.fastface_embed.argtypes = [_p, _f32p, _f32p]
@@ -282,6 +310,27 @@ class Ref:
         self.lib.fastface_conv2d_i8_nhwc_batched(x.reshape(-1), B, Cin, H, W, Cout, KH, KW,
                                                  stride, pad, wpk, cs, Ho, Wo, out, scratch)
         return out[:B * Ho * Wo * Cout].reshape(B, Ho, Wo, Cout)
+
+    def winograd_weights(self, w_oihw):
+        w = np.ascontiguousarray(w_oihw, np.int8)
+        Cout, Cin = w.shape[:2]
+        u = np.empty((16, Cout, Cin), np.int16)
+        self.lib.winograd_int8_transform_weights_ref(w.reshape(-1), Cout, Cin, u.reshape(-1))
+        return u
+
+    def conv_winograd(self, x, u):
+        """One image at a time (the reference function is per image)."""
+        x = np.ascontiguousarray(x, np.int8)
+        B, H, W, Cin = x.shape
+        Cout = u.shape[1]
+        out = np.empty((B, H, W, Cout), np.int32)
+        uu = np.ascontiguousarray(u, np.int16).reshape(-1)
+        for b in range(B):
+            o = np.empty(H * W * Cout, np.int32)
+            self.lib.fastface_conv2d_i8_winograd_f23_ref(np.ascontiguousarray(x[b]).reshape(-1),
+                                                         Cin, H, W, Cout, uu, o)
+            out[b] = o.reshape(H, W, Cout)
+        return out
 
     def fc(self, a, W, ws, bias, a_scale=1.0):
         a = np.ascontiguousarray(a, np.int8).reshape(-1)

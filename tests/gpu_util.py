@@ -98,7 +98,7 @@ def split_counters_zero(lib, ws):
 
 
 def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=False,
-             want_x=True, want_bn=False, in_inv=None, in_scale=1.0, split=True):
+             want_x=True, want_bn=False, in_inv=None, in_scale=1.0, split=True, in_lut=None):
     """One ffk_conv call; returns int32 acc (raw) or (X, BN(X)) int8 arrays.
     split: give the call the split-K workspace it asks for (small batches take
     the split path); False: no workspace (whole-K tiling)."""
@@ -117,6 +117,9 @@ def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=Fa
     if in_inv is not None:
         di = Dev(lib, host=np.asarray(list(in_inv) + [0.0], np.float32)); keep.append(di)
         d.in_inv = di.ptr
+    if in_lut is not None:
+        dl = Dev(lib, host=np.ascontiguousarray(in_lut, np.int8)); keep.append(dl)
+        d.in_lut = dl.ptr
     if params is not None:
         dp = Dev(lib, host=params); keep.append(dp)
         d.params = dp.ptr

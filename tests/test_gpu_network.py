@@ -59,6 +59,37 @@ def test_batch_equals_single(ff):
         assert np.array_equal(batch[i], ff.embed(x[i]))
 
 
+def test_rgb8_input_equals_sdk_normalized_fp32(ff):
+    """uint8 RGB faces through the input table give bit-for-bit the embeddings
+    of the fp32 faces the reference SDK builds from them, in both orders of
+    capture (rgb8 and fp32 chains of one batch size coexist)."""
+    r = np.random.default_rng(31)
+    imgs = r.integers(0, 256, size=(3, 112, 112, 3), dtype=np.uint8)
+    imgs[0, :8] = 0
+    imgs[0, 8:16] = 255
+    faces = (imgs.astype(np.float32) - 127.5) / 127.5
+    got = ff.embed_batch_rgb8(imgs)
+    exp = ff.embed_batch(faces)
+    assert np.array_equal(got, exp)
+    assert np.array_equal(ff.embed_batch_rgb8(imgs[:1])[0], ff.embed(faces[0]))
+    assert np.array_equal(ff.embed_batch_rgb8(imgs), got)
+
+
+def test_rgb8_stem_kernel_vs_oracle(gpu_lib, oracle):
+    """The input layer alone: uint8 pixels -> table -> int32 accumulators,
+    against the oracle's quantization of the SDK-normalized pixels."""
+    from gpu_util import run_conv
+    r = np.random.default_rng(32)
+    imgs = r.integers(0, 256, size=(2, 112, 112, 3), dtype=np.uint8)
+    w = r.integers(-128, 128, size=(64, 3, 3, 3), dtype=np.int8)
+    inv = np.array([127.0, 126.9, 127.3], np.float32)
+    lut = np.empty((3, 256), np.int8)
+    assert gpu_lib.ffk_make_rgb8_lut(inv.ctypes.data, lut.ctypes.data) == 0
+    got = run_conv(gpu_lib, imgs, w, 1, 1, raw=True, in_lut=lut, flags=fa.FFK_IN_RGB8)
+    q = oracle.quant_input((imgs.astype(np.float32) - 127.5) / 127.5, inv)
+    assert np.array_equal(got, oracle.conv_i32(q, w, 1, 1))
+
+
 def test_graph_replays_and_batch_switching(ff):
     x = synth.faces_uniform(5, 22)
     first = ff.embed_batch(x)

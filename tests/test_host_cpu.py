@@ -142,3 +142,20 @@ def test_split_workspace_only_for_small_batches():
     assert need(64, 64, 1, 2, 112, 1) == 0            # 1x1: one K stage, nothing to split
     assert need(96, 64, 3, 1, 112, 1) == 0            # no kernel
     assert lib.ffk_conv_workspace_bytes(None) == 0
+
+
+def test_rgb8_table_matches_sdk_normalization_and_reference_quant(oracle):
+    """lut[c][x] == the reference's input quantization of the fp32 pixel the
+    SDKs feed it: numpy float32 (x - 127.5) / 127.5 (fastface.py:10)."""
+    lib = fa.load()
+    x = np.arange(256, dtype=np.uint8)
+    norm = (x.astype(np.float32) - 127.5) / 127.5            # numpy float32 semantics
+    assert norm.dtype == np.float32
+    for inv in ([127.0, 127.0, 127.0], [127.00001, 126.5, 3.0e9], [1e-3, 0.5, 254.99]):
+        inv = np.asarray(inv, np.float32)
+        lut = np.empty((3, 256), np.int8)
+        assert lib.ffk_make_rgb8_lut(inv.ctypes.data, lut.ctypes.data) == 0
+        faces = np.repeat(norm[:, None], 3, axis=1)           # [256, 3]: pixel value per channel
+        exp = oracle.quant_input(faces, inv)                  # [256, 3]
+        assert np.array_equal(lut.T, exp), inv
+    assert lib.ffk_make_rgb8_lut(None, lut.ctypes.data) != 0

@@ -161,6 +161,48 @@ def test_conv_i32_brute_force(oracle):
         assert np.array_equal(got, exp)
 
 
+WINO_SHAPES = [(64, 64, 56, 1), (64, 64, 112, 1), (16, 8, 6, 2)]
+
+
+@pytest.mark.parametrize("cin,cout,H,B", WINO_SHAPES)
+def test_winograd_f23_vs_reference(oracle, ref, cin, cout, H, B):
+    """Integer Winograd F(2,3) (kernels/winograd_int8_ref.c): weight transform
+    and tile conv bit-exact with the reference's own scalar code."""
+    r = rng(900 + cin + H)
+    x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, 3, 3), dtype=np.int8)
+    x[0, :2] = -128
+    w[0] = -128
+    w[1] = 127
+    u = oracle.winograd_weights(w)
+    assert np.array_equal(u, ref.winograd_weights(w))
+    assert np.array_equal(oracle.conv_winograd(x, u), ref.conv_winograd(x, u))
+
+
+def test_winograd_f23_is_four_times_direct(oracle):
+    """Closed form, independent of the reference: with G' = 2G the F(2,3)
+    output is exactly 4x the 3x3 s1 p1 convolution (brute force), and the
+    transformed weights stay inside int16 at the int8 extremes."""
+    r = rng(77)
+    x = r.integers(-128, 128, size=(2, 8, 10, 24), dtype=np.int8)
+    w = r.integers(-128, 128, size=(12, 24, 3, 3), dtype=np.int8)
+    x[1] = -128
+    w[3] = -128
+    w[4, :, 1, :] = 127
+    u = oracle.winograd_weights(w)
+    assert np.abs(u.astype(np.int32)).max() <= 1152      # 4*2*... bound: |2a|+|a+b+c| combos
+    B, H, W, Cin = x.shape
+    xp = np.pad(x.astype(np.int64), ((0, 0), (1, 1), (1, 1), (0, 0)))
+    direct = np.zeros((B, H, W, w.shape[0]), np.int64)
+    for kh in range(3):
+        for kw in range(3):
+            direct += np.einsum("bhwc,oc->bhwo", xp[:, kh:kh + H, kw:kw + W, :],
+                                w[:, :, kh, kw].astype(np.int64))
+    assert np.array_equal(oracle.conv_winograd(x, u).astype(np.int64), 4 * direct)
+    # one transform cell by hand: u[0] = G'[0] g G'[0]^T = 4 * g[0][0]
+    assert np.array_equal(u[0], 4 * w[:, :, 0, 0].astype(np.int16))
+
+
 def test_fc_vs_reference_and_closed_form(oracle, ref):
     r = rng(17)
     K, N = 25088, 64

@@ -9,8 +9,12 @@
 // MFMA needs no correction, and integer sums do not depend on their order,
 // so the accumulators are bit-identical.
 //
-// K loop: workgroup = 4 wave64s computing a BM x BN tile (each wave MI x NJ
-// MFMA 32x32 tiles).  Per K stage of KB = 64 or 128 bytes each thread fetches
+// Two kernels share the epilogue: conv_dma_kernel (large grids: operands go
+// straight from global into a swizzled LDS ring with global_load_lds_dwordx4)
+// and conv_i8_kernel (small grids and split-K: register-staged operands).
+//
+// conv_i8_kernel K loop: workgroup = 4 wave64s computing a BM x BN tile (each
+// wave MI x NJ MFMA 32x32 tiles).  Per K stage of KB = 64 or 128 bytes each thread fetches
 // 16-byte pieces of the implicit im2col rows (one input pixel's channel run;
 // padding taps read a zero page, so there are no branches) and of the packed
 // weights.  PF stages of loads are in flight in registers; each stage goes

@@ -41,26 +41,73 @@ def check(lib, rc, what):
         raise RuntimeError("%s failed (%d): %s" % (what, rc, fastface_amd.last_error()))
 
 
+def host_cpu():
+    """CPU model, physical cores and SMT state of this host (from /proc/cpuinfo)."""
+    model, cores, logical = "?", set(), 0
+    try:
+        phys = None
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "processor":
+                logical += 1
+            elif k == "model name":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                cores.add((phys, v))
+    except OSError:
+        pass
+    n = len(cores) or logical
+    return {"model": model, "physical_cores": n, "logical_cpus": logical, "smt": logical > n}
+
+
+def _ref_best(exe, args, threads, env):
+    """Run one of the reference's binaries in its built-in bench mode; returns
+    (faces/s, ms/face) of its best trial or None."""
+    env = dict(env, OMP_NUM_THREADS=str(threads))
+    r = subprocess.run([exe] + args + ["--threads", str(threads)], cwd=ROOT, env=env,
+                       capture_output=True, text=True, timeout=600)
+    m = re.search(r"Best:\s*([\d.]+) ms/batch = ([\d.]+) ms/face\s*\(([\d.]+) face/s\)", r.stdout)
+    if r.returncode == 0 and m:
+        return float(m.group(3)), float(m.group(2))
+    m = re.search(r"Best:\s*([\d.]+) ms/inference\s*\(([\d.]+) face/s\)", r.stdout)
+    if r.returncode == 0 and m:
+        return float(m.group(2)), float(m.group(1))
+    log("reference binary %s failed (rc %d): %s" % (exe, r.returncode, r.stderr[-300:]))
+    return None
+
+
 def cpu_baseline(ffw):
-    """The reference's own batched CPU binary (oracle/_ref, built from its
-    sources) on this host: --batch 8, its built-in bench (5 trials x 30
-    passes, best).  Falls back to the C restatement when the host lacks
-    AVX-VNNI (the reference build would SIGILL)."""
+    """The reference's own CPU binaries (oracle/_ref, built from its sources)
+    on this host, their built-in bench (5 trials x 30 passes, best):
+    fastface_int8_batched --batch 8 on all (up to 16) cores -- `value` -- and
+    on its default 8 threads, and fastface_int8 at b=1.  About 15 s of CPU
+    work.  Falls back to the C restatement when the host lacks AVX-VNNI (the
+    reference build would SIGILL)."""
     from oracle.oracle import host_has_avx_vnni
-    cores = min(16, os.cpu_count() or 1)
+    cpu = host_cpu()
+    cores = min(16, cpu["physical_cores"] or os.cpu_count() or 1)
     exe = os.path.join(ROOT, "oracle", "_ref", "fastface_int8_batched")
-    env = dict(os.environ, OMP_NUM_THREADS=str(cores), OMP_PROC_BIND="close", OMP_PLACES="cores")
+    exe1 = os.path.join(ROOT, "oracle", "_ref", "fastface_int8")
+    env = dict(os.environ, OMP_PROC_BIND="close", OMP_PLACES="cores")
     if os.path.exists(exe) and host_has_avx_vnni():
         log("cpu baseline: reference fastface_int8_batched --batch 8, %d threads" % cores)
-        r = subprocess.run([exe, ffw, "--batch", "8", "--threads", str(cores)], cwd=ROOT, env=env,
-                           capture_output=True, text=True, timeout=600)
-        m = re.search(r"Best:\s*([\d.]+) ms/batch = ([\d.]+) ms/face\s*\(([\d.]+) face/s\)", r.stdout)
-        if r.returncode == 0 and m:
-            return {"value": float(m.group(3)), "unit": "faces/s", "cores": cores,
-                    "kind": "reference",
-                    "sample": "reference fastface_int8_batched, B=8 synthetic faces, best of 5x30 "
-                              "passes (%s ms/face); synthetic FFW4 + committed OPSC2" % m.group(2)}
-        log("reference binary failed (rc %d): %s" % (r.returncode, r.stderr[-300:]))
+        best = _ref_best(exe, [ffw, "--batch", "8"], cores, env)
+        if best:
+            rec = {"value": best[0], "unit": "faces/s", "cores": cores, "kind": "reference",
+                   "sample": "reference fastface_int8_batched, B=8 synthetic faces, best of 5x30 "
+                             "passes (%.2f ms/face); synthetic FFW4 + committed OPSC2" % best[1],
+                   "host": cpu}
+            b8 = _ref_best(exe, [ffw, "--batch", "8"], 8, env)
+            if b8:
+                rec["value_8_threads"] = b8[0]
+            if os.path.exists(exe1):
+                b1 = _ref_best(exe1, [ffw], 8, env)
+                if b1:
+                    rec["b1_ms_8_threads"] = b1[1]
+            return rec
     from fastface_amd import synth
     from oracle.oracle import Oracle
     log("cpu baseline: C restatement (oracle), B=4")
@@ -78,8 +125,8 @@ def cpu_baseline(ffw):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--batch", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-reps", type=int, default=3)
@@ -116,22 +163,31 @@ def main():
     for _ in range(max(W, 1)):
         step()
     check(lib, lib.ffk_stream_sync(stream), "sync")
-    ev0, ev1 = C.c_void_p(), C.c_void_p()
-    check(lib, lib.ffk_event_create(C.byref(ev0)), "event")
-    check(lib, lib.ffk_event_create(C.byref(ev1)), "event")
+    # one HIP event between consecutive graph launches: the whole timed region
+    # and each step's duration (median / p10 / p90)
+    evs = [C.c_void_p() for _ in range(K + 1)]
+    for e in evs:
+        check(lib, lib.ffk_event_create(C.byref(e)), "event")
+    ev0, ev1 = evs[0], evs[K]
     log("timing %d steps" % K)
     t0 = time.perf_counter()
-    check(lib, lib.ffk_event_record(ev0, stream), "record")
-    for _ in range(K):
+    for i in range(K):
+        check(lib, lib.ffk_event_record(evs[i], stream), "record")
         step()
-    check(lib, lib.ffk_event_record(ev1, stream), "record")
+    check(lib, lib.ffk_event_record(evs[K], stream), "record")
     check(lib, lib.ffk_stream_sync(stream), "sync")
     wall = time.perf_counter() - t0
     ms = C.c_float()
     check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
     ms_per_step = ms.value / K
     faces_per_s = B * K / (ms.value / 1e3)
-    log("%.3f ms/step, %.0f faces/s (wall %.3f s)" % (ms_per_step, faces_per_s, wall))
+    per_step = []
+    for i in range(K):
+        check(lib, lib.ffk_event_elapsed_ms(evs[i], evs[i + 1], C.byref(ms)), "elapsed")
+        per_step.append(ms.value)
+    p10, p50, p90 = (float(np.percentile(per_step, q)) for q in (10, 50, 90))
+    log("%.3f ms/step (median %.3f, p10 %.3f, p90 %.3f), %.0f faces/s (wall %.3f s)"
+        % (ms_per_step, p50, p10, p90, faces_per_s, wall))
     out = np.empty((B, 512), np.float32)
     check(lib, lib.ffk_memcpy_d2h(out.ctypes.data, d_out, out.nbytes, stream), "download")
     check(lib, lib.ffk_stream_sync(stream), "sync")
@@ -177,10 +233,14 @@ def main():
         if st["kind"] != 1:
             continue
         key = "stage%d" % {112: 1, 56: 1, 28: 2, 14: 3, 7: 4}[st["hout"]] if st["cin"] != 3 else "stem"
-        d = stages.setdefault(key, [0.0, 0.0])
+        d = stages.setdefault(key, [0.0, 0.0, 0.0])
         d[0] += st["ops"] * B
         d[1] += st["ms"]
+        d[2] += st["act"] * B + st["wbytes"]
     stage_util = {k: round(v[0] / (v[1] * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4) for k, v in stages.items()}
+    # algorithmic HBM rate of each stage (activation bytes in + out + residual +
+    # BN output, plus weights): the epilogue-bound stem / stage 1 against 8 TB/s
+    stage_gbs = {k: round(v[2] / (v[1] * 1e-3) / 1e9, 1) for k, v in stages.items()}
     log("dominant conv 256x256x3x3@14: %.4f ms/launch, %.1f TOP/s (%.1f%% of peak)"
         % (dom_ms, dom_tops, 100 * dom_tops / PEAK_INT8_TOPS))
 
@@ -259,6 +319,9 @@ def main():
         "steps": K,
         "warmup": W,
         "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step_median": round(p50, 4),
+        "ms_per_step_p10": round(p10, 4),
+        "ms_per_step_p90": round(p90, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -275,6 +338,7 @@ def main():
         "chain_int8_tops": round(chain_tops, 2),
         "chain_frac_of_int8_peak": round(chain_tops / PEAK_INT8_TOPS, 4),
         "stage_frac_of_int8_peak": stage_util,
+        "stage_hbm_gbs": stage_gbs,
         "fc_ms": round(fc["ms"], 4),
         "fc_hbm_gbs": round((fc["wbytes"] + fc["act"] * B) / (fc["ms"] * 1e-3) / 1e9, 1),
         "roofline": {"bound": "mfma", "kernel": DOMINANT_KERNEL,

@@ -80,9 +80,34 @@ struct ConvArgs {
 template <int MI, int NJ>
 constexpr int wave_tile_bytes() { return MI * 32 * (NJ * 32 + 16); }
 
+// Per-channel parameters of the NJ channels a lane owns (columns ncol0 +
+// j*32 + lane%32).  Loaded separately so that a kernel walking several tiles
+// of the same channels loads them once.
+template <int NJ>
+struct EpiParams {
+    float ws[NJ], bias[NJ], slope[NJ], adds[NJ], inv[NJ];
+};
+
+template <int COUT, int NJ>
+__device__ __forceinline__ EpiParams<NJ> load_epi_params(const ConvArgs& a, int ncol0) {
+    EpiParams<NJ> P;
+    const int lc = threadIdx.x & 31;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int c = ncol0 + j * 32 + lc;
+        P.ws[j] = a.params[FFK_P_WS * COUT + c];
+        P.bias[j] = a.params[FFK_P_BIAS * COUT + c];
+        P.inv[j] = a.params[FFK_P_INV * COUT + c];
+        P.slope[j] = a.params[FFK_P_SLOPE * COUT + c];
+        P.adds[j] = a.params[FFK_P_ADDSCALE * COUT + c];
+    }
+    return P;
+}
+
 template <int COUT, int MI, int NJ, bool PRELU, bool ADD, bool BN2>
-__device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a, int mrow0,
-                                            int ncol0, int8_t* Ws, const int8_t* Lw) {
+__device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a,
+                                            const EpiParams<NJ>& prm, int mrow0, int ncol0, int8_t* Ws,
+                                            const int8_t* Lw) {
     constexpr int P = NJ * 32 + 16;
     constexpr int ROWS = MI * 32;
     constexpr int CH = NJ * 2;          // 16-byte chunks per tile row
@@ -91,16 +116,11 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
     const int lc = lane & 31;
     const int lh = lane >> 5;
     const bool inscale = (a.flags & FFK_EPI_INSCALE) != 0;
-    float ws[NJ], bias[NJ], p2[NJ], adds[NJ], inv[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int c = ncol0 + j * 32 + lc;
-        ws[j] = a.params[FFK_P_WS * COUT + c];
-        bias[j] = a.params[FFK_P_BIAS * COUT + c];
-        inv[j] = a.params[FFK_P_INV * COUT + c];
-        p2[j] = PRELU ? a.params[FFK_P_SLOPE * COUT + c] : 0.0f;
-        adds[j] = ADD ? a.params[FFK_P_ADDSCALE * COUT + c] : 0.0f;
-    }
+    const float* ws = prm.ws;
+    const float* bias = prm.bias;
+    const float* p2 = prm.slope;
+    const float* adds = prm.adds;
+    const float* inv = prm.inv;
     if (ADD) {      // residual tile -> LDS (coalesced 16-byte loads)
 #pragma unroll
         for (int k = 0; k < ROWS / RPI; k++) {
@@ -201,6 +221,30 @@ __device__ __forceinline__ void wave_epi_wide(const v16i (&acc)[MI][NJ], const C
     }
 }
 
+// int8 epilogue variants dispatched on the (uniform) flags, parameters given
+template <int COUT, int MI, int NJ>
+__device__ __forceinline__ void wave_epilogue_p(const v16i (&acc)[MI][NJ], const ConvArgs& a,
+                                                const EpiParams<NJ>& P, int mrow0, int ncol0, int8_t* Ws,
+                                                const int8_t* Lw) {
+    if (a.out_i32) {
+        wave_epi_wide<COUT, MI, NJ, false>(acc, a, mrow0, ncol0);
+        return;
+    }
+    switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN)) {
+    case 0: wave_epi_i8<COUT, MI, NJ, false, false, false>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_PRELU: wave_epi_i8<COUT, MI, NJ, true, false, false>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_ADD: wave_epi_i8<COUT, MI, NJ, false, true, false>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_BN: wave_epi_i8<COUT, MI, NJ, false, false, true>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_PRELU | FFK_EPI_BN:
+        wave_epi_i8<COUT, MI, NJ, true, false, true>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_ADD | FFK_EPI_BN:
+        wave_epi_i8<COUT, MI, NJ, false, true, true>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_PRELU | FFK_EPI_ADD:
+        wave_epi_i8<COUT, MI, NJ, true, true, false>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    default: wave_epi_i8<COUT, MI, NJ, true, true, true>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    }
+}
+
 template <int COUT, int MI, int NJ, bool FC = false>
 __device__ __forceinline__ void wave_epilogue(const v16i (&acc)[MI][NJ], const ConvArgs& a, int mrow0,
                                               int ncol0, int8_t* Ws, const int8_t* Lw) {
@@ -212,19 +256,7 @@ __device__ __forceinline__ void wave_epilogue(const v16i (&acc)[MI][NJ], const C
         wave_epi_wide<COUT, MI, NJ, false>(acc, a, mrow0, ncol0);
         return;
     }
-    switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN)) {
-    case 0: wave_epi_i8<COUT, MI, NJ, false, false, false>(acc, a, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_PRELU: wave_epi_i8<COUT, MI, NJ, true, false, false>(acc, a, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_ADD: wave_epi_i8<COUT, MI, NJ, false, true, false>(acc, a, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_BN: wave_epi_i8<COUT, MI, NJ, false, false, true>(acc, a, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_PRELU | FFK_EPI_BN:
-        wave_epi_i8<COUT, MI, NJ, true, false, true>(acc, a, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_ADD | FFK_EPI_BN:
-        wave_epi_i8<COUT, MI, NJ, false, true, true>(acc, a, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_PRELU | FFK_EPI_ADD:
-        wave_epi_i8<COUT, MI, NJ, true, true, false>(acc, a, mrow0, ncol0, Ws, Lw); break;
-    default: wave_epi_i8<COUT, MI, NJ, true, true, true>(acc, a, mrow0, ncol0, Ws, Lw); break;
-    }
+    wave_epilogue_p<COUT, MI, NJ>(acc, a, load_epi_params<COUT, NJ>(a, ncol0), mrow0, ncol0, Ws, Lw);
 }
 
 // BN tables of channels [c0, c0 + nch) -> LDS (pitch FF_LUT_PITCH)
@@ -666,7 +698,18 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
 constexpr int STEM_WAVES = 7;
 constexpr int STEM_NT = STEM_WAVES * 64;
 
-__global__ __launch_bounds__(STEM_NT, 1) void stem_kernel(ConvArgs a) {
+// Persistent: a workgroup loads the BN table and its weight fragments once and
+// walks a contiguous run of tiles (neighbouring row pairs share input rows in
+// cache); STEM_WG_PER_CU workgroups share a CU.
+#ifndef FF_STEM_WG_PER_CU
+#define FF_STEM_WG_PER_CU 2
+#endif
+constexpr int STEM_WG_PER_CU = FF_STEM_WG_PER_CU;
+
+// (7 waves per workgroup over 4 SIMDs: STEM_WG_PER_CU * 7 / 4 waves per SIMD)
+template <bool RGB8>
+__global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) void stem_kernel(ConvArgs a,
+                                                                                        int tiles_per_wg) {
     constexpr int COUT = 64, H = 112, W = 112, HW = H * W;
     constexpr int PW = W + 2;                       // patch row: 114 pixels x 4 bytes
     constexpr int PATCH = 4 * PW * 4;
@@ -677,77 +720,116 @@ __global__ __launch_bounds__(STEM_NT, 1) void stem_kernel(ConvArgs a) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int t = xcd_tile(blockIdx.x, gridDim.x);   // one tile = 2 output rows
-    const int b = t / (H / 2);
-    const int oh0 = (t - b * (H / 2)) * 2;
-    const int m0 = b * HW + oh0 * W;
+    const int ntiles = a.M / (2 * W);               // one tile = 2 output rows of one face
+    const int t_beg = blockIdx.x * tiles_per_wg;
+    const int t_end = t_beg + tiles_per_wg < ntiles ? t_beg + tiles_per_wg : ntiles;
     const void* x = a.in_f32 ? (const void*)a.in_f32 : (const void*)a.io->in;
-    const bool rgb8 = (a.flags & FFK_IN_RGB8) != 0;
+    constexpr bool rgb8 = RGB8;
+    const float inv0 = rgb8 ? 0.0f : a.in_inv[0];
+    const float inv1 = rgb8 ? 0.0f : a.in_inv[1];
+    const float inv2 = rgb8 ? 0.0f : a.in_inv[2];
 
-    // input rows oh0-1 .. oh0+2, columns -1 .. 112, channels 0..2 (+1 zero):
-    // fp32 faces quantized in place, or uint8 pixels through the table
-    if (rgb8) {
-        const uint8_t* img = (const uint8_t*)x + (size_t)b * HW * 3;
-        for (int e = tid; e < PATCH; e += STEM_NT) {
-            const int pr = e / (PW * 4);
-            const int rem = e - pr * (PW * 4);
-            const int pc = rem >> 2;
-            const int ci = rem & 3;
-            const int ih = oh0 - 1 + pr;
-            const int iw = pc - 1;
-            int8_t q = 0;
-            if (ci < 3 && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W && b * HW < a.M)
-                q = a.in_lut[ci * 256 + img[(ih * W + iw) * 3 + ci]];
-            Ps[e] = q;
-        }
-    } else {
-        const float* img = (const float*)x + (size_t)b * HW * 3;
-        const float inv0 = a.in_inv[0], inv1 = a.in_inv[1], inv2 = a.in_inv[2];
-        for (int e = tid; e < PATCH; e += STEM_NT) {
-            const int pr = e / (PW * 4);
-            const int rem = e - pr * (PW * 4);
-            const int pc = rem >> 2;
-            const int ci = rem & 3;
-            const int ih = oh0 - 1 + pr;
-            const int iw = pc - 1;
-            int8_t q = 0;
-            if (ci < 3 && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W && b * HW < a.M) {
-                const float v = img[(ih * W + iw) * 3 + ci];
-                q = (int8_t)ff::quant_input(v, ci == 0 ? inv0 : (ci == 1 ? inv1 : inv2));
-            }
-            Ps[e] = q;
-        }
-    }
+    // tile-invariant: the BN table (made visible by the loop's first barrier),
+    // the weight fragments, and where this lane's A operand sits in the patch
     if (a.flags & FFK_EPI_BN && !a.out_i32) load_bn_lut<STEM_NT>(Ls, a.bn_lut, 0, COUT);
-    __syncthreads();
-
-    // A operand: lane -> pixel (row of the MFMA tile) and K half g
-    const int p = wave * 32 + (lane & 31);           // 0..223
+    const int p = wave * 32 + (lane & 31);           // 0..223: pixel of the tile
     const int orow = p / W;
     const int ow = p - orow * W;
-    const int g = lane >> 5;
-    uint32_t aw[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int e = 0; e < 16; e++) {
-        const int k = g * 16 + e;
-        if (k < 27) {
-            const int tap = k / 3;
-            const int ci = k - tap * 3;
-            const int kh = tap / 3;
-            const int kw = tap - kh * 3;
-            const uint32_t q = (uint8_t)Ps[((orow + kh) * PW + ow + kw) * 4 + ci];
-            aw[e >> 2] |= q << ((e & 3) * 8);
-        }
-    }
-    const v4i av = {(int)aw[0], (int)aw[1], (int)aw[2], (int)aw[3]};
+    const int g = lane >> 5;                         // K half
     const v4i b0 = *reinterpret_cast<const v4i*>(a.w + (lane & 31) * FF_KSTEP + g * 16);
     const v4i b1 = *reinterpret_cast<const v4i*>(a.w + (32 + (lane & 31)) * FF_KSTEP + g * 16);
-    v16i acc[1][2];
+    // (raw int32 output: no parameter block is passed, a.params may be null)
+    EpiParams<2> prm = {};
+    if (!a.out_i32) prm = load_epi_params<COUT, 2>(a, 0);
+
+    // The patch of tile t+1 is fetched into registers (PE elements per thread)
+    // while tile t runs its MFMAs and epilogue: the loads' latency, not their
+    // bytes, bounds this layer.
+    constexpr int PE = (PATCH + STEM_NT - 1) / STEM_NT;
+    float pv[RGB8 ? 1 : PE];                         // fp32 faces: the raw values
+    int pq[RGB8 ? PE : 1];                           // uint8 pixels: the byte, or -1 for padding
+    auto fetch = [&](int t) {
+        const int b = t / (H / 2);
+        const int oh0 = (t - b * (H / 2)) * 2;
 #pragma unroll
-    for (int r = 0; r < 16; r++) { acc[0][0][r] = 0; acc[0][1][r] = 0; }
-    acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, acc[0][0], 0, 0, 0);
-    acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, acc[0][1], 0, 0, 0);
-    wave_epilogue<COUT, 1, 2>(acc, a, m0 + wave * 32, 0, Es + wave * (32 * 80), Ls);
+        for (int j = 0; j < PE; j++) {
+            const int e = tid + j * STEM_NT;
+            const int pr = e / (PW * 4);
+            const int rem = e - pr * (PW * 4);
+            const int pc = rem >> 2;
+            const int ci = rem & 3;
+            const int ih = oh0 - 1 + pr;
+            const int iw = pc - 1;
+            const bool in = e < PATCH && ci < 3 && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+            const size_t off = (size_t)b * HW * 3 + (ih * W + iw) * 3 + ci;
+            if constexpr (RGB8) pq[j] = in ? (int)((const uint8_t*)x)[off] : -1;
+            else pv[j] = in ? ((const float*)x)[off] : __builtin_nanf("");
+        }
+    };
+    if (t_beg < t_end) fetch(t_beg);
+
+    for (int t = t_beg; t < t_end; t++) {
+        const int b = t / (H / 2);
+        const int oh0 = (t - b * (H / 2)) * 2;
+        const int m0 = b * HW + oh0 * W;
+        __syncthreads();                             // the previous tile is done with Ps / Es
+
+        // input rows oh0-1 .. oh0+2, columns -1 .. 112, channels 0..2 (+1 zero):
+        // fp32 faces quantized in place, or uint8 pixels through the table;
+        // padding and the fourth channel are zero
+#pragma unroll
+        for (int j = 0; j < PE; j++) {
+            const int e = tid + j * STEM_NT;
+            if (e < PATCH) {
+                const int ci = e & 3;
+                int8_t q = 0;
+                if constexpr (RGB8) {
+                    if (pq[j] >= 0) q = a.in_lut[ci * 256 + pq[j]];
+                } else {
+                    const int pr = e / (PW * 4);
+                    const int pc = (e - pr * (PW * 4)) >> 2;
+                    const int ih = oh0 - 1 + pr, iw = pc - 1;
+                    if (ci < 3 && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
+                        q = (int8_t)ff::quant_input(pv[j], ci == 0 ? inv0 : (ci == 1 ? inv1 : inv2));
+                }
+                Ps[e] = q;
+            }
+        }
+        if (t + 1 < t_end) fetch(t + 1);
+        __syncthreads();
+
+        // A operand: lane -> pixel (row of the MFMA tile) and K half g;
+        // K = 27 (3x3 taps x 3 channels) zero-padded to one 32-deep MFMA
+        uint32_t aw[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int k = g * 16 + e;
+            if (k < 27) {
+                const int tap = k / 3;
+                const int ci = k - tap * 3;
+                const int kh = tap / 3;
+                const int kw = tap - kh * 3;
+                const uint32_t q = (uint8_t)Ps[((orow + kh) * PW + ow + kw) * 4 + ci];
+                aw[e >> 2] |= q << ((e & 3) * 8);
+            }
+        }
+        const v4i av = {(int)aw[0], (int)aw[1], (int)aw[2], (int)aw[3]};
+        v16i acc[1][2];
+#pragma unroll
+        for (int r = 0; r < 16; r++) { acc[0][0][r] = 0; acc[0][1][r] = 0; }
+        acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, acc[0][1], 0, 0, 0);
+        // the input layer has no residual input (ffk_conv rejects FFK_EPI_ADD here)
+        int8_t* Ws = Es + wave * (32 * 80);
+        const int mw = m0 + wave * 32;
+        if (a.out_i32) wave_epi_wide<COUT, 1, 2, false>(acc, a, mw, 0);
+        else switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_BN)) {
+        case 0: wave_epi_i8<COUT, 1, 2, false, false, false>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case FFK_EPI_PRELU: wave_epi_i8<COUT, 1, 2, true, false, false>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case FFK_EPI_BN: wave_epi_i8<COUT, 1, 2, false, false, true>(acc, a, prm, mw, 0, Ws, Ls); break;
+        default: wave_epi_i8<COUT, 1, 2, true, false, true>(acc, a, prm, mw, 0, Ws, Ls); break;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -775,7 +857,13 @@ void launch_conv_dma(const ConvArgs& a, int grid, hipStream_t s) {
 void launch_stem(const ConvArgs& a, int grid, hipStream_t s) {
     (void)grid;
     const int tiles = a.M / (112 * 2);
-    hipLaunchKernelGGL(stem_kernel, dim3(tiles), dim3(STEM_NT), 0, s, a);
+    const int slots = 256 * STEM_WG_PER_CU;
+    const int per_wg = (tiles + slots - 1) / slots;
+    const dim3 grid_dim((tiles + per_wg - 1) / per_wg);
+    if (a.flags & FFK_IN_RGB8)
+        hipLaunchKernelGGL(stem_kernel<true>, grid_dim, dim3(STEM_NT), 0, s, a, per_wg);
+    else
+        hipLaunchKernelGGL(stem_kernel<false>, grid_dim, dim3(STEM_NT), 0, s, a, per_wg);
 }
 
 // Small-batch split-K tiling: 64x64 workgroup tiles (one 32x32 MFMA tile per
@@ -1032,6 +1120,10 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     const bool stem = d->cin == 3;
     const bool raw = d->out_i32 != nullptr;
     const bool rgb8 = stem && (d->flags & FFK_IN_RGB8);
+    if (stem && (d->flags & FFK_EPI_ADD)) {
+        ffk_set_error("conv: the 3-channel input layer takes no residual input%s%s", nullptr, nullptr);
+        return FFK_ERR_UNSUPPORTED;
+    }
     if ((d->flags & FFK_IN_RGB8) && !stem) {
         ffk_set_error("conv: FFK_IN_RGB8 applies to the 3-channel input layer only%s%s", nullptr, nullptr);
         return FFK_ERR_ARG;

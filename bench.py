@@ -28,7 +28,7 @@ METRIC = "faces/sec at B=1024 INT8 IResNet-50 (1 GPU); b=1 latency ms; % int8 MF
 PEAK_INT8_TOPS = 5000.0          # MI355X dense int8, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0
 # the instantiation that runs the 26 dominant convs at B=1024 (rocprofv3 name)
-DOMINANT_KERNEL = "conv_dma_kernel<256, 256, 3, 1, 14, 14, 4, 2, 2, 2, 3, 4>"
+DOMINANT_KERNEL = "conv3_patch_kernel<256, 256, 14, 14, 4, 2, 2, 2, 4>"
 
 
 def log(msg):

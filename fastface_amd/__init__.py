@@ -101,6 +101,7 @@ EXPORTS = [
     ("ffk_pack_conv_weights", C.c_int, [_p, C.c_int, C.c_int, C.c_int, C.c_int, _p]),
     ("ffk_conv_workspace_bytes", C.c_size_t, [C.POINTER(ffk_conv_desc)]),
     ("ffk_conv", C.c_int, [C.POINTER(ffk_conv_desc), _p]),
+    ("ffk_conv_variant", C.c_char_p, [C.POINTER(ffk_conv_desc)]),
     ("ffk_make_bn_lut", C.c_int, [_p, _p, _p, _p, C.c_int, _p]),
     ("ffk_make_rgb8_lut", C.c_int, [_p, _p]),
     ("ffk_fc_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),

@@ -30,6 +30,8 @@
 // coalesced 16-byte stores.  The BN second output is a per-channel 256-entry
 // table lookup (BN is a fixed function of the int8 value; the table is built
 // bit-exactly on the host, ffk_make_bn_lut).
+#include <algorithm>
+
 #include "ff_internal.h"
 #include "ff_numerics.h"
 
@@ -522,19 +524,21 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
 // run).  Global loads go straight into an NST-deep LDS ring -- no register
 // staging and no LDS store instructions, so the registers go to occupancy
 // (WPE waves per SIMD) instead.  One wave load instruction writes 1 KB of LDS,
-// lane L at byte 16*L.  A stage tile is a run of 128-byte lines of two 64-byte
-// rows; the 16-byte slot of (row r, piece p) in line r/2 is
-// ((r%2)*4 + p) XOR (r/2 % 8), which keeps the ds_read_b128 operand reads
-// conflict-free.  The swizzle is realised by choosing which global piece each
-// lane fetches: a line's 8 lanes still read one 128-byte window.
+// lane L at byte 16*L.  A stage tile is a run of 256-byte lines of four
+// 64-byte rows; the 16-byte slot of (row r, piece p) in line r/4 is
+// ((r%4)*4 + p) XOR (r/4 % 4).  gfx950's LDS serves a ds_read_b128 in groups
+// of 16 lanes over 64 banks (256 bytes), and the 16 rows such a group reads
+// then land in 16 distinct slots: the operand reads are conflict-free.  The
+// swizzle is realised by choosing which global piece each lane fetches: a
+// line's 16 lanes still read four whole 64-byte rows.
 // Per stage: wait for this thread's loads of the stage (vmcnt), barrier (every
 // thread's loads landed; every wave is done with the stage the next loads
 // overwrite), issue the loads of stage s+NST-1, then the MFMAs of stage s.
 constexpr int DMA_KB = 64;
 
 __device__ __forceinline__ int dma_slot(int r, int p) {
-    const int line = r >> 1;
-    return line * 128 + ((((r & 1) << 2) | p) ^ (line & 7)) * 16;
+    const int line = r >> 2;
+    return line * 256 + ((((r & 3) << 2) | p) ^ (line & 3)) * 16;
 }
 
 // Wait until at most N of this wave's global loads are in flight (and its LDS
@@ -583,17 +587,17 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
     const int tm = xbid / a.tiles_n;
     const int m0 = tm * BM;
 
-    // This thread's pieces: wave load j of wave w fills lines (j*NW + w)*8 ..
-    // +7 of the stage tile; lane L takes line +L/8, slot L%8.  Registers are
+    // This thread's pieces: wave load j of wave w fills lines (j*NW + w)*4 ..
+    // +3 of the stage tile; lane L takes line +L/16, slot L%16.  Registers are
     // kept few (occupancy): a 32-bit image offset per piece, the piece's input
     // origin (a row past the tile's end gets an origin that fails every bounds
     // check), and its 16-byte slot in a 64-byte channel run.
     int a_off[A_LD], a_ih0[A_LD], a_iw0[A_LD], a_p[A_LD];
 #pragma unroll
     for (int j = 0; j < A_LD; j++) {
-        const int line = (j * NW + wave) * 8 + (lane >> 3);
-        const int s = (lane & 7) ^ (line & 7);
-        const int r = line * 2 + (s >> 2);
+        const int line = (j * NW + wave) * 4 + (lane >> 4);
+        const int s = (lane & 15) ^ (line & 3);
+        const int r = line * 4 + (s >> 2);
         const int p = s & 3;
         const int m = m0 + r;
         const bool ok = m < a.M;
@@ -610,9 +614,9 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
     int b_off[B_LD];
 #pragma unroll
     for (int j = 0; j < B_LD; j++) {
-        const int line = (j * NW + wave) * 8 + (lane >> 3);
-        const int s = (lane & 7) ^ (line & 7);
-        const int n = line * 2 + (s >> 2);
+        const int line = (j * NW + wave) * 4 + (lane >> 4);
+        const int s = (lane & 15) ^ (line & 3);
+        const int n = line * 4 + (s >> 2);
         b_off[j] = (tn * BN + n) * FF_KSTEP + (s & 3) * 16;
     }
     auto issue = [&](int st, int buf) {
@@ -638,7 +642,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
     const int wm = wave / WN;
     const int wn = wave % WN;
     // Fragment (i, ks) of this lane sits at a_rd + i*2048, XOR ks*32: 32 rows
-    // are 16 lines (the swizzle key line%8 repeats), and the second 32-byte
+    // are 8 lines (the swizzle key line%4 repeats), and the second 32-byte
     // k half flips bit 1 of the slot.
     const int a_rd = dma_slot(wm * MI * 32 + (lane & 31), lane >> 5);
     const int b_rd = A_BYTES + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
@@ -676,6 +680,200 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
         rbuf = rbuf == NST - 1 ? 0 : rbuf + 1;
     }
     __syncthreads();                       // every wave is done with the ring
+
+    int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
+    int8_t* Ls = smem + NW * wave_tile_bytes<MI, NJ>();
+    if (a.flags & FFK_EPI_BN && !a.out_i32) {
+        load_bn_lut<NT>(Ls, a.bn_lut, tn * BN, BN);
+        __syncthreads();
+    }
+    wave_epilogue<COUT, MI, NJ>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
+                                Ls + (wn * NJ * 32) * FF_LUT_PITCH);
+}
+
+// ---------------------------------------------------------------------------
+// 3x3 stride-1 conv with the input staged once per 64-channel run.
+// ---------------------------------------------------------------------------
+// A workgroup computes BM consecutive output pixels m0 .. m0+BM-1 (NHWC
+// flattening over the whole batch) for BN channels.  With stride 1 the output
+// and input pixel grids coincide, and tap (kh, kw) of output pixel m reads
+// input pixel m + (kh-1)*W + (kw-1): for all nine taps these lie in one
+// contiguous run, pixels m0-W-1 .. m0+BM+W, the tile's patch.  Each 64-channel
+// run of the patch is loaded into LDS once (direct-to-LDS loads, double
+// buffered: the next run loads during the nine taps of this one), instead of
+// the 9 x BM rows a per-tap im2col tile would take, and tap (kh, kw) reads it
+// at the fixed offset of kh*W + kw pixels.  A tap that falls into the zero
+// padding (first / last row of an image, first / last pixel of a row) would
+// read a neighbouring pixel of the run instead, so that lane's fragment address
+// goes to a zero block.  Patch pixels are PATCH_PITCH = 80 bytes apart (64 data
+// + 16 unused): the 16 consecutive pixels one 16-lane group of a ds_read_b128
+// fetches then fall in 16 distinct bank slots (5 is odd), and every tap and
+// K half is a constant offset.  The weights of each tap (BN x 64 bytes) go
+// through a 3-stage ring with the conv_dma_kernel layout.
+//
+// Per step (one tap of one 64-channel run): wait for this step's weights (the
+// in-order load counter also covers the patch, issued earlier), barrier,
+// issue the weights of the step two ahead (and at tap 0 the next run's patch),
+// then the MFMAs of the step.
+constexpr int PATCH_PITCH = 80;
+
+template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int WPE>
+__global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs a) {
+    constexpr int NW = WM * WN;
+    constexpr int NT = NW * 64;
+    constexpr int BM = WM * MI * 32, BN = WN * NJ * 32;
+    constexpr int CSTEPS = CIN / DMA_KB;                     // 64-channel runs
+    constexpr int NP = BM + 2 * W + 2;                       // patch pixels
+    constexpr int PSLOTS = NP * (PATCH_PITCH / 16);          // 16-byte slots of a patch
+    constexpr int PLOADS = (PSLOTS + 63) / 64;               // 1 KB wave loads of a patch
+    constexpr int LA = (PLOADS + NW - 1) / NW;               // patch loads per thread
+    constexpr int PATCH_BYTES = PLOADS * 1024;
+    constexpr int B_BYTES = BN * DMA_KB;
+    constexpr int B_LD = B_BYTES / (NT * 16);                // weight loads per thread and step
+    constexpr int NSTB = 3;                                  // weight ring depth (9 % 3 == 0)
+    constexpr int ZERO_OFF = 2 * PATCH_BYTES;                // 1 KB of zeros
+    constexpr int RING_OFF = ZERO_OFF + 1024;
+    constexpr int LDS_K = RING_OFF + NSTB * B_BYTES;
+    constexpr int LDS_E = NW * wave_tile_bytes<MI, NJ>() + BN * FF_LUT_PITCH;
+    constexpr int LDS = LDS_K > LDS_E ? LDS_K : LDS_E;
+    static_assert(CIN % DMA_KB == 0, "Cin must be a multiple of 64");
+    static_assert(B_BYTES % (NT * 16) == 0, "whole wave loads");
+    static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
+    static_assert(B_LD + LA < 64, "load counter range");
+    static_assert((2 * W + 2) * PATCH_PITCH + 32 + 16 < 65536, "tap offsets fit the ds_read offset field");
+
+    __shared__ __align__(1024) int8_t smem[LDS];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int xbid = xcd_tile(blockIdx.x, gridDim.x);
+    const int tn = xbid % a.tiles_n;
+    const int tm = xbid / a.tiles_n;
+    const int m0 = tm * BM;
+    const int first = m0 - W - 1;                            // input pixel of patch pixel 0
+
+    // Zero block: masked taps read it.  Wave loads beyond the patch's PLOADS
+    // (every thread issues LA, so that all waves count the same loads) fetch
+    // the zero page into it as well.
+    for (int i = tid; i < 64; i += NT) reinterpret_cast<v4i*>(smem + ZERO_OFF)[i] = v4i{0, 0, 0, 0};
+
+    // Patch slots of this thread: wave load j of wave w is patch block j*NW + w,
+    // lane L its slot L, i.e. patch pixel slot/5, piece slot%5 (piece 4 is the
+    // unused 16 bytes).  Input offset of the slot at channel run 0, or -1 for
+    // the zero page (unused piece, or a pixel outside the batch).
+    int p_src[LA];
+#pragma unroll
+    for (int j = 0; j < LA; j++) {
+        const int blk = j * NW + wave;
+        const int slot = blk * 64 + lane;
+        const int px = slot / 5;
+        const int piece = slot - px * 5;
+        const int g = first + px;
+        const bool ok = blk < PLOADS && piece < 4 && g >= 0 && g < a.M;
+        p_src[j] = ok ? g * CIN + piece * 16 : -1;
+    }
+    auto issue_patch = [&](int c, int buf) {
+#pragma unroll
+        for (int j = 0; j < LA; j++) {
+            const int blk = j * NW + wave;
+            const int8_t* src = p_src[j] >= 0 ? a.in + (p_src[j] + c * DMA_KB) : ff_zero_page;
+            dma16(src, smem + (blk < PLOADS ? buf * PATCH_BYTES + blk * 1024 : ZERO_OFF));
+        }
+    };
+    int b_off[B_LD];
+#pragma unroll
+    for (int j = 0; j < B_LD; j++) {
+        const int line = (j * NW + wave) * 4 + (lane >> 4);
+        const int sl = (lane & 15) ^ (line & 3);
+        const int n = line * 4 + (sl >> 2);
+        b_off[j] = (tn * BN + n) * FF_KSTEP + (sl & 3) * 16;
+    }
+    // step s = c*9 + t: tap t of channel run c, packed weight stage t*CSTEPS + c
+    auto issue_b = [&](int c, int t, int slot) {
+        const int8_t* wst = a.w + (size_t)(t * CSTEPS + c) * COUT * FF_KSTEP;
+#pragma unroll
+        for (int j = 0; j < B_LD; j++)
+            dma16(wst + b_off[j], smem + RING_OFF + slot * B_BYTES + (j * NW + wave) * 1024);
+    };
+
+    const int wm = wave / WN;
+    const int wn = wave % WN;
+    // A fragment of row tile i: patch pixel (row + kh*W + kw) at PATCH_PITCH
+    // bytes each, K piece lane/32 (+2 for the second 32-byte K half).  Edge
+    // bits: 1 first row of its image, 2 last row, 4 first pixel of its row,
+    // 8 last pixel.
+    int a_base[MI], a_edge[MI];
+#pragma unroll
+    for (int i = 0; i < MI; i++) {
+        const int r = wm * MI * 32 + i * 32 + (lane & 31);
+        const int m = m0 + r;
+        const int rr = m % (H * W);
+        const int oh = rr / W;
+        const int ow = rr - oh * W;
+        a_edge[i] = (oh == 0 ? 1 : 0) | (oh == H - 1 ? 2 : 0) | (ow == 0 ? 4 : 0) | (ow == W - 1 ? 8 : 0);
+        a_base[i] = r * PATCH_PITCH + (lane >> 5) * 16;
+    }
+    const int z_addr = ZERO_OFF + (lane >> 5) * 16;
+    const int b_rd = RING_OFF + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
+
+    v16i acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+    issue_patch(0, 0);
+    issue_b(0, 0, 0);
+    issue_b(0, 1, 1);
+    for (int c = 0; c < CSTEPS; c++) {
+        const bool more = c + 1 < CSTEPS;
+        const int pb = (c & 1) * PATCH_BYTES;
+        // (opaque per run: the nine taps' addresses are recomputed from these
+        // instead of being kept live across the loop in 18 more registers)
+#pragma unroll
+        for (int i = 0; i < MI; i++) asm volatile("" : "+v"(a_base[i]), "+v"(a_edge[i]));
+#pragma unroll
+        for (int t = 0; t < 9; t++) {
+            // loads issued after this step's weights: the next step's weights
+            // and, at taps 1-2, the next run's patch (issued at tap 0)
+            if (t == 1 || t == 2) {
+                if (more) dma_wait_barrier<B_LD + LA>();
+                else dma_wait_barrier<B_LD>();
+            } else if (t == 8) {
+                if (more) dma_wait_barrier<B_LD>();
+                else dma_wait_barrier<0>();
+            } else {
+                dma_wait_barrier<B_LD>();
+            }
+            if (t + 2 < 9) issue_b(c, t + 2, (t + 2) % NSTB);
+            else if (more) issue_b(c + 1, t + 2 - 9, (t + 2) % NSTB);
+            if (t == 0 && more) issue_patch(c + 1, (c + 1) & 1);
+
+            const int kh = t / 3, kw = t % 3;
+            const int emask = (kh == 0 ? 1 : 0) | (kh == 2 ? 2 : 0) | (kw == 0 ? 4 : 0) | (kw == 2 ? 8 : 0);
+            const int toff = pb + (kh * W + kw) * PATCH_PITCH;
+            int aa[MI];
+#pragma unroll
+            for (int i = 0; i < MI; i++) aa[i] = (a_edge[i] & emask) ? z_addr : a_base[i] + toff;
+            const int br = b_rd + (t % NSTB) * B_BYTES;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                v4i af[MI], bf[NJ];
+#pragma unroll
+                for (int i = 0; i < MI; i++) af[i] = *reinterpret_cast<const v4i*>(smem + aa[i] + ks * 32);
+#pragma unroll
+                for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((br + j * 2048) ^ (ks * 32)));
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();                       // every wave is done with the patch and the ring
 
     int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
     int8_t* Ls = smem + NW * wave_tile_bytes<MI, NJ>();
@@ -854,6 +1052,12 @@ void launch_conv_dma(const ConvArgs& a, int grid, hipStream_t s) {
                        dim3(grid), dim3(WM * WN * 64), 0, s, a);
 }
 
+template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int WPE>
+void launch_patch(const ConvArgs& a, int grid, hipStream_t s) {
+    hipLaunchKernelGGL((conv3_patch_kernel<CIN, COUT, H, H, WM, WN, MI, NJ, WPE>), dim3(grid),
+                       dim3(WM * WN * 64), 0, s, a);
+}
+
 void launch_stem(const ConvArgs& a, int grid, hipStream_t s) {
     (void)grid;
     const int tiles = a.M / (112 * 2);
@@ -885,6 +1089,7 @@ struct ConvEntry {
     launch_fn small;    // 64x64-tile split-K variant, or none
     launch_fn mid;      // 128x128-tile register-staged variant for grids too small
                         // for the big direct-to-LDS tiles, or none
+    const char* kind;   // name of `fn` (ffk_conv_variant)
 };
 
 // A grid of fewer big tiles than this leaves CUs idle; the 128x128 variant
@@ -921,7 +1126,7 @@ constexpr launch_fn split_launch() {
 #define FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, KB, PF, BM, BN, MI, NJ, OCC)       \
     {CIN, COUT, KS, S, H, H, BM, BN,                                             \
      &launch_conv<CIN, COUT, KS, S, H, H, BM, BN, KB, PF, MI, NJ, OCC, 1>, SPLIT, \
-     split_launch<CIN, COUT, KS, S, H, SPLIT>(), nullptr}
+     split_launch<CIN, COUT, KS, S, H, SPLIT>(), nullptr, "staged"}
 #define FF_CONV(CIN, COUT, KS, S, H, SPLIT, TILE) \
     FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, FF_KB(CIN), FF_PFS(CIN), TILE)
 #define FF_CONV_K(CIN, COUT, KS, S, H, SPLIT, KB, PF, TILE) \
@@ -938,13 +1143,13 @@ constexpr launch_fn split_launch() {
     {CIN, COUT, KS, S, H, H, WM * MI * 32, WN * NJ * 32,                             \
      &launch_conv_dma<CIN, COUT, KS, S, H, H, WM, WN, MI, NJ, NST, WPE>, SPLIT,      \
      split_launch<CIN, COUT, KS, S, H, SPLIT>(),                                     \
-     &launch_conv<CIN, COUT, KS, S, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>}
+     &launch_conv<CIN, COUT, KS, S, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>, "direct"}
 #define FF_CONVD_K(CIN, COUT, KS, S, H, SPLIT, TILE) FF_DENTRY(CIN, COUT, KS, S, H, SPLIT, TILE)
 #define FF_CONVD(CIN, COUT, KS, S, H, SPLIT) FF_CONVD_K(CIN, COUT, KS, S, H, SPLIT, FF_TDMA)
 #define FF_DENTRY_NOMID(CIN, COUT, KS, S, H, SPLIT, WM, WN, MI, NJ, NST, WPE)        \
     {CIN, COUT, KS, S, H, H, WM * MI * 32, WN * NJ * 32,                             \
      &launch_conv_dma<CIN, COUT, KS, S, H, H, WM, WN, MI, NJ, NST, WPE>, SPLIT,      \
-     split_launch<CIN, COUT, KS, S, H, SPLIT>(), nullptr}
+     split_launch<CIN, COUT, KS, S, H, SPLIT>(), nullptr, "direct"}
 #define FF_CONVD64_K(CIN, COUT, KS, S, H, SPLIT, TILE) FF_DENTRY_NOMID(CIN, COUT, KS, S, H, SPLIT, TILE)
 // Cout = 64: 4 waves of 2x2 MFMA tiles -> 256x64, a 2-stage ring, 4 waves per
 // SIMD (four workgroups per CU)
@@ -964,28 +1169,53 @@ constexpr launch_fn split_launch() {
 #define FF_CBIG(CIN, COUT, KS, S, H, SPLIT) FF_CONVD(CIN, COUT, KS, S, H, SPLIT)
 #endif
 
+// 3x3 stride-1 layers: the patch kernel (WM, WN, MI, NJ, WPE).  8 waves of
+// 2x2 MFMA tiles -> 256x128, two workgroups per CU; Cout = 64: 4 waves ->
+// 256x64, two workgroups per CU (the patch double buffer sets the LDS size).
+#ifndef FF_TPATCH
+#define FF_TPATCH 4, 2, 2, 2, 4
+#endif
+#ifndef FF_TPATCH64
+#define FF_TPATCH64 4, 1, 2, 2, 2
+#endif
+#define FF_PENTRY(CIN, COUT, H, SPLIT, MID, WM, WN, MI, NJ, WPE)                      \
+    {CIN, COUT, 3, 1, H, H, WM * MI * 32, WN * NJ * 32,                              \
+     &launch_patch<CIN, COUT, H, WM, WN, MI, NJ, WPE>, SPLIT,                         \
+     split_launch<CIN, COUT, 3, 1, H, SPLIT>(), MID, "patch"}
+#define FF_PENTRY_K(CIN, COUT, H, SPLIT, MID, TILE) FF_PENTRY(CIN, COUT, H, SPLIT, MID, TILE)
+#ifdef FF_NO_PATCH
+#define FF_P(CIN, COUT, H, SPLIT) FF_CBIG(CIN, COUT, 3, 1, H, SPLIT)
+#define FF_P64(CIN, COUT, H, SPLIT) FF_C64(CIN, COUT, 3, 1, H, SPLIT)
+#else
+#define FF_P(CIN, COUT, H, SPLIT)                                                   \
+    FF_PENTRY_K(CIN, COUT, H, SPLIT,                                                \
+                (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>), \
+                FF_TPATCH)
+#define FF_P64(CIN, COUT, H, SPLIT) FF_PENTRY_K(CIN, COUT, H, SPLIT, nullptr, FF_TPATCH64)
+#endif
+
 // split: how many workgroups share the K stages of one small-batch tile (1:
 // never split).  Only the long K chains of stages 3-4 (18 or 36 stages of
 // 128 bytes) gain from it; the split is sized so that one face gives 72-144
 // workgroups.
 const ConvEntry kConvTable[] = {
-    {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem, 1, nullptr, nullptr},
+    {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem, 1, nullptr, nullptr, "stem"},
     FF_C64(64, 64, 3, 1, 112, 1),
     FF_C64(64, 64, 3, 2, 112, 1),
     FF_C64(64, 64, 1, 2, 112, 1),
-    FF_C64(64, 64, 3, 1, 56, 1),
+    FF_P64(64, 64, 56, 1),
     FF_C128(64, 128, 3, 1, 56, 1),
     FF_C128(128, 128, 3, 2, 56, 1),
     FF_C128(64, 128, 1, 2, 56, 1),
-    FF_C128(128, 128, 3, 1, 28, 1),
-    FF_CBIG(128, 256, 3, 1, 28, 1),
+    FF_P(128, 128, 28, 1),
+    FF_P(128, 256, 28, 1),
     FF_CBIG(256, 256, 3, 2, 28, 6),
     FF_CBIG(128, 256, 1, 2, 28, 1),
-    FF_CBIG(256, 256, 3, 1, 14, 9),
-    FF_CBIG(256, 512, 3, 1, 14, 3),
+    FF_P(256, 256, 14, 9),
+    FF_P(256, 512, 14, 3),
     FF_CBIG(512, 512, 3, 2, 14, 9),
     FF_CBIG(256, 512, 1, 2, 14, 1),
-    FF_CBIG(512, 512, 3, 1, 7, 9),
+    FF_P(512, 512, 7, 9),
 };
 
 const ConvEntry* find_conv(int cin, int cout, int kh, int kw, int stride, int pad, int hin, int win) {
@@ -1000,6 +1230,7 @@ const ConvEntry* find_conv(int cin, int cout, int kh, int kw, int stride, int pa
 // Launch choice for one layer at M output pixels.
 struct ConvLaunch {
     launch_fn fn;
+    const char* kind;
     int bn;             // workgroup tile width (tiles_n = cout / bn)
     int grid;
     int split;
@@ -1010,10 +1241,10 @@ struct ConvLaunch {
 // needs more falls back to the whole-K tiling).
 ConvLaunch choose_launch(const ConvEntry* e, long long M, size_t ws_avail) {
     long long big = ((M + e->bm - 1) / e->bm) * (e->cout / e->bn);
-    ConvLaunch l = {e->fn, e->bn, (int)big, 1, 0, 0};
+    ConvLaunch l = {e->fn, e->kind, e->bn, (int)big, 1, 0, 0};
     if (e->mid && big < FF_MID_MAX_WG) {
         big = ((M + 127) / 128) * (e->cout / 128);
-        l = {e->mid, 128, (int)big, 1, 0, 0};
+        l = {e->mid, "staged128", 128, (int)big, 1, 0, 0};
     }
     if (!e->small || big >= FF_SPLIT_MIN_WG) return l;
     const long long tiles = ((M + FF_SM_BM - 1) / FF_SM_BM) * (e->cout / FF_SM_BN);
@@ -1030,6 +1261,7 @@ ConvLaunch choose_launch(const ConvEntry* e, long long M, size_t ws_avail) {
         l.ws_bytes = need;
     }
     l.fn = e->small;
+    l.kind = "splitk";
     l.bn = FF_SM_BN;
     l.grid = (int)wgs;
     l.split = e->split;
@@ -1154,18 +1386,37 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     a.out = d->out;
     a.out_bn = d->out_bn;
     a.out_i32 = d->out_i32;
-    a.M = (int)M;
     a.flags = d->flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_BIAS | FFK_EPI_INSCALE |
                           FFK_IN_RGB8);
     a.in_scale = d->in_scale;
-    const ConvLaunch l = choose_launch(e, M, d->workspace ? d->workspace_bytes : 0);
-    if (l.split > 1) {
-        a.counters = (unsigned*)d->workspace;
-        a.ws = (int32_t*)((int8_t*)d->workspace + l.counter_bytes);
+    // The direct-to-LDS kernels address the int8 input with 32-bit offsets:
+    // a batch whose input tensor reaches 2 GiB runs as several launches over
+    // consecutive image ranges (images are independent).
+    const long long px_out = M / d->batch;
+    const long long in_img = (long long)d->hin * d->win * d->cin;
+    const int slice = stem ? d->batch : (int)std::min<long long>(d->batch, 0x7fffffffLL / in_img);
+    for (int b0 = 0; b0 < d->batch; b0 += slice) {
+        const int nb = std::min(slice, d->batch - b0);
+        const long long ms = (long long)nb * px_out;
+        ConvArgs as = a;
+        if (!stem) as.in = a.in + (size_t)b0 * in_img;
+        const size_t o = (size_t)b0 * px_out * d->cout;
+        if (a.add_src) as.add_src = a.add_src + o;
+        if (a.out) as.out = a.out + o;
+        if (a.out_bn) as.out_bn = a.out_bn + o;
+        if (a.out_i32) as.out_i32 = a.out_i32 + o;
+        as.M = (int)ms;
+        const ConvLaunch l = choose_launch(e, ms, d->workspace ? d->workspace_bytes : 0);
+        if (l.split > 1) {
+            as.counters = (unsigned*)d->workspace;
+            as.ws = (int32_t*)((int8_t*)d->workspace + l.counter_bytes);
+        }
+        as.tiles_n = d->cout / l.bn;
+        l.fn(as, l.grid, (hipStream_t)stream);
+        const int rc = ffk_check_launch("conv launch");
+        if (rc != FFK_OK) return rc;
     }
-    a.tiles_n = d->cout / l.bn;
-    l.fn(a, l.grid, (hipStream_t)stream);
-    return ffk_check_launch("conv launch");
+    return FFK_OK;
 }
 
 size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d) {
@@ -1175,6 +1426,15 @@ size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d) {
     const long long M = conv_pixels(d);
     if (M > 0x7fffffffLL) return 0;
     return choose_launch(e, M, (size_t)-1).ws_bytes;
+}
+
+const char* ffk_conv_variant(const ffk_conv_desc* d) {
+    if (!d || d->batch <= 0) return nullptr;
+    const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);
+    if (!e) return nullptr;
+    const long long M = conv_pixels(d);
+    if (M > 0x7fffffffLL) return nullptr;
+    return choose_launch(e, M, d->workspace ? d->workspace_bytes : 0).kind;
 }
 
 // BN second output as a table: lut[c][q + 128] = BN-requant of the int8

@@ -126,6 +126,13 @@ int    ffk_pack_conv_weights(const int8_t* w_oihw, int cout, int cin, int kh, in
  * workspace_bytes fields are not read. */
 size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d);
 int    ffk_conv(const ffk_conv_desc* d, void* stream);
+/* Name of the kernel variant ffk_conv would run for this descriptor (its
+ * geometry, batch and workspace): "stem", "patch" (3x3 stride-1 layers:
+ * input patch staged once per channel run), "direct" (direct-to-LDS tiles),
+ * "staged" / "staged128" (register-staged tiles), "splitk" (split-K);
+ * NULL when no kernel applies.  No counterpart in the reference: it lets
+ * tests and benchmarks name the code path they exercise. */
+const char* ffk_conv_variant(const ffk_conv_desc* d);
 
 /* The BN second output as a table: lut[c*256 + q + 128] is the reference's
  * BN requant (kernels/int8_epilogue.c:273-303 with bn != NULL) of the int8

@@ -112,14 +112,64 @@ EPI_SHAPES = [(64, 64, 3, 1, 56), (64, 64, 1, 2, 112), (128, 256, 1, 2, 28),
               (256, 256, 3, 1, 14), (512, 512, 3, 1, 7)]
 
 
-@pytest.mark.parametrize("split", [True, False], ids=["splitk", "wholek"])
+def _variant(lib, cin, cout, k, s, H, B):
+    import ctypes as C
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, k, k
+    d.stride, d.pad, d.hin, d.win = s, k // 2, H, H
+    v = lib.ffk_conv_variant(C.byref(d))
+    return v.decode() if v else None
+
+
+BIG_GRID_VARIANTS = ("direct", "patch")
+
+
+def _direct_batch(lib, cin, cout, k, s, H):
+    """Smallest odd batch of the list at which the layer runs its large-grid
+    kernel (direct-to-LDS tiles, or the 3x3 patch kernel) with a ragged last
+    tile."""
+    for B in (1, 3, 5, 45, 91, 171, 341, 401, 701):
+        if _variant(lib, cin, cout, k, s, H, B) in BIG_GRID_VARIANTS:
+            return B
+    raise AssertionError("no batch takes the large-grid kernel")
+
+
+def test_patch_kernel_takes_the_3x3_stride1_layers(gpu_lib):
+    for cin, cout, k, s, H in SHAPES:
+        if k == 3 and s == 1 and H in (7, 14, 28) or (cin, cout, H) == (64, 64, 56):
+            assert _variant(gpu_lib, cin, cout, k, s, H, 1024) == "patch", (cin, cout, H)
+
+
+@pytest.mark.parametrize("cin,cout,k,s,H", SHAPES)
+def test_conv_direct_tiles_large_batch(gpu_lib, oracle, cin, cout, k, s, H):
+    """The large-grid kernels (direct-to-LDS tiles; the 3x3 stride-1 patch
+    kernel) on sampled images of a batch big enough to take them: first,
+    middle and last image (ragged last tile)."""
+    r = rng(200 + cin + cout + k * 7 + s * 3 + H)
+    B = _direct_batch(gpu_lib, cin, cout, k, s, H)
+    x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
+    x[B - 1, -1, :, :] = -128
+    w[-1] = -128
+    got = run_conv(gpu_lib, x, w, s, k // 2, raw=True, split=False)
+    idx = [0, B // 2, B - 1]
+    assert np.array_equal(got[idx], oracle.conv_i32(x[idx], w, s, k // 2))
+
+
+@pytest.mark.parametrize("split", [True, False, "direct"], ids=["splitk", "wholek", "direct"])
 @pytest.mark.parametrize("mode", EPI_MODES)
 @pytest.mark.parametrize("cin,cout,k,s,H", EPI_SHAPES)
 def test_conv_fused_epilogue(gpu_lib, oracle, mode, cin, cout, k, s, H, split):
-    if split and (cin, cout, k, s, H) not in SPLIT_SHAPES:
+    if split is True and (cin, cout, k, s, H) not in SPLIT_SHAPES:
         pytest.skip("no split-K variant for this geometry")
     r = rng(300 + cin + cout + H + EPI_MODES.index(mode))
-    B = 1 if split else 2
+    if split == "direct":
+        B = _direct_batch(gpu_lib, cin, cout, k, s, H)
+        idx = [0, B // 2, B - 1]
+        split = False
+    else:
+        B = 1 if split else 2
+        idx = list(range(B))
     if split:
         _assert_split_taken(gpu_lib, cin, cout, k, s, H, B)
     x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
@@ -146,17 +196,19 @@ def test_conv_fused_epilogue(gpu_lib, oracle, mode, cin, cout, k, s, H, split):
         binv = (1.0 / r.uniform(0.01, 0.1, cout)).astype(F32)
         rows.update(bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
         flags |= fa.FFK_EPI_BN
-    acc = oracle.conv_i32(x, w, s, k // 2)
+    acc = oracle.conv_i32(x[idx], w, s, k // 2)
+    if add is not None:
+        ekw["add_src"] = add[idx]
     exp_x = oracle.fused_epilogue(acc, **ekw)
     got_x, got_bn = run_conv(gpu_lib, x, w, s, k // 2, params=params_block(cout, **rows),
                              flags=flags, add=add, want_x=(mode != "bn_only"), want_bn=want_bn,
                              split=split)
     if mode != "bn_only":
-        assert np.array_equal(got_x, exp_x)
+        assert np.array_equal(got_x[idx], exp_x)
     if want_bn:
         exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno,
                                          inv_pc=binv)
-        assert np.array_equal(got_bn, exp_bn)
+        assert np.array_equal(got_bn[idx], exp_bn)
 
 
 def test_inscale_path(gpu_lib, oracle):

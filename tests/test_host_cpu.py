@@ -144,6 +144,29 @@ def test_split_workspace_only_for_small_batches():
     assert lib.ffk_conv_workspace_bytes(None) == 0
 
 
+def test_conv_variant_policy():
+    """Which kernel variant a layer runs at a batch (host-side launch policy)."""
+    lib = fa.load()
+    d = fa.ffk_conv_desc()
+
+    def variant(cin, cout, k, s, H, B, ws=0):
+        d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, k, k
+        d.stride, d.pad, d.hin, d.win = s, k // 2, H, H
+        d.workspace, d.workspace_bytes = (4096, ws) if ws else (None, 0)
+        v = lib.ffk_conv_variant(C.byref(d))
+        return v.decode() if v else None
+    assert variant(3, 64, 3, 1, 112, 1) == "stem"
+    assert variant(256, 256, 3, 1, 14, 1024) == "patch"          # 3x3 stride 1
+    assert variant(256, 256, 3, 2, 28, 1024) == "direct"
+    assert variant(256, 256, 3, 1, 14, 64) == "staged128"
+    assert variant(256, 256, 3, 1, 14, 1) == "staged128"          # no workspace given
+    assert variant(256, 256, 3, 1, 14, 1, ws=1 << 30) == "splitk"
+    assert variant(64, 64, 3, 1, 56, 1) == "patch"                # Cout 64: one variant
+    assert variant(64, 64, 3, 1, 112, 1) == "direct"
+    assert variant(96, 64, 3, 1, 112, 1) is None
+    assert lib.ffk_conv_variant(None) is None
+
+
 def test_rgb8_table_matches_sdk_normalization_and_reference_quant(oracle):
     """lut[c][x] == the reference's input quantization of the fp32 pixel the
     SDKs feed it: numpy float32 (x - 127.5) / 127.5 (fastface.py:10)."""

@@ -31,6 +31,7 @@
 // table lookup (BN is a fixed function of the int8 value; the table is built
 // bit-exactly on the host, ffk_make_bn_lut).
 #include <algorithm>
+#include <cmath>
 
 #include "ff_internal.h"
 #include "ff_numerics.h"
@@ -106,7 +107,10 @@ __device__ __forceinline__ EpiParams<NJ> load_epi_params(const ConvArgs& a, int 
     return P;
 }
 
-template <int COUT, int MI, int NJ, bool PRELU, bool ADD, bool BN2>
+// PRELU: 0 none, 1 f < 0 ? f*slope : f, 2 max(f, f*slope) (the same values
+// when every slope is at most 1 and f is never infinite: FFK_EPI_PRELU_LE1).
+// INSC: f = f * in_scale first (FFW2/FFW3 models; FFW4 skips the multiply).
+template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC>
 __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                             const EpiParams<NJ>& prm, int mrow0, int ncol0, int8_t* Ws,
                                             const int8_t* Lw) {
@@ -117,7 +121,6 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
     const int lane = threadIdx.x & 63;
     const int lc = lane & 31;
     const int lh = lane >> 5;
-    const bool inscale = (a.flags & FFK_EPI_INSCALE) != 0;
     const float* ws = prm.ws;
     const float* bias = prm.bias;
     const float* p2 = prm.slope;
@@ -143,11 +146,12 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
                 const int row = i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
                 const int col = j * 32 + lc;
                 float f = (float)acc[i][j][r];
-                if (inscale) f = f * a.in_scale;
+                if (INSC) f = f * a.in_scale;
                 f = f * ws[j];
                 f = f + bias[j];
                 if (ADD) f = ff::add_residual(f, (int32_t)Ws[row * P + col], adds[j]);
-                if (PRELU) f = ff::prelu(f, p2[j]);
+                if (PRELU == 1) f = ff::prelu(f, p2[j]);
+                if (PRELU == 2) f = ff::prelu_le1(f, p2[j]);
                 Ws[row * P + col] = (int8_t)ff::requant_haz(f * inv[j]);
                 // one 32x32 tile at a time: keeps the compiler from hoisting
                 // every residual read of the wave tile into registers
@@ -224,6 +228,31 @@ __device__ __forceinline__ void wave_epi_wide(const v16i (&acc)[MI][NJ], const C
 }
 
 // int8 epilogue variants dispatched on the (uniform) flags, parameters given
+template <int COUT, int MI, int NJ, bool INSC>
+__device__ __forceinline__ void wave_epilogue_f(const v16i (&acc)[MI][NJ], const ConvArgs& a,
+                                                const EpiParams<NJ>& P, int mrow0, int ncol0, int8_t* Ws,
+                                                const int8_t* Lw) {
+    const bool le1 = !INSC && (a.flags & FFK_EPI_PRELU_LE1);
+    switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN)) {
+    case 0: wave_epi_i8<COUT, MI, NJ, 0, false, false, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_PRELU:
+        if (le1) wave_epi_i8<COUT, MI, NJ, 2, false, false, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw);
+        else wave_epi_i8<COUT, MI, NJ, 1, false, false, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw);
+        break;
+    case FFK_EPI_ADD: wave_epi_i8<COUT, MI, NJ, 0, true, false, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_BN: wave_epi_i8<COUT, MI, NJ, 0, false, true, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_PRELU | FFK_EPI_BN:
+        if (le1) wave_epi_i8<COUT, MI, NJ, 2, false, true, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw);
+        else wave_epi_i8<COUT, MI, NJ, 1, false, true, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw);
+        break;
+    case FFK_EPI_ADD | FFK_EPI_BN:
+        wave_epi_i8<COUT, MI, NJ, 0, true, true, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_PRELU | FFK_EPI_ADD:
+        wave_epi_i8<COUT, MI, NJ, 1, true, false, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    default: wave_epi_i8<COUT, MI, NJ, 1, true, true, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    }
+}
+
 template <int COUT, int MI, int NJ>
 __device__ __forceinline__ void wave_epilogue_p(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                                 const EpiParams<NJ>& P, int mrow0, int ncol0, int8_t* Ws,
@@ -232,19 +261,8 @@ __device__ __forceinline__ void wave_epilogue_p(const v16i (&acc)[MI][NJ], const
         wave_epi_wide<COUT, MI, NJ, false>(acc, a, mrow0, ncol0);
         return;
     }
-    switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN)) {
-    case 0: wave_epi_i8<COUT, MI, NJ, false, false, false>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_PRELU: wave_epi_i8<COUT, MI, NJ, true, false, false>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_ADD: wave_epi_i8<COUT, MI, NJ, false, true, false>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_BN: wave_epi_i8<COUT, MI, NJ, false, false, true>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_PRELU | FFK_EPI_BN:
-        wave_epi_i8<COUT, MI, NJ, true, false, true>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_ADD | FFK_EPI_BN:
-        wave_epi_i8<COUT, MI, NJ, false, true, true>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_PRELU | FFK_EPI_ADD:
-        wave_epi_i8<COUT, MI, NJ, true, true, false>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    default: wave_epi_i8<COUT, MI, NJ, true, true, true>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    }
+    if (a.flags & FFK_EPI_INSCALE) wave_epilogue_f<COUT, MI, NJ, true>(acc, a, P, mrow0, ncol0, Ws, Lw);
+    else wave_epilogue_f<COUT, MI, NJ, false>(acc, a, P, mrow0, ncol0, Ws, Lw);
 }
 
 template <int COUT, int MI, int NJ, bool FC = false>
@@ -1020,12 +1038,16 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
         // the input layer has no residual input (ffk_conv rejects FFK_EPI_ADD here)
         int8_t* Ws = Es + wave * (32 * 80);
         const int mw = m0 + wave * 32;
+        const int pf = a.flags & FFK_EPI_PRELU ? (a.flags & FFK_EPI_PRELU_LE1 ? 2 : 1) : 0;
         if (a.out_i32) wave_epi_wide<COUT, 1, 2, false>(acc, a, mw, 0);
-        else switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_BN)) {
-        case 0: wave_epi_i8<COUT, 1, 2, false, false, false>(acc, a, prm, mw, 0, Ws, Ls); break;
-        case FFK_EPI_PRELU: wave_epi_i8<COUT, 1, 2, true, false, false>(acc, a, prm, mw, 0, Ws, Ls); break;
-        case FFK_EPI_BN: wave_epi_i8<COUT, 1, 2, false, false, true>(acc, a, prm, mw, 0, Ws, Ls); break;
-        default: wave_epi_i8<COUT, 1, 2, true, false, true>(acc, a, prm, mw, 0, Ws, Ls); break;
+        else if (a.flags & FFK_EPI_INSCALE) wave_epilogue_f<COUT, 1, 2, true>(acc, a, prm, mw, 0, Ws, Ls);
+        else switch (pf + (a.flags & FFK_EPI_BN ? 3 : 0)) {
+        case 0: wave_epi_i8<COUT, 1, 2, 0, false, false, false>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case 1: wave_epi_i8<COUT, 1, 2, 1, false, false, false>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case 2: wave_epi_i8<COUT, 1, 2, 2, false, false, false>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case 3: wave_epi_i8<COUT, 1, 2, 0, false, true, false>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case 4: wave_epi_i8<COUT, 1, 2, 1, false, true, false>(acc, a, prm, mw, 0, Ws, Ls); break;
+        default: wave_epi_i8<COUT, 1, 2, 2, false, true, false>(acc, a, prm, mw, 0, Ws, Ls); break;
         }
     }
 }
@@ -1178,6 +1200,10 @@ constexpr launch_fn split_launch() {
 #ifndef FF_TPATCH64
 #define FF_TPATCH64 4, 1, 2, 2, 2
 #endif
+// Cout >= 256 (stages 3-4)
+#ifndef FF_TPATCH_BIG
+#define FF_TPATCH_BIG FF_TPATCH
+#endif
 #define FF_PENTRY(CIN, COUT, H, SPLIT, MID, WM, WN, MI, NJ, WPE)                      \
     {CIN, COUT, 3, 1, H, H, WM * MI * 32, WN * NJ * 32,                              \
      &launch_patch<CIN, COUT, H, WM, WN, MI, NJ, WPE>, SPLIT,                         \
@@ -1185,12 +1211,17 @@ constexpr launch_fn split_launch() {
 #define FF_PENTRY_K(CIN, COUT, H, SPLIT, MID, TILE) FF_PENTRY(CIN, COUT, H, SPLIT, MID, TILE)
 #ifdef FF_NO_PATCH
 #define FF_P(CIN, COUT, H, SPLIT) FF_CBIG(CIN, COUT, 3, 1, H, SPLIT)
+#define FF_PB(CIN, COUT, H, SPLIT) FF_CBIG(CIN, COUT, 3, 1, H, SPLIT)
 #define FF_P64(CIN, COUT, H, SPLIT) FF_C64(CIN, COUT, 3, 1, H, SPLIT)
 #else
 #define FF_P(CIN, COUT, H, SPLIT)                                                   \
     FF_PENTRY_K(CIN, COUT, H, SPLIT,                                                \
                 (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>), \
                 FF_TPATCH)
+#define FF_PB(CIN, COUT, H, SPLIT)                                                  \
+    FF_PENTRY_K(CIN, COUT, H, SPLIT,                                                \
+                (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>), \
+                FF_TPATCH_BIG)
 #define FF_P64(CIN, COUT, H, SPLIT) FF_PENTRY_K(CIN, COUT, H, SPLIT, nullptr, FF_TPATCH64)
 #endif
 
@@ -1211,11 +1242,11 @@ const ConvEntry kConvTable[] = {
     FF_P(128, 256, 28, 1),
     FF_CBIG(256, 256, 3, 2, 28, 6),
     FF_CBIG(128, 256, 1, 2, 28, 1),
-    FF_P(256, 256, 14, 9),
-    FF_P(256, 512, 14, 3),
+    FF_PB(256, 256, 14, 9),
+    FF_PB(256, 512, 14, 3),
     FF_CBIG(512, 512, 3, 2, 14, 9),
     FF_CBIG(256, 512, 1, 2, 14, 1),
-    FF_P(512, 512, 7, 9),
+    FF_PB(512, 512, 7, 9),
 };
 
 const ConvEntry* find_conv(int cin, int cout, int kh, int kw, int stride, int pad, int hin, int win) {
@@ -1306,6 +1337,22 @@ int ffk_conv_supported(int cin, int cout, int kh, int kw, int stride, int pad, i
     return find_conv(cin, cout, kh, kw, stride, pad, hin, win) != nullptr;
 }
 
+int ffk_prelu_le1_ok(const float* params, int cout, int ktotal, int with_add) {
+    if (!params || cout <= 0 || ktotal <= 0) return 0;
+    const double acc_max = (double)ktotal * 128.0 * 128.0;
+    for (int c = 0; c < cout; c++) {
+        const double s = params[FFK_P_SLOPE * cout + c];
+        const double ws = params[FFK_P_WS * cout + c];
+        const double bias = params[FFK_P_BIAS * cout + c];
+        const double adds = with_add ? params[FFK_P_ADDSCALE * cout + c] : 0.0;
+        if (!(s <= 1.0) || !std::isfinite(ws) || !std::isfinite(bias) || !std::isfinite(adds)) return 0;
+        // each fp32 rounding is within a factor 1 + 2^-23 of its exact value
+        const double bound = (acc_max * std::fabs(ws) + std::fabs(bias) + 128.0 * std::fabs(adds)) * 1.0001;
+        if (!(bound < 3.0e38)) return 0;
+    }
+    return 1;
+}
+
 size_t ffk_conv_packed_bytes(int cin, int cout, int kh, int kw) {
     const size_t ktot = (size_t)kh * kw * cin;
     const size_t steps = (ktot + FF_KSTEP - 1) / FF_KSTEP;
@@ -1387,6 +1434,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     a.out_bn = d->out_bn;
     a.out_i32 = d->out_i32;
     a.flags = d->flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_BIAS | FFK_EPI_INSCALE |
+                          FFK_EPI_PRELU_LE1 |
                           FFK_IN_RGB8);
     a.in_scale = d->in_scale;
     // The direct-to-LDS kernels address the int8 input with 32-bit offsets:

@@ -58,6 +58,15 @@ __device__ __forceinline__ float prelu(float f, float slope) {
     return (f < 0.0f) ? neg : f;
 }
 
+// The same PReLU in two operations, max(f, RN(f * slope)), for slope <= 1
+// and f never +-inf: for f < 0, f * slope >= f and RN is monotone, so the max
+// is RN(f * slope); for f >= 0, f * slope <= f, so it is f (a zero may change
+// sign, which no later step can tell apart: the int8 result of +-0 is 0);
+// for NaN f both operands are NaN.
+__device__ __forceinline__ float prelu_le1(float f, float slope) {
+    return __builtin_fmaxf(f, f * slope);
+}
+
 // BN requant of an int8 value (bn_prelu_requant_int8 with bn != NULL,
 // int8_epilogue.c:273-303): f = fma(RN(x * s_in), bn_s, bn_o); HAZ(RN(f*inv)).
 __device__ __forceinline__ int32_t bn_requant(int32_t x, float s_in, float bn_s, float bn_o,

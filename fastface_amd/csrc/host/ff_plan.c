@@ -229,6 +229,9 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
                 fill_rowf(P + FFK_P_ADDSCALE * C, C, v4 ? slot_pc[add_k] : NULL, slot_scale[add_k]);
                 add_idx++;
             }
+            /* PReLU as max(f, f*slope) where the parameters allow it (same values) */
+            if (slope && ffk_prelu_le1_ok(P, C, op->Kh * op->Kw * op->Cin, add_k >= 0))
+                s->flags |= FFK_EPI_PRELU_LE1;
             A = X; A_scale = eff_scale;
             if (pc && m->scale_pc[eff]) A_pc = m->scale_pc[eff];
             last_conv = p->n_steps - 1;

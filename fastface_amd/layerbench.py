@@ -30,7 +30,7 @@ def main():
     ap.add_argument("--hin", type=int, default=14)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--iters", type=int, default=200)
-    ap.add_argument("--epi", default="prelu", choices=["prelu", "add_bn", "none", "raw"])
+    ap.add_argument("--epi", default="prelu", choices=["prelu", "prelu_le1", "add_bn", "none", "raw"])
     ap.add_argument("--no-split", action="store_true",
                     help="give no split-K workspace (small batches then use the whole-K tiling)")
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -85,8 +85,10 @@ def main():
         d.out_i32 = dev(nbytes=n_out * 4)
     else:
         d.out = dev(nbytes=n_out)
-    if a.epi == "prelu":
+    if a.epi.startswith("prelu"):
         d.flags |= fa.FFK_EPI_PRELU
+    if a.epi == "prelu_le1":
+        d.flags |= fa.FFK_EPI_PRELU_LE1
     if a.epi == "add_bn":
         d.flags |= fa.FFK_EPI_ADD | fa.FFK_EPI_BN
         d.add_src = dev(r.integers(-127, 128, size=n_out, dtype=np.int8))

@@ -72,6 +72,12 @@ typedef struct { const float* in; float* out; } ffk_io;
 #define FFK_EPI_INSCALE  0x10   /* f = f * in_scale before ws (FFW2/FFW3)    */
 #define FFK_IN_RGB8      0x20   /* cin == 3: `in` holds uint8 RGB pixels, each
                                    channel quantized through in_lut          */
+#define FFK_EPI_PRELU_LE1 0x40  /* with FFK_EPI_PRELU: the caller guarantees
+                                   every slope is <= 1 (not NaN) and the
+                                   pre-activation value never reaches -inf,
+                                   so the kernel may take PReLU as
+                                   max(f, f*slope) -- the same values, one
+                                   operation fewer (ffk_prelu_le1_ok)        */
 
 /* rows of the per-layer parameter block, each `cout` floats (device) */
 enum {
@@ -113,6 +119,14 @@ typedef struct {
     size_t         workspace_bytes;
     const int8_t*  in_lut;   /* FFK_IN_RGB8: [3][256] from ffk_make_rgb8_lut */
 } ffk_conv_desc;
+
+/* 1 if a conv's parameter block (host memory, [FFK_NPARAM][cout]) allows
+ * FFK_EPI_PRELU_LE1 for a reduction of ktotal = kh*kw*cin int8 products:
+ * every PReLU slope is <= 1 and not NaN, every weight scale, bias and
+ * residual scale is finite, and |acc|*|ws| + |bias| + 128*|add_scale| stays
+ * below FLT_MAX for the largest |acc| = ktotal*128*128, so the
+ * pre-activation value is never infinite.  Else 0. */
+int    ffk_prelu_le1_ok(const float* params, int cout, int ktotal, int with_add);
 
 /* 1 if a kernel is compiled for this layer geometry, else 0. */
 int    ffk_conv_supported(int cin, int cout, int kh, int kw, int stride, int pad,

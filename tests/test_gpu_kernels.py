@@ -107,7 +107,7 @@ def _special_params(r, C):
     return ws, bias, inv
 
 
-EPI_MODES = ["none", "prelu", "add", "add_bn", "prelu_bn", "bn_only"]
+EPI_MODES = ["none", "prelu", "add", "add_bn", "prelu_bn", "bn_only", "prelu_le1", "prelu_bn_le1"]
 EPI_SHAPES = [(64, 64, 3, 1, 56), (64, 64, 1, 2, 112), (128, 256, 1, 2, 28),
               (256, 256, 3, 1, 14), (512, 512, 3, 1, 7)]
 
@@ -182,12 +182,17 @@ def test_conv_fused_epilogue(gpu_lib, oracle, mode, cin, cout, k, s, H, split):
     add = None
     if "prelu" in mode:
         slope = r.uniform(0, 0.3, cout).astype(F32)
+        if mode.endswith("le1"):
+            # PReLU taken as max(f, f*slope): slopes up to exactly 1, zero and
+            # negative slopes, a NaN pre-activation (ws[3]) and denormals
+            slope[7:12] = [1.0, 0.0, -0.0, -0.5, np.float32(1e-45)]
+            flags |= fa.FFK_EPI_PRELU_LE1
         rows["slope"] = slope; ekw["prelu"] = slope; flags |= fa.FFK_EPI_PRELU
     if "add" in mode:
         add = r.integers(-128, 128, size=(B, Ho, Ho, cout), dtype=np.int8)
         adds = r.uniform(1e-3, 5e-2, cout).astype(F32)
         rows["adds"] = adds; ekw.update(add_src=add, add_scale_pc=adds); flags |= fa.FFK_EPI_ADD
-    want_bn = mode.endswith("bn") or mode == "bn_only"
+    want_bn = "bn" in mode
     if want_bn:
         bsin = r.uniform(1e-3, 5e-2, cout).astype(F32)
         bsin[6] = np.float32(3e-45)

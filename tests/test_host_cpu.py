@@ -182,3 +182,28 @@ def test_rgb8_table_matches_sdk_normalization_and_reference_quant(oracle):
         exp = oracle.quant_input(faces, inv)                  # [256, 3]
         assert np.array_equal(lut.T, exp), inv
     assert lib.ffk_make_rgb8_lut(None, lut.ctypes.data) != 0
+
+
+def test_prelu_le1_condition():
+    """ffk_prelu_le1_ok: the plan takes PReLU as max(f, f*slope) only when
+    every slope is at most 1 and the pre-activation cannot reach -inf."""
+    import numpy as np
+    import fastface_amd as fa
+    lib = fa.load()
+    C = 8
+    P = np.zeros((fa.FFK_NPARAM, C), np.float32)
+    P[fa.FFK_P_WS] = 1e-3
+    P[fa.FFK_P_BIAS] = 0.1
+    P[fa.FFK_P_SLOPE] = np.linspace(-1, 1, C)
+    ok = lambda q, k=2304, add=1: lib.ffk_prelu_le1_ok(np.ascontiguousarray(q).ctypes.data, C, k, add)
+    assert ok(P) == 1
+    q = P.copy(); q[fa.FFK_P_SLOPE, 3] = np.float32(1.0000001)
+    assert ok(q) == 0
+    q = P.copy(); q[fa.FFK_P_SLOPE, 0] = np.nan
+    assert ok(q) == 0
+    q = P.copy(); q[fa.FFK_P_WS, 5] = np.inf
+    assert ok(q) == 0
+    q = P.copy(); q[fa.FFK_P_WS, 5] = 1e32        # 2304*16384*1e32 overflows fp32
+    assert ok(q) == 0
+    q = P.copy(); q[fa.FFK_P_ADDSCALE, 1] = np.nan
+    assert ok(q) == 0 and ok(q, add=0) == 1        # the residual scale counts only with an add

@@ -130,6 +130,8 @@ def main():
     ap.add_argument("--batch", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-reps", type=int, default=3)
+    ap.add_argument("--no-winograd", action="store_true",
+                    help="skip the config-5 run of the stage-1 layers as Winograd F(2,3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the path is per-face data "
@@ -192,6 +194,7 @@ def main():
     check(lib, lib.ffk_memcpy_d2h(out.ctypes.data, d_out, out.nbytes, stream), "download")
     check(lib, lib.ffk_stream_sync(stream), "sync")
     assert np.isfinite(out).all()
+    out_direct = out.copy()          # embeddings of x on the direct path
 
     # per-launch durations of every step of the chain (events between launches)
     n_steps = lib.fastface_num_steps(ff.ff)
@@ -305,6 +308,58 @@ def main():
     log("B=%d host buffers: fp32 %.0f faces/s, uint8 RGB %.0f faces/s; uint8 RGB resident %.0f faces/s"
         % (B, host_fp32, host_rgb8, dev_rgb8))
 
+    # BASELINE config 5 also runs the stage-1 64-channel 3x3 stride-1 convs as
+    # integer Winograd F(2,3): same batch, same timing; the embeddings must be
+    # bit-identical to the direct path's
+    wino = None
+    if not args.no_winograd:
+        n_w = lib.fastface_set_conv_algo(ff.ff, 1)
+        if n_w <= 0:
+            raise RuntimeError("fastface_set_conv_algo failed (%d)" % n_w)
+        for _ in range(3):
+            step()
+        check(lib, lib.ffk_stream_sync(stream), "sync")
+        kw = max(K // 4, 5)
+        check(lib, lib.ffk_event_record(ev0, stream), "record")
+        for _ in range(kw):
+            step()
+        check(lib, lib.ffk_event_record(ev1, stream), "record")
+        check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
+        w_ms = ms.value / kw
+        out_w = np.empty((B, 512), np.float32)
+        check(lib, lib.ffk_memcpy_d2h(out_w.ctypes.data, d_out, out_w.nbytes, stream), "download")
+        check(lib, lib.ffk_stream_sync(stream), "sync")
+        same = bool(np.array_equal(out_w, out_direct))
+        w_steps = np.zeros(n_steps, np.float32)
+        if lib.fastface_profile_steps(ff.ff, B, args.profile_reps, w_steps.ctypes.data) != n_steps:
+            raise RuntimeError("profile_steps failed: %s" % fastface_amd.last_error())
+        layers = {}
+        for s_ in range(n_steps):
+            check(lib, lib.fastface_get_step(ff.ff, s_, C.byref(info)), "step info")
+            if not info.flags & fastface_amd.FFK_ALGO_WINOGRAD:
+                continue
+            key = "64->64 k3 s1 @%d" % info.hin
+            e = layers.setdefault(key, {"n": 0, "winograd_ms": 0.0, "direct_ms": 0.0,
+                                        "ops": info.ops_per_face * B})
+            e["n"] += 1
+            e["winograd_ms"] += float(w_steps[s_])
+            e["direct_ms"] += steps[s_]["ms"]
+        for key, e in layers.items():
+            n = e.pop("n")
+            ops = e.pop("ops")
+            e.update(count=n, winograd_ms=round(e["winograd_ms"] / n, 4),
+                     direct_ms=round(e["direct_ms"] / n, 4))
+            e["winograd_frac_of_int8_peak"] = round(ops / (e["winograd_ms"] * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)
+            log("B=%d %s x%d: Winograd F(2,3) %.4f ms, direct %.4f ms" % (B, key, n, e["winograd_ms"],
+                                                                         e["direct_ms"]))
+        wino = {"layers": n_w, "faces_s": round(B / (w_ms * 1e-3), 1), "ms_per_step": round(w_ms, 4),
+                "embeddings_equal_direct": same, "per_layer": layers}
+        log("B=%d Winograd stage 1: %.3f ms/step, %.0f faces/s, embeddings %s the direct path's"
+            % (B, w_ms, wino["faces_s"], "equal to" if same else "DIFFERENT FROM"))
+        if not same:
+            raise RuntimeError("Winograd embeddings differ from the direct path")
+        check(lib, lib.fastface_set_conv_algo(ff.ff, 0), "algo direct")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(ffw)
@@ -345,6 +400,7 @@ def main():
                      "achieved": round(dom_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": round(dom_tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
                      "launch_ms": round(dom_ms, 5), "ops_per_launch": dom_ops},
+        "stage1_winograd": wino,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

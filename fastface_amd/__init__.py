@@ -23,6 +23,7 @@ FASTFACE_OUTPUT_N = 512
 FFK_EPI_PRELU, FFK_EPI_ADD, FFK_EPI_BN, FFK_EPI_BIAS, FFK_EPI_INSCALE = 1, 2, 4, 8, 16
 FFK_IN_RGB8 = 0x20
 FFK_EPI_PRELU_LE1 = 0x40
+FFK_ALGO_WINOGRAD = 0x80
 (FFK_P_WS, FFK_P_BIAS, FFK_P_SLOPE, FFK_P_ADDSCALE, FFK_P_INV, FFK_P_BN_SIN, FFK_P_BN_S,
  FFK_P_BN_O, FFK_P_BN_INV, FFK_NPARAM) = range(10)
 
@@ -70,6 +71,7 @@ EXPORTS = [
     ("fastface_embed_batch_rgb8_device", C.c_int, [_p, _p, C.c_int, _p, _p]),
     ("fastface_reserve", C.c_int, [_p, C.c_int]),
     ("fastface_stream", _p, [_p]),
+    ("fastface_set_conv_algo", C.c_int, [_p, C.c_int]),
     ("fastface_num_steps", C.c_int, [_p]),
     ("fastface_get_step", C.c_int, [_p, C.c_int, C.POINTER(fastface_step_info)]),
     ("fastface_profile_steps", C.c_int, [_p, C.c_int, C.c_int, _p]),
@@ -104,6 +106,9 @@ EXPORTS = [
     ("ffk_conv_workspace_bytes", C.c_size_t, [C.POINTER(ffk_conv_desc)]),
     ("ffk_conv", C.c_int, [C.POINTER(ffk_conv_desc), _p]),
     ("ffk_conv_variant", C.c_char_p, [C.POINTER(ffk_conv_desc)]),
+    ("ffk_winograd_supported", C.c_int, [C.c_int] * 8),
+    ("ffk_winograd_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),
+    ("ffk_pack_winograd_weights", C.c_int, [_p, C.c_int, C.c_int, _p]),
     ("ffk_make_bn_lut", C.c_int, [_p, _p, _p, _p, C.c_int, _p]),
     ("ffk_make_rgb8_lut", C.c_int, [_p, _p]),
     ("ffk_fc_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),

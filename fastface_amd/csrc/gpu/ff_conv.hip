@@ -1103,6 +1103,7 @@ constexpr int FF_SPLIT_MIN_WG = 256;
 constexpr int FF_SPLIT_MAX_WG = 160;
 // split-K workspace: [counter per tile, fixed size][int32 partial tiles]
 constexpr size_t FF_SPLIT_COUNTER_BYTES = FF_SPLIT_MAX_WG * sizeof(unsigned);
+static_assert(FF_SPLIT_COUNTER_BYTES <= FF_WS_COUNTER_AREA, "counters stay in the reserved area");
 
 struct ConvEntry {
     int cin, cout, ks, stride, hin, win, bm, bn;
@@ -1420,6 +1421,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
         return FFK_ERR_ARG;
     }
     if (M == 0) return FFK_OK;
+    if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_conv(d, (hipStream_t)stream);
     ConvArgs a = {};
     if (stem) a.in_f32 = (const float*)d->in;
     else a.in = (const int8_t*)d->in;
@@ -1471,6 +1473,7 @@ size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d) {
     if (!d || d->batch <= 0) return 0;
     const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);
     if (!e) return 0;
+    if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_ws_bytes(d);
     const long long M = conv_pixels(d);
     if (M > 0x7fffffffLL) return 0;
     return choose_launch(e, M, (size_t)-1).ws_bytes;
@@ -1480,6 +1483,7 @@ const char* ffk_conv_variant(const ffk_conv_desc* d) {
     if (!d || d->batch <= 0) return nullptr;
     const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);
     if (!e) return nullptr;
+    if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_eligible(d) ? "winograd" : nullptr;
     const long long M = conv_pixels(d);
     if (M > 0x7fffffffLL) return nullptr;
     return choose_launch(e, M, d->workspace ? d->workspace_bytes : 0).kind;

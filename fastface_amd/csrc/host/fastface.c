@@ -42,6 +42,7 @@ struct FastFace {
     ffk_io* h_io;               /* pinned staging */
     ffk_io io_cur;              /* what d_io holds now */
     int keep_all;
+    int algo;                   /* FASTFACE_CONV_* of the 64-channel 3x3 s1 layers */
     GraphEntry graphs[FF_MAX_GRAPHS];
     int n_graphs, graph_rr;
 };
@@ -92,18 +93,20 @@ static int set_io(FastFace* ff, const float* in, float* out, void* stream)
 
 static void step_desc(FastFace* ff, int s, int batch, int fmt, ffk_conv_desc* d);
 
-/* Largest split-K workspace any conv step asks for at 1..max_batch faces.
- * Only small batches split (the split grid is capped at a few thousand
- * 64x64 tiles, i.e. below ~4096 faces for every IResNet layer). */
+/* Largest workspace any conv step asks for at 1..max_batch faces.  Only
+ * small batches split K (the split grid is capped at a few thousand 64x64
+ * tiles, i.e. below ~4096 faces for every IResNet layer); the Winograd
+ * layers' transformed input grows with the batch up to a fixed slice, so
+ * max_batch covers it. */
 static size_t workspace_bytes(FastFace* ff, int max_batch)
 {
     size_t best = 0;
     const int top = max_batch < 4096 ? max_batch : 4096;
     for (int s = 0; s < ff->plan.n_steps; s++) {
         if (ff->plan.steps[s].kind != 1) continue;
-        for (int b = 1; b <= top; b++) {
+        for (int b = 1; b <= top + 1; b++) {
             ffk_conv_desc d;
-            step_desc(ff, s, b, 0, &d);
+            step_desc(ff, s, b <= top ? b : max_batch, 0, &d);
             const size_t n = ffk_conv_workspace_bytes(&d);
             if (n > best) best = n;
         }
@@ -175,6 +178,10 @@ static void step_desc(FastFace* ff, int s, int batch, int fmt, ffk_conv_desc* d)
     }
     if (st->flags & FFK_EPI_BN) d->bn_lut = ff->d_weights + st->lut_off;
     d->flags = st->flags | ((fmt && st->t_in == FF_T_INPUT) ? FFK_IN_RGB8 : 0);
+    if (ff->algo == FASTFACE_CONV_WINOGRAD_F23 && st->wino_off != (size_t)-1) {
+        d->flags |= FFK_ALGO_WINOGRAD;
+        d->w = ff->d_weights + st->wino_off;
+    }
     d->in_scale = st->in_scale;
     d->workspace = ff->d_ws;
     d->workspace_bytes = ff->ws_bytes;
@@ -382,6 +389,22 @@ int fastface_embed_batch_rgb8_device(FastFace* ff, const uint8_t* d_in, int batc
     return 0;
 }
 
+int fastface_set_conv_algo(FastFace* ff, int algo)
+{
+    if (!ff || (algo != FASTFACE_CONV_DIRECT && algo != FASTFACE_CONV_WINOGRAD_F23)) return -1;
+    int n = 0;
+    if (algo == FASTFACE_CONV_WINOGRAD_F23)
+        for (int s = 0; s < ff->plan.n_steps; s++)
+            if (ff->plan.steps[s].kind == 1 && ff->plan.steps[s].wino_off != (size_t)-1) n++;
+    if (algo == ff->algo) return n;
+    if (ffk_stream_sync(ff->stream)) return -2;
+    /* other launch chains, and another workspace size */
+    const int cap = ff->capacity;
+    free_activations(ff);
+    ff->algo = algo;
+    return ensure_capacity(ff, cap > 0 ? cap : 1) ? -2 : n;
+}
+
 int fastface_num_steps(const FastFace* ff) { return ff ? ff->plan.n_steps : -1; }
 
 int fastface_get_step(const FastFace* ff, int s, fastface_step_info* info)
@@ -396,6 +419,8 @@ int fastface_get_step(const FastFace* ff, int s, fastface_step_info* info)
         info->cin = st->cin; info->cout = st->cout; info->kh = st->kh; info->kw = st->kw;
         info->stride = st->stride; info->pad = st->pad; info->hin = st->hin; info->win = st->win;
         info->hout = st->hout; info->wout = st->wout; info->flags = st->flags;
+        if (ff->algo == FASTFACE_CONV_WINOGRAD_F23 && st->wino_off != (size_t)-1)
+            info->flags |= FFK_ALGO_WINOGRAD;
         info->stores_x = st->t_out >= 0;
         const double pix_out = (double)st->hout * st->wout;
         info->ops_per_face = 2.0 * pix_out * st->cout * st->kh * st->kw * st->cin;

@@ -57,6 +57,8 @@ typedef struct {
     size_t w_off;               /* bytes into the weight arena */
     size_t p_off;               /* floats into the parameter arena */
     size_t lut_off;             /* bytes into the weight arena: BN table */
+    size_t wino_off;            /* bytes into the weight arena: Winograd-packed
+                                   weights, or (size_t)-1 if the layer has none */
     /* fc */
     int fc_n, fc_k; float a_scale; size_t ws_off, bias_off;
 } FfStep;

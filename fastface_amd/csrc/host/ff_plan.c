@@ -212,6 +212,12 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
             s->flags = FFK_EPI_BIAS | (in_scale != 1.0f ? FFK_EPI_INSCALE : 0);
             s->w_off = alloc_weights(&B, ffk_conv_packed_bytes(op->Cin, op->Cout, op->Kh, op->Kw));
             ffk_pack_conv_weights(op->conv_w, op->Cout, op->Cin, op->Kh, op->Kw, p->w_host + s->w_off);
+            s->wino_off = (size_t)-1;
+            if (ffk_winograd_supported(op->Cin, op->Cout, op->Kh, op->Kw, op->stride, op->pad, si.H, si.W)) {
+                /* the same layer as integer Winograd F(2,3) (fastface_set_conv_algo) */
+                s->wino_off = alloc_weights(&B, ffk_winograd_packed_bytes(op->Cin, op->Cout));
+                ffk_pack_winograd_weights(op->conv_w, op->Cout, op->Cin, p->w_host + s->wino_off);
+            }
             s->p_off = alloc_params(&B, (size_t)FFK_NPARAM * op->Cout);
             float* P = p->p_host + s->p_off;
             const int C = op->Cout;

@@ -76,6 +76,19 @@ int fastface_reserve(FastFace* ff, int max_batch);
 /* The context's HIP stream (hipStream_t). */
 void* fastface_stream(FastFace* ff);
 
+/* Convolution algorithm of the 64-channel 3x3 stride-1 layers (stage 1 of
+ * IResNet, at 56x56 and 112x112).  The integer Winograd F(2,3) path of the
+ * reference (kernels/winograd_int8_ref.c, output 4x the direct conv, divided
+ * back exactly) gives the same int32 accumulators, activations and
+ * embeddings bit for bit as the direct implicit GEMM; it exists to run
+ * those layers both ways, and is slower here (its int8 operand limbs cost
+ * more MFMA work than the transform saves).  Returns the number of layers
+ * the algorithm now runs, -1 on bad arguments, -2 if the larger workspace
+ * cannot be allocated.  Captured launch chains are rebuilt on next use. */
+#define FASTFACE_CONV_DIRECT       0
+#define FASTFACE_CONV_WINOGRAD_F23 1
+int fastface_set_conv_algo(FastFace* ff, int algo);
+
 /* ---------------- introspection (tests, bench) ---------------------------- */
 typedef struct {
     int kind;                 /* 1 conv, 2 FC                                   */

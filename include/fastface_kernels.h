@@ -120,6 +120,25 @@ typedef struct {
     const int8_t*  in_lut;   /* FFK_IN_RGB8: [3][256] from ffk_make_rgb8_lut */
 } ffk_conv_desc;
 
+/* FFK_ALGO_WINOGRAD (flags): run a 3x3 stride-1 pad-1 layer with
+ * cin == cout == 64 at 56x56 or 112x112 as integer Winograd F(2,3)
+ * (kernels/winograd_int8_ref.c:36-179: G' = 2G, output = 4 x direct, here
+ * divided back exactly) instead of the direct implicit GEMM.  Same int32
+ * accumulators and outputs bit for bit; `w` must hold
+ * ffk_pack_winograd_weights output, and the call needs the workspace
+ * ffk_conv_workspace_bytes reports (the transformed input of up to 2 GiB of
+ * images at a time).  ffk_conv_variant names it "winograd". */
+#define FFK_ALGO_WINOGRAD 0x80
+/* 1 if FFK_ALGO_WINOGRAD serves this layer geometry, else 0. */
+int    ffk_winograd_supported(int cin, int cout, int kh, int kw, int stride, int pad,
+                              int hin, int win);
+/* Bytes of the Winograd-packed weights: 16 cells x cout x 2 int8 limbs x cin. */
+size_t ffk_winograd_packed_bytes(int cin, int cout);
+/* U = G' g G'^T per (cell, co, ci) (winograd_int8_ref.c:36-60) cut into
+ * int8 limbs u = 64*u1 + u0 (u0 in [0,63]):
+ * packed[((cell*cout + co)*2 + limb)*cin + ci], limb 0 = u1, 1 = u0. */
+int    ffk_pack_winograd_weights(const int8_t* w_oihw, int cout, int cin, int8_t* packed);
+
 /* 1 if a conv's parameter block (host memory, [FFK_NPARAM][cout]) allows
  * FFK_EPI_PRELU_LE1 for a reduction of ktotal = kh*kw*cin int8 products:
  * every PReLU slope is <= 1 and not NaN, every weight scale, bias and

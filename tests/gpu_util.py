@@ -97,8 +97,17 @@ def split_counters_zero(lib, ws):
     return not ws.get(np.uint32, (SPLIT_COUNTERS,)).any()
 
 
+def pack_winograd(lib, w_oihw):
+    cout, cin = w_oihw.shape[:2]
+    packed = np.empty(lib.ffk_winograd_packed_bytes(cin, cout), np.int8)
+    check(lib, lib.ffk_pack_winograd_weights(np.ascontiguousarray(w_oihw, np.int8).ctypes.data,
+                                             cout, cin, packed.ctypes.data))
+    return packed
+
+
 def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=False,
-             want_x=True, want_bn=False, in_inv=None, in_scale=1.0, split=True, in_lut=None):
+             want_x=True, want_bn=False, in_inv=None, in_scale=1.0, split=True, in_lut=None,
+             winograd=False, workspace=None):
     """One ffk_conv call; returns int32 acc (raw) or (X, BN(X)) int8 arrays.
     split: give the call the split-K workspace it asks for (small batches take
     the split path); False: no workspace (whole-K tiling)."""
@@ -112,7 +121,11 @@ def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=Fa
     d.stride, d.pad, d.hin, d.win = stride, pad, H, W
     dx = Dev(lib, host=x); keep.append(dx)
     d.in_ = dx.ptr
-    dw = Dev(lib, host=pack_conv(lib, w_oihw)); keep.append(dw)
+    dw = Dev(lib, host=pack_winograd(lib, w_oihw) if winograd else pack_conv(lib, w_oihw))
+    keep.append(dw)
+    if winograd:
+        flags |= fa.FFK_ALGO_WINOGRAD
+        split = True            # the transformed input lives in the workspace
     d.w = dw.ptr
     if in_inv is not None:
         di = Dev(lib, host=np.asarray(list(in_inv) + [0.0], np.float32)); keep.append(di)
@@ -144,10 +157,12 @@ def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=Fa
             d.out_bn = dob.ptr
     d.flags = flags
     d.in_scale = in_scale
-    ws = conv_workspace(lib, d) if split else None
+    ws = workspace if workspace is not None else (conv_workspace(lib, d) if split else None)
     if ws is not None:
         keep.append(ws)
         d.workspace, d.workspace_bytes = ws.ptr, ws.nbytes
+    if winograd:
+        assert ws is not None and lib.ffk_conv_variant(C.byref(d)) == b"winograd"
     check(lib, lib.ffk_conv(C.byref(d), None))
     check(lib, lib.ffk_stream_sync(None))
     if ws is not None:

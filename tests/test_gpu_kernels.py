@@ -267,3 +267,116 @@ def test_fc_head(gpu_lib, oracle, B, path):
     got = run_fc(gpu_lib, a, W, ws, bias, path=path)
     for b in range(B):
         assert np.array_equal(got[b], oracle.fc(a[b], W, ws, bias)), "face %d" % b
+
+
+# ---- integer Winograd F(2,3) path of the 64-channel 3x3 stride-1 layers ----
+
+@pytest.mark.parametrize("H,B", [(56, 3), (112, 1)])
+def test_winograd_int32_accumulators(gpu_lib, oracle, H, B):
+    """The Winograd path's int32 accumulators equal the direct conv (brute
+    force) and, times 4, the restated kernels/winograd_int8_ref.c output --
+    the reference's own exactness statement (F(2,3) with G' = 2G is 4x the
+    direct conv).  Extreme operands make the limb products reach their
+    bounds (|v| = 510, |u| = 1152)."""
+    r = rng(700 + H)
+    x = r.integers(-128, 128, size=(B, H, H, 64), dtype=np.int8)
+    w = r.integers(-128, 128, size=(64, 64, 3, 3), dtype=np.int8)
+    x[0, 0:4, :, :] = -128
+    x[0, 4:8, ::2, :] = 127                 # alternating rows: |v| = 510
+    x[-1, -3:, :, :] = 127
+    w[0] = -128
+    w[1] = 127
+    w[2, :, 0, :] = -128; w[2, :, 1, :] = 127; w[2, :, 2, :] = -128   # |u| = 1152
+    got = run_conv(gpu_lib, x, w, 1, 1, raw=True, winograd=True)
+    assert np.array_equal(got, oracle.conv_i32(x, w, 1, 1))
+    u = oracle.winograd_weights(w)
+    assert np.abs(u.astype(np.int32)).max() == 1152
+    assert np.array_equal(4 * got.astype(np.int64), oracle.conv_winograd(x, u).astype(np.int64))
+
+
+@pytest.mark.parametrize("mode", ["none", "prelu", "prelu_le1", "add_bn", "prelu_bn", "bn_only"])
+@pytest.mark.parametrize("H,B", [(56, 2), (112, 1)])
+def test_winograd_fused_epilogue(gpu_lib, oracle, mode, H, B):
+    """The Winograd path's requant epilogue: bit-exact with the oracle in
+    every mode, with the special parameters (ties, overflow, NaN and denormal
+    scales, -0) of the direct kernels' test."""
+    r = rng(750 + H + len(mode))
+    x = r.integers(-128, 128, size=(B, H, H, 64), dtype=np.int8)
+    w = r.integers(-128, 128, size=(64, 64, 3, 3), dtype=np.int8)
+    ws, bias, inv = _special_params(r, 64)
+    rows = dict(ws=ws, bias=bias, inv=inv)
+    flags = fa.FFK_EPI_BIAS
+    ekw = dict(ws=ws, bias=bias, inv_pc=inv)
+    add = None
+    if "prelu" in mode:
+        slope = r.uniform(0, 0.3, 64).astype(F32)
+        if mode.endswith("le1"):
+            slope[7:12] = [1.0, 0.0, -0.0, -0.5, np.float32(1e-45)]
+            flags |= fa.FFK_EPI_PRELU_LE1
+        rows["slope"] = slope; ekw["prelu"] = slope; flags |= fa.FFK_EPI_PRELU
+    if "add" in mode:
+        add = r.integers(-128, 128, size=(B, H, H, 64), dtype=np.int8)
+        adds = r.uniform(1e-3, 5e-2, 64).astype(F32)
+        rows["adds"] = adds; ekw.update(add_src=add, add_scale_pc=adds); flags |= fa.FFK_EPI_ADD
+    want_bn = "bn" in mode
+    if want_bn:
+        bsin = r.uniform(1e-3, 5e-2, 64).astype(F32)
+        bns = r.uniform(0.5, 1.5, 64).astype(F32)
+        bno = r.normal(0, 0.05, 64).astype(F32)
+        binv = (1.0 / r.uniform(0.01, 0.1, 64)).astype(F32)
+        rows.update(bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
+        flags |= fa.FFK_EPI_BN
+    exp_x = oracle.fused_epilogue(oracle.conv_i32(x, w, 1, 1), **ekw)
+    got_x, got_bn = run_conv(gpu_lib, x, w, 1, 1, params=params_block(64, **rows), flags=flags,
+                             add=add, want_x=(mode != "bn_only"), want_bn=want_bn, winograd=True)
+    if mode != "bn_only":
+        assert np.array_equal(got_x, exp_x)
+    if want_bn:
+        exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno,
+                                         inv_pc=binv)
+        assert np.array_equal(got_bn, exp_bn)
+
+
+def test_winograd_large_batch_slices(gpu_lib, oracle):
+    """A 112x112 batch larger than one transformed-input slice (334 images
+    stay under 2 GiB) runs as several launches: sampled images exact."""
+    import ctypes as C
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw, d.stride, d.pad, d.hin, d.win = 400, 64, 64, 3, 3, 1, 1, 112, 112
+    d.flags = fa.FFK_ALGO_WINOGRAD
+    ws1 = gpu_lib.ffk_conv_workspace_bytes(C.byref(d))
+    d.batch = 1000
+    assert gpu_lib.ffk_conv_workspace_bytes(C.byref(d)) == ws1 < 2 ** 31 + 4096
+    r = rng(790)
+    B = 400
+    x = r.integers(-128, 128, size=(B, 112, 112, 64), dtype=np.int8)
+    w = r.integers(-128, 128, size=(64, 64, 3, 3), dtype=np.int8)
+    got = run_conv(gpu_lib, x, w, 1, 1, raw=True, winograd=True)
+    idx = [0, 333, 334, B - 1]
+    assert np.array_equal(got[idx], oracle.conv_i32(x[idx], w, 1, 1))
+
+
+def test_winograd_and_splitk_share_a_workspace(gpu_lib, oracle):
+    """One workspace serves a whole launch chain: the Winograd path keeps
+    out of the split-K arrival counters at its start, so a b=1 split-K layer
+    after a Winograd layer still sums exactly and leaves its counters at 0."""
+    import ctypes as C
+    from gpu_util import Dev, check
+    r = rng(795)
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw, d.stride, d.pad, d.hin, d.win = 1, 64, 64, 3, 3, 1, 1, 112, 112
+    d.flags = fa.FFK_ALGO_WINOGRAD
+    n = gpu_lib.ffk_conv_workspace_bytes(C.byref(d))
+    d.cin, d.cout, d.hin, d.win, d.flags = 512, 512, 7, 7, 0
+    n = max(n, gpu_lib.ffk_conv_workspace_bytes(C.byref(d)))
+    ws = Dev(gpu_lib, nbytes=n)
+    check(gpu_lib, gpu_lib.ffk_zero(ws.ptr, n, None))
+    x1 = r.integers(-128, 128, size=(1, 112, 112, 64), dtype=np.int8)
+    w1 = r.integers(-128, 128, size=(64, 64, 3, 3), dtype=np.int8)
+    x2 = r.integers(-128, 128, size=(1, 7, 7, 512), dtype=np.int8)
+    w2 = r.integers(-128, 128, size=(512, 512, 3, 3), dtype=np.int8)
+    for _ in range(2):
+        got1 = run_conv(gpu_lib, x1, w1, 1, 1, raw=True, winograd=True, workspace=ws)
+        got2 = run_conv(gpu_lib, x2, w2, 1, 1, raw=True, workspace=ws)
+        assert np.array_equal(got1, oracle.conv_i32(x1, w1, 1, 1))
+        assert np.array_equal(got2, oracle.conv_i32(x2, w2, 1, 1))

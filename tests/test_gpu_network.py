@@ -163,3 +163,35 @@ def test_reference_regression_with_real_weights(gpu_lib):
     f.close()
     assert np.array_equal(got, np.fromfile(os.path.join(GOLDEN, "golden_int8_emb.bin"), np.float32))
     assert _cos(got, np.fromfile(os.path.join(GOLDEN, "golden_ort_fp32_emb.bin"), np.float32)) >= 0.98
+
+
+def test_winograd_stage1_network(gpu_lib, synth_ffw4, oracle, oracle_model):
+    """fastface_set_conv_algo(WINOGRAD_F23): the five 64-channel 3x3
+    stride-1 layers (4 at 56x56, 1 at 112x112) run as integer Winograd; every
+    intermediate int8 tensor and the embeddings stay bit-exact with the
+    oracle interpreter, and switching back restores the direct path."""
+    f = fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT)
+    try:
+        x = synth.faces_uniform(3, 31)
+        direct = f.embed_batch(x)
+        assert gpu_lib.fastface_set_conv_algo(f.ff, 1) == 5
+        info = fa.fastface_step_info()
+        wino = [s for s in range(gpu_lib.fastface_num_steps(f.ff))
+                if gpu_lib.fastface_get_step(f.ff, s, C.byref(info)) == 0
+                and info.flags & fa.FFK_ALGO_WINOGRAD]
+        assert len(wino) == 5
+        assert gpu_lib.fastface_debug_keep_tensors(f.ff, 1) == 0
+        got = f.embed_batch(x)
+        exp, dumps = oracle.forward(oracle_model, x, dump_ops=set(range(177)))
+        for op, t in sorted(dumps.items()):
+            buf = np.empty(t.size, np.int8)
+            assert gpu_lib.fastface_debug_read(f.ff, op, 3, buf.ctypes.data, buf.nbytes) == t.size
+            assert np.array_equal(buf.reshape(t.shape), t), "op %d differs" % op
+        assert np.array_equal(got, exp) and np.array_equal(got, direct)
+        assert gpu_lib.fastface_debug_keep_tensors(f.ff, 0) == 0
+        assert np.array_equal(f.embed(x[1]), exp[1])          # b=1, Winograd, graph
+        assert gpu_lib.fastface_set_conv_algo(f.ff, 0) == 0
+        assert np.array_equal(f.embed_batch(x), exp)
+        assert gpu_lib.fastface_set_conv_algo(f.ff, 7) == -1
+    finally:
+        f.close()

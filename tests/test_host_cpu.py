@@ -207,3 +207,28 @@ def test_prelu_le1_condition():
     assert ok(q) == 0
     q = P.copy(); q[fa.FFK_P_ADDSCALE, 1] = np.nan
     assert ok(q) == 0 and ok(q, add=0) == 1        # the residual scale counts only with an add
+
+
+def test_winograd_weight_packing(oracle):
+    """ffk_pack_winograd_weights: the int8 limbs recombine to the restated
+    reference transform U = G' g G'^T (64*u1 + u0, u0 in [0, 63])."""
+    import numpy as np
+    import fastface_amd as fa
+    from conftest import rng
+    lib = fa.load()
+    r = rng(61)
+    w = r.integers(-128, 128, size=(64, 64, 3, 3), dtype=np.int8)
+    w[0] = -128
+    w[1, :, 0, :] = -128; w[1, :, 1, :] = 127; w[1, :, 2, :] = -128
+    n = lib.ffk_winograd_packed_bytes(64, 64)
+    assert n == 16 * 64 * 2 * 64
+    packed = np.empty(n, np.int8)
+    assert lib.ffk_pack_winograd_weights(w.ctypes.data, 64, 64, packed.ctypes.data) == 0
+    p = packed.reshape(16, 64, 2, 64).astype(np.int32)
+    u1, u0 = p[:, :, 0, :], p[:, :, 1, :]
+    assert u0.min() >= 0 and u0.max() <= 63 and np.abs(u1).max() <= 18
+    assert np.array_equal(64 * u1 + u0, oracle.winograd_weights(w).astype(np.int32))
+    sup = lambda *g: lib.ffk_winograd_supported(*g)
+    assert sup(64, 64, 3, 3, 1, 1, 56, 56) == 1 and sup(64, 64, 3, 3, 1, 1, 112, 112) == 1
+    assert sup(64, 64, 3, 3, 2, 1, 112, 112) == 0 and sup(128, 128, 3, 3, 1, 1, 28, 28) == 0
+    assert sup(64, 128, 3, 3, 1, 1, 56, 56) == 0 and sup(64, 64, 1, 1, 1, 0, 56, 56) == 0

@@ -318,10 +318,15 @@ __global__ __launch_bounds__(256, 2) void wino_gemm_kernel(WinoArgs a) {
     }
 }
 
-// images per launch: the transformed input of a slice stays below 2 GiB
+// images per launch pair: the transformed input of a slice (written by the
+// input transform, read right after by the cell GEMMs) is sized to stay in
+// the 256 MB memory-side cache instead of round-tripping through HBM
+#ifndef FF_WINO_SLICE_MB
+#define FF_WINO_SLICE_MB 192
+#endif
 template <int H, int W>
 constexpr int slice_images() {
-    return (int)((0x7fffffffLL) / ((long long)(H / 2) * (W / 2) * 16 * KP));
+    return (int)(((long long)FF_WINO_SLICE_MB << 20) / ((long long)(H / 2) * (W / 2) * 16 * KP));
 }
 
 int eligible(const ffk_conv_desc* d) {

@@ -31,6 +31,8 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--epi", default="prelu", choices=["prelu", "prelu_le1", "add_bn", "none", "raw"])
+    ap.add_argument("--winograd", action="store_true",
+                    help="64-channel 3x3 stride-1 layers: the integer Winograd F(2,3) path")
     ap.add_argument("--no-split", action="store_true",
                     help="give no split-K workspace (small batches then use the whole-K tiling)")
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -55,8 +57,12 @@ def main():
     r = np.random.default_rng(1)
     x = r.integers(-127, 128, size=(a.batch, a.hin, a.hin, a.cin), dtype=np.int8)
     w = r.integers(-127, 128, size=(a.cout, a.cin, a.k, a.k), dtype=np.int8)
-    packed = np.empty(lib.ffk_conv_packed_bytes(a.cin, a.cout, a.k, a.k), np.int8)
-    lib.ffk_pack_conv_weights(w.ctypes.data, a.cout, a.cin, a.k, a.k, packed.ctypes.data)
+    if a.winograd:
+        packed = np.empty(lib.ffk_winograd_packed_bytes(a.cin, a.cout), np.int8)
+        lib.ffk_pack_winograd_weights(w.ctypes.data, a.cout, a.cin, packed.ctypes.data)
+    else:
+        packed = np.empty(lib.ffk_conv_packed_bytes(a.cin, a.cout, a.k, a.k), np.int8)
+        lib.ffk_pack_conv_weights(w.ctypes.data, a.cout, a.cin, a.k, a.k, packed.ctypes.data)
     P = np.zeros((fa.FFK_NPARAM, a.cout), np.float32)
     P[fa.FFK_P_WS] = r.uniform(1e-3, 1e-2, a.cout)
     P[fa.FFK_P_BIAS] = r.normal(0, 0.1, a.cout)
@@ -80,7 +86,7 @@ def main():
     d.in_ = dev(x)
     d.w = dev(packed)
     d.params = dev(P)
-    d.flags = fa.FFK_EPI_BIAS
+    d.flags = fa.FFK_EPI_BIAS | (fa.FFK_ALGO_WINOGRAD if a.winograd else 0)
     if a.epi == "raw":
         d.out_i32 = dev(nbytes=n_out * 4)
     else:

@@ -47,7 +47,7 @@ class ffk_conv_desc(C.Structure):
 class ffk_fc_desc(C.Structure):
     _fields_ = [("batch", C.c_int), ("n", C.c_int), ("k", C.c_int), ("a", _p), ("w", _p),
                 ("ws", _p), ("bias", _p), ("a_scale", C.c_float), ("out", _p), ("io", _p),
-                ("path", C.c_int)]
+                ("path", C.c_int), ("workspace", _p), ("workspace_bytes", C.c_size_t)]
 
 
 class fastface_step_info(C.Structure):
@@ -114,6 +114,7 @@ EXPORTS = [
     ("ffk_fc_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("ffk_pack_fc_weights", C.c_int, [_p, C.c_int, C.c_int, _p]),
     ("ffk_fc", C.c_int, [C.POINTER(ffk_fc_desc), _p]),
+    ("ffk_fc_workspace_bytes", C.c_size_t, [C.POINTER(ffk_fc_desc)]),
     ("ffk_selftest_mfma", C.c_int, []),
 ]
 

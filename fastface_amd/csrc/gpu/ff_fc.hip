@@ -11,6 +11,7 @@
 #include "ff_numerics.h"
 
 int ffk_fc_gemm_launch(const ffk_fc_desc* d, hipStream_t s);
+size_t ffk_fc_split_ws_bytes(int batch);
 
 namespace {
 
@@ -104,6 +105,12 @@ int ffk_pack_fc_weights(const int8_t* w, int n, int k, int8_t* packed) {
             for (int kk = 0; kk < FF_KSTEP; kk++)
                 packed[((size_t)s * n + r) * FF_KSTEP + kk] = w[(size_t)r * k + s * FF_KSTEP + kk];
     return FFK_OK;
+}
+
+size_t ffk_fc_workspace_bytes(const ffk_fc_desc* d) {
+    if (!d || d->batch <= 0 || d->n != 512 || d->k != 25088) return 0;
+    const int path = d->path ? d->path : (d->batch <= FC_MAXB ? 1 : 2);
+    return path == 2 ? ffk_fc_split_ws_bytes(d->batch) : 0;
 }
 
 int ffk_fc(const ffk_fc_desc* d, void* stream) {

@@ -103,6 +103,16 @@ static size_t workspace_bytes(FastFace* ff, int max_batch)
     size_t best = 0;
     const int top = max_batch < 4096 ? max_batch : 4096;
     for (int s = 0; s < ff->plan.n_steps; s++) {
+        if (ff->plan.steps[s].kind == 2) {          /* FC head: split-K of mid-size batches */
+            for (int b = 1; b <= top; b++) {
+                ffk_fc_desc f;
+                memset(&f, 0, sizeof f);
+                f.batch = b; f.n = ff->plan.steps[s].fc_n; f.k = ff->plan.steps[s].fc_k;
+                const size_t n = ffk_fc_workspace_bytes(&f);
+                if (n > best) best = n;
+            }
+            continue;
+        }
         if (ff->plan.steps[s].kind != 1) continue;
         for (int b = 1; b <= top + 1; b++) {
             ffk_conv_desc d;
@@ -206,6 +216,8 @@ static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt)
     f.out = NULL;
     f.io = ff->d_io;
     f.path = 0;
+    f.workspace = ff->d_ws;
+    f.workspace_bytes = ff->ws_bytes;
     return ffk_fc(&f, stream);
 }
 

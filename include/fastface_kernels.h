@@ -196,8 +196,18 @@ typedef struct {
     float*         out;      /* [batch][n] fp32, or NULL: io->out             */
     const ffk_io*  io;
     int            path;     /* 0 auto, 1 matvec, 2 MFMA GEMM                 */
+    /* Optional workspace (device memory, zero-filled once, the same rules as
+     * ffk_conv_desc.workspace; one workspace can serve both): the MFMA GEMM
+     * path then shares each output tile's K reduction among several
+     * workgroups, which fills the GPU at a few thousand faces.  NULL or too
+     * small: one workgroup per output tile. */
+    void*          workspace;
+    size_t         workspace_bytes;
 } ffk_fc_desc;
 
+/* Workspace bytes ffk_fc would use for this descriptor's batch and path
+ * (0: none); the workspace fields are not read. */
+size_t ffk_fc_workspace_bytes(const ffk_fc_desc* d);
 size_t ffk_fc_packed_bytes(int n, int k);
 int    ffk_pack_fc_weights(const int8_t* w_nk, int n, int k, int8_t* packed);
 int    ffk_fc(const ffk_fc_desc* d, void* stream);

@@ -174,7 +174,7 @@ def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=Fa
     return x_out, bn_out
 
 
-def run_fc(lib, a, W_nk, ws, bias, a_scale=1.0, path=0):
+def run_fc(lib, a, W_nk, ws, bias, a_scale=1.0, path=0, split=False):
     a = np.ascontiguousarray(a, np.int8)
     B, K = a.shape
     N = W_nk.shape[0]
@@ -189,6 +189,15 @@ def run_fc(lib, a, W_nk, ws, bias, a_scale=1.0, path=0):
     d.a, d.w, d.ws, d.bias, d.out = da.ptr, dw.ptr, dws.ptr, db.ptr, do.ptr
     d.a_scale = a_scale
     d.path = path
+    wsp = None
+    if split:
+        n = lib.ffk_fc_workspace_bytes(C.byref(d))
+        assert n > 0
+        wsp = Dev(lib, nbytes=n)
+        check(lib, lib.ffk_zero(wsp.ptr, n, None))
+        d.workspace, d.workspace_bytes = wsp.ptr, n
     check(lib, lib.ffk_fc(C.byref(d), None))
     check(lib, lib.ffk_stream_sync(None))
+    if wsp is not None:
+        assert split_counters_zero(lib, wsp)
     return do.get(np.float32, (B, N))

@@ -256,16 +256,21 @@ def test_config2_microbench_layer(gpu_lib, oracle):
     assert np.abs(exp.astype(np.int32)).max() == 127       # the scale reaches full range
 
 
-@pytest.mark.parametrize("B,path", [(1, 0), (3, 1), (16, 0), (17, 0), (40, 2), (5, 2), (130, 0)])
-def test_fc_head(gpu_lib, oracle, B, path):
+@pytest.mark.parametrize("B,path,split", [(1, 0, False), (3, 1, False), (16, 0, False), (17, 0, False),
+                                          (40, 2, False), (5, 2, False), (130, 0, False),
+                                          (17, 0, True), (130, 0, True), (1024, 0, True)])
+def test_fc_head(gpu_lib, oracle, B, path, split):
+    """FC head in every path: matvec (b <= 16), one MFMA GEMM workgroup per
+    128x128 output tile, and split-K (several workgroups share a tile's K
+    reduction through the workspace)."""
     r = rng(500 + B + path)
     K, N = 25088, 512
     a = r.integers(-128, 128, size=(B, K), dtype=np.int8)
     W = r.integers(-127, 128, size=(N, K), dtype=np.int8)
     ws = r.uniform(1e-7, 1e-5, N).astype(F32)
     bias = r.normal(0, 0.05, N).astype(F32)
-    got = run_fc(gpu_lib, a, W, ws, bias, path=path)
-    for b in range(B):
+    got = run_fc(gpu_lib, a, W, ws, bias, path=path, split=split)
+    for b in (range(B) if B <= 130 else [0, 1, 127, 128, 500, B - 1]):
         assert np.array_equal(got[b], oracle.fc(a[b], W, ws, bias)), "face %d" % b
 
 

@@ -281,6 +281,24 @@ def main():
                 st["cout"], st["k"], st["s"], st["hin"]))
         log("b=1 sum of step times %.4f ms" % float(b1_steps.sum()))
 
+    # B=8 (the reference README's batched operating point),
+    # device-resident chain, ms per face
+    check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 8, d_out, stream), "b8 dev")
+    check(lib, lib.ffk_stream_sync(stream), "sync")
+    check(lib, lib.ffk_event_record(ev0, stream), "record")
+    for _ in range(50):
+        check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 8, d_out, stream), "b8 dev")
+    check(lib, lib.ffk_event_record(ev1, stream), "record")
+    check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
+    b8_ms_face = ms.value / 50 / 8
+    log("B=8: %.4f ms/face (%.3f ms per batch), device chain" % (b8_ms_face, b8_ms_face * 8))
+
+    # the single 256->256 3x3 layer microbench at N=64
+    from fastface_amd.layerbench import time_layer
+    cfg2 = time_layer(lib, 256, 256, 3, 1, 14, batch=64, iters=200, epi="prelu")
+    log("config 2 layer (N=64, 14x14, 256->256, PReLU): %.4f ms, %.1f TOP/s (%.1f%% of peak), %s"
+        % (cfg2["ms_per_launch"], cfg2["int8_tops"], 100 * cfg2["frac_of_peak"], cfg2["kernel"]))
+
     # Host-buffer (PCIe-inclusive) rates of the boundary: fp32 faces and the
     # uint8 RGB entry point (a quarter of the input bytes).  Reported beside
     # `value`, never as it.  Pageable numpy buffers, as a caller would pass.
@@ -390,6 +408,8 @@ def main():
         "host_rgb8_faces_s": round(host_rgb8, 1),
         "rgb8_resident_faces_s": round(dev_rgb8, 1),
         "b1_device_ms": round(b1_dev_ms, 4),
+        "b8_ms_per_face": round(b8_ms_face, 5),
+        "config2_layer": cfg2,
         "chain_int8_tops": round(chain_tops, 2),
         "chain_frac_of_int8_peak": round(chain_tops / PEAK_INT8_TOPS, 4),
         "stage_frac_of_int8_peak": stage_util,

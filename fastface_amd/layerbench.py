@@ -21,6 +21,105 @@ sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 import fastface_amd as fa  # noqa: E402
 
 
+def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=200, epi="prelu",
+               winograd=False, no_split=False):
+    """Mean launch time of one conv layer (HIP events on the launch stream)
+    over `iters` launches after 3 warm-up launches; frees what it allocates.
+    Inputs: seeded int8 U[-127,127] activations and weights (seed 1), ws
+    U[1e-3,1e-2], bias N(0,0.1), PReLU slope 0.25."""
+    pad = k // 2
+    ho = (hin + 2 * pad - k) // stride + 1
+    if not lib.ffk_conv_supported(cin, cout, k, k, stride, pad, hin, hin):
+        raise ValueError("unsupported layer geometry")
+    r = np.random.default_rng(1)
+    x = r.integers(-127, 128, size=(batch, hin, hin, cin), dtype=np.int8)
+    w = r.integers(-127, 128, size=(cout, cin, k, k), dtype=np.int8)
+    if winograd:
+        packed = np.empty(lib.ffk_winograd_packed_bytes(cin, cout), np.int8)
+        lib.ffk_pack_winograd_weights(w.ctypes.data, cout, cin, packed.ctypes.data)
+    else:
+        packed = np.empty(lib.ffk_conv_packed_bytes(cin, cout, k, k), np.int8)
+        lib.ffk_pack_conv_weights(w.ctypes.data, cout, cin, k, k, packed.ctypes.data)
+    P = np.zeros((fa.FFK_NPARAM, cout), np.float32)
+    P[fa.FFK_P_WS] = r.uniform(1e-3, 1e-2, cout)
+    P[fa.FFK_P_BIAS] = r.normal(0, 0.1, cout)
+    P[fa.FFK_P_SLOPE] = 0.25
+    P[fa.FFK_P_ADDSCALE] = 0.02
+    P[fa.FFK_P_INV] = 1.0 / 40.0
+    P[fa.FFK_P_BN_SIN] = 0.02
+    P[fa.FFK_P_BN_S] = 1.0
+    P[fa.FFK_P_BN_INV] = 50.0
+    held = []
+
+    def dev(arr=None, nbytes=None):
+        n = arr.nbytes if arr is not None else nbytes
+        p = lib.ffk_malloc(n)
+        if not p:
+            raise MemoryError(fa.last_error())
+        held.append(p)
+        if arr is not None:
+            lib.ffk_memcpy_h2d(p, arr.ctypes.data, n, None)
+        return p
+    n_out = batch * ho * ho * cout
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw = batch, cin, cout, k, k
+    d.stride, d.pad, d.hin, d.win = stride, pad, hin, hin
+    d.in_ = dev(x)
+    d.w = dev(packed)
+    d.params = dev(P)
+    d.flags = fa.FFK_EPI_BIAS | (fa.FFK_ALGO_WINOGRAD if winograd else 0)
+    if epi == "raw":
+        d.out_i32 = dev(nbytes=n_out * 4)
+    else:
+        d.out = dev(nbytes=n_out)
+    if epi.startswith("prelu"):
+        d.flags |= fa.FFK_EPI_PRELU
+    if epi == "prelu_le1":
+        d.flags |= fa.FFK_EPI_PRELU_LE1
+    if epi == "add_bn":
+        d.flags |= fa.FFK_EPI_ADD | fa.FFK_EPI_BN
+        d.add_src = dev(r.integers(-127, 128, size=n_out, dtype=np.int8))
+        d.out_bn = dev(nbytes=n_out)
+        lut = np.empty((cout, 256), np.int8)
+        rows = [np.ascontiguousarray(P[i]) for i in (fa.FFK_P_BN_SIN, fa.FFK_P_BN_S,
+                                                       fa.FFK_P_BN_O, fa.FFK_P_BN_INV)]
+        lib.ffk_make_bn_lut(rows[0].ctypes.data, rows[1].ctypes.data, rows[2].ctypes.data,
+                            rows[3].ctypes.data, cout, lut.ctypes.data)
+        d.bn_lut = dev(lut)
+    ws_bytes = 0 if no_split else lib.ffk_conv_workspace_bytes(C.byref(d))
+    if ws_bytes:
+        d.workspace, d.workspace_bytes = dev(nbytes=ws_bytes), ws_bytes
+        assert lib.ffk_zero(d.workspace, ws_bytes, None) == 0, fa.last_error()
+    stream = C.c_void_p()
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    lib.ffk_stream_create(C.byref(stream))
+    lib.ffk_event_create(C.byref(e0))
+    lib.ffk_event_create(C.byref(e1))
+    try:
+        variant = lib.ffk_conv_variant(C.byref(d))
+        for _ in range(3):
+            assert lib.ffk_conv(C.byref(d), stream) == 0, fa.last_error()
+        lib.ffk_event_record(e0, stream)
+        for _ in range(iters):
+            lib.ffk_conv(C.byref(d), stream)
+        lib.ffk_event_record(e1, stream)
+        ms = C.c_float()
+        assert lib.ffk_event_elapsed_ms(e0, e1, C.byref(ms)) == 0, fa.last_error()
+    finally:
+        lib.ffk_stream_sync(stream)
+        lib.ffk_event_destroy(e0)
+        lib.ffk_event_destroy(e1)
+        lib.ffk_stream_destroy(stream)
+        for p in held:
+            lib.ffk_free(p)
+    per = ms.value / iters
+    ops = 2.0 * batch * ho * ho * cout * k * k * cin
+    return {"layer": "%d->%d k%d s%d @%d" % (cin, cout, k, stride, hin), "batch": batch, "epi": epi,
+            "kernel": variant.decode() if variant else None, "split_ws_bytes": ws_bytes,
+            "ms_per_launch": round(per, 5), "int8_tops": round(ops / (per * 1e-3) / 1e12, 2),
+            "frac_of_peak": round(ops / (per * 1e-3) / 5e15, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--cin", type=int, default=256)
@@ -50,85 +149,12 @@ def main():
         lib.ffk_stream_sync(None)
         print(json.dumps({"copy_bytes": n, "iters": a.iters}), flush=True)
         return
-    pad = a.k // 2
-    ho = (a.hin + 2 * pad - a.k) // a.stride + 1
-    if not lib.ffk_conv_supported(a.cin, a.cout, a.k, a.k, a.stride, pad, a.hin, a.hin):
-        raise SystemExit("unsupported layer geometry")
-    r = np.random.default_rng(1)
-    x = r.integers(-127, 128, size=(a.batch, a.hin, a.hin, a.cin), dtype=np.int8)
-    w = r.integers(-127, 128, size=(a.cout, a.cin, a.k, a.k), dtype=np.int8)
-    if a.winograd:
-        packed = np.empty(lib.ffk_winograd_packed_bytes(a.cin, a.cout), np.int8)
-        lib.ffk_pack_winograd_weights(w.ctypes.data, a.cout, a.cin, packed.ctypes.data)
-    else:
-        packed = np.empty(lib.ffk_conv_packed_bytes(a.cin, a.cout, a.k, a.k), np.int8)
-        lib.ffk_pack_conv_weights(w.ctypes.data, a.cout, a.cin, a.k, a.k, packed.ctypes.data)
-    P = np.zeros((fa.FFK_NPARAM, a.cout), np.float32)
-    P[fa.FFK_P_WS] = r.uniform(1e-3, 1e-2, a.cout)
-    P[fa.FFK_P_BIAS] = r.normal(0, 0.1, a.cout)
-    P[fa.FFK_P_SLOPE] = 0.25
-    P[fa.FFK_P_ADDSCALE] = 0.02
-    P[fa.FFK_P_INV] = 1.0 / 40.0
-    P[fa.FFK_P_BN_SIN] = 0.02
-    P[fa.FFK_P_BN_S] = 1.0
-    P[fa.FFK_P_BN_INV] = 50.0
-
-    def dev(arr=None, nbytes=None):
-        n = arr.nbytes if arr is not None else nbytes
-        p = lib.ffk_malloc(n)
-        if arr is not None:
-            lib.ffk_memcpy_h2d(p, arr.ctypes.data, n, None)
-        return p
-    n_out = a.batch * ho * ho * a.cout
-    d = fa.ffk_conv_desc()
-    d.batch, d.cin, d.cout, d.kh, d.kw = a.batch, a.cin, a.cout, a.k, a.k
-    d.stride, d.pad, d.hin, d.win = a.stride, pad, a.hin, a.hin
-    d.in_ = dev(x)
-    d.w = dev(packed)
-    d.params = dev(P)
-    d.flags = fa.FFK_EPI_BIAS | (fa.FFK_ALGO_WINOGRAD if a.winograd else 0)
-    if a.epi == "raw":
-        d.out_i32 = dev(nbytes=n_out * 4)
-    else:
-        d.out = dev(nbytes=n_out)
-    if a.epi.startswith("prelu"):
-        d.flags |= fa.FFK_EPI_PRELU
-    if a.epi == "prelu_le1":
-        d.flags |= fa.FFK_EPI_PRELU_LE1
-    if a.epi == "add_bn":
-        d.flags |= fa.FFK_EPI_ADD | fa.FFK_EPI_BN
-        d.add_src = dev(r.integers(-127, 128, size=n_out, dtype=np.int8))
-        d.out_bn = dev(nbytes=n_out)
-        lut = np.empty((a.cout, 256), np.int8)
-        rows = [np.ascontiguousarray(P[i]) for i in (fa.FFK_P_BN_SIN, fa.FFK_P_BN_S,
-                                                       fa.FFK_P_BN_O, fa.FFK_P_BN_INV)]
-        lib.ffk_make_bn_lut(rows[0].ctypes.data, rows[1].ctypes.data, rows[2].ctypes.data,
-                            rows[3].ctypes.data, a.cout, lut.ctypes.data)
-        d.bn_lut = dev(lut)
-    ws_bytes = 0 if a.no_split else lib.ffk_conv_workspace_bytes(C.byref(d))
-    if ws_bytes:
-        d.workspace, d.workspace_bytes = dev(nbytes=ws_bytes), ws_bytes
-        assert lib.ffk_zero(d.workspace, ws_bytes, None) == 0, fa.last_error()
-    stream = C.c_void_p()
-    lib.ffk_stream_create(C.byref(stream))
-    for _ in range(3):
-        assert lib.ffk_conv(C.byref(d), stream) == 0, fa.last_error()
-    e0, e1 = C.c_void_p(), C.c_void_p()
-    lib.ffk_event_create(C.byref(e0))
-    lib.ffk_event_create(C.byref(e1))
-    lib.ffk_event_record(e0, stream)
-    for _ in range(a.iters):
-        lib.ffk_conv(C.byref(d), stream)
-    lib.ffk_event_record(e1, stream)
-    ms = C.c_float()
-    assert lib.ffk_event_elapsed_ms(e0, e1, C.byref(ms)) == 0, fa.last_error()
-    per = ms.value / a.iters
-    ops = 2.0 * a.batch * ho * ho * a.cout * a.k * a.k * a.cin
-    print(json.dumps({"layer": "%d->%d k%d s%d @%d" % (a.cin, a.cout, a.k, a.stride, a.hin),
-                      "batch": a.batch, "epi": a.epi, "split_ws_bytes": ws_bytes,
-                      "ms_per_launch": round(per, 5),
-                      "int8_tops": round(ops / (per * 1e-3) / 1e12, 2),
-                      "frac_of_peak": round(ops / (per * 1e-3) / 5e15, 4)}), flush=True)
+    try:
+        res = time_layer(lib, a.cin, a.cout, a.k, a.stride, a.hin, a.batch, a.iters, a.epi,
+                         winograd=a.winograd, no_split=a.no_split)
+    except ValueError as e:
+        raise SystemExit(str(e))
+    print(json.dumps(res), flush=True)
 
 
 if __name__ == "__main__":

@@ -749,7 +749,8 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     constexpr int B_BYTES = BN * DMA_KB;
     constexpr int B_LD = B_BYTES / (NT * 16);                // weight loads per thread and step
     constexpr int NSTB = 3;                                  // weight ring depth (9 % 3 == 0)
-    constexpr int ZERO_OFF = 2 * PATCH_BYTES;                // 1 KB of zeros
+    constexpr int NPB = CSTEPS > 1 ? 2 : 1;                  // patch buffers (one run: no double buffer)
+    constexpr int ZERO_OFF = NPB * PATCH_BYTES;              // 1 KB of zeros
     constexpr int RING_OFF = ZERO_OFF + 1024;
     constexpr int LDS_K = RING_OFF + NSTB * B_BYTES;
     constexpr int LDS_E = NW * wave_tile_bytes<MI, NJ>() + BN * FF_LUT_PITCH;
@@ -1194,12 +1195,13 @@ constexpr launch_fn split_launch() {
 
 // 3x3 stride-1 layers: the patch kernel (WM, WN, MI, NJ, WPE).  8 waves of
 // 2x2 MFMA tiles -> 256x128, two workgroups per CU; Cout = 64: 4 waves ->
-// 256x64, two workgroups per CU (the patch double buffer sets the LDS size).
+// 256x64 and one 64-channel run, so a single patch buffer: three workgroups
+// per CU at 56x56 and at 112x112.
 #ifndef FF_TPATCH
 #define FF_TPATCH 4, 2, 2, 2, 4
 #endif
 #ifndef FF_TPATCH64
-#define FF_TPATCH64 4, 1, 2, 2, 2
+#define FF_TPATCH64 4, 1, 2, 2, 3
 #endif
 // Cout >= 256 (stages 3-4)
 #ifndef FF_TPATCH_BIG
@@ -1225,6 +1227,9 @@ constexpr launch_fn split_launch() {
                 FF_TPATCH_BIG)
 #define FF_P64(CIN, COUT, H, SPLIT) FF_PENTRY_K(CIN, COUT, H, SPLIT, nullptr, FF_TPATCH64)
 #endif
+#ifndef FF_P112
+#define FF_P112(CIN, COUT, H, SPLIT) FF_P64(CIN, COUT, H, SPLIT)
+#endif
 
 // split: how many workgroups share the K stages of one small-batch tile (1:
 // never split).  Only the long K chains of stages 3-4 (18 or 36 stages of
@@ -1232,7 +1237,7 @@ constexpr launch_fn split_launch() {
 // workgroups.
 const ConvEntry kConvTable[] = {
     {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem, 1, nullptr, nullptr, "stem"},
-    FF_C64(64, 64, 3, 1, 112, 1),
+    FF_P112(64, 64, 112, 1),
     FF_C64(64, 64, 3, 2, 112, 1),
     FF_C64(64, 64, 1, 2, 112, 1),
     FF_P64(64, 64, 56, 1),

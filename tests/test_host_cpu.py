@@ -162,7 +162,7 @@ def test_conv_variant_policy():
     assert variant(256, 256, 3, 1, 14, 1) == "staged128"          # no workspace given
     assert variant(256, 256, 3, 1, 14, 1, ws=1 << 30) == "splitk"
     assert variant(64, 64, 3, 1, 56, 1) == "patch"                # Cout 64: one variant
-    assert variant(64, 64, 3, 1, 112, 1) == "direct"
+    assert variant(64, 64, 3, 1, 112, 1) == "patch"               # one 64-channel run
     assert variant(96, 64, 3, 1, 112, 1) is None
     assert lib.ffk_conv_variant(None) is None
 

@@ -1230,6 +1230,11 @@ constexpr launch_fn split_launch() {
 #ifndef FF_P112
 #define FF_P112(CIN, COUT, H, SPLIT) FF_P64(CIN, COUT, H, SPLIT)
 #endif
+// 64 -> 128 at 56x56 (one 64-channel run): the patch kernel's single-buffer
+// LDS footprint fits two 256x128 workgroups per CU
+#ifndef FF_P56W
+#define FF_P56W(CIN, COUT, H, SPLIT) FF_P(CIN, COUT, H, SPLIT)
+#endif
 
 // split: how many workgroups share the K stages of one small-batch tile (1:
 // never split).  Only the long K chains of stages 3-4 (18 or 36 stages of
@@ -1241,7 +1246,7 @@ const ConvEntry kConvTable[] = {
     FF_C64(64, 64, 3, 2, 112, 1),
     FF_C64(64, 64, 1, 2, 112, 1),
     FF_P64(64, 64, 56, 1),
-    FF_C128(64, 128, 3, 1, 56, 1),
+    FF_P56W(64, 128, 56, 1),
     FF_C128(128, 128, 3, 2, 56, 1),
     FF_C128(64, 128, 1, 2, 56, 1),
     FF_P(128, 128, 28, 1),

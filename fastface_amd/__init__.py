@@ -24,6 +24,7 @@ FFK_EPI_PRELU, FFK_EPI_ADD, FFK_EPI_BN, FFK_EPI_BIAS, FFK_EPI_INSCALE = 1, 2, 4,
 FFK_IN_RGB8 = 0x20
 FFK_EPI_PRELU_LE1 = 0x40
 FFK_ALGO_WINOGRAD = 0x80
+FFK_OUT_X_EVEN = 0x100
 (FFK_P_WS, FFK_P_BIAS, FFK_P_SLOPE, FFK_P_ADDSCALE, FFK_P_INV, FFK_P_BN_SIN, FFK_P_BN_S,
  FFK_P_BN_O, FFK_P_BN_INV, FFK_NPARAM) = range(10)
 

@@ -107,10 +107,28 @@ __device__ __forceinline__ EpiParams<NJ> load_epi_params(const ConvArgs& a, int 
     return P;
 }
 
+// Where output pixel m's X row goes: out + m*COUT, or with FFK_OUT_X_EVEN
+// (HO x WO images, both even) its slot in the [HO/2][WO/2] tensor of the
+// even-row, even-column pixels, and null for every other pixel.
+template <int COUT, int HO, int WO>
+__device__ __forceinline__ int8_t* x_row(const ConvArgs& a, int m) {
+    if constexpr (HO % 2 == 0 && WO % 2 == 0) {
+        if (a.flags & FFK_OUT_X_EVEN) {
+            const int img = m / (HO * WO);
+            const int rem = m - img * (HO * WO);
+            const int oh = rem / WO, ow = rem - oh * WO;
+            if ((oh | ow) & 1) return nullptr;
+            return a.out + (((size_t)img * (HO / 2) + (oh >> 1)) * (WO / 2) + (ow >> 1)) * COUT;
+        }
+    }
+    return a.out + (size_t)m * COUT;
+}
+
 // PRELU: 0 none, 1 f < 0 ? f*slope : f, 2 max(f, f*slope) (the same values
 // when every slope is at most 1 and f is never infinite: FFK_EPI_PRELU_LE1).
 // INSC: f = f * in_scale first (FFW2/FFW3 models; FFW4 skips the multiply).
-template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC>
+// HO x WO: output image size (FFK_OUT_X_EVEN addressing).
+template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC, int HO, int WO>
 __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                             const EpiParams<NJ>& prm, int mrow0, int ncol0, int8_t* Ws,
                                             const int8_t* Lw) {
@@ -167,7 +185,10 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
         const int m = mrow0 + row;
         const v4i v = *reinterpret_cast<const v4i*>(Ws + row * P + ch * 16);
         if (m < a.M) {
-            if (a.out) *reinterpret_cast<v4i*>(a.out + (size_t)m * COUT + ncol0 + ch * 16) = v;
+            if (a.out) {
+                int8_t* xo = x_row<COUT, HO, WO>(a, m);
+                if (xo) *reinterpret_cast<v4i*>(xo + ncol0 + ch * 16) = v;
+            }
             if (BN2) {
                 const int8_t* L = Lw + (ch * 16) * FF_LUT_PITCH + 128;
                 v4i o;
@@ -228,32 +249,32 @@ __device__ __forceinline__ void wave_epi_wide(const v16i (&acc)[MI][NJ], const C
 }
 
 // int8 epilogue variants dispatched on the (uniform) flags, parameters given
-template <int COUT, int MI, int NJ, bool INSC>
+template <int COUT, int MI, int NJ, bool INSC, int HO, int WO>
 __device__ __forceinline__ void wave_epilogue_f(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                                 const EpiParams<NJ>& P, int mrow0, int ncol0, int8_t* Ws,
                                                 const int8_t* Lw) {
     const bool le1 = !INSC && (a.flags & FFK_EPI_PRELU_LE1);
     switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN)) {
-    case 0: wave_epi_i8<COUT, MI, NJ, 0, false, false, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case 0: wave_epi_i8<COUT, MI, NJ, 0, false, false, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
     case FFK_EPI_PRELU:
-        if (le1) wave_epi_i8<COUT, MI, NJ, 2, false, false, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw);
-        else wave_epi_i8<COUT, MI, NJ, 1, false, false, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw);
+        if (le1) wave_epi_i8<COUT, MI, NJ, 2, false, false, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw);
+        else wave_epi_i8<COUT, MI, NJ, 1, false, false, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw);
         break;
-    case FFK_EPI_ADD: wave_epi_i8<COUT, MI, NJ, 0, true, false, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_BN: wave_epi_i8<COUT, MI, NJ, 0, false, true, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_ADD: wave_epi_i8<COUT, MI, NJ, 0, true, false, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_BN: wave_epi_i8<COUT, MI, NJ, 0, false, true, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
     case FFK_EPI_PRELU | FFK_EPI_BN:
-        if (le1) wave_epi_i8<COUT, MI, NJ, 2, false, true, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw);
-        else wave_epi_i8<COUT, MI, NJ, 1, false, true, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw);
+        if (le1) wave_epi_i8<COUT, MI, NJ, 2, false, true, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw);
+        else wave_epi_i8<COUT, MI, NJ, 1, false, true, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw);
         break;
     case FFK_EPI_ADD | FFK_EPI_BN:
-        wave_epi_i8<COUT, MI, NJ, 0, true, true, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+        wave_epi_i8<COUT, MI, NJ, 0, true, true, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
     case FFK_EPI_PRELU | FFK_EPI_ADD:
-        wave_epi_i8<COUT, MI, NJ, 1, true, false, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    default: wave_epi_i8<COUT, MI, NJ, 1, true, true, INSC>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+        wave_epi_i8<COUT, MI, NJ, 1, true, false, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    default: wave_epi_i8<COUT, MI, NJ, 1, true, true, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
     }
 }
 
-template <int COUT, int MI, int NJ>
+template <int COUT, int MI, int NJ, int HO, int WO>
 __device__ __forceinline__ void wave_epilogue_p(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                                 const EpiParams<NJ>& P, int mrow0, int ncol0, int8_t* Ws,
                                                 const int8_t* Lw) {
@@ -261,11 +282,11 @@ __device__ __forceinline__ void wave_epilogue_p(const v16i (&acc)[MI][NJ], const
         wave_epi_wide<COUT, MI, NJ, false>(acc, a, mrow0, ncol0);
         return;
     }
-    if (a.flags & FFK_EPI_INSCALE) wave_epilogue_f<COUT, MI, NJ, true>(acc, a, P, mrow0, ncol0, Ws, Lw);
-    else wave_epilogue_f<COUT, MI, NJ, false>(acc, a, P, mrow0, ncol0, Ws, Lw);
+    if (a.flags & FFK_EPI_INSCALE) wave_epilogue_f<COUT, MI, NJ, true, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw);
+    else wave_epilogue_f<COUT, MI, NJ, false, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw);
 }
 
-template <int COUT, int MI, int NJ, bool FC = false>
+template <int COUT, int MI, int NJ, int HO, int WO, bool FC = false>
 __device__ __forceinline__ void wave_epilogue(const v16i (&acc)[MI][NJ], const ConvArgs& a, int mrow0,
                                               int ncol0, int8_t* Ws, const int8_t* Lw) {
     if (FC) {
@@ -276,7 +297,7 @@ __device__ __forceinline__ void wave_epilogue(const v16i (&acc)[MI][NJ], const C
         wave_epi_wide<COUT, MI, NJ, false>(acc, a, mrow0, ncol0);
         return;
     }
-    wave_epilogue_p<COUT, MI, NJ>(acc, a, load_epi_params<COUT, NJ>(a, ncol0), mrow0, ncol0, Ws, Lw);
+    wave_epilogue_p<COUT, MI, NJ, HO, WO>(acc, a, load_epi_params<COUT, NJ>(a, ncol0), mrow0, ncol0, Ws, Lw);
 }
 
 // BN tables of channels [c0, c0 + nch) -> LDS (pitch FF_LUT_PITCH)
@@ -530,7 +551,7 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
         __syncthreads();
     }
     // the FC head runs this kernel as a 1x1 "conv" over a 1x1 image
-    wave_epilogue<COUT, MI, NJ, HIN == 1 && WIN == 1>(acc, a, m0 + wm * WTM, tn * BN + wn * WTN, Ws,
+    wave_epilogue<COUT, MI, NJ, HOUT, WOUT, HIN == 1 && WIN == 1>(acc, a, m0 + wm * WTM, tn * BN + wn * WTN, Ws,
                                 Ls + (wn * WTN) * FF_LUT_PITCH);
 }
 
@@ -705,7 +726,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
         load_bn_lut<NT>(Ls, a.bn_lut, tn * BN, BN);
         __syncthreads();
     }
-    wave_epilogue<COUT, MI, NJ>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
+    wave_epilogue<COUT, MI, NJ, HOUT, WOUT>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
                                 Ls + (wn * NJ * 32) * FF_LUT_PITCH);
 }
 
@@ -900,7 +921,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
         load_bn_lut<NT>(Ls, a.bn_lut, tn * BN, BN);
         __syncthreads();
     }
-    wave_epilogue<COUT, MI, NJ>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
+    wave_epilogue<COUT, MI, NJ, H, W>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
                                 Ls + (wn * NJ * 32) * FF_LUT_PITCH);
 }
 
@@ -1041,14 +1062,14 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
         const int mw = m0 + wave * 32;
         const int pf = a.flags & FFK_EPI_PRELU ? (a.flags & FFK_EPI_PRELU_LE1 ? 2 : 1) : 0;
         if (a.out_i32) wave_epi_wide<COUT, 1, 2, false>(acc, a, mw, 0);
-        else if (a.flags & FFK_EPI_INSCALE) wave_epilogue_f<COUT, 1, 2, true>(acc, a, prm, mw, 0, Ws, Ls);
+        else if (a.flags & FFK_EPI_INSCALE) wave_epilogue_f<COUT, 1, 2, true, H, W>(acc, a, prm, mw, 0, Ws, Ls);
         else switch (pf + (a.flags & FFK_EPI_BN ? 3 : 0)) {
-        case 0: wave_epi_i8<COUT, 1, 2, 0, false, false, false>(acc, a, prm, mw, 0, Ws, Ls); break;
-        case 1: wave_epi_i8<COUT, 1, 2, 1, false, false, false>(acc, a, prm, mw, 0, Ws, Ls); break;
-        case 2: wave_epi_i8<COUT, 1, 2, 2, false, false, false>(acc, a, prm, mw, 0, Ws, Ls); break;
-        case 3: wave_epi_i8<COUT, 1, 2, 0, false, true, false>(acc, a, prm, mw, 0, Ws, Ls); break;
-        case 4: wave_epi_i8<COUT, 1, 2, 1, false, true, false>(acc, a, prm, mw, 0, Ws, Ls); break;
-        default: wave_epi_i8<COUT, 1, 2, 2, false, true, false>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case 0: wave_epi_i8<COUT, 1, 2, 0, false, false, false, H, W>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case 1: wave_epi_i8<COUT, 1, 2, 1, false, false, false, H, W>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case 2: wave_epi_i8<COUT, 1, 2, 2, false, false, false, H, W>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case 3: wave_epi_i8<COUT, 1, 2, 0, false, true, false, H, W>(acc, a, prm, mw, 0, Ws, Ls); break;
+        case 4: wave_epi_i8<COUT, 1, 2, 1, false, true, false, H, W>(acc, a, prm, mw, 0, Ws, Ls); break;
+        default: wave_epi_i8<COUT, 1, 2, 2, false, true, false, H, W>(acc, a, prm, mw, 0, Ws, Ls); break;
         }
     }
 }
@@ -1258,6 +1279,12 @@ const ConvEntry kConvTable[] = {
     FF_CBIG(512, 512, 3, 2, 14, 9),
     FF_CBIG(256, 512, 1, 2, 14, 1),
     FF_PB(512, 512, 7, 9),
+    // the 1x1 shortcuts over a block input stored at its even pixels only
+    // (FFK_OUT_X_EVEN): stride 1 over the compact tensor
+    FF_C64(64, 64, 1, 1, 56, 1),
+    FF_C128(64, 128, 1, 1, 28, 1),
+    FF_CBIG(128, 256, 1, 1, 14, 1),
+    FF_CBIG(256, 512, 1, 1, 7, 1),
 };
 
 const ConvEntry* find_conv(int cin, int cout, int kh, int kw, int stride, int pad, int hin, int win) {
@@ -1452,6 +1479,16 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
         ffk_set_error("conv: missing pointer for the requested flags%s%s", nullptr, nullptr);
         return FFK_ERR_ARG;
     }
+    const bool x_even = (d->flags & FFK_OUT_X_EVEN) != 0;
+    if (x_even) {
+        const int hout = (d->hin + 2 * d->pad - d->kh) / d->stride + 1;
+        const int wout = (d->win + 2 * d->pad - d->kw) / d->stride + 1;
+        if (raw || !d->out || (hout & 1) || (wout & 1)) {
+            ffk_set_error("conv: FFK_OUT_X_EVEN needs an int8 output X of even height and width%s%s",
+                          nullptr, nullptr);
+            return FFK_ERR_ARG;
+        }
+    }
     if (M == 0) return FFK_OK;
     if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_conv(d, (hipStream_t)stream);
     ConvArgs a = {};
@@ -1468,7 +1505,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     a.out_bn = d->out_bn;
     a.out_i32 = d->out_i32;
     a.flags = d->flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_BIAS | FFK_EPI_INSCALE |
-                          FFK_EPI_PRELU_LE1 |
+                          FFK_EPI_PRELU_LE1 | FFK_OUT_X_EVEN |
                           FFK_IN_RGB8);
     a.in_scale = d->in_scale;
     // The direct-to-LDS kernels address the int8 input with 32-bit offsets:
@@ -1484,7 +1521,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
         if (!stem) as.in = a.in + (size_t)b0 * in_img;
         const size_t o = (size_t)b0 * px_out * d->cout;
         if (a.add_src) as.add_src = a.add_src + o;
-        if (a.out) as.out = a.out + o;
+        if (a.out) as.out = a.out + (x_even ? o / 4 : o);     // even/even pixels: a quarter
         if (a.out_bn) as.out_bn = a.out_bn + o;
         if (a.out_i32) as.out_i32 = a.out_i32 + o;
         as.M = (int)ms;

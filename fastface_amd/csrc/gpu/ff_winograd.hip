@@ -269,6 +269,7 @@ __global__ __launch_bounds__(256, 2) void wino_gemm_kernel(WinoArgs a) {
     auto chunk_lds = [&](int row, int pr, int k) { return (row * 4 + pr * 2 + (k >> 2)) * PX_PITCH + (k & 3) * 16; };
     const bool add = (a.flags & FFK_EPI_ADD) != 0;
     const bool bn = (a.flags & FFK_EPI_BN) != 0;
+    const bool x_even = (a.flags & FFK_OUT_X_EVEN) != 0;
     if (bn)
         for (int i = tid; i < WC * 16; i += 256)
             *reinterpret_cast<v4i*>(Ls + (i >> 4) * LUT_PITCH + (i & 15) * 16) =
@@ -298,7 +299,12 @@ __global__ __launch_bounds__(256, 2) void wino_gemm_kernel(WinoArgs a) {
         if (blk >= a.n_tiles) continue;
         const size_t off = pix(blk, pr * 2) * WC + k * 16;
         const v4i v = *reinterpret_cast<const v4i*>(T8 + chunk_lds(row, pr, k));
-        if (a.out) *reinterpret_cast<v4i*>(a.out + off) = v;
+        if (a.out) {
+            // FFK_OUT_X_EVEN keeps pixel (0, 0) of each 2x2 block (output row
+            // pr = 0, chunks 0-3); the compact tensor's pixel index is `blk`
+            if (!x_even) *reinterpret_cast<v4i*>(a.out + off) = v;
+            else if (pr == 0 && k < 4) *reinterpret_cast<v4i*>(a.out + (size_t)blk * WC + k * 16) = v;
+        }
         if (bn) {
             const int c0 = (k & 3) * 16;                   // first channel of the chunk
             const int8_t* L = Ls + c0 * LUT_PITCH + 128;
@@ -348,7 +354,8 @@ int launch(const ffk_conv_desc* d, hipStream_t s) {
         a.params = d->params;
         a.add_src = d->add_src ? d->add_src + pix0 * WC : nullptr;
         a.bn_lut = d->bn_lut;
-        a.out = d->out ? d->out + pix0 * WC : nullptr;
+        // FFK_OUT_X_EVEN: one pixel of four (the top left of each 2x2 block)
+        a.out = d->out ? d->out + ((d->flags & FFK_OUT_X_EVEN) ? pix0 / 4 : pix0) * WC : nullptr;
         a.out_bn = d->out_bn ? d->out_bn + pix0 * WC : nullptr;
         a.out_i32 = d->out_i32 ? d->out_i32 + pix0 * WC : nullptr;
         a.n_tiles = nb * per_img;

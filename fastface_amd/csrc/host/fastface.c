@@ -165,12 +165,25 @@ static int8_t* tensor_ptr(FastFace* ff, int t)
 
 /* conv descriptor of step s (pointers are NULL while no activations exist);
  * fmt 1: the input layer reads uint8 RGB pixels through the input table */
+/* A conv over a tensor stored at its even pixels only (a 1x1 stride-2
+ * shortcut) runs at stride 1 over the compact tensor. */
+static int reads_even(const FastFace* ff, const FfStep* st)
+{
+    return st->kind == 1 && st->t_in > FF_T_INPUT && ff->plan.tensors[st->t_in].even;
+}
+
+static int writes_even(const FastFace* ff, const FfStep* st)
+{
+    return st->kind == 1 && st->t_out >= 0 && ff->plan.tensors[st->t_out].even;
+}
+
 static void step_desc(FastFace* ff, int s, int batch, int fmt, ffk_conv_desc* d)
 {
     const FfStep* st = &ff->plan.steps[s];
     memset(d, 0, sizeof *d);
     d->batch = batch; d->cin = st->cin; d->cout = st->cout; d->kh = st->kh; d->kw = st->kw;
     d->stride = st->stride; d->pad = st->pad; d->hin = st->hin; d->win = st->win;
+    if (reads_even(ff, st)) { d->stride = 1; d->hin = st->hin / 2; d->win = st->win / 2; }
     if (st->t_in == FF_T_INPUT) {
         d->in = NULL;
         d->io = ff->d_io;
@@ -187,7 +200,8 @@ static void step_desc(FastFace* ff, int s, int batch, int fmt, ffk_conv_desc* d)
         d->out_bn = tensor_ptr(ff, st->t_bn);
     }
     if (st->flags & FFK_EPI_BN) d->bn_lut = ff->d_weights + st->lut_off;
-    d->flags = st->flags | ((fmt && st->t_in == FF_T_INPUT) ? FFK_IN_RGB8 : 0);
+    d->flags = st->flags | ((fmt && st->t_in == FF_T_INPUT) ? FFK_IN_RGB8 : 0) |
+               (writes_even(ff, st) ? FFK_OUT_X_EVEN : 0);
     if (ff->algo == FASTFACE_CONV_WINOGRAD_F23 && st->wino_off != (size_t)-1) {
         d->flags |= FFK_ALGO_WINOGRAD;
         d->w = ff->d_weights + st->wino_off;
@@ -429,8 +443,12 @@ int fastface_get_step(const FastFace* ff, int s, fastface_step_info* info)
     info->op_last = st->op_last;
     if (st->kind == 1) {
         info->cin = st->cin; info->cout = st->cout; info->kh = st->kh; info->kw = st->kw;
-        info->stride = st->stride; info->pad = st->pad; info->hin = st->hin; info->win = st->win;
-        info->hout = st->hout; info->wout = st->wout; info->flags = st->flags;
+        /* the geometry and flags of the launch (step_desc) */
+        const int ev_in = reads_even(ff, st), ev_out = writes_even(ff, st);
+        info->stride = ev_in ? 1 : st->stride; info->pad = st->pad;
+        info->hin = ev_in ? st->hin / 2 : st->hin; info->win = ev_in ? st->win / 2 : st->win;
+        info->hout = st->hout; info->wout = st->wout;
+        info->flags = st->flags | (ev_out ? FFK_OUT_X_EVEN : 0);
         if (ff->algo == FASTFACE_CONV_WINOGRAD_F23 && st->wino_off != (size_t)-1)
             info->flags |= FFK_ALGO_WINOGRAD;
         info->stores_x = st->t_out >= 0;
@@ -440,7 +458,8 @@ int fastface_get_step(const FastFace* ff, int s, fastface_step_info* info)
         double pix_in = (st->kh == 1) ? pix_out : (double)st->hin * st->win;
         double in_bytes = pix_in * st->cin * (st->cin == 3 ? 4.0 : 1.0);
         double out_b = pix_out * st->cout;
-        info->act_bytes_per_face = in_bytes + out_b * ((st->t_out >= 0) + (st->t_bn >= 0) + (st->t_add >= 0));
+        const double x_b = st->t_out < 0 ? 0.0 : (ev_out ? 0.25 : 1.0);
+        info->act_bytes_per_face = in_bytes + out_b * (x_b + (st->t_bn >= 0) + (st->t_add >= 0));
         info->weight_bytes = (double)ffk_conv_packed_bytes(st->cin, st->cout, st->kh, st->kw);
     } else {
         info->cin = st->fc_k; info->cout = st->fc_n; info->kh = info->kw = 1; info->stride = 1;

@@ -45,6 +45,9 @@ typedef struct {
     int def_step, last_use;     /* -1 when never read */
     int buf;                    /* buffer slot, -1 if none */
     int op;                     /* reference op index after which A holds it */
+    int even;                   /* stored at its even-row, even-column pixels
+                                   only (FFK_OUT_X_EVEN): every reader is a
+                                   1x1 stride-2 conv, run at stride 1 */
 } FfTensor;
 
 typedef struct {

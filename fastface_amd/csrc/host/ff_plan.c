@@ -51,7 +51,7 @@ static int new_tensor(Builder* b, int C, int H, int W, int op)
     }
     FfTensor* t = &p->tensors[p->n_tensors];
     t->C = C; t->H = H; t->W = W; t->def_step = p->n_steps; t->last_use = -1; t->buf = -1;
-    t->op = op;
+    t->op = op; t->even = 0;
     return p->n_tensors++;
 }
 
@@ -337,7 +337,9 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
 
 int ff_plan_assign_buffers(FfPlan* p, int keep_all)
 {
-    for (int t = 0; t < p->n_tensors; t++) { p->tensors[t].last_use = -1; p->tensors[t].buf = -1; }
+    for (int t = 0; t < p->n_tensors; t++) {
+        p->tensors[t].last_use = -1; p->tensors[t].buf = -1; p->tensors[t].even = 0;
+    }
     for (int s = 0; s < p->n_steps; s++) {
         const FfStep* st = &p->steps[s];
         if (st->t_in >= 0) p->tensors[st->t_in].last_use = s;
@@ -354,6 +356,27 @@ int ff_plan_assign_buffers(FfPlan* p, int keep_all)
         if (st->kind != 1) continue;
         st->t_out = st->t_x;
         if (st->t_bn >= 0 && p->tensors[st->t_x].last_use < 0 && !keep_all) st->t_out = -1;
+    }
+    /* A stored tensor whose every reader is a 1x1 stride-2 pad-0 conv (the
+     * downsample shortcut of the next stage's first block, the only reader of
+     * a stage's output X) is stored at its even pixels only: those readers
+     * see nothing else, and run as 1x1 stride-1 convs over the compact tensor.
+     * keep_all (debug reads) keeps every tensor whole. */
+    for (int s = 0; s < p->n_steps && !keep_all; s++) {
+        const FfStep* st = &p->steps[s];
+        if (st->kind != 1 || st->t_out < 0) continue;
+        FfTensor* T = &p->tensors[st->t_out];
+        if ((T->H & 1) || (T->W & 1)) continue;
+        int readers = 0, ok = 1;
+        for (int r = s + 1; r < p->n_steps && ok; r++) {
+            const FfStep* rd = &p->steps[r];
+            if (rd->t_add == st->t_out) ok = 0;
+            if (rd->t_in != st->t_out) continue;
+            readers++;
+            ok = rd->kind == 1 && rd->kh == 1 && rd->kw == 1 && rd->stride == 2 && rd->pad == 0 &&
+                 ffk_conv_supported(rd->cin, rd->cout, 1, 1, 1, 0, T->H / 2, T->W / 2);
+        }
+        T->even = ok && readers > 0;
     }
     int* free_list = (int*)malloc((size_t)(p->n_tensors + 1) * sizeof(int));
     int n_free = 0, n_buf = 0;

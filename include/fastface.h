@@ -93,8 +93,10 @@ int fastface_set_conv_algo(FastFace* ff, int algo);
 typedef struct {
     int kind;                 /* 1 conv, 2 FC                                   */
     int op_first, op_last;    /* reference op indices this launch covers        */
-    int cin, cout, kh, kw, stride, pad, hin, win, hout, wout;
-    int flags;                /* FFK_EPI_* of fastface_kernels.h                */
+    int cin, cout, kh, kw, stride, pad, hin, win, hout, wout;   /* as launched:
+                                 a 1x1 stride-2 shortcut over a tensor stored
+                                 at its even pixels runs at stride 1, hin/2  */
+    int flags;                /* FFK_EPI_* / FFK_OUT_X_EVEN of the launch       */
     int stores_x;             /* writes the pre-BN tensor                       */
     double ops_per_face;      /* 2 * multiply-accumulates                       */
     double act_bytes_per_face;/* activation bytes read + written, algorithmic   */

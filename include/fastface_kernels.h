@@ -78,6 +78,16 @@ typedef struct { const float* in; float* out; } ffk_io;
                                    so the kernel may take PReLU as
                                    max(f, f*slope) -- the same values, one
                                    operation fewer (ffk_prelu_le1_ok)        */
+#define FFK_OUT_X_EVEN   0x100  /* `out` receives X only at the output pixels
+                                   of even row and even column, as int8
+                                   [batch, hout/2, wout/2, cout] (hout and
+                                   wout even; out_bn stays full size).  The
+                                   one reader of a block input that feeds
+                                   only a 1x1 stride-2 shortcut reads exactly
+                                   these pixels, so it then runs as a 1x1
+                                   stride-1 conv over the compact tensor.  No
+                                   reference counterpart: the reference
+                                   stores the whole tensor. */
 
 /* rows of the per-layer parameter block, each `cout` floats (device) */
 enum {
@@ -104,7 +114,8 @@ typedef struct {
     const float*   params;   /* [FFK_NPARAM][cout]                            */
     const int8_t*  add_src;  /* FFK_EPI_ADD: int8 [batch,hout,wout,cout]      */
     const int8_t*  bn_lut;   /* FFK_EPI_BN: [cout][256] from ffk_make_bn_lut  */
-    int8_t*        out;      /* int8 output X, or NULL                        */
+    int8_t*        out;      /* int8 output X (FFK_OUT_X_EVEN: its even-row,
+                                even-column pixels only), or NULL             */
     int8_t*        out_bn;   /* FFK_EPI_BN: BN(X), or NULL                    */
     int32_t*       out_i32;  /* non-NULL: store raw int32 accumulators only   */
     int            flags;

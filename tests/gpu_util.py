@@ -107,10 +107,12 @@ def pack_winograd(lib, w_oihw):
 
 def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=False,
              want_x=True, want_bn=False, in_inv=None, in_scale=1.0, split=True, in_lut=None,
-             winograd=False, workspace=None):
+             winograd=False, workspace=None, x_even=False):
     """One ffk_conv call; returns int32 acc (raw) or (X, BN(X)) int8 arrays.
     split: give the call the split-K workspace it asks for (small batches take
-    the split path); False: no workspace (whole-K tiling)."""
+    the split path); False: no workspace (whole-K tiling).
+    x_even: FFK_OUT_X_EVEN -- X comes back as [B, Ho/2, Wo/2, Cout] (its
+    even-row, even-column pixels), from a buffer of exactly that size."""
     B, H, W, cin = x.shape
     cout, _, kh, kw = w_oihw.shape
     ho = (H + 2 * pad - kh) // stride + 1
@@ -150,11 +152,13 @@ def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=Fa
         d.out_i32 = do.ptr
     else:
         if want_x:
-            dox = Dev(lib, nbytes=n_out); keep.append(dox)
+            dox = Dev(lib, nbytes=n_out // 4 if x_even else n_out); keep.append(dox)
             d.out = dox.ptr
         if want_bn:
             dob = Dev(lib, nbytes=n_out); keep.append(dob)
             d.out_bn = dob.ptr
+    if x_even:
+        flags |= fa.FFK_OUT_X_EVEN
     d.flags = flags
     d.in_scale = in_scale
     ws = workspace if workspace is not None else (conv_workspace(lib, d) if split else None)
@@ -169,7 +173,8 @@ def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=Fa
         assert split_counters_zero(lib, ws)
     if raw:
         return do.get(np.int32, (B, ho, wo, cout))
-    x_out = dox.get(np.int8, (B, ho, wo, cout)) if want_x else None
+    xshape = (B, ho // 2, wo // 2, cout) if x_even else (B, ho, wo, cout)
+    x_out = dox.get(np.int8, xshape) if want_x else None
     bn_out = dob.get(np.int8, (B, ho, wo, cout)) if want_bn else None
     return x_out, bn_out
 

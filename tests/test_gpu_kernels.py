@@ -386,3 +386,164 @@ def test_winograd_and_splitk_share_a_workspace(gpu_lib, oracle):
         got2 = run_conv(gpu_lib, x2, w2, 1, 1, raw=True, workspace=ws)
         assert np.array_equal(got1, oracle.conv_i32(x1, w1, 1, 1))
         assert np.array_equal(got2, oracle.conv_i32(x2, w2, 1, 1))
+
+
+# ---- X stored at its even pixels only (FFK_OUT_X_EVEN), and the 1x1 stride-1
+# shortcuts that read it in place of the 1x1 stride-2 ones over the whole X ----
+SHORTCUT_S1 = [(64, 64, 56), (64, 128, 28), (128, 256, 14), (256, 512, 7)]
+
+# (cin, cout, k, s, H, batch, kernel variant): the stage outputs on their
+# large-batch kernels, the split-K and 128x128 variants of small batches, a
+# direct-to-LDS layer
+X_EVEN_CASES = [
+    (64, 64, 3, 1, 56, "big", "patch"), (128, 128, 3, 1, 28, "big", "patch"),
+    (256, 256, 3, 1, 14, "big", "patch"), (256, 256, 3, 1, 14, 1, "splitk"),
+    (256, 256, 3, 1, 14, 7, "staged128"), (64, 64, 3, 2, 112, "big", "direct"),
+    (64, 128, 3, 1, 56, 2, "staged128"),
+]
+
+
+def _unsaturated_params(r, cout, ktot):
+    """ws, bias, inv putting most outputs well inside int8 for uniform int8
+    operands (accumulator spread ~ sqrt(K) * 74^2)."""
+    ws = r.uniform(1e-3, 1e-2, cout).astype(F32)
+    bias = r.normal(0, 0.1, cout).astype(F32)
+    inv = (40.0 / (ws * np.sqrt(ktot) * 5460.0)).astype(F32)
+    return ws, bias, inv
+
+
+@pytest.mark.parametrize("mode", ["add_bn", "prelu"])
+@pytest.mark.parametrize("cin,cout,k,s,H,B,variant", X_EVEN_CASES)
+def test_x_even_output(gpu_lib, oracle, cin, cout, k, s, H, B, variant, mode):
+    """FFK_OUT_X_EVEN: X comes out at its even-row, even-column pixels only,
+    as a compact tensor, bit-exact with the oracle's X there; BN(X) stays whole."""
+    r = rng(900 + cin + cout + H + (B if isinstance(B, int) else 0) + len(mode))
+    if B == "big":
+        B = _direct_batch(gpu_lib, cin, cout, k, s, H)
+        idx = sorted({0, B // 2, B - 1})
+    else:
+        idx = list(range(B))
+    assert _variant_ws(gpu_lib, cin, cout, k, s, H, B) == variant
+    x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
+    Ho = (H + 2 * (k // 2) - k) // s + 1
+    ws, bias, inv = _unsaturated_params(r, cout, k * k * cin)
+    rows = dict(ws=ws, bias=bias, inv=inv)
+    ekw = dict(ws=ws, bias=bias, inv_pc=inv)
+    flags = fa.FFK_EPI_BIAS
+    add = None
+    bn = mode == "add_bn"
+    if bn:
+        add = r.integers(-128, 128, size=(B, Ho, Ho, cout), dtype=np.int8)
+        adds = r.uniform(1e-3, 5e-2, cout).astype(F32)
+        bsin = r.uniform(1e-3, 5e-2, cout).astype(F32)
+        bns = r.uniform(0.5, 1.5, cout).astype(F32)
+        bno = r.normal(0, 0.05, cout).astype(F32)
+        binv = (1.0 / r.uniform(0.01, 0.1, cout)).astype(F32)
+        rows.update(adds=adds, bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
+        ekw.update(add_src=add[idx], add_scale_pc=adds)
+        flags |= fa.FFK_EPI_ADD | fa.FFK_EPI_BN
+    else:
+        slope = r.uniform(0, 0.3, cout).astype(F32)
+        rows["slope"] = slope
+        ekw["prelu"] = slope
+        flags |= fa.FFK_EPI_PRELU
+    got_x, got_bn = run_conv(gpu_lib, x, w, s, k // 2, params=params_block(cout, **rows), flags=flags,
+                             add=add, want_bn=bn, x_even=True)
+    exp_x = oracle.fused_epilogue(oracle.conv_i32(x[idx], w, s, k // 2), **ekw)
+    assert 0.05 < np.mean(np.abs(exp_x) < 127)          # not a saturated test
+    assert got_x.shape == (B, Ho // 2, Ho // 2, cout)
+    assert np.array_equal(got_x[idx], exp_x[:, ::2, ::2])
+    if bn:
+        exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno, inv_pc=binv)
+        assert np.array_equal(got_bn[idx], exp_bn)
+
+
+def _variant_ws(lib, cin, cout, k, s, H, B):
+    """Kernel variant of a layer at batch B when given the workspace it asks for."""
+    import ctypes as C
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, k, k
+    d.stride, d.pad, d.hin, d.win = s, k // 2, H, H
+    n = lib.ffk_conv_workspace_bytes(C.byref(d))
+    d.workspace, d.workspace_bytes = (4096, n) if n else (None, 0)
+    v = lib.ffk_conv_variant(C.byref(d))
+    return v.decode() if v else None
+
+
+@pytest.mark.parametrize("rgb8", [False, True], ids=["fp32", "rgb8"])
+def test_x_even_stem(gpu_lib, oracle, rgb8):
+    """The input layer with its production epilogue (PReLU + BN second output)
+    and X at its even pixels."""
+    r = rng(951 + rgb8)
+    B = 3
+    w = r.integers(-128, 128, size=(64, 3, 3, 3), dtype=np.int8)
+    inv = np.array([127.0, 126.9, 127.3], np.float32)
+    imgs = r.integers(0, 256, size=(B, 112, 112, 3), dtype=np.uint8)
+    faces = (imgs.astype(np.float32) - 127.5) / 127.5
+    ws, bias, winv = _unsaturated_params(r, 64, 27)
+    slope = r.uniform(0, 0.3, 64).astype(F32)
+    bsin = r.uniform(1e-3, 5e-2, 64).astype(F32)
+    bns = r.uniform(0.5, 1.5, 64).astype(F32)
+    bno = r.normal(0, 0.05, 64).astype(F32)
+    binv = (1.0 / r.uniform(0.01, 0.1, 64)).astype(F32)
+    P = params_block(64, ws=ws, bias=bias, inv=winv, slope=slope, bn_sin=bsin, bn_s=bns, bn_o=bno,
+                     bn_inv=binv)
+    flags = fa.FFK_EPI_BIAS | fa.FFK_EPI_PRELU | fa.FFK_EPI_BN
+    if rgb8:
+        lut = np.empty((3, 256), np.int8)
+        assert gpu_lib.ffk_make_rgb8_lut(inv.ctypes.data, lut.ctypes.data) == 0
+        got_x, got_bn = run_conv(gpu_lib, imgs, w, 1, 1, params=P, flags=flags | fa.FFK_IN_RGB8,
+                                 in_lut=lut, want_bn=True, x_even=True)
+    else:
+        got_x, got_bn = run_conv(gpu_lib, faces, w, 1, 1, params=P, flags=flags, in_inv=inv,
+                                 want_bn=True, x_even=True)
+    q = oracle.quant_input(faces, inv)
+    exp_x = oracle.fused_epilogue(oracle.conv_i32(q, w, 1, 1), ws=ws, bias=bias, prelu=slope, inv_pc=winv)
+    assert 0.05 < np.mean(np.abs(exp_x) < 127)
+    assert np.array_equal(got_x, exp_x[:, ::2, ::2])
+    exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno, inv_pc=binv)
+    assert np.array_equal(got_bn, exp_bn)
+
+
+@pytest.mark.parametrize("B", [2, 341])
+def test_x_even_winograd(gpu_lib, oracle, B):
+    """The Winograd path keeps pixel (0, 0) of each 2x2 output block; at 341
+    faces the 112x112 layer runs as two slices of transformed input."""
+    r = rng(960 + B)
+    H = 112 if B > 2 else 56
+    x = r.integers(-128, 128, size=(B, H, H, 64), dtype=np.int8)
+    w = r.integers(-128, 128, size=(64, 64, 3, 3), dtype=np.int8)
+    ws, bias, inv = _unsaturated_params(r, 64, 576)
+    add = r.integers(-128, 128, size=(B, H, H, 64), dtype=np.int8)
+    adds = r.uniform(1e-3, 5e-2, 64).astype(F32)
+    bsin = r.uniform(1e-3, 5e-2, 64).astype(F32)
+    bns = r.uniform(0.5, 1.5, 64).astype(F32)
+    bno = r.normal(0, 0.05, 64).astype(F32)
+    binv = (1.0 / r.uniform(0.01, 0.1, 64)).astype(F32)
+    P = params_block(64, ws=ws, bias=bias, inv=inv, adds=adds, bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
+    flags = fa.FFK_EPI_BIAS | fa.FFK_EPI_ADD | fa.FFK_EPI_BN
+    got_x, got_bn = run_conv(gpu_lib, x, w, 1, 1, params=P, flags=flags, add=add, want_bn=True,
+                             winograd=True, x_even=True)
+    idx = sorted({0, B // 2, B - 1})
+    exp_x = oracle.fused_epilogue(oracle.conv_i32(x[idx], w, 1, 1), ws=ws, bias=bias, inv_pc=inv,
+                                  add_src=add[idx], add_scale_pc=adds)
+    assert np.array_equal(got_x[idx], exp_x[:, ::2, ::2])
+    exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno, inv_pc=binv)
+    assert np.array_equal(got_bn[idx], exp_bn)
+
+
+@pytest.mark.parametrize("B", ["small", "big"])
+@pytest.mark.parametrize("cin,cout,Hc", SHORTCUT_S1)
+def test_shortcut_stride1_over_compact_x(gpu_lib, oracle, cin, cout, Hc, B):
+    """A 1x1 stride-1 conv over the even pixels of X equals the 1x1 stride-2
+    conv over the whole X (the oracle's), int32 for int32."""
+    r = rng(970 + cin + cout + Hc)
+    B = 2 if B == "small" else _direct_batch(gpu_lib, cin, cout, 1, 1, Hc)
+    full = r.integers(-128, 128, size=(B, 2 * Hc, 2 * Hc, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, 1, 1), dtype=np.int8)
+    full[-1, 0] = -128
+    w[0] = -128
+    got = run_conv(gpu_lib, np.ascontiguousarray(full[:, ::2, ::2]), w, 1, 0, raw=True)
+    idx = sorted({0, B // 2, B - 1})
+    assert np.array_equal(got[idx], oracle.conv_i32(full[idx], w, 2, 0))

@@ -114,8 +114,31 @@ def test_per_layer_int8_activations(gpu_lib, synth_ffw4, oracle, oracle_model):
             assert n == t.size, "op %d: read %d" % (op, n)
             assert np.array_equal(buf.reshape(t.shape), t), "op %d differs" % op
         assert np.array_equal(got_emb, exp_emb)
+        # back to the serving plan (stage outputs stored at their even pixels)
+        assert gpu_lib.fastface_debug_keep_tensors(f.ff, 0) == 0
+        assert np.array_equal(f.embed_batch(x), exp_emb)
     finally:
         f.close()
+
+
+def test_stage_outputs_stored_at_even_pixels(ff, gpu_lib):
+    """The stem's output X and each stage's last X are read only by the next
+    stage's 1x1 stride-2 shortcut: the plan stores them at their even pixels
+    and runs those shortcuts at stride 1 over the compact tensors."""
+    info = fa.fastface_step_info()
+    writers, shortcuts = [], []
+    for s in range(gpu_lib.fastface_num_steps(ff.ff)):
+        assert gpu_lib.fastface_get_step(ff.ff, s, C.byref(info)) == 0
+        if info.kind != 1:
+            continue
+        if info.flags & fa.FFK_OUT_X_EVEN:
+            writers.append((info.cout, info.hout))
+            assert info.stores_x and info.flags & fa.FFK_EPI_BN
+        if info.kh == 1:
+            shortcuts.append((info.cin, info.cout, info.stride, info.hin, info.hout))
+    assert writers == [(64, 112), (64, 56), (128, 28), (256, 14)]
+    assert shortcuts == [(64, 64, 1, 56, 56), (64, 128, 1, 28, 28), (128, 256, 1, 14, 14),
+                         (256, 512, 1, 7, 7)]
 
 
 def test_device_resident_api(ff, gpu_lib):

@@ -102,6 +102,9 @@ def test_every_iresnet_conv_has_a_kernel():
         elif op["type"] == synth.OP_BLOCK_START:
             blk = cur
     assert seen == 53
+    # the 1x1 shortcuts over a block input stored at its even pixels (stride 1)
+    for cin, cout, hc in [(64, 64, 56), (64, 128, 28), (128, 256, 14), (256, 512, 7)]:
+        assert lib.ffk_conv_supported(cin, cout, 1, 1, 1, 0, hc, hc) == 1
     assert lib.ffk_conv_supported(64, 64, 3, 3, 1, 0, H, H) == 0      # pad must be k/2
     assert lib.ffk_conv_supported(96, 64, 3, 3, 1, 1, H, H) == 0
 
@@ -232,3 +235,23 @@ def test_winograd_weight_packing(oracle):
     assert sup(64, 64, 3, 3, 1, 1, 56, 56) == 1 and sup(64, 64, 3, 3, 1, 1, 112, 112) == 1
     assert sup(64, 64, 3, 3, 2, 1, 112, 112) == 0 and sup(128, 128, 3, 3, 1, 1, 28, 28) == 0
     assert sup(64, 128, 3, 3, 1, 1, 56, 56) == 0 and sup(64, 64, 1, 1, 1, 0, 56, 56) == 0
+
+
+def test_x_even_argument_checks():
+    """FFK_OUT_X_EVEN needs an int8 X output of even height and width; the
+    checks fail before anything touches a device (the pointers are never
+    dereferenced)."""
+    lib = fa.load()
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw, d.stride, d.pad, d.hin, d.win = 1, 512, 512, 3, 3, 1, 1, 7, 7
+    d.in_, d.w, d.params, d.out = 4096, 8192, 12288, 16384
+    d.flags = fa.FFK_EPI_BIAS | fa.FFK_OUT_X_EVEN
+    assert lib.ffk_conv(C.byref(d), None) == -1                    # 7x7 output
+    assert "even" in fa.last_error()
+    d.cin = d.cout = 256
+    d.hin = d.win = 14                                             # 14x14 output
+    d.out, d.out_i32 = None, 16384                                 # raw int32 output
+    assert lib.ffk_conv(C.byref(d), None) == -1
+    d.out_i32, d.out_bn, d.bn_lut = None, 16384, 20480             # BN output only, no X
+    d.flags |= fa.FFK_EPI_BN
+    assert lib.ffk_conv(C.byref(d), None) == -1

@@ -95,6 +95,7 @@ EXPORTS = [
     ("ffk_event_create", C.c_int, [C.POINTER(_p)]),
     ("ffk_event_destroy", C.c_int, [_p]),
     ("ffk_event_record", C.c_int, [_p, _p]),
+    ("ffk_stream_wait_event", C.c_int, [_p, _p]),
     ("ffk_event_elapsed_ms", C.c_int, [_p, _p, C.POINTER(C.c_float)]),
     ("ffk_graph_begin", C.c_int, [_p]),
     ("ffk_graph_end", C.c_int, [_p, C.POINTER(_p)]),

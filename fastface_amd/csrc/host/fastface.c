@@ -20,6 +20,17 @@
 
 #define FF_MAX_GRAPHS 16
 
+/* Host-buffer batches of at least two chunks stream: the host-to-device copy
+ * of chunk k+1 (copy stream) runs while chunk k computes (context stream),
+ * each chunk in its own region of the input buffer.  A chunk must fill the
+ * GPU by itself (at 256 faces the stage-3 layers have fewer workgroups than
+ * the CUs hold), and the copy it hides must be worth a second launch chain:
+ * fp32 faces (4 bytes a pixel, ~40% of the compute time over PCIe) stream in
+ * chunks of 512, uint8 faces (a quarter of that) only in chunks of 1024. */
+#define FF_STREAM_CHUNK_F32 512
+#define FF_STREAM_CHUNK_U8 1024
+#define FF_MAX_CHUNKS 64
+
 /* one captured chain per (batch, input format: 0 fp32 faces, 1 uint8 RGB) */
 typedef struct { int batch, fmt; void* exec; } GraphEntry;
 
@@ -39,7 +50,9 @@ struct FastFace {
     void* d_ws;                 /* split-K workspace of the small-batch convs */
     size_t ws_bytes;
     ffk_io* d_io;               /* device I/O descriptor */
-    ffk_io* h_io;               /* pinned staging */
+    ffk_io* h_io;               /* pinned staging: [0] set_io, [1 + k] chunk k */
+    void* cstream;              /* host-to-device copies of streamed chunks */
+    void* ev_chunk[FF_MAX_CHUNKS];
     ffk_io io_cur;              /* what d_io holds now */
     int keep_all;
     int algo;                   /* FASTFACE_CONV_* of the 64-channel 3x3 s1 layers */
@@ -298,7 +311,10 @@ FastFace* fastface_create(const char* ffw4_path)
     ff->d_in_inv = (float*)ffk_malloc(4 * sizeof(float));
     ff->d_in_lut = (int8_t*)ffk_malloc(3 * 256);
     ff->d_io = (ffk_io*)ffk_malloc(sizeof(ffk_io));
-    ff->h_io = (ffk_io*)ffk_host_alloc(sizeof(ffk_io));
+    ff->h_io = (ffk_io*)ffk_host_alloc((1 + FF_MAX_CHUNKS) * sizeof(ffk_io));
+    if (ffk_stream_create(&ff->cstream)) { report("stream", FFK_ERR_HIP); goto fail; }
+    for (int k = 0; k < FF_MAX_CHUNKS; k++)
+        if (ffk_event_create(&ff->ev_chunk[k])) { report("event", FFK_ERR_HIP); goto fail; }
     if (!ff->d_weights || !ff->d_params || !ff->d_in_inv || !ff->d_in_lut || !ff->d_io || !ff->h_io) {
         report("device allocation", FFK_ERR_NOMEM);
         goto fail;
@@ -338,6 +354,9 @@ void fastface_destroy(FastFace* ff)
     ffk_free(ff->d_in_lut);
     ffk_free(ff->d_io);
     ffk_host_free(ff->h_io);
+    if (ff->cstream) { ffk_stream_sync(ff->cstream); ffk_stream_destroy(ff->cstream); }
+    for (int k = 0; k < FF_MAX_CHUNKS; k++)
+        if (ff->ev_chunk[k]) ffk_event_destroy(ff->ev_chunk[k]);
     if (ff->stream) ffk_stream_destroy(ff->stream);
     ff_plan_free(&ff->plan);
     ff_model_free(&ff->model);
@@ -352,19 +371,61 @@ int fastface_reserve(FastFace* ff, int max_batch)
 
 void* fastface_stream(FastFace* ff) { return ff ? ff->stream : NULL; }
 
+/* A batch from host memory (fmt 0: fp32 faces, 1: uint8 RGB; face_bytes
+ * each) to host embeddings.  Up to one chunk: copy in, replay the chain,
+ * copy out.  More: chunk k's copy goes to its own region of the input buffer
+ * on the copy stream; the context stream waits for it, points the I/O
+ * descriptor at the chunk (a pinned slot per chunk, so no staging slot is
+ * rewritten while a copy may still read it) and replays the chain for the
+ * chunk's size.  Faces are independent: the results equal the one-shot
+ * path's bit for bit. */
+static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, int batch, float* out)
+{
+    int rc = ensure_capacity(ff, batch);
+    if (rc) { report("activation allocation", rc); return -2; }
+    int8_t* d_in = fmt ? (int8_t*)ff->d_input_u8 : (int8_t*)ff->d_input;
+    const size_t out_bytes = (size_t)batch * FASTFACE_OUTPUT_N * sizeof(float);
+    int chunk = fmt ? FF_STREAM_CHUNK_U8 : FF_STREAM_CHUNK_F32;
+    if (batch > chunk * FF_MAX_CHUNKS) chunk = (batch + FF_MAX_CHUNKS - 1) / FF_MAX_CHUNKS;
+    const int n = (batch + chunk - 1) / chunk;
+    if (n < 2 || ff->keep_all) {
+        rc = set_io(ff, (const float*)d_in, ff->d_output, ff->stream);
+        if (!rc) rc = ffk_memcpy_h2d(d_in, in, (size_t)batch * face_bytes, ff->stream);
+        if (!rc) rc = enqueue(ff, batch, ff->stream, fmt);
+    } else {
+        /* capture the chains first: no capture while copies are being issued */
+        const int last = batch - (n - 1) * chunk;
+        if (!graph_for(ff, chunk, fmt) || !graph_for(ff, last, fmt)) rc = FFK_ERR_HIP;
+        for (int k = 0; k < n && !rc; k++) {
+            const size_t b0 = (size_t)k * chunk;
+            const int nb = k + 1 < n ? chunk : last;
+            rc = ffk_memcpy_h2d(d_in + b0 * face_bytes, (const int8_t*)in + b0 * face_bytes,
+                                (size_t)nb * face_bytes, ff->cstream);
+            if (!rc) rc = ffk_event_record(ff->ev_chunk[k], ff->cstream);
+            if (!rc) rc = ffk_stream_wait_event(ff->stream, ff->ev_chunk[k]);
+            ffk_io* slot = &ff->h_io[1 + k];
+            slot->in = (const float*)(d_in + b0 * face_bytes);
+            slot->out = ff->d_output + b0 * FASTFACE_OUTPUT_N;
+            if (!rc) rc = ffk_memcpy_h2d(ff->d_io, slot, sizeof(ffk_io), ff->stream);
+            if (!rc) rc = enqueue(ff, nb, ff->stream, fmt);
+            if (!rc) ff->io_cur = *slot;
+        }
+        if (rc) {           /* leave no copy running into the buffers */
+            ffk_stream_sync(ff->cstream);
+            ff->io_cur.in = NULL; ff->io_cur.out = NULL;
+        }
+    }
+    if (!rc) rc = ffk_memcpy_d2h(out, ff->d_output, out_bytes, ff->stream);
+    if (!rc) rc = ffk_stream_sync(ff->stream);
+    if (rc) { report("embed", rc); return -3; }
+    return 0;
+}
+
 int fastface_embed_batch(FastFace* ff, const float* in, int batch, float* out)
 {
     if (!ff || !in || !out || batch < 0) return -1;
     if (batch == 0) return 0;
-    int rc = ensure_capacity(ff, batch);
-    if (rc) { report("activation allocation", rc); return -2; }
-    rc = set_io(ff, ff->d_input, ff->d_output, ff->stream);
-    if (!rc) rc = ffk_memcpy_h2d(ff->d_input, in, (size_t)batch * FASTFACE_INPUT_N * sizeof(float), ff->stream);
-    if (!rc) rc = enqueue(ff, batch, ff->stream, 0);
-    if (!rc) rc = ffk_memcpy_d2h(out, ff->d_output, (size_t)batch * FASTFACE_OUTPUT_N * sizeof(float), ff->stream);
-    if (!rc) rc = ffk_stream_sync(ff->stream);
-    if (rc) { report("embed", rc); return -3; }
-    return 0;
+    return embed_host(ff, in, FASTFACE_INPUT_N * sizeof(float), 0, batch, out);
 }
 
 int fastface_embed(FastFace* ff, const float* input_hwc, float* out_emb)
@@ -390,15 +451,7 @@ int fastface_embed_batch_rgb8(FastFace* ff, const uint8_t* in, int batch, float*
 {
     if (!ff || !in || !out || batch < 0) return -1;
     if (batch == 0) return 0;
-    int rc = ensure_capacity(ff, batch);
-    if (rc) { report("activation allocation", rc); return -2; }
-    rc = set_io(ff, (const float*)ff->d_input_u8, ff->d_output, ff->stream);
-    if (!rc) rc = ffk_memcpy_h2d(ff->d_input_u8, in, (size_t)batch * FASTFACE_INPUT_N, ff->stream);
-    if (!rc) rc = enqueue(ff, batch, ff->stream, 1);
-    if (!rc) rc = ffk_memcpy_d2h(out, ff->d_output, (size_t)batch * FASTFACE_OUTPUT_N * sizeof(float), ff->stream);
-    if (!rc) rc = ffk_stream_sync(ff->stream);
-    if (rc) { report("embed_rgb8", rc); return -3; }
-    return 0;
+    return embed_host(ff, in, FASTFACE_INPUT_N, 1, batch, out);
 }
 
 int fastface_embed_batch_rgb8_device(FastFace* ff, const uint8_t* d_in, int batch, float* d_out,

@@ -45,6 +45,8 @@ int   ffk_stream_sync(void* stream);            /* NULL: device-wide sync */
 int   ffk_event_create(void** event);
 int   ffk_event_destroy(void* event);
 int   ffk_event_record(void* event, void* stream);
+/* later work on `stream` waits for `event` (recorded on another stream) */
+int   ffk_stream_wait_event(void* stream, void* event);
 int   ffk_event_elapsed_ms(void* start, void* stop, float* ms);
 int   ffk_graph_begin(void* stream);            /* start stream capture */
 int   ffk_graph_end(void* stream, void** graph_exec);

@@ -218,3 +218,28 @@ def test_winograd_stage1_network(gpu_lib, synth_ffw4, oracle, oracle_model):
         assert gpu_lib.fastface_set_conv_algo(f.ff, 7) == -1
     finally:
         f.close()
+
+
+def test_streamed_host_batch_equals_one_shot(ff, gpu_lib):
+    """Host batches stream in chunks (copy of one chunk during the compute of
+    the previous): 600 fp32 faces as 512 + 88, 2100 uint8 faces as 1024 +
+    1024 + 52.  Embeddings equal the device-resident one-shot path's and the
+    single-face path's; a small batch afterwards still reads its own buffers."""
+    B = 600
+    x = synth.faces_uniform(B, 41)
+    got = ff.embed_batch(x)
+    din, dout = Dev(gpu_lib, host=x), Dev(gpu_lib, nbytes=B * 512 * 4)
+    assert gpu_lib.fastface_embed_batch_device(ff.ff, din.ptr, B, dout.ptr, None) == 0
+    check(gpu_lib, gpu_lib.ffk_stream_sync(gpu_lib.fastface_stream(ff.ff)))
+    assert np.array_equal(got, dout.get(np.float32, (B, 512)))
+    for i in (0, 511, 512, 599):
+        assert np.array_equal(ff.embed(x[i]), got[i]), i
+    B8 = 2100
+    imgs = np.random.default_rng(42).integers(0, 256, size=(B8, 112, 112, 3), dtype=np.uint8)
+    got8 = ff.embed_batch_rgb8(imgs)
+    d8, dout8 = Dev(gpu_lib, host=imgs), Dev(gpu_lib, nbytes=B8 * 512 * 4)
+    assert gpu_lib.fastface_embed_batch_rgb8_device(ff.ff, d8.ptr, B8, dout8.ptr, None) == 0
+    check(gpu_lib, gpu_lib.ffk_stream_sync(gpu_lib.fastface_stream(ff.ff)))
+    assert np.array_equal(got8, dout8.get(np.float32, (B8, 512)))
+    assert np.array_equal(ff.embed_batch_rgb8(imgs[2047:2049]), got8[2047:2049])
+    assert np.array_equal(ff.embed_batch(x[:3]), got[:3])

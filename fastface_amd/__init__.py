@@ -25,6 +25,7 @@ FFK_IN_RGB8 = 0x20
 FFK_EPI_PRELU_LE1 = 0x40
 FFK_ALGO_WINOGRAD = 0x80
 FFK_OUT_X_EVEN = 0x100
+FFK_EPI_IN_RANGE = 0x200
 (FFK_P_WS, FFK_P_BIAS, FFK_P_SLOPE, FFK_P_ADDSCALE, FFK_P_INV, FFK_P_BN_SIN, FFK_P_BN_S,
  FFK_P_BN_O, FFK_P_BN_INV, FFK_NPARAM) = range(10)
 
@@ -103,6 +104,7 @@ EXPORTS = [
     ("ffk_graph_destroy", C.c_int, [_p]),
     ("ffk_conv_supported", C.c_int, [C.c_int] * 8),
     ("ffk_prelu_le1_ok", C.c_int, [_p, C.c_int, C.c_int, C.c_int]),
+    ("ffk_requant_in_range", C.c_int, [_p, C.c_int, C.c_int, C.c_int]),
     ("ffk_conv_packed_bytes", C.c_size_t, [C.c_int] * 4),
     ("ffk_pack_conv_weights", C.c_int, [_p, C.c_int, C.c_int, C.c_int, C.c_int, _p]),
     ("ffk_conv_workspace_bytes", C.c_size_t, [C.POINTER(ffk_conv_desc)]),

@@ -133,8 +133,9 @@ __device__ __forceinline__ int8_t* x_row(const ConvArgs& a, int m) {
 // PRELU: 0 none, 1 f < 0 ? f*slope : f, 2 max(f, f*slope) (the same values
 // when every slope is at most 1 and f is never infinite: FFK_EPI_PRELU_LE1).
 // INSC: f = f * in_scale first (FFW2/FFW3 models; FFW4 skips the multiply).
+// RANGE: every requant value is known in range (FFK_EPI_IN_RANGE).
 // HO x WO: output image size (FFK_OUT_X_EVEN addressing).
-template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC, int HO, int WO>
+template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC, bool RANGE, int HO, int WO>
 __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                             const EpiParams<NJ>& prm, int mrow0, int ncol0, int8_t* Ws,
                                             const int8_t* Lw) {
@@ -176,7 +177,8 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
                 if (ADD) f = ff::add_residual(f, (int32_t)Ws[row * P + col], adds[j]);
                 if (PRELU == 1) f = ff::prelu(f, p2[j]);
                 if (PRELU == 2) f = ff::prelu_le1(f, p2[j]);
-                Ws[row * P + col] = (int8_t)ff::requant_haz(f * inv[j]);
+                Ws[row * P + col] = (int8_t)(RANGE ? ff::requant_haz_in_range(f * inv[j])
+                                                   : ff::requant_haz(f * inv[j]));
                 // one 32x32 tile at a time: keeps the compiler from hoisting
                 // every residual read of the wave tile into registers
                 if (r == 15) asm volatile("" ::: "memory");
@@ -254,30 +256,49 @@ __device__ __forceinline__ void wave_epi_wide(const v16i (&acc)[MI][NJ], const C
     }
 }
 
-// int8 epilogue variants dispatched on the (uniform) flags, parameters given
+// int8 epilogue variants dispatched on the (uniform) flags, parameters given.
+// FFK_EPI_PRELU_LE1 and FFK_EPI_IN_RANGE apply to the FFW4 path (no in-scale);
+// the in-range variants exist for the PReLU forms FFW4 models use (none, or
+// max(f, f*slope)).
 template <int COUT, int MI, int NJ, bool INSC, int HO, int WO>
 __device__ __forceinline__ void wave_epilogue_f(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                                 const EpiParams<NJ>& P, int mrow0, int ncol0, int8_t* Ws,
                                                 const int8_t* Lw) {
     const bool le1 = !INSC && (a.flags & FFK_EPI_PRELU_LE1);
+    const bool rng = !INSC && (a.flags & FFK_EPI_IN_RANGE);
+#define FF_EPI(PR, AD, BN, RG) \
+    wave_epi_i8<COUT, MI, NJ, PR, AD, BN, INSC, RG, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw)
     switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN)) {
-    case 0: wave_epi_i8<COUT, MI, NJ, 0, false, false, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_PRELU:
-        if (le1) wave_epi_i8<COUT, MI, NJ, 2, false, false, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw);
-        else wave_epi_i8<COUT, MI, NJ, 1, false, false, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw);
+    case 0:
+        if (rng) FF_EPI(0, false, false, true);
+        else FF_EPI(0, false, false, false);
         break;
-    case FFK_EPI_ADD: wave_epi_i8<COUT, MI, NJ, 0, true, false, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_BN: wave_epi_i8<COUT, MI, NJ, 0, false, true, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+    case FFK_EPI_PRELU:
+        if (le1 && rng) FF_EPI(2, false, false, true);
+        else if (le1) FF_EPI(2, false, false, false);
+        else FF_EPI(1, false, false, false);
+        break;
+    case FFK_EPI_ADD:
+        if (rng) FF_EPI(0, true, false, true);
+        else FF_EPI(0, true, false, false);
+        break;
+    case FFK_EPI_BN:
+        if (rng) FF_EPI(0, false, true, true);
+        else FF_EPI(0, false, true, false);
+        break;
     case FFK_EPI_PRELU | FFK_EPI_BN:
-        if (le1) wave_epi_i8<COUT, MI, NJ, 2, false, true, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw);
-        else wave_epi_i8<COUT, MI, NJ, 1, false, true, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw);
+        if (le1 && rng) FF_EPI(2, false, true, true);
+        else if (le1) FF_EPI(2, false, true, false);
+        else FF_EPI(1, false, true, false);
         break;
     case FFK_EPI_ADD | FFK_EPI_BN:
-        wave_epi_i8<COUT, MI, NJ, 0, true, true, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    case FFK_EPI_PRELU | FFK_EPI_ADD:
-        wave_epi_i8<COUT, MI, NJ, 1, true, false, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
-    default: wave_epi_i8<COUT, MI, NJ, 1, true, true, INSC, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw); break;
+        if (rng) FF_EPI(0, true, true, true);
+        else FF_EPI(0, true, true, false);
+        break;
+    case FFK_EPI_PRELU | FFK_EPI_ADD: FF_EPI(1, true, false, false); break;
+    default: FF_EPI(1, true, true, false); break;
     }
+#undef FF_EPI
 }
 
 template <int COUT, int MI, int NJ, int HO, int WO>
@@ -966,6 +987,7 @@ constexpr int STEM_WG_PER_CU = FF_STEM_WG_PER_CU;
 //   3-5  the same with the BN second output
 //   6    FFK_EPI_INSCALE (FFW2/FFW3: flags dispatched inside)
 //   7    raw int32 accumulators
+//   8-13 0-5 with FFK_EPI_IN_RANGE
 constexpr int STEM_EPI_INSC = 6, STEM_EPI_RAW = 7;
 
 // (7 waves per workgroup over 4 SIMDs: STEM_WG_PER_CU * 7 / 4 waves per SIMD)
@@ -1086,7 +1108,8 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
         const int mw = m0 + wave * 32;
         if constexpr (EPI == STEM_EPI_RAW) wave_epi_wide<COUT, 1, 2, false>(acc, a, mw, 0);
         else if constexpr (EPI == STEM_EPI_INSC) wave_epilogue_f<COUT, 1, 2, true, H, W>(acc, a, prm, mw, 0, Ws, Ls);
-        else wave_epi_i8<COUT, 1, 2, EPI % 3, false, (EPI >= 3), false, H, W>(acc, a, prm, mw, 0, Ws, Ls);
+        else wave_epi_i8<COUT, 1, 2, (EPI & 7) % 3, false, ((EPI & 7) >= 3), false, (EPI >= 8), H, W>(
+            acc, a, prm, mw, 0, Ws, Ls);
     }
 }
 
@@ -1133,12 +1156,14 @@ void launch_stem(const ConvArgs& a, int grid, hipStream_t s) {
     int epi;
     if (a.out_i32) epi = STEM_EPI_RAW;
     else if (a.flags & FFK_EPI_INSCALE) epi = STEM_EPI_INSC;
-    else epi = (a.flags & FFK_EPI_PRELU ? (a.flags & FFK_EPI_PRELU_LE1 ? 2 : 1) : 0) + (a.flags & FFK_EPI_BN ? 3 : 0);
+    else epi = (a.flags & FFK_EPI_PRELU ? (a.flags & FFK_EPI_PRELU_LE1 ? 2 : 1) : 0) + (a.flags & FFK_EPI_BN ? 3 : 0) +
+               (a.flags & FFK_EPI_IN_RANGE ? 8 : 0);
     stem_fn fn;
     const bool rgb8 = (a.flags & FFK_IN_RGB8) != 0;
     switch (epi) {
 #define FF_STEM_CASE(E) case E: fn = rgb8 ? &launch_stem_as<true, E> : &launch_stem_as<false, E>; break;
     FF_STEM_CASE(0) FF_STEM_CASE(1) FF_STEM_CASE(2) FF_STEM_CASE(3) FF_STEM_CASE(4) FF_STEM_CASE(5)
+    FF_STEM_CASE(8) FF_STEM_CASE(9) FF_STEM_CASE(10) FF_STEM_CASE(11) FF_STEM_CASE(12) FF_STEM_CASE(13)
     FF_STEM_CASE(STEM_EPI_INSC)
     default: fn = rgb8 ? &launch_stem_as<true, STEM_EPI_RAW> : &launch_stem_as<false, STEM_EPI_RAW>; break;
 #undef FF_STEM_CASE
@@ -1445,6 +1470,28 @@ int ffk_prelu_le1_ok(const float* params, int cout, int ktotal, int with_add) {
     return 1;
 }
 
+int ffk_requant_in_range(const float* params, int cout, int ktotal, int flags) {
+    if (!params || cout <= 0 || ktotal <= 0 || (flags & FFK_EPI_INSCALE)) return 0;
+    const double acc_max = (double)ktotal * 128.0 * 128.0;
+    // each fp32 rounding is within a factor 1 + 2^-24 of its exact value;
+    // five of them (conversion, ws, bias, residual, PReLU) before the inv one
+    const double widen = 1.000001;
+    for (int c = 0; c < cout; c++) {
+        const double ws = params[FFK_P_WS * cout + c];
+        const double bias = params[FFK_P_BIAS * cout + c];
+        const double inv = params[FFK_P_INV * cout + c];
+        const double adds = (flags & FFK_EPI_ADD) ? params[FFK_P_ADDSCALE * cout + c] : 0.0;
+        const double slope = (flags & FFK_EPI_PRELU) ? params[FFK_P_SLOPE * cout + c] : 0.0;
+        if (!std::isfinite(ws) || !std::isfinite(bias) || !std::isfinite(inv) || !std::isfinite(adds) ||
+            !std::isfinite(slope))
+            return 0;
+        const double f = (acc_max * std::fabs(ws) + std::fabs(bias) + 128.0 * std::fabs(adds)) * widen;
+        const double t = f * std::max(1.0, std::fabs(slope)) * std::fabs(inv) * widen;
+        if (!(t < 2147483520.0)) return 0;              // 2^31 - 128
+    }
+    return 1;
+}
+
 size_t ffk_conv_packed_bytes(int cin, int cout, int kh, int kw) {
     const size_t ktot = (size_t)kh * kw * cin;
     const size_t steps = (ktot + FF_KSTEP - 1) / FF_KSTEP;
@@ -1537,7 +1584,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     a.out_bn = d->out_bn;
     a.out_i32 = d->out_i32;
     a.flags = d->flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_BIAS | FFK_EPI_INSCALE |
-                          FFK_EPI_PRELU_LE1 | FFK_OUT_X_EVEN |
+                          FFK_EPI_PRELU_LE1 | FFK_OUT_X_EVEN | FFK_EPI_IN_RANGE |
                           FFK_IN_RGB8);
     a.in_scale = d->in_scale;
     // The direct-to-LDS kernels address the int8 input with 32-bit offsets:

@@ -34,6 +34,14 @@ __device__ __forceinline__ int32_t requant_haz(float t) {
     return cvtt_clamp_i8(r);
 }
 
+// The same for t known finite with |t| < 2^31 - 128 (FFK_EPI_IN_RANGE): then
+// |t| + 0.5 rounds to at most 2^31 - 128 (2^31 - 128 is a float), so
+// cvttps2dq is in range and the clamp alone decides.
+__device__ __forceinline__ int32_t requant_haz_in_range(float t) {
+    float r = t + copysignf(0.5f, t);
+    return (int32_t)__builtin_amdgcn_fmed3f(r, -128.0f, 127.0f);
+}
+
 // Conv epilogue for one element (int8_epilogue.c:52-93, FFW4 call site
 // libfastface.c:389-392):
 //   f = RN(RN(RN((float)acc * in_scale) * ws) + bias)

@@ -238,6 +238,9 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
             /* PReLU as max(f, f*slope) where the parameters allow it (same values) */
             if (slope && ffk_prelu_le1_ok(P, C, op->Kh * op->Kw * op->Cin, add_k >= 0))
                 s->flags |= FFK_EPI_PRELU_LE1;
+            /* requant values provably finite and below 2^31: no x86 out-of-range case */
+            if (ffk_requant_in_range(P, C, op->Kh * op->Kw * op->Cin, s->flags))
+                s->flags |= FFK_EPI_IN_RANGE;
             A = X; A_scale = eff_scale;
             if (pc && m->scale_pc[eff]) A_pc = m->scale_pc[eff];
             last_conv = p->n_steps - 1;

@@ -90,6 +90,13 @@ typedef struct { const float* in; float* out; } ffk_io;
                                    stride-1 conv over the compact tensor.  No
                                    reference counterpart: the reference
                                    stores the whole tensor. */
+#define FFK_EPI_IN_RANGE 0x200  /* the caller guarantees that every requant
+                                   value RN(f*inv) is finite and below 2^31 -
+                                   128 in magnitude (ffk_requant_in_range), so
+                                   the kernel may skip the x86 out-of-range
+                                   case (NaN or |r| >= 2^31 -> -128): the same
+                                   values, two operations fewer.  Ignored with
+                                   FFK_EPI_INSCALE. */
 
 /* rows of the per-layer parameter block, each `cout` floats (device) */
 enum {
@@ -159,6 +166,13 @@ int    ffk_pack_winograd_weights(const int8_t* w_oihw, int cout, int cin, int8_t
  * below FLT_MAX for the largest |acc| = ktotal*128*128, so the
  * pre-activation value is never infinite.  Else 0. */
 int    ffk_prelu_le1_ok(const float* params, int cout, int ktotal, int with_add);
+/* 1 if a conv's parameter block (host memory) allows FFK_EPI_IN_RANGE for
+ * a reduction of ktotal = kh*kw*cin int8 products with these epilogue flags
+ * (FFK_EPI_PRELU / FFK_EPI_ADD select the rows that take part): every used
+ * parameter is finite and (ktotal*128*128*|ws| + |bias| + 128*|add_scale|)
+ * * max(1, |slope|) * |inv|, widened for the fp32 roundings, stays below
+ * 2^31 - 128.  0 with FFK_EPI_INSCALE. */
+int    ffk_requant_in_range(const float* params, int cout, int ktotal, int flags);
 
 /* 1 if a kernel is compiled for this layer geometry, else 0. */
 int    ffk_conv_supported(int cin, int cout, int kh, int kw, int stride, int pad,

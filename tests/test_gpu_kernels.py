@@ -471,10 +471,11 @@ def _variant_ws(lib, cin, cout, k, s, H, B):
     return v.decode() if v else None
 
 
+@pytest.mark.parametrize("in_range", [False, True], ids=["checked", "in_range"])
 @pytest.mark.parametrize("rgb8", [False, True], ids=["fp32", "rgb8"])
-def test_x_even_stem(gpu_lib, oracle, rgb8):
+def test_x_even_stem(gpu_lib, oracle, rgb8, in_range):
     """The input layer with its production epilogue (PReLU + BN second output)
-    and X at its even pixels."""
+    and X at its even pixels, with and without FFK_EPI_IN_RANGE."""
     r = rng(951 + rgb8)
     B = 3
     w = r.integers(-128, 128, size=(64, 3, 3, 3), dtype=np.int8)
@@ -490,6 +491,9 @@ def test_x_even_stem(gpu_lib, oracle, rgb8):
     P = params_block(64, ws=ws, bias=bias, inv=winv, slope=slope, bn_sin=bsin, bn_s=bns, bn_o=bno,
                      bn_inv=binv)
     flags = fa.FFK_EPI_BIAS | fa.FFK_EPI_PRELU | fa.FFK_EPI_BN
+    if in_range:
+        flags |= fa.FFK_EPI_PRELU_LE1 | fa.FFK_EPI_IN_RANGE
+        assert gpu_lib.ffk_requant_in_range(P.ctypes.data, 64, 27, flags) == 1
     if rgb8:
         lut = np.empty((3, 256), np.int8)
         assert gpu_lib.ffk_make_rgb8_lut(inv.ctypes.data, lut.ctypes.data) == 0
@@ -547,3 +551,63 @@ def test_shortcut_stride1_over_compact_x(gpu_lib, oracle, cin, cout, Hc, B):
     got = run_conv(gpu_lib, np.ascontiguousarray(full[:, ::2, ::2]), w, 1, 0, raw=True)
     idx = sorted({0, B // 2, B - 1})
     assert np.array_equal(got[idx], oracle.conv_i32(full[idx], w, 2, 0))
+
+
+# ---- FFK_EPI_IN_RANGE: the requant without the x86 out-of-range case ----
+RANGE_MODES = ["none", "prelu_le1", "add_bn", "prelu_bn_le1"]
+
+
+@pytest.mark.parametrize("split", [True, False, "direct"], ids=["splitk", "wholek", "direct"])
+@pytest.mark.parametrize("mode", RANGE_MODES)
+@pytest.mark.parametrize("cin,cout,k,s,H", EPI_SHAPES)
+def test_in_range_epilogue(gpu_lib, oracle, mode, cin, cout, k, s, H, split):
+    """With parameters the host check accepts (ffk_requant_in_range), the
+    in-range epilogue gives the oracle's int8 values, ties and negative zero
+    included."""
+    if split is True and (cin, cout, k, s, H) not in SPLIT_SHAPES:
+        pytest.skip("no split-K variant for this geometry")
+    r = rng(1100 + cin + cout + H + RANGE_MODES.index(mode))
+    if split == "direct":
+        B = _direct_batch(gpu_lib, cin, cout, k, s, H)
+        idx = sorted({0, B // 2, B - 1})
+        split = False
+    else:
+        B = 1 if split else 2
+        idx = list(range(B))
+    x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
+    Ho = (H + 2 * (k // 2) - k) // s + 1
+    ws, bias, inv = _unsaturated_params(r, cout, k * k * cin)
+    ws[0], bias[0], inv[0] = 0.5, 0.0, 1.0 / 64        # exact .5 ties after scaling
+    ws[4], bias[4] = -1e-3, -0.0
+    rows = dict(ws=ws, bias=bias, inv=inv)
+    ekw = dict(ws=ws, bias=bias, inv_pc=inv)
+    flags = fa.FFK_EPI_BIAS
+    add = None
+    if "prelu" in mode:
+        slope = r.uniform(0, 0.3, cout).astype(F32)
+        slope[7:10] = [1.0, 0.0, -0.5]
+        rows["slope"] = slope; ekw["prelu"] = slope
+        flags |= fa.FFK_EPI_PRELU | fa.FFK_EPI_PRELU_LE1
+    if "add" in mode:
+        add = r.integers(-128, 128, size=(B, Ho, Ho, cout), dtype=np.int8)
+        adds = r.uniform(1e-3, 5e-2, cout).astype(F32)
+        rows["adds"] = adds; ekw.update(add_src=add[idx], add_scale_pc=adds); flags |= fa.FFK_EPI_ADD
+    bn = "bn" in mode
+    if bn:
+        bsin = r.uniform(1e-3, 5e-2, cout).astype(F32)
+        bns = r.uniform(0.5, 1.5, cout).astype(F32)
+        bno = r.normal(0, 0.05, cout).astype(F32)
+        binv = (1.0 / r.uniform(0.01, 0.1, cout)).astype(F32)
+        rows.update(bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
+        flags |= fa.FFK_EPI_BN
+    P = params_block(cout, **rows)
+    assert gpu_lib.ffk_requant_in_range(P.ctypes.data, cout, k * k * cin, flags) == 1
+    got_x, got_bn = run_conv(gpu_lib, x, w, s, k // 2, params=P, flags=flags | fa.FFK_EPI_IN_RANGE,
+                             add=add, want_bn=bn, split=split)
+    exp_x = oracle.fused_epilogue(oracle.conv_i32(x[idx], w, s, k // 2), **ekw)
+    assert 0.05 < np.mean(np.abs(exp_x) < 127)
+    assert np.array_equal(got_x[idx], exp_x)
+    if bn:
+        exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno, inv_pc=binv)
+        assert np.array_equal(got_bn[idx], exp_bn)

@@ -137,6 +137,10 @@ def test_stage_outputs_stored_at_even_pixels(ff, gpu_lib):
         if info.kh == 1:
             shortcuts.append((info.cin, info.cout, info.stride, info.hin, info.hout))
     assert writers == [(64, 112), (64, 56), (128, 28), (256, 14)]
+    # every conv of the synthetic model has requant values provably in range
+    for s in range(gpu_lib.fastface_num_steps(ff.ff)):
+        assert gpu_lib.fastface_get_step(ff.ff, s, C.byref(info)) == 0
+        assert info.kind != 1 or info.flags & fa.FFK_EPI_IN_RANGE, s
     assert shortcuts == [(64, 64, 1, 56, 56), (64, 128, 1, 28, 28), (128, 256, 1, 14, 14),
                          (256, 512, 1, 7, 7)]
 

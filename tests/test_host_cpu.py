@@ -255,3 +255,40 @@ def test_x_even_argument_checks():
     d.out_i32, d.out_bn, d.bn_lut = None, 16384, 20480             # BN output only, no X
     d.flags |= fa.FFK_EPI_BN
     assert lib.ffk_conv(C.byref(d), None) == -1
+
+
+def test_requant_in_range_condition():
+    """ffk_requant_in_range: FFK_EPI_IN_RANGE only where every requant value
+    is provably finite and below 2^31 - 128 (then the x86 out-of-range case,
+    NaN or |r| >= 2^31 -> -128, cannot occur)."""
+    lib = fa.load()
+    C_ = 4
+    P = np.zeros((fa.FFK_NPARAM, C_), np.float32)
+    P[fa.FFK_P_WS] = 1e-3
+    P[fa.FFK_P_BIAS] = 0.1
+    P[fa.FFK_P_INV] = 20.0
+    P[fa.FFK_P_SLOPE] = 0.25
+    P[fa.FFK_P_ADDSCALE] = 0.05
+    K = 2304
+    PR, AD = fa.FFK_EPI_PRELU, fa.FFK_EPI_ADD
+    ok = lambda q, flags=PR, k=K: lib.ffk_requant_in_range(np.ascontiguousarray(q).ctypes.data, C_, k, flags)
+    assert ok(P) == 1 and ok(P, AD) == 1 and ok(P, 0) == 1
+    # the bound: K*128^2*ws*inv just below / above 2^31 - 128
+    acc_max = K * 128 * 128
+    Q = P.copy(); Q[fa.FFK_P_BIAS] = 0; Q[fa.FFK_P_WS] = 1.0
+    Q[fa.FFK_P_INV, 2] = np.float32(2147483520.0 / acc_max * 0.9999)
+    assert ok(Q, 0) == 1
+    Q[fa.FFK_P_INV, 2] = np.float32(2147483520.0 / acc_max * 1.0001)
+    assert ok(Q, 0) == 0
+    Q = P.copy(); Q[fa.FFK_P_INV, 1] = 3.0e38          # requant overflow
+    assert ok(Q) == 0
+    Q = P.copy(); Q[fa.FFK_P_WS, 0] = np.nan
+    assert ok(Q) == 0
+    Q = P.copy(); Q[fa.FFK_P_SLOPE, 3] = np.inf         # only checked with PReLU
+    assert ok(Q, PR) == 0 and ok(Q, 0) == 1
+    Q = P.copy(); Q[fa.FFK_P_ADDSCALE, 3] = np.inf      # only checked with the residual
+    assert ok(Q, AD) == 0 and ok(Q, 0) == 1
+    Q = P.copy(); Q[fa.FFK_P_SLOPE] = 1e4               # a slope above 1 scales the bound
+    assert ok(Q, PR) == 0 and ok(Q, 0) == 1
+    assert ok(P, PR | fa.FFK_EPI_INSCALE) == 0          # the in-scale path always checks
+    assert ok(P, PR, 0) == 0

@@ -130,6 +130,10 @@ def main():
     ap.add_argument("--batch", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-reps", type=int, default=3)
+    ap.add_argument("--b1024-only", action="store_true",
+                    help="time only the B=%d chain, its per-step profile and the Winograd leg "
+                         "(the rocprofv3 kernel-statistics run: b=1, B=8, the config-2 layer and "
+                         "the host-buffer rates are left out)" % 1024)
     ap.add_argument("--no-winograd", action="store_true",
                     help="skip the config-5 run of the stage-1 layers as Winograd F(2,3)")
     args = ap.parse_args()
@@ -225,8 +229,21 @@ def main():
             (B, key, n, tms, tms / n, ops / (tms / n * 1e-3) / 1e12))
     dom = [st for st in steps if st["kind"] == 1 and st["cin"] == 256 and st["cout"] == 256
            and st["k"] == 3 and st["s"] == 1]
-    dom_ms = statistics.mean(st["ms"] for st in dom)
+    # in-chain figure: HIP events between the eager launches of the per-step
+    # profile, so it includes the host's launch gap before each launch
+    dom_chain_ms = statistics.mean(st["ms"] for st in dom)
     dom_ops = dom[0]["ops"] * B
+    # roofline figure: the same kernel at the same batch in the network's two
+    # epilogue forms (13 x PReLU max form, 13 x residual + BN second output,
+    # both in range), 26 launches captured in one hipGraph and replayed
+    # between HIP events on the launch stream -- kernel time without launch
+    # gaps, the quantity a kernel trace reports as the launch duration
+    from fastface_amd.layerbench import time_layer
+    dom_g = time_layer(lib, 256, 256, 3, 1, 14, batch=B, iters=26, graph_reps=20,
+                       epis=["prelu_le1_rng", "add_bn_rng"])
+    if dom_g["kernel"] != "patch":
+        raise RuntimeError("the dominant layer did not take the patch kernel: %s" % dom_g["kernel"])
+    dom_ms = dom_g["ms_per_launch"]
     dom_tops = dom_ops / (dom_ms * 1e-3) / 1e12
     total_ops = sum(st["ops"] for st in steps) * B
     chain_tops = total_ops / (ms_per_step * 1e-3) / 1e12
@@ -244,8 +261,9 @@ def main():
     # algorithmic HBM rate of each stage (activation bytes in + out + residual +
     # BN output, plus weights): the epilogue-bound stem / stage 1 against 8 TB/s
     stage_gbs = {k: round(v[2] / (v[1] * 1e-3) / 1e9, 1) for k, v in stages.items()}
-    log("dominant conv 256x256x3x3@14: %.4f ms/launch, %.1f TOP/s (%.1f%% of peak)"
-        % (dom_ms, dom_tops, 100 * dom_tops / PEAK_INT8_TOPS))
+    log("dominant conv 256x256x3x3@14: %.4f ms/launch, %.1f TOP/s (%.1f%% of peak) from a graph of "
+        "26 launches; %.4f ms per launch in the eager per-step chain profile"
+        % (dom_ms, dom_tops, 100 * dom_tops / PEAK_INT8_TOPS, dom_chain_ms))
 
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic_conv256_b1024.json")
@@ -255,76 +273,78 @@ def main():
         if DOMINANT_KERNEL in tj.get("kernel", ""):      # counters of this very kernel only
             traffic = tj.get("bytes_per_launch")
 
-    # b=1 latency: host buffers in, host buffers out (fastface_embed), and the
-    # device-only chain
-    lat = []
-    for i in range(60):
-        t = time.perf_counter()
-        check(lib, lib.fastface_embed(ff.ff, x1.ctypes.data, e1.ctypes.data), "embed b1")
-        lat.append((time.perf_counter() - t) * 1e3)
-    lat = sorted(lat[10:])
-    b1_ms = statistics.median(lat)
-    check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 1, d_out, stream), "b1 dev")
-    check(lib, lib.ffk_stream_sync(stream), "sync")
-    check(lib, lib.ffk_event_record(ev0, stream), "record")
-    for _ in range(50):
+    b1_ms = b1_dev_ms = b8_ms_face = host_fp32 = host_rgb8 = dev_rgb8 = cfg2 = None
+    if not args.b1024_only:
+        # b=1 latency: host buffers in, host buffers out (fastface_embed), and the
+        # device-only chain
+        lat = []
+        for i in range(60):
+            t = time.perf_counter()
+            check(lib, lib.fastface_embed(ff.ff, x1.ctypes.data, e1.ctypes.data), "embed b1")
+            lat.append((time.perf_counter() - t) * 1e3)
+        lat = sorted(lat[10:])
+        b1_ms = statistics.median(lat)
         check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 1, d_out, stream), "b1 dev")
-    check(lib, lib.ffk_event_record(ev1, stream), "record")
-    check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
-    b1_dev_ms = ms.value / 50
-    log("b=1: %.3f ms host-to-host median, %.3f ms device chain" % (b1_ms, b1_dev_ms))
-    b1_steps = np.zeros(n_steps, np.float32)
-    if lib.fastface_profile_steps(ff.ff, 1, 20, b1_steps.ctypes.data) == n_steps:
-        for s in np.argsort(-b1_steps)[:8]:
-            st = steps[s]
-            log("b=1 step %2d: %.4f ms  conv %d->%d k%d s%d @%d" % (s, b1_steps[s], st["cin"],
-                st["cout"], st["k"], st["s"], st["hin"]))
-        log("b=1 sum of step times %.4f ms" % float(b1_steps.sum()))
+        check(lib, lib.ffk_stream_sync(stream), "sync")
+        check(lib, lib.ffk_event_record(ev0, stream), "record")
+        for _ in range(50):
+            check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 1, d_out, stream), "b1 dev")
+        check(lib, lib.ffk_event_record(ev1, stream), "record")
+        check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
+        b1_dev_ms = ms.value / 50
+        log("b=1: %.3f ms host-to-host median, %.3f ms device chain" % (b1_ms, b1_dev_ms))
+        b1_steps = np.zeros(n_steps, np.float32)
+        if lib.fastface_profile_steps(ff.ff, 1, 20, b1_steps.ctypes.data) == n_steps:
+            for s in np.argsort(-b1_steps)[:8]:
+                st = steps[s]
+                log("b=1 step %2d: %.4f ms  conv %d->%d k%d s%d @%d" % (s, b1_steps[s], st["cin"],
+                    st["cout"], st["k"], st["s"], st["hin"]))
+            log("b=1 sum of step times %.4f ms" % float(b1_steps.sum()))
 
-    # B=8 (the reference README's batched operating point),
-    # device-resident chain, ms per face
-    check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 8, d_out, stream), "b8 dev")
-    check(lib, lib.ffk_stream_sync(stream), "sync")
-    check(lib, lib.ffk_event_record(ev0, stream), "record")
-    for _ in range(50):
+        # B=8 (the reference README's batched operating point),
+        # device-resident chain, ms per face
         check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 8, d_out, stream), "b8 dev")
-    check(lib, lib.ffk_event_record(ev1, stream), "record")
-    check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
-    b8_ms_face = ms.value / 50 / 8
-    log("B=8: %.4f ms/face (%.3f ms per batch), device chain" % (b8_ms_face, b8_ms_face * 8))
+        check(lib, lib.ffk_stream_sync(stream), "sync")
+        check(lib, lib.ffk_event_record(ev0, stream), "record")
+        for _ in range(50):
+            check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 8, d_out, stream), "b8 dev")
+        check(lib, lib.ffk_event_record(ev1, stream), "record")
+        check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
+        b8_ms_face = ms.value / 50 / 8
+        log("B=8: %.4f ms/face (%.3f ms per batch), device chain" % (b8_ms_face, b8_ms_face * 8))
 
-    # the single 256->256 3x3 layer microbench at N=64
-    from fastface_amd.layerbench import time_layer
-    cfg2 = time_layer(lib, 256, 256, 3, 1, 14, batch=64, iters=200, epi="prelu")
-    log("config 2 layer (N=64, 14x14, 256->256, PReLU): %.4f ms, %.1f TOP/s (%.1f%% of peak), %s"
-        % (cfg2["ms_per_launch"], cfg2["int8_tops"], 100 * cfg2["frac_of_peak"], cfg2["kernel"]))
+        # the single 256->256 3x3 layer microbench at N=64
+        from fastface_amd.layerbench import time_layer
+        cfg2 = time_layer(lib, 256, 256, 3, 1, 14, batch=64, iters=200, epi="prelu")
+        log("config 2 layer (N=64, 14x14, 256->256, PReLU): %.4f ms, %.1f TOP/s (%.1f%% of peak), %s"
+            % (cfg2["ms_per_launch"], cfg2["int8_tops"], 100 * cfg2["frac_of_peak"], cfg2["kernel"]))
 
-    # Host-buffer (PCIe-inclusive) rates of the boundary: fp32 faces and the
-    # uint8 RGB entry point (a quarter of the input bytes).  Reported beside
-    # `value`, never as it.  Pageable numpy buffers, as a caller would pass.
-    imgs = np.random.default_rng(5).integers(0, 256, size=(B, 112, 112, 3), dtype=np.uint8)
+        # Host-buffer (PCIe-inclusive) rates of the boundary: fp32 faces and the
+        # uint8 RGB entry point (a quarter of the input bytes).  Reported beside
+        # `value`, never as it.  Pageable numpy buffers, as a caller would pass.
+        imgs = np.random.default_rng(5).integers(0, 256, size=(B, 112, 112, 3), dtype=np.uint8)
 
-    def host_rate(fn, arr, reps=3):
-        fn(ff.ff, arr.ctypes.data, B, out.ctypes.data)           # capture / warm
-        t = time.perf_counter()
-        for _ in range(reps):
-            check(lib, fn(ff.ff, arr.ctypes.data, B, out.ctypes.data), "host embed")
-        return B * reps / (time.perf_counter() - t)
-    host_fp32 = host_rate(lib.fastface_embed_batch, x)
-    host_rgb8 = host_rate(lib.fastface_embed_batch_rgb8, imgs)
-    d_img = lib.ffk_malloc(imgs.nbytes)
-    check(lib, lib.ffk_memcpy_h2d(d_img, imgs.ctypes.data, imgs.nbytes, stream), "upload rgb8")
-    check(lib, lib.fastface_embed_batch_rgb8_device(ff.ff, d_img, B, d_out, stream), "rgb8 dev")
-    check(lib, lib.ffk_stream_sync(stream), "sync")
-    check(lib, lib.ffk_event_record(ev0, stream), "record")
-    for _ in range(K):
+        def host_rate(fn, arr, reps=3):
+            fn(ff.ff, arr.ctypes.data, B, out.ctypes.data)           # capture / warm
+            t = time.perf_counter()
+            for _ in range(reps):
+                check(lib, fn(ff.ff, arr.ctypes.data, B, out.ctypes.data), "host embed")
+            return B * reps / (time.perf_counter() - t)
+        host_fp32 = host_rate(lib.fastface_embed_batch, x)
+        host_rgb8 = host_rate(lib.fastface_embed_batch_rgb8, imgs)
+        d_img = lib.ffk_malloc(imgs.nbytes)
+        check(lib, lib.ffk_memcpy_h2d(d_img, imgs.ctypes.data, imgs.nbytes, stream), "upload rgb8")
         check(lib, lib.fastface_embed_batch_rgb8_device(ff.ff, d_img, B, d_out, stream), "rgb8 dev")
-    check(lib, lib.ffk_event_record(ev1, stream), "record")
-    check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
-    dev_rgb8 = B * K / (ms.value / 1e3)
-    lib.ffk_free(d_img)
-    log("B=%d host buffers: fp32 %.0f faces/s, uint8 RGB %.0f faces/s; uint8 RGB resident %.0f faces/s"
-        % (B, host_fp32, host_rgb8, dev_rgb8))
+        check(lib, lib.ffk_stream_sync(stream), "sync")
+        check(lib, lib.ffk_event_record(ev0, stream), "record")
+        for _ in range(K):
+            check(lib, lib.fastface_embed_batch_rgb8_device(ff.ff, d_img, B, d_out, stream), "rgb8 dev")
+        check(lib, lib.ffk_event_record(ev1, stream), "record")
+        check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
+        dev_rgb8 = B * K / (ms.value / 1e3)
+        lib.ffk_free(d_img)
+        log("B=%d host buffers: fp32 %.0f faces/s, uint8 RGB %.0f faces/s; uint8 RGB resident %.0f faces/s"
+            % (B, host_fp32, host_rgb8, dev_rgb8))
 
     # BASELINE config 5 also runs the stage-1 64-channel 3x3 stride-1 convs as
     # integer Winograd F(2,3): same batch, same timing; the embeddings must be
@@ -384,6 +404,9 @@ def main():
         log("cpu baseline: %.1f %s (%s)" % (cpu["value"], cpu["unit"], cpu["kind"]))
 
     ff.close()
+
+    def rnd(v, n):
+        return None if v is None else round(v, n)
     rec = {
         "metric": METRIC,
         "value": round(faces_per_s, 1),
@@ -403,12 +426,12 @@ def main():
         "config": {"workload": "ArcFace IResNet-50 INT8 forward, B=%d (BASELINE config 5), "
                                "inputs resident in HBM, one hipGraph per step" % B,
                    "global_batch": B, "input": "112x112x3 fp32 NHWC", "parallelism": "single GPU"},
-        "b1_latency_ms": round(b1_ms, 4),
-        "host_fp32_faces_s": round(host_fp32, 1),
-        "host_rgb8_faces_s": round(host_rgb8, 1),
-        "rgb8_resident_faces_s": round(dev_rgb8, 1),
-        "b1_device_ms": round(b1_dev_ms, 4),
-        "b8_ms_per_face": round(b8_ms_face, 5),
+        "b1_latency_ms": rnd(b1_ms, 4),
+        "host_fp32_faces_s": rnd(host_fp32, 1),
+        "host_rgb8_faces_s": rnd(host_rgb8, 1),
+        "rgb8_resident_faces_s": rnd(dev_rgb8, 1),
+        "b1_device_ms": rnd(b1_dev_ms, 4),
+        "b8_ms_per_face": rnd(b8_ms_face, 5),
         "config2_layer": cfg2,
         "chain_int8_tops": round(chain_tops, 2),
         "chain_frac_of_int8_peak": round(chain_tops / PEAK_INT8_TOPS, 4),
@@ -419,7 +442,10 @@ def main():
         "roofline": {"bound": "mfma", "kernel": DOMINANT_KERNEL,
                      "achieved": round(dom_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": round(dom_tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
-                     "launch_ms": round(dom_ms, 5), "ops_per_launch": dom_ops},
+                     "launch_ms": round(dom_ms, 5), "ops_per_launch": dom_ops,
+                     "launch_ms_in_eager_chain": round(dom_chain_ms, 5),
+                     "timing": "26 launches (13 PReLU, 13 residual+BN) in one hipGraph, 20 replays "
+                               "between HIP events on the launch stream"},
         "stage1_winograd": wino,
         "cpu_baseline": cpu,
     }

@@ -22,11 +22,17 @@ import fastface_amd as fa  # noqa: E402
 
 
 def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=200, epi="prelu",
-               winograd=False, no_split=False):
+               winograd=False, no_split=False, graph_reps=0, epis=None):
     """Mean launch time of one conv layer (HIP events on the launch stream)
     over `iters` launches after 3 warm-up launches; frees what it allocates.
     Inputs: seeded int8 U[-127,127] activations and weights (seed 1), ws
-    U[1e-3,1e-2], bias N(0,0.1), PReLU slope 0.25."""
+    U[1e-3,1e-2], bias N(0,0.1), PReLU slope 0.25.
+    epi: prelu | prelu_le1 | add_bn | none | raw; an "_rng" suffix adds
+    FFK_EPI_IN_RANGE (the parameters here satisfy ffk_requant_in_range).
+    graph_reps > 0: the `iters` launches are captured in one hipGraph (epis,
+    if given, cycles the epilogue form per launch) and the graph is replayed
+    graph_reps times between the events: the per-launch time then excludes
+    the host's launch gaps, as a kernel trace's durations do."""
     pad = k // 2
     ho = (hin + 2 * pad - k) // stride + 1
     if not lib.ffk_conv_supported(cin, cout, k, k, stride, pad, hin, hin):
@@ -61,6 +67,8 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
             lib.ffk_memcpy_h2d(p, arr.ctypes.data, n, None)
         return p
     n_out = batch * ho * ho * cout
+    forms = list(epis) if epis else [epi]
+    epi = forms[0]
     d = fa.ffk_conv_desc()
     d.batch, d.cin, d.cout, d.kh, d.kw = batch, cin, cout, k, k
     d.stride, d.pad, d.hin, d.win = stride, pad, hin, hin
@@ -72,12 +80,7 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
         d.out_i32 = dev(nbytes=n_out * 4)
     else:
         d.out = dev(nbytes=n_out)
-    if epi.startswith("prelu"):
-        d.flags |= fa.FFK_EPI_PRELU
-    if epi == "prelu_le1":
-        d.flags |= fa.FFK_EPI_PRELU_LE1
-    if epi == "add_bn":
-        d.flags |= fa.FFK_EPI_ADD | fa.FFK_EPI_BN
+    if any(f.startswith("add_bn") for f in forms):
         d.add_src = dev(r.integers(-127, 128, size=n_out, dtype=np.int8))
         d.out_bn = dev(nbytes=n_out)
         lut = np.empty((cout, 256), np.int8)
@@ -86,6 +89,20 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
         lib.ffk_make_bn_lut(rows[0].ctypes.data, rows[1].ctypes.data, rows[2].ctypes.data,
                             rows[3].ctypes.data, cout, lut.ctypes.data)
         d.bn_lut = dev(lut)
+
+    def form_flags(f):
+        fl = d.flags & (fa.FFK_EPI_BIAS | fa.FFK_ALGO_WINOGRAD)
+        if f.startswith("prelu"):
+            fl |= fa.FFK_EPI_PRELU
+        if f.startswith("prelu_le1"):
+            fl |= fa.FFK_EPI_PRELU_LE1
+        if f.startswith("add_bn"):
+            fl |= fa.FFK_EPI_ADD | fa.FFK_EPI_BN
+        if f.endswith("_rng"):
+            fl |= fa.FFK_EPI_IN_RANGE
+            assert lib.ffk_requant_in_range(P.ctypes.data, cout, k * k * cin, fl) == 1
+        return fl
+    d.flags = form_flags(epi)
     ws_bytes = 0 if no_split else lib.ffk_conv_workspace_bytes(C.byref(d))
     if ws_bytes:
         d.workspace, d.workspace_bytes = dev(nbytes=ws_bytes), ws_bytes
@@ -95,26 +112,48 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
     lib.ffk_stream_create(C.byref(stream))
     lib.ffk_event_create(C.byref(e0))
     lib.ffk_event_create(C.byref(e1))
+    g = C.c_void_p()
+    ms = C.c_float()
     try:
         variant = lib.ffk_conv_variant(C.byref(d))
-        for _ in range(3):
-            assert lib.ffk_conv(C.byref(d), stream) == 0, fa.last_error()
-        lib.ffk_event_record(e0, stream)
-        for _ in range(iters):
-            lib.ffk_conv(C.byref(d), stream)
-        lib.ffk_event_record(e1, stream)
-        ms = C.c_float()
+        descs = []
+        for f in forms:
+            df = fa.ffk_conv_desc.from_buffer_copy(d)
+            df.flags = form_flags(f)
+            if not f.startswith("add_bn"):
+                df.add_src, df.out_bn, df.bn_lut = None, None, None
+            descs.append(df)
+        for i in range(3):
+            assert lib.ffk_conv(C.byref(descs[i % len(descs)]), stream) == 0, fa.last_error()
+        if graph_reps > 0:
+            assert lib.ffk_graph_begin(stream) == 0, fa.last_error()
+            for i in range(iters):
+                assert lib.ffk_conv(C.byref(descs[i % len(descs)]), stream) == 0, fa.last_error()
+            assert lib.ffk_graph_end(stream, C.byref(g)) == 0, fa.last_error()
+            assert lib.ffk_graph_launch(g, stream) == 0, fa.last_error()          # warm
+            lib.ffk_event_record(e0, stream)
+            for _ in range(graph_reps):
+                lib.ffk_graph_launch(g, stream)
+            lib.ffk_event_record(e1, stream)
+        else:
+            lib.ffk_event_record(e0, stream)
+            for i in range(iters):
+                lib.ffk_conv(C.byref(descs[i % len(descs)]), stream)
+            lib.ffk_event_record(e1, stream)
         assert lib.ffk_event_elapsed_ms(e0, e1, C.byref(ms)) == 0, fa.last_error()
     finally:
         lib.ffk_stream_sync(stream)
+        if g.value:
+            lib.ffk_graph_destroy(g)
         lib.ffk_event_destroy(e0)
         lib.ffk_event_destroy(e1)
         lib.ffk_stream_destroy(stream)
         for p in held:
             lib.ffk_free(p)
-    per = ms.value / iters
+    per = ms.value / (iters * max(graph_reps, 1))
     ops = 2.0 * batch * ho * ho * cout * k * k * cin
-    return {"layer": "%d->%d k%d s%d @%d" % (cin, cout, k, stride, hin), "batch": batch, "epi": epi,
+    return {"layer": "%d->%d k%d s%d @%d" % (cin, cout, k, stride, hin), "batch": batch,
+            "epi": "/".join(forms), "graph": graph_reps > 0,
             "kernel": variant.decode() if variant else None, "split_ws_bytes": ws_bytes,
             "ms_per_launch": round(per, 5), "int8_tops": round(ops / (per * 1e-3) / 1e12, 2),
             "frac_of_peak": round(ops / (per * 1e-3) / 5e15, 4)}
@@ -129,7 +168,9 @@ def main():
     ap.add_argument("--hin", type=int, default=14)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--iters", type=int, default=200)
-    ap.add_argument("--epi", default="prelu", choices=["prelu", "prelu_le1", "add_bn", "none", "raw"])
+    ap.add_argument("--epi", default="prelu",
+                    choices=["prelu", "prelu_le1", "add_bn", "none", "raw", "prelu_le1_rng", "add_bn_rng",
+                             "none_rng"])
     ap.add_argument("--winograd", action="store_true",
                     help="64-channel 3x3 stride-1 layers: the integer Winograd F(2,3) path")
     ap.add_argument("--no-split", action="store_true",

@@ -139,7 +139,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the path is per-face data "
-              "parallel; multi-GPU sharding is described in DESIGN.md).", file=sys.stderr)
+              "parallel: N GPUs would each run their own context on a slice of the batch, "
+              "with no exchange inside the forward pass).", file=sys.stderr)
         sys.exit(2)
 
     import fastface_amd

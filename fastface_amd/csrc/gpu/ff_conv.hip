@@ -1327,14 +1327,6 @@ constexpr launch_fn split_launch() {
                 FF_TPATCH_BIG)
 #define FF_P64(CIN, COUT, H, SPLIT) FF_PENTRY_K(CIN, COUT, H, SPLIT, nullptr, FF_TPATCH64)
 #endif
-#ifndef FF_P112
-#define FF_P112(CIN, COUT, H, SPLIT) FF_P64(CIN, COUT, H, SPLIT)
-#endif
-// 64 -> 128 at 56x56 (one 64-channel run): the patch kernel's single-buffer
-// LDS footprint fits two 256x128 workgroups per CU
-#ifndef FF_P56W
-#define FF_P56W(CIN, COUT, H, SPLIT) FF_P(CIN, COUT, H, SPLIT)
-#endif
 
 // split: how many workgroups share the K stages of one small-batch tile (1:
 // never split).  Only the long K chains of stages 3-4 (18 or 36 stages of
@@ -1342,11 +1334,13 @@ constexpr launch_fn split_launch() {
 // workgroups.
 const ConvEntry kConvTable[] = {
     {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem, 1, nullptr, nullptr, "stem"},
-    FF_P112(64, 64, 112, 1),
+    FF_P64(64, 64, 112, 1),
     FF_C64(64, 64, 3, 2, 112, 1),
     FF_C64(64, 64, 1, 2, 112, 1),
     FF_P64(64, 64, 56, 1),
-    FF_P56W(64, 128, 56, 1),
+    // 64 -> 128 at 56x56: one 64-channel run, so the patch kernel's single
+    // input buffer fits two 256x128 workgroups per CU
+    FF_P(64, 128, 56, 1),
     FF_C128(128, 128, 3, 2, 56, 1),
     FF_C128(64, 128, 1, 2, 56, 1),
     FF_P(128, 128, 28, 1),

@@ -410,8 +410,9 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
             if (!rc) rc = enqueue(ff, nb, ff->stream, fmt);
             if (!rc) ff->io_cur = *slot;
         }
-        if (rc) {           /* leave no copy running into the buffers */
+        if (rc) {           /* leave no copy or chunk running into the buffers */
             ffk_stream_sync(ff->cstream);
+            ffk_stream_sync(ff->stream);
             ff->io_cur.in = NULL; ff->io_cur.out = NULL;
         }
     }

@@ -803,7 +803,12 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     constexpr int LA = (PLOADS + NW - 1) / NW;               // patch loads per thread
     constexpr int PATCH_BYTES = PLOADS * 1024;
     constexpr int B_BYTES = BN * DMA_KB;
-    constexpr int B_LD = B_BYTES / (NT * 16);                // weight loads per thread and step
+    // A step's weights are B_BYTES / 1 KB wave loads.  With fewer such loads
+    // than waves (B_PART: 64 output channels over 8 waves) only waves
+    // 0 .. BW-1 load weights, one each; the others load patches only.
+    constexpr int BW = B_BYTES / 1024;
+    constexpr bool B_PART = BW < NW;
+    constexpr int B_LD = B_PART ? 1 : B_BYTES / (NT * 16);   // weight loads per loading thread and step
     constexpr int NSTB = 3;                                  // weight ring depth (9 % 3 == 0)
     constexpr int NPB = CSTEPS > 1 ? 2 : 1;                  // patch buffers (one run: no double buffer)
     constexpr int ZERO_OFF = NPB * PATCH_BYTES;              // 1 KB of zeros
@@ -812,7 +817,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     constexpr int LDS_E = NW * wave_tile_bytes<MI, NJ>() + BN * FF_LUT_PITCH;
     constexpr int LDS = LDS_K > LDS_E ? LDS_K : LDS_E;
     static_assert(CIN % DMA_KB == 0, "Cin must be a multiple of 64");
-    static_assert(B_BYTES % (NT * 16) == 0, "whole wave loads");
+    static_assert(B_BYTES % 1024 == 0 && (B_PART || B_BYTES % (NT * 16) == 0), "whole wave loads");
     static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
     static_assert(B_LD + LA < 64, "load counter range");
     static_assert((2 * W + 2) * PATCH_PITCH + 32 + 16 < 65536, "tap offsets fit the ds_read offset field");
@@ -864,7 +869,9 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
         b_off[j] = (tn * BN + n) * FF_KSTEP + (sl & 3) * 16;
     }
     // step s = c*9 + t: tap t of channel run c, packed weight stage t*CSTEPS + c
+    const bool loads_b = !B_PART || wave < BW;               // (uniform per wave)
     auto issue_b = [&](int c, int t, int slot) {
+        if (!loads_b) return;
         const int8_t* wst = a.w + (size_t)(t * CSTEPS + c) * COUT * FF_KSTEP;
 #pragma unroll
         for (int j = 0; j < B_LD; j++)
@@ -913,14 +920,22 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
         for (int t = 0; t < 9; t++) {
             // loads issued after this step's weights: the next step's weights
             // and, at taps 1-2, the next run's patch (issued at tap 0)
-            if (t == 1 || t == 2) {
-                if (more) dma_wait_barrier<B_LD + LA>();
-                else dma_wait_barrier<B_LD>();
-            } else if (t == 8) {
-                if (more) dma_wait_barrier<B_LD>();
-                else dma_wait_barrier<0>();
+            if (loads_b) {
+                if (t == 1 || t == 2) {
+                    if (more) dma_wait_barrier<B_LD + LA>();
+                    else dma_wait_barrier<B_LD>();
+                } else if (t == 8) {
+                    if (more) dma_wait_barrier<B_LD>();
+                    else dma_wait_barrier<0>();
+                } else {
+                    dma_wait_barrier<B_LD>();
+                }
             } else {
-                dma_wait_barrier<B_LD>();
+                // patch loads only: the next run's (issued at tap 0) may still
+                // be in flight at taps 1-2; from tap 3 on, like the weight
+                // loaders' counts imply, nothing is
+                if ((t == 1 || t == 2) && more) dma_wait_barrier<LA>();
+                else dma_wait_barrier<0>();
             }
             if (t + 2 < 9) issue_b(c, t + 2, (t + 2) % NSTB);
             else if (more) issue_b(c + 1, t + 2 - 9, (t + 2) % NSTB);
@@ -1211,9 +1226,11 @@ struct ConvEntry {
     launch_fn fn;
     int split;          // K split of the small-batch variant (1: no partial tiles)
     launch_fn small;    // 64x64-tile split-K variant, or none
-    launch_fn mid;      // 128x128-tile register-staged variant for grids too small
-                        // for the big direct-to-LDS tiles, or none
+    launch_fn mid;      // variant for grids too small for the big tiles (default:
+                        // the 128x128-tile register-staged kernel), or none
     const char* kind;   // name of `fn` (ffk_conv_variant)
+    int mid_bm, mid_bn; // tile of `mid` when it is not 128x128
+    const char* mid_kind;
 };
 
 // A grid of fewer big tiles than this leaves CUs idle; the 128x128 variant
@@ -1303,6 +1320,12 @@ constexpr launch_fn split_launch() {
 #ifndef FF_TPATCH64
 #define FF_TPATCH64 4, 1, 2, 2, 3
 #endif
+// 64 -> 64 at 56x56: 8 waves -> 512x64 tiles, two workgroups per CU (4 waves
+// per SIMD; half the per-tile setup and patch halo per output; only waves 0-3
+// load a step's 4 KB of weights).  3 % faster there, slower at 112x112.
+#ifndef FF_TPATCH64W
+#define FF_TPATCH64W 8, 1, 2, 2, 4
+#endif
 // Cout >= 256 (stages 3-4)
 #ifndef FF_TPATCH_BIG
 #define FF_TPATCH_BIG FF_TPATCH
@@ -1316,6 +1339,7 @@ constexpr launch_fn split_launch() {
 #define FF_P(CIN, COUT, H, SPLIT) FF_CBIG(CIN, COUT, 3, 1, H, SPLIT)
 #define FF_PB(CIN, COUT, H, SPLIT) FF_CBIG(CIN, COUT, 3, 1, H, SPLIT)
 #define FF_P64(CIN, COUT, H, SPLIT) FF_C64(CIN, COUT, 3, 1, H, SPLIT)
+#define FF_P64W(CIN, COUT, H, SPLIT) FF_C64(CIN, COUT, 3, 1, H, SPLIT)
 #else
 #define FF_P(CIN, COUT, H, SPLIT)                                                   \
     FF_PENTRY_K(CIN, COUT, H, SPLIT,                                                \
@@ -1326,6 +1350,11 @@ constexpr launch_fn split_launch() {
                 (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>), \
                 FF_TPATCH_BIG)
 #define FF_P64(CIN, COUT, H, SPLIT) FF_PENTRY_K(CIN, COUT, H, SPLIT, nullptr, FF_TPATCH64)
+// (small grids: the 256x64 tiles, twice the workgroups)
+#define FF_P64W(CIN, COUT, H, SPLIT)                                                \
+    {CIN, COUT, 3, 1, H, H, 512, 64, &launch_patch<CIN, COUT, H, FF_TPATCH64W>, SPLIT, \
+     split_launch<CIN, COUT, 3, 1, H, SPLIT>(), &launch_patch<CIN, COUT, H, FF_TPATCH64>, "patch", \
+     256, 64, "patch"}
 #endif
 
 // split: how many workgroups share the K stages of one small-batch tile (1:
@@ -1337,7 +1366,7 @@ const ConvEntry kConvTable[] = {
     FF_P64(64, 64, 112, 1),
     FF_C64(64, 64, 3, 2, 112, 1),
     FF_C64(64, 64, 1, 2, 112, 1),
-    FF_P64(64, 64, 56, 1),
+    FF_P64W(64, 64, 56, 1),
     // 64 -> 128 at 56x56: one 64-channel run, so the patch kernel's single
     // input buffer fits two 256x128 workgroups per CU
     FF_P(64, 128, 56, 1),
@@ -1385,8 +1414,9 @@ ConvLaunch choose_launch(const ConvEntry* e, long long M, size_t ws_avail) {
     long long big = ((M + e->bm - 1) / e->bm) * (e->cout / e->bn);
     ConvLaunch l = {e->fn, e->kind, e->bn, (int)big, 1, 0, 0};
     if (e->mid && big < FF_MID_MAX_WG) {
-        big = ((M + 127) / 128) * (e->cout / 128);
-        l = {e->mid, "staged128", 128, (int)big, 1, 0, 0};
+        const int mbm = e->mid_bm ? e->mid_bm : 128, mbn = e->mid_bn ? e->mid_bn : 128;
+        big = ((M + mbm - 1) / mbm) * (e->cout / mbn);
+        l = {e->mid, e->mid_kind ? e->mid_kind : "staged128", mbn, (int)big, 1, 0, 0};
     }
     if (!e->small || big >= FF_SPLIT_MIN_WG) return l;
     const long long tiles = ((M + FF_SM_BM - 1) / FF_SM_BM) * (e->cout / FF_SM_BN);

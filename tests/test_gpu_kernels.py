@@ -611,3 +611,36 @@ def test_in_range_epilogue(gpu_lib, oracle, mode, cin, cout, k, s, H, split):
     if bn:
         exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno, inv_pc=binv)
         assert np.array_equal(got_bn[idx], exp_bn)
+
+
+@pytest.mark.parametrize("mode", ["raw", "add_bn"])
+def test_patch_64_wide_tiles(gpu_lib, oracle, mode):
+    """The 64->64 3x3 layer at 56x56 takes 512x64 tiles (8 waves, waves 0-3
+    loading the weights) from 84 faces on; 91 faces leave a ragged last tile.
+    Bit-exact against the oracle on the first, middle and last image."""
+    B = 91
+    assert _variant(gpu_lib, 64, 64, 3, 1, 56, B) == "patch"
+    r = rng(1400 + len(mode))
+    x = r.integers(-128, 128, size=(B, 56, 56, 64), dtype=np.int8)
+    w = r.integers(-128, 128, size=(64, 64, 3, 3), dtype=np.int8)
+    x[B - 1, -1] = -128
+    idx = [0, B // 2, B - 1]
+    if mode == "raw":
+        got = run_conv(gpu_lib, x, w, 1, 1, raw=True)
+        assert np.array_equal(got[idx], oracle.conv_i32(x[idx], w, 1, 1))
+        return
+    ws, bias, inv = _unsaturated_params(r, 64, 576)
+    add = r.integers(-128, 128, size=(B, 56, 56, 64), dtype=np.int8)
+    adds = r.uniform(1e-3, 5e-2, 64).astype(F32)
+    bsin = r.uniform(1e-3, 5e-2, 64).astype(F32)
+    bns = r.uniform(0.5, 1.5, 64).astype(F32)
+    bno = r.normal(0, 0.05, 64).astype(F32)
+    binv = (1.0 / r.uniform(0.01, 0.1, 64)).astype(F32)
+    P = params_block(64, ws=ws, bias=bias, inv=inv, adds=adds, bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
+    flags = fa.FFK_EPI_BIAS | fa.FFK_EPI_ADD | fa.FFK_EPI_BN | fa.FFK_EPI_IN_RANGE
+    gx, gb = run_conv(gpu_lib, x, w, 1, 1, params=P, flags=flags, add=add, want_bn=True)
+    exp_x = oracle.fused_epilogue(oracle.conv_i32(x[idx], w, 1, 1), ws=ws, bias=bias, inv_pc=inv,
+                                  add_src=add[idx], add_scale_pc=adds)
+    assert np.array_equal(gx[idx], exp_x)
+    assert np.array_equal(gb[idx], oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns,
+                                                           bn_offset=bno, inv_pc=binv))

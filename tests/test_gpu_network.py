@@ -247,3 +247,37 @@ def test_streamed_host_batch_equals_one_shot(ff, gpu_lib):
     assert np.array_equal(got8, dout8.get(np.float32, (B8, 512)))
     assert np.array_equal(ff.embed_batch_rgb8(imgs[2047:2049]), got8[2047:2049])
     assert np.array_equal(ff.embed_batch(x[:3]), got[:3])
+
+
+def test_concurrent_contexts(gpu_lib, synth_ffw4):
+    """One context per thread (fastface.h): two contexts embedding on two
+    threads at once -- each with its own stream, buffers and captured chains
+    -- give the embeddings one context gives alone (the reference Go SDK's
+    concurrent-instances test)."""
+    import threading
+    xs = [synth.faces_uniform(5, 50), synth.faces_uniform(3, 51)]
+    ctxs = [fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT) for _ in range(2)]
+    try:
+        exp = [ctxs[0].embed_batch(x) for x in xs]
+        out, errs = [[], []], []
+
+        def work(i):
+            try:
+                for _ in range(6):
+                    out[i].append(ctxs[i].embed_batch(xs[i]))
+                    out[i].append(ctxs[i].embed(xs[i][0])[None])
+            except Exception as e:          # reported below, in the main thread
+                errs.append(e)
+        th = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+        for t in th:
+            t.start()
+        for t in th:
+            t.join(timeout=60)
+        assert not errs and not any(t.is_alive() for t in th)
+        for i in range(2):
+            for k, got in enumerate(out[i]):
+                want = exp[i] if k % 2 == 0 else exp[i][:1]
+                assert np.array_equal(got, want), (i, k)
+    finally:
+        for c in ctxs:
+            c.close()

@@ -59,6 +59,27 @@ def test_conv_int32_accumulators(gpu_lib, oracle, cin, cout, k, s, H, split):
     assert np.array_equal(got, oracle.conv_i32(x, w, s, k // 2))
 
 
+@pytest.mark.parametrize("B", [2, 23])
+def test_stem_int32_with_fused_input_quant(gpu_lib, oracle, B):
+    """The input layer quantizes the fp32 faces on load (glibc lrintf
+    semantics: +-inf, NaN, |v| >= 2^31, .5 ties) and accumulates int32
+    exactly.  At 23 faces each workgroup walks several tiles, so most tiles
+    fetch only their two new input rows into the ring of patch rows."""
+    r = rng(7 + B)
+    x = r.uniform(-1, 1, size=(B, 112, 112, 3)).astype(F32)
+    x[0, 0, :4, 0] = [0.5 / 127, -2.5 / 127, 1e10, -1e10]
+    x[0, 1, :3, 1] = [np.inf, -np.inf, np.nan]
+    x[1, 5, 5, :] = [3e9, -3e9, 2.5 / 127]
+    x[B - 1, 57, 100, :] = [np.nan, 1e10, -0.0]
+    x[B - 1, 111, 111, :] = [np.inf, 3e9, -1e10]
+    x[B // 2, 64, :3, 2] = [1.5 / 127, -1.5 / 127, 0.49999997 / 127]
+    inv = np.array([127.0, 127.00001, 126.5], F32)
+    w = r.integers(-128, 128, size=(64, 3, 3, 3), dtype=np.int8)
+    got = run_conv(gpu_lib, x, w, 1, 1, raw=True, in_inv=inv)
+    q = oracle.quant_input(x, inv)
+    assert np.array_equal(got, oracle.conv_i32(q, w, 1, 1))
+
+
 @pytest.mark.parametrize("cin,cout,s,H,batches", [(512, 512, 1, 7, (2, 1, 2)),
                                                    (512, 512, 2, 14, (1, 2))])
 def test_split_workspace_reused_across_calls(gpu_lib, oracle, cin, cout, s, H, batches):

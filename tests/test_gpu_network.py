@@ -75,12 +75,14 @@ def test_rgb8_input_equals_sdk_normalized_fp32(ff):
     assert np.array_equal(ff.embed_batch_rgb8(imgs), got)
 
 
-def test_rgb8_stem_kernel_vs_oracle(gpu_lib, oracle):
+@pytest.mark.parametrize("B", [2, 23])
+def test_rgb8_stem_kernel_vs_oracle(gpu_lib, oracle, B):
     """The input layer alone: uint8 pixels -> table -> int32 accumulators,
-    against the oracle's quantization of the SDK-normalized pixels."""
+    against the oracle's quantization of the SDK-normalized pixels (at 23
+    faces workgroups walk several tiles and reuse patch rows)."""
     from gpu_util import run_conv
     r = np.random.default_rng(32)
-    imgs = r.integers(0, 256, size=(2, 112, 112, 3), dtype=np.uint8)
+    imgs = r.integers(0, 256, size=(B, 112, 112, 3), dtype=np.uint8)
     w = r.integers(-128, 128, size=(64, 3, 3, 3), dtype=np.int8)
     inv = np.array([127.0, 126.9, 127.3], np.float32)
     lut = np.empty((3, 256), np.int8)

@@ -60,6 +60,12 @@ constexpr int FF_LUT_PITCH = 272;   // LDS row pitch of a 256-entry table
 // 64 zero bytes: the source of every padding tap / out-of-range row load
 __device__ __align__(64) int8_t ff_zero_page[64];
 
+// Direct-to-LDS load of 16 bytes per lane: lane L of the wave writes
+// lds_wave_base + 16 L (1 KB per wave load); counted by vmcnt.
+__device__ __forceinline__ void dma16(const int8_t* g, int8_t* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+}
+
 struct ConvArgs {
     const int8_t* in;
     const float* in_f32;
@@ -140,7 +146,10 @@ __device__ __forceinline__ int8_t* x_row(const ConvArgs& a, int m) {
 // INSC: f = f * in_scale first (FFW2/FFW3 models; FFW4 skips the multiply).
 // RANGE: every requant value is known in range (FFK_EPI_IN_RANGE).
 // HO x WO: output image size (FFK_OUT_X_EVEN addressing).
-template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC, bool RANGE, int HO, int WO>
+// LUT_DMA: the BN table was issued as direct-to-LDS loads (issue_bn_lut) that
+// may still be in flight; they are waited for before the flush.
+template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC, bool RANGE, int HO, int WO,
+          bool LUT_DMA = false>
 __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                             const EpiParams<NJ>& prm, int mrow0, int ncol0, int8_t* Ws,
                                             const int8_t* Lw) {
@@ -148,6 +157,8 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
     constexpr int ROWS = MI * 32;
     constexpr int CH = NJ * 2;          // 16-byte chunks per tile row
     constexpr int RPI = 64 / CH;        // tile rows per copy instruction
+    constexpr int SPR = P / 16;         // 16-byte slots per tile row (the last one unused)
+    constexpr int RSLOTS = ROWS * SPR;
     const int lane = threadIdx.x & 63;
     const int lc = lane & 31;
     const int lh = lane >> 5;
@@ -156,7 +167,27 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
     const float* p2 = prm.slope;
     const float* adds = prm.adds;
     const float* inv = prm.inv;
-    if (ADD) {      // residual tile -> LDS (coalesced 16-byte loads)
+    if (ADD && RSLOTS % 64 == 0) {
+        // residual tile -> this wave's LDS tile as direct-to-LDS loads: slot s
+        // of wave load k is tile row (64k+s)/SPR, piece (64k+s)%SPR; unused
+        // pieces and rows past M fetch the zero page.  One wait covers them
+        // and any BN-table loads issued before; the tile is this wave's own,
+        // so no barrier.
+        // (opaque: computed here, not folded into values kept across the
+        // main loop)
+        int lane_o = lane, m_o = mrow0;
+        asm volatile("" : "+v"(lane_o), "+v"(m_o));
+#pragma unroll
+        for (int k = 0; k < RSLOTS / 64; k++) {
+            const int slot = k * 64 + lane_o;
+            const int row = slot / SPR;
+            const int pc = slot - row * SPR;
+            const int m = m_o + row;
+            const int8_t* src = pc < CH && m < a.M ? a.add_src + (size_t)m * COUT + ncol0 + pc * 16 : ff_zero_page;
+            dma16(src, Ws + k * 1024);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else if (ADD) {   // residual tile -> LDS (coalesced 16-byte loads)
 #pragma unroll
         for (int k = 0; k < ROWS / RPI; k++) {
             const int row = lane / CH + k * RPI;
@@ -188,6 +219,7 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
                 // every residual read of the wave tile into registers
                 if (r == 15) asm volatile("" ::: "memory");
             }
+    if (BN2 && LUT_DMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     // Flush: 16-byte chunks of the X tile go out as they are; the BN second
     // output maps each byte through its channel's table on the way.
@@ -272,7 +304,7 @@ __device__ __forceinline__ void wave_epilogue_f(const v16i (&acc)[MI][NJ], const
     const bool le1 = !INSC && (a.flags & FFK_EPI_PRELU_LE1);
     const bool rng = !INSC && (a.flags & FFK_EPI_IN_RANGE);
 #define FF_EPI(PR, AD, BN, RG) \
-    wave_epi_i8<COUT, MI, NJ, PR, AD, BN, INSC, RG, HO, WO>(acc, a, P, mrow0, ncol0, Ws, Lw)
+    wave_epi_i8<COUT, MI, NJ, PR, AD, BN, INSC, RG, HO, WO, true>(acc, a, P, mrow0, ncol0, Ws, Lw)
     switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN)) {
     case 0:
         if (rng) FF_EPI(0, false, false, true);
@@ -330,6 +362,32 @@ __device__ __forceinline__ void wave_epilogue(const v16i (&acc)[MI][NJ], const C
         return;
     }
     wave_epilogue_p<COUT, MI, NJ, HO, WO>(acc, a, load_epi_params<COUT, NJ>(a, ncol0), mrow0, ncol0, Ws, Lw);
+}
+
+// BN tables of channels [c0, c0 + NCH) -> LDS (pitch FF_LUT_PITCH) as
+// direct-to-LDS loads, not waited for: wave load b fills LDS slots
+// 64b .. 64b+63 of 16 bytes, slot s being piece s%17 of table s/17 (piece 16
+// is the row padding and fetches the zero page).  The epilogue waits for them
+// (vmcnt) and a barrier before it reads the tables.
+template <int NW, int NCH>
+__device__ __forceinline__ void issue_bn_lut(int8_t* Ls, const int8_t* lut, int c0) {
+    constexpr int SPR = FF_LUT_PITCH / 16;
+    constexpr int BLKS = NCH * SPR / 64;
+    static_assert(FF_LUT_PITCH % 16 == 0 && (NCH * SPR) % 64 == 0, "whole wave loads");
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));           // (opaque, as in the residual loads)
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+#pragma unroll
+    for (int k = 0; k < (BLKS + NW - 1) / NW; k++) {
+        const int blk = k * NW + wave;
+        if (blk < BLKS) {                           // (uniform per wave)
+            const int slot = blk * 64 + lane;
+            const int c = slot / SPR;
+            const int pc = slot - c * SPR;
+            dma16(pc < 16 ? lut + (size_t)(c0 + c) * 256 + pc * 16 : ff_zero_page, Ls + blk * 1024);
+        }
+    }
 }
 
 // BN tables of channels [c0, c0 + nch) -> LDS (pitch FF_LUT_PITCH)
@@ -578,10 +636,7 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
     // epilogue (the loop's last barrier freed the K buffers)
     int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
     int8_t* Ls = smem + 4 * wave_tile_bytes<MI, NJ>();
-    if (a.flags & FFK_EPI_BN && !a.out_i32) {
-        load_bn_lut<256>(Ls, a.bn_lut, tn * BN, BN);
-        __syncthreads();
-    }
+    if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<4, BN>(Ls, a.bn_lut, tn * BN);
     // the FC head runs this kernel as a 1x1 "conv" over a 1x1 image
     wave_epilogue<COUT, MI, NJ, HOUT, WOUT, HIN == 1 && WIN == 1>(acc, a, m0 + wm * WTM, tn * BN + wn * WTN, Ws,
                                 Ls + (wn * WTN) * FF_LUT_PITCH);
@@ -619,10 +674,6 @@ template <int N>
 __device__ __forceinline__ void dma_wait_barrier() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ void dma16(const int8_t* g, int8_t* lds_wave_base) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
 }
 
 template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int WM, int WN, int MI, int NJ,
@@ -757,10 +808,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
 
     int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
     int8_t* Ls = smem + NW * wave_tile_bytes<MI, NJ>();
-    if (a.flags & FFK_EPI_BN && !a.out_i32) {
-        load_bn_lut<NT>(Ls, a.bn_lut, tn * BN, BN);
-        __syncthreads();
-    }
+    if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<NW, BN>(Ls, a.bn_lut, tn * BN);
     wave_epilogue<COUT, MI, NJ, HOUT, WOUT>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
                                 Ls + (wn * NJ * 32) * FF_LUT_PITCH);
 }
@@ -972,10 +1020,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
 
     int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
     int8_t* Ls = smem + NW * wave_tile_bytes<MI, NJ>();
-    if (a.flags & FFK_EPI_BN && !a.out_i32) {
-        load_bn_lut<NT>(Ls, a.bn_lut, tn * BN, BN);
-        __syncthreads();
-    }
+    if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<NW, BN>(Ls, a.bn_lut, tn * BN);
     wave_epilogue<COUT, MI, NJ, H, W>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
                                 Ls + (wn * NJ * 32) * FF_LUT_PITCH);
 }

@@ -2,11 +2,13 @@
 // fastface_gemm_i8_matvec_vnni, libfastface.c:441-455,
 // kernels/gemm_int8_matvec.c:33-81) and the MFMA layout self check.
 //
-// Small batches: HBM-bound matvec.  One wave per output row streams that
-// row's 25088 weight bytes once (16 B per lane per load, v_dot4 signed int8
-// products into exact int32), the batch's activation rows come from L2, and
-// a cross-lane reduction gives the exact dot product per face.  Larger
-// batches use the MFMA conv kernel as a 1x1 GEMM (ff_conv.hip).
+// Small batches: HBM-bound matvec.  Each output row's 25088 weight bytes are
+// streamed once, split over FC_KSPLIT waves (contiguous ranges of K steps,
+// 16 B per lane per load, v_dot4 signed int8 products into exact int32), so
+// that the whole 12.8 MB weight matrix is in flight at once; the batch's
+// activation rows come from L2.  Cross-lane and then cross-wave (LDS) sums
+// give the exact dot product per face.  Larger batches use the MFMA conv
+// kernel as a 1x1 GEMM (ff_conv.hip).
 #include "ff_internal.h"
 #include "ff_numerics.h"
 
@@ -25,42 +27,64 @@ __device__ __forceinline__ int dot16(v4i a, v4i w, int acc) {
     return acc;
 }
 
-// Packed weights: [K/64][N][64] (the conv packing with Cin = K).  Lane l of
-// the wave for row n reads piece (l & 3) of K step (it*16 + l/4).
-__global__ __launch_bounds__(256) void fc_matvec_kernel(const int8_t* __restrict__ a,
-                                                        const int8_t* __restrict__ w,
-                                                        const float* __restrict__ ws,
-                                                        const float* __restrict__ bias,
-                                                        float a_scale, float* out,
-                                                        const ffk_io* io, int B, int N, int K) {
+// Packed weights: [K/64][N][64] (the conv packing with Cin = K).  A
+// workgroup takes FC_ROWS consecutive rows (they share 128-byte weight
+// lines) with FC_KSPLIT waves each; wave (r, q) covers K steps
+// [q*per, (q+1)*per) of row n, lane l reading piece (l & 3) of step
+// q*per + it*16 + l/4.  Integer sums are exact in any order, so the split
+// changes no bit of the result.
+constexpr int FC_ROWS = 2;
+constexpr int FC_KSPLIT = 8;
+constexpr int FC_NT = FC_ROWS * FC_KSPLIT * 64;
+
+__global__ __launch_bounds__(FC_NT) void fc_matvec_kernel(const int8_t* __restrict__ a,
+                                                          const int8_t* __restrict__ w,
+                                                          const float* __restrict__ ws,
+                                                          const float* __restrict__ bias,
+                                                          float a_scale, float* out,
+                                                          const ffk_io* io, int B, int N, int K) {
+    __shared__ int part[FC_ROWS][FC_KSPLIT][FC_MAXB];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int n = blockIdx.x * 4 + wave;
-    if (n >= N) return;
+    const int r = wave / FC_KSPLIT;
+    const int q = wave - r * FC_KSPLIT;
+    const int n = blockIdx.x * FC_ROWS + r;
     const int ksteps = K / FF_KSTEP;
+    const int per = (ksteps + FC_KSPLIT - 1) / FC_KSPLIT;
+    const int s1 = min(ksteps, (q + 1) * per);
     int acc[FC_MAXB];
 #pragma unroll
     for (int b = 0; b < FC_MAXB; b++) acc[b] = 0;
-    for (int s = lane >> 2; s < ksteps; s += 16) {
-        const int kofs = s * FF_KSTEP + (lane & 3) * 16;
-        const v4i wv = *reinterpret_cast<const v4i*>(w + ((size_t)s * N + n) * FF_KSTEP + (lane & 3) * 16);
+    if (n < N) {
+#pragma unroll 4
+        for (int s = q * per + (lane >> 2); s < s1; s += 16) {
+            const int kofs = s * FF_KSTEP + (lane & 3) * 16;
+            const v4i wv = *reinterpret_cast<const v4i*>(w + ((size_t)s * N + n) * FF_KSTEP + (lane & 3) * 16);
 #pragma unroll
-        for (int b = 0; b < FC_MAXB; b++) {
-            if (b < B) {
-                const v4i av = *reinterpret_cast<const v4i*>(a + (size_t)b * K + kofs);
-                acc[b] = dot16(av, wv, acc[b]);
+            for (int b = 0; b < FC_MAXB; b++) {
+                if (b < B) {
+                    const v4i av = *reinterpret_cast<const v4i*>(a + (size_t)b * K + kofs);
+                    acc[b] = dot16(av, wv, acc[b]);
+                }
             }
         }
     }
-    float* o = out ? out : io->out;
 #pragma unroll
     for (int b = 0; b < FC_MAXB; b++) {
         if (b < B) {
             int v = acc[b];
 #pragma unroll
             for (int sh = 32; sh >= 1; sh >>= 1) v += __shfl_xor(v, sh, 64);
-            if (lane == 0) o[(size_t)b * N + n] = ff::fc_out(v, a_scale, ws[n], bias[n]);
+            if (lane == 0) part[r][q][b] = v;
         }
+    }
+    __syncthreads();
+    if (q == 0 && n < N && lane < B) {      // lane b: face b of row n
+        int v = 0;
+#pragma unroll
+        for (int k = 0; k < FC_KSPLIT; k++) v += part[r][k][lane];
+        float* o = out ? out : io->out;
+        o[(size_t)lane * N + n] = ff::fc_out(v, a_scale, ws[n], bias[n]);
     }
 }
 
@@ -132,7 +156,7 @@ int ffk_fc(const ffk_fc_desc* d, void* stream) {
             ffk_set_error("fc: io output needs batch <= 16 on the matvec path%s%s", nullptr, nullptr);
             return FFK_ERR_ARG;
         }
-        hipLaunchKernelGGL(fc_matvec_kernel, dim3((d->n + 3) / 4), dim3(256), 0, s,
+        hipLaunchKernelGGL(fc_matvec_kernel, dim3((d->n + FC_ROWS - 1) / FC_ROWS), dim3(FC_NT), 0, s,
                            d->a + (size_t)b0 * d->k, d->w, d->ws, d->bias, d->a_scale, out, d->io,
                            nb, d->n, d->k);
         int rc = ffk_check_launch("fc matvec launch");

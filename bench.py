@@ -274,7 +274,7 @@ def main():
         if DOMINANT_KERNEL in tj.get("kernel", ""):      # counters of this very kernel only
             traffic = tj.get("bytes_per_launch")
 
-    b1_ms = b1_dev_ms = b8_ms_face = host_fp32 = host_rgb8 = dev_rgb8 = cfg2 = None
+    b1_ms = b1_dev_ms = b1_fc_ms = b8_ms_face = host_fp32 = host_rgb8 = dev_rgb8 = cfg2 = None
     if not args.b1024_only:
         # b=1 latency: host buffers in, host buffers out (fastface_embed), and the
         # device-only chain
@@ -301,6 +301,11 @@ def main():
                 log("b=1 step %2d: %.4f ms  conv %d->%d k%d s%d @%d" % (s, b1_steps[s], st["cin"],
                     st["cout"], st["k"], st["s"], st["hin"]))
             log("b=1 sum of step times %.4f ms" % float(b1_steps.sum()))
+            fc_steps = [s for s in range(n_steps) if steps[s]["kind"] == 2]
+            if fc_steps:
+                b1_fc_ms = float(b1_steps[fc_steps[0]])
+                log("b=1 FC head: %.4f ms, %.0f GB/s of weights" % (b1_fc_ms, steps[fc_steps[0]]["wbytes"]
+                                                                    / (b1_fc_ms * 1e-3) / 1e9))
 
         # B=8 (the reference README's batched operating point),
         # device-resident chain, ms per face
@@ -432,6 +437,7 @@ def main():
         "host_rgb8_faces_s": rnd(host_rgb8, 1),
         "rgb8_resident_faces_s": rnd(dev_rgb8, 1),
         "b1_device_ms": rnd(b1_dev_ms, 4),
+        "b1_fc_ms": rnd(b1_fc_ms, 4),
         "b8_ms_per_face": rnd(b8_ms_face, 5),
         "config2_layer": cfg2,
         "chain_int8_tops": round(chain_tops, 2),

@@ -390,16 +390,6 @@ __device__ __forceinline__ void issue_bn_lut(int8_t* Ls, const int8_t* lut, int 
     }
 }
 
-// BN tables of channels [c0, c0 + nch) -> LDS (pitch FF_LUT_PITCH)
-template <int NT>
-__device__ __forceinline__ void load_bn_lut(int8_t* Ls, const int8_t* lut, int c0, int nch) {
-    for (int idx = threadIdx.x; idx < nch * 16; idx += NT) {
-        const int c = idx >> 4, piece = idx & 15;
-        *reinterpret_cast<v4i*>(Ls + c * FF_LUT_PITCH + piece * 16) =
-            *reinterpret_cast<const v4i*>(lut + (size_t)(c0 + c) * 256 + piece * 16);
-    }
-}
-
 // Workgroup index -> tile.  Workgroups are dispatched round-robin over the 8
 // XCDs; give each XCD a contiguous run of tiles (N fastest) so the tiles that
 // share an im2col row block sit in the same L2.
@@ -1078,9 +1068,10 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
     const float inv1 = rgb8 ? 0.0f : a.in_inv[1];
     const float inv2 = rgb8 ? 0.0f : a.in_inv[2];
 
-    // tile-invariant: the BN table (made visible by the loop's first barrier),
-    // the weight fragments, and where this lane's A operand sits in the patch
-    if (EPI != STEM_EPI_RAW && a.flags & FFK_EPI_BN) load_bn_lut<STEM_NT>(Ls, a.bn_lut, 0, COUT);
+    // tile-invariant: the BN table (direct-to-LDS loads, waited for at the
+    // first tile and made visible by its barrier), the weight fragments, and
+    // where this lane's A operand sits in the patch
+    if (EPI != STEM_EPI_RAW && a.flags & FFK_EPI_BN) issue_bn_lut<STEM_WAVES, COUT>(Ls, a.bn_lut, 0);
     const int p = wave * 32 + (lane & 31);           // 0..223: pixel of the tile
     const int orow = p / W;
     const int ow = p - orow * W;
@@ -1170,6 +1161,9 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
                 Ps[e] = q;
             }
         }
+        // the BN table's loads land before the first tile's barrier (nothing
+        // else is in flight here: the next tile's fetch comes after)
+        if (t == t_beg) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (t + 1 < t_end) fetch(t + 1);
         __syncthreads();
 

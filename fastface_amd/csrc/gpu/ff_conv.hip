@@ -1396,10 +1396,15 @@ constexpr launch_fn split_launch() {
      256, 64, "patch"}
 #endif
 
+#ifndef FF_S2_SPLIT
+#define FF_S2_SPLIT 3
+#endif
 // split: how many workgroups share the K stages of one small-batch tile (1:
-// never split).  Only the long K chains of stages 3-4 (18 or 36 stages of
-// 128 bytes) gain from it; the split is sized so that one face gives 72-144
-// workgroups.
+// never split).  The 3x3 layers with 128 input channels or more gain from it
+// (9, 18 or 36 stages of 128 bytes; the stage-2 layers measured 0.511 ->
+// 0.486 ms for the b=1 chain with 3 ranges of 3 stages); the split is sized
+// so that one face gives 72-156 workgroups.  The 64-channel layers' 9
+// stages of 64 bytes are too short to pay for the partial-sum exchange.
 const ConvEntry kConvTable[] = {
     {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem, 1, nullptr, nullptr, "stem"},
     FF_P64(64, 64, 112, 1),
@@ -1409,10 +1414,10 @@ const ConvEntry kConvTable[] = {
     // 64 -> 128 at 56x56: one 64-channel run, so the patch kernel's single
     // input buffer fits two 256x128 workgroups per CU
     FF_P(64, 128, 56, 1),
-    FF_C128(128, 128, 3, 2, 56, 1),
+    FF_C128(128, 128, 3, 2, 56, FF_S2_SPLIT),
     FF_C128(64, 128, 1, 2, 56, 1),
-    FF_P(128, 128, 28, 1),
-    FF_P(128, 256, 28, 1),
+    FF_P(128, 128, 28, FF_S2_SPLIT),
+    FF_P(128, 256, 28, FF_S2_SPLIT),
     FF_CBIG(256, 256, 3, 2, 28, 6),
     FF_CBIG(128, 256, 1, 2, 28, 1),
     FF_PB(256, 256, 14, 9),

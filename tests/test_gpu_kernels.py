@@ -30,7 +30,8 @@ def test_mfma_lane_layout(gpu_lib):
 
 
 # geometries with a split-K small-batch variant (one face takes it)
-SPLIT_SHAPES = [(256, 256, 3, 2, 28), (256, 256, 3, 1, 14), (256, 512, 3, 1, 14),
+SPLIT_SHAPES = [(128, 128, 3, 2, 56), (128, 128, 3, 1, 28), (128, 256, 3, 1, 28),
+                (256, 256, 3, 2, 28), (256, 256, 3, 1, 14), (256, 512, 3, 1, 14),
                 (512, 512, 3, 2, 14), (512, 512, 3, 1, 7)]
 
 

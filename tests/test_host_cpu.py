@@ -131,7 +131,8 @@ def test_split_workspace_only_for_small_batches():
         d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, k, k
         d.stride, d.pad, d.hin, d.win = s, k // 2, H, H
         return lib.ffk_conv_workspace_bytes(C.byref(d))
-    for cin, cout, s, H in [(256, 256, 2, 28), (256, 256, 1, 14), (256, 512, 1, 14),
+    for cin, cout, s, H in [(128, 128, 2, 56), (128, 128, 1, 28), (128, 256, 1, 28),
+                            (256, 256, 2, 28), (256, 256, 1, 14), (256, 512, 1, 14),
                             (512, 512, 1, 7), (512, 512, 2, 14)]:
         n = need(cin, cout, 3, s, H, 1)
         ho = (H - 1) // s + 1
@@ -141,7 +142,7 @@ def test_split_workspace_only_for_small_batches():
         assert need(cin, cout, 3, s, H, 1024) == 0
     assert need(3, 64, 3, 1, 112, 1) == 0
     assert need(64, 64, 3, 1, 56, 1) == 0             # short K chains never split
-    assert need(128, 256, 3, 1, 28, 1) == 0
+    assert need(64, 128, 3, 1, 56, 1) == 0
     assert need(64, 64, 1, 2, 112, 1) == 0            # 1x1: one K stage, nothing to split
     assert need(96, 64, 3, 1, 112, 1) == 0            # no kernel
     assert lib.ffk_conv_workspace_bytes(None) == 0

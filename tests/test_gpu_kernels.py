@@ -297,6 +297,25 @@ def test_fc_head(gpu_lib, oracle, B, path, split):
         assert np.array_equal(got[b], oracle.fc(a[b], W, ws, bias)), "face %d" % b
 
 
+@pytest.mark.parametrize("B", [1, 2, 16])
+def test_fc_matvec_extreme_values(gpu_lib, oracle, B):
+    """Matvec path (each row's K range split over several waves, partial sums
+    added through LDS) at the largest dot products int8 allows: every product
+    +-128*127, |dot| = 25088*128*127 ~ 4.08e8, plus rows of mixed sign."""
+    r = rng(560 + B)
+    K, N = 25088, 512
+    a = np.full((B, K), -128, np.int8)
+    if B > 1:
+        a[1] = r.integers(-128, 128, size=K, dtype=np.int8)
+    W = np.where(np.arange(N)[:, None] % 2 == 0, 127, -127).astype(np.int8) * np.ones((1, K), np.int8)
+    W[5] = r.integers(-127, 128, size=K, dtype=np.int8)
+    ws = r.uniform(1e-9, 1e-8, N).astype(F32)
+    bias = r.normal(0, 0.05, N).astype(F32)
+    got = run_fc(gpu_lib, a, W, ws, bias, path=1)
+    for b in range(B):
+        assert np.array_equal(got[b], oracle.fc(a[b], W, ws, bias)), "face %d" % b
+
+
 # ---- integer Winograd F(2,3) path of the 64-channel 3x3 stride-1 layers ----
 
 @pytest.mark.parametrize("H,B", [(56, 3), (112, 1)])

@@ -1399,12 +1399,25 @@ constexpr launch_fn split_launch() {
 #ifndef FF_S2_SPLIT
 #define FF_S2_SPLIT 3
 #endif
+#ifndef FF_S3_SPLIT
+#define FF_S3_SPLIT 3
+#endif
+#ifndef FF_S3S2_SPLIT
+#define FF_S3S2_SPLIT 6
+#endif
+#ifndef FF_S4_SPLIT
+#define FF_S4_SPLIT 9
+#endif
 // split: how many workgroups share the K stages of one small-batch tile (1:
 // never split).  The 3x3 layers with 128 input channels or more gain from it
 // (9, 18 or 36 stages of 128 bytes; the stage-2 layers measured 0.511 ->
-// 0.486 ms for the b=1 chain with 3 ranges of 3 stages); the split is sized
-// so that one face gives 72-156 workgroups.  The 64-channel layers' 9
-// stages of 64 bytes are too short to pay for the partial-sum exchange.
+// 0.486 ms for the b=1 chain with 3 ranges of 3 stages).  Each workgroup's
+// partial tile costs an L2 write-back and those serialize per XCD, so fewer
+// splits can win: 256->256 @14 (12 launches at b=1) with 3 instead of 9
+// took the b=1 chain from 0.485 to 0.433 ms; 3 for the stride-2 and
+// 512-channel layers measured the same as their 6 and 9, 2 (and 4) slower.
+// One face gives 48-156 workgroups.  The 64-channel layers' 9 stages of 64
+// bytes are too short to pay for the partial-sum exchange.
 const ConvEntry kConvTable[] = {
     {3, 64, 3, 1, 112, 112, 224, 64, &launch_stem, 1, nullptr, nullptr, "stem"},
     FF_P64(64, 64, 112, 1),
@@ -1418,13 +1431,13 @@ const ConvEntry kConvTable[] = {
     FF_C128(64, 128, 1, 2, 56, 1),
     FF_P(128, 128, 28, FF_S2_SPLIT),
     FF_P(128, 256, 28, FF_S2_SPLIT),
-    FF_CBIG(256, 256, 3, 2, 28, 6),
+    FF_CBIG(256, 256, 3, 2, 28, FF_S3S2_SPLIT),
     FF_CBIG(128, 256, 1, 2, 28, 1),
-    FF_PB(256, 256, 14, 9),
+    FF_PB(256, 256, 14, FF_S3_SPLIT),
     FF_PB(256, 512, 14, 3),
-    FF_CBIG(512, 512, 3, 2, 14, 9),
+    FF_CBIG(512, 512, 3, 2, 14, FF_S4_SPLIT),
     FF_CBIG(256, 512, 1, 2, 14, 1),
-    FF_PB(512, 512, 7, 9),
+    FF_PB(512, 512, 7, FF_S4_SPLIT),
     // the 1x1 shortcuts over a block input stored at its even pixels only
     // (FFK_OUT_X_EVEN): stride 1 over the compact tensor
     FF_C64(64, 64, 1, 1, 56, 1),

@@ -65,6 +65,7 @@ class fastface_step_info(C.Structure):
 EXPORTS = [
     # fastface.h
     ("fastface_create", _p, [C.c_char_p]),
+    ("fastface_create_with_scales", _p, [C.c_char_p, C.c_char_p, C.c_char_p]),
     ("fastface_embed", C.c_int, [_p, _p, _p]),
     ("fastface_destroy", None, [_p]),
     ("fastface_embed_batch", C.c_int, [_p, _p, C.c_int, _p]),
@@ -96,6 +97,7 @@ EXPORTS = [
     ("ffk_event_create", C.c_int, [C.POINTER(_p)]),
     ("ffk_event_destroy", C.c_int, [_p]),
     ("ffk_event_record", C.c_int, [_p, _p]),
+    ("ffk_event_sync", C.c_int, [_p]),
     ("ffk_stream_wait_event", C.c_int, [_p, _p]),
     ("ffk_event_elapsed_ms", C.c_int, [_p, _p, C.POINTER(C.c_float)]),
     ("ffk_graph_begin", C.c_int, [_p]),

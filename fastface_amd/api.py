@@ -19,17 +19,20 @@ from . import FASTFACE_INPUT_N, FASTFACE_OUTPUT_N, load
 class FastFace:
     def __init__(self, weights: str = "models/w600k_r50_ffw4.bin", batch: int = 1,
                  cwd: str | None = None):
-        """`cwd`: directory holding models/op_scales.bin (the C API opens it
-        relative to the working directory, like the reference)."""
+        """`cwd`: directory holding models/op_scales.bin and
+        models/op_scales_v2.bin (fastface_create opens them relative to the
+        working directory, like the reference; with `cwd` they are named
+        explicitly instead, so the process's working directory is left alone
+        and contexts can be created on several threads)."""
         self.lib = load()
         self.batch = int(batch)
-        old = os.getcwd()
+        w = os.path.abspath(weights).encode()
         if cwd:
-            os.chdir(cwd)
-        try:
-            self.ff = self.lib.fastface_create(os.path.abspath(weights).encode())
-        finally:
-            os.chdir(old)
+            opsc = os.path.join(cwd, "models", "op_scales.bin")
+            opsc2 = os.environ.get("OPSC2_PATH") or os.path.join(cwd, "models", "op_scales_v2.bin")
+            self.ff = self.lib.fastface_create_with_scales(w, opsc.encode(), opsc2.encode())
+        else:
+            self.ff = self.lib.fastface_create(w)
         if not self.ff:
             raise RuntimeError("fastface_create failed for %s" % weights)
         if self.batch > 1:

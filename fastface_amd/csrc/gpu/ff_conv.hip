@@ -1289,6 +1289,9 @@ constexpr int FF_MID_MAX_WG = 512;
 // 128-byte stages wherever Cin allows (twice the MFMA work per barrier)
 #define FF_KB(CIN) ((CIN) % 128 == 0 ? 128 : 64)
 #define FF_PFS(CIN) (FF_KB(CIN) == 128 ? FF_PF128 : FF_PF)
+// The 128x128 mid-size variants of the 512-channel layers keep two stages in
+// flight: with three their address registers spilled to scratch.
+#define FF_PF_MID(CIN) ((CIN) >= 512 ? 2 : FF_PFS(CIN))
 #ifdef FF_KB_BIG_V
 #define FF_KB_BIG(CIN) FF_KB_BIG_V
 #define FF_PF_BIG(CIN) FF_PF_BIG_V
@@ -1323,7 +1326,7 @@ constexpr launch_fn split_launch() {
     {CIN, COUT, KS, S, H, H, WM * MI * 32, WN * NJ * 32,                             \
      &launch_conv_dma<CIN, COUT, KS, S, H, H, WM, WN, MI, NJ, NST, WPE>, SPLIT,      \
      split_launch<CIN, COUT, KS, S, H, SPLIT>(),                                     \
-     &launch_conv<CIN, COUT, KS, S, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>, "direct"}
+     &launch_conv<CIN, COUT, KS, S, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>, "direct"}
 #define FF_CONVD_K(CIN, COUT, KS, S, H, SPLIT, TILE) FF_DENTRY(CIN, COUT, KS, S, H, SPLIT, TILE)
 #define FF_CONVD(CIN, COUT, KS, S, H, SPLIT) FF_CONVD_K(CIN, COUT, KS, S, H, SPLIT, FF_TDMA)
 #define FF_DENTRY_NOMID(CIN, COUT, KS, S, H, SPLIT, WM, WN, MI, NJ, NST, WPE)        \
@@ -1382,11 +1385,11 @@ constexpr launch_fn split_launch() {
 #else
 #define FF_P(CIN, COUT, H, SPLIT)                                                   \
     FF_PENTRY_K(CIN, COUT, H, SPLIT,                                                \
-                (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>), \
+                (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>), \
                 FF_TPATCH)
 #define FF_PB(CIN, COUT, H, SPLIT)                                                  \
     FF_PENTRY_K(CIN, COUT, H, SPLIT,                                                \
-                (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PFS(CIN), 2, 2, 2, 1>), \
+                (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>), \
                 FF_TPATCH_BIG)
 #define FF_P64(CIN, COUT, H, SPLIT) FF_PENTRY_K(CIN, COUT, H, SPLIT, nullptr, FF_TPATCH64)
 // (small grids: the 256x64 tiles, twice the workgroups)

@@ -133,6 +133,11 @@ int ffk_event_record(void* ev, void* s) {
     return e == hipSuccess ? FFK_OK : ffk_hip_fail(e, "hipEventRecord");
 }
 
+int ffk_event_sync(void* ev) {
+    hipError_t e = hipEventSynchronize((hipEvent_t)ev);
+    return e == hipSuccess ? FFK_OK : ffk_hip_fail(e, "hipEventSynchronize");
+}
+
 int ffk_stream_wait_event(void* s, void* ev) {
     hipError_t e = hipStreamWaitEvent((hipStream_t)s, (hipEvent_t)ev, 0);
     return e == hipSuccess ? FFK_OK : ffk_hip_fail(e, "hipStreamWaitEvent");

@@ -34,6 +34,17 @@
 /* one captured chain per (batch, input format: 0 fp32 faces, 1 uint8 RGB) */
 typedef struct { int batch, fmt; void* exec; } GraphEntry;
 
+/* Stream ordering.  A context's device state (the I/O descriptor, the
+ * activation buffers, the split-K workspace and its counters, the captured
+ * chains) is used by whatever stream the last call enqueued on: the context
+ * stream, or a caller stream given to a *_device entry point.  After every
+ * enqueue, ev_last is recorded on that stream.  A later enqueue on another
+ * stream first makes that stream wait for ev_last (device-side ordering, no
+ * host wait), and anything that rewrites or frees that state from the host
+ * (the I/O staging slot, buffer growth, graph eviction, destroy) first waits
+ * for ev_last on the host.  So calls on different streams never overlap on
+ * one context's buffers. */
+
 struct FastFace {
     FfModel model;
     FfPlan plan;
@@ -58,11 +69,37 @@ struct FastFace {
     int algo;                   /* FASTFACE_CONV_* of the 64-channel 3x3 s1 layers */
     GraphEntry graphs[FF_MAX_GRAPHS];
     int n_graphs, graph_rr;
+    void* ev_last;              /* recorded after the last enqueue, on last_stream */
+    void* last_stream;          /* stream of the last enqueue (NULL: none pending) */
 };
 
 static void report(const char* what, int rc)
 {
     fprintf(stderr, "fastface: %s failed (%d): %s\n", what, rc, ffk_last_error());
+}
+
+/* host wait for everything this context enqueued (on any stream) */
+static int drain(FastFace* ff)
+{
+    if (!ff->last_stream) return 0;
+    int rc = ffk_event_sync(ff->ev_last);
+    if (!rc) ff->last_stream = NULL;
+    return rc;
+}
+
+/* order `stream` after the context's last enqueue on another stream */
+static int order_after_last(FastFace* ff, void* stream)
+{
+    if (!ff->last_stream || ff->last_stream == stream) return 0;
+    return ffk_stream_wait_event(stream, ff->ev_last);
+}
+
+/* record the end of an enqueue on `stream` */
+static int mark_enqueued(FastFace* ff, void* stream)
+{
+    int rc = ffk_event_record(ff->ev_last, stream);
+    if (!rc) ff->last_stream = stream;
+    return rc;
 }
 
 static void drop_graphs(FastFace* ff)
@@ -88,11 +125,16 @@ static void free_activations(FastFace* ff)
     ff->capacity = 0;
 }
 
+/* Point the device I/O descriptor at (in, out) for work enqueued next on
+ * `stream`.  Unchanged pointers: nothing to do (the enqueue orders itself
+ * after the last one).  Changed: every earlier enqueue of this context, on
+ * any stream, may still read the descriptor or the staging slot, so wait for
+ * them on the host first. */
 static int set_io(FastFace* ff, const float* in, float* out, void* stream)
 {
     if (ff->io_cur.in == in && ff->io_cur.out == out) return 0;
-    /* the staging slot may still feed an earlier copy: drain first */
-    int rc = ffk_stream_sync(ff->stream);
+    int rc = drain(ff);
+    if (!rc) rc = ffk_stream_sync(ff->stream);
     if (!rc && stream != ff->stream) rc = ffk_stream_sync(stream);
     if (rc) return rc;
     ff->h_io->in = in;
@@ -140,7 +182,8 @@ static size_t workspace_bytes(FastFace* ff, int max_batch)
 static int ensure_capacity(FastFace* ff, int batch)
 {
     if (batch <= ff->capacity) return 0;
-    int rc = ffk_stream_sync(ff->stream);
+    int rc = drain(ff);
+    if (!rc) rc = ffk_stream_sync(ff->stream);
     if (rc) return rc;
     free_activations(ff);
     FfPlan* p = &ff->plan;
@@ -257,7 +300,11 @@ static int run_direct(FastFace* ff, int batch, void* stream, int fmt)
     return 0;
 }
 
-static void* graph_for(FastFace* ff, int batch, int fmt)
+/* The captured chain for (batch, fmt), capturing it on first use.  A full
+ * cache evicts round-robin, never the entry holding `keep` (a chain the
+ * caller is about to launch); an evicted chain may still be in flight, so
+ * the context's work is waited for before it is destroyed. */
+static void* graph_for(FastFace* ff, int batch, int fmt, const void* keep)
 {
     for (int i = 0; i < ff->n_graphs; i++)
         if (ff->graphs[i].batch == batch && ff->graphs[i].fmt == fmt) return ff->graphs[i].exec;
@@ -267,25 +314,50 @@ static void* graph_for(FastFace* ff, int batch, int fmt)
     int rc2 = ffk_graph_end(ff->stream, &exec);
     if (rc || rc2) { if (exec) ffk_graph_destroy(exec); return NULL; }
     int slot;
-    if (ff->n_graphs < FF_MAX_GRAPHS) slot = ff->n_graphs++;
-    else { slot = ff->graph_rr; ff->graph_rr = (ff->graph_rr + 1) % FF_MAX_GRAPHS;
-           ffk_graph_destroy(ff->graphs[slot].exec); }
+    if (ff->n_graphs < FF_MAX_GRAPHS) {
+        slot = ff->n_graphs++;
+    } else {
+        slot = ff->graph_rr;
+        if (ff->graphs[slot].exec == keep) slot = (slot + 1) % FF_MAX_GRAPHS;
+        ff->graph_rr = (slot + 1) % FF_MAX_GRAPHS;
+        if (drain(ff) || ffk_stream_sync(ff->stream)) { ffk_graph_destroy(exec); return NULL; }
+        ffk_graph_destroy(ff->graphs[slot].exec);
+    }
     ff->graphs[slot].batch = batch;
     ff->graphs[slot].fmt = fmt;
     ff->graphs[slot].exec = exec;
     return exec;
 }
 
-/* enqueue one batch whose I/O pointers are already in d_io */
+/* Enqueue one batch whose I/O pointers are already in d_io: ordered after
+ * the context's last enqueue (whatever stream that was on), then marked as
+ * the new last one.  `exec`: a chain already looked up, or NULL. */
+static int enqueue_exec(FastFace* ff, int batch, void* stream, int fmt, void* exec)
+{
+    int rc = order_after_last(ff, stream);
+    if (rc) return rc;
+    if (ff->keep_all) {
+        rc = run_direct(ff, batch, stream, fmt);
+    } else {
+        void* g = exec ? exec : graph_for(ff, batch, fmt, NULL);
+        rc = g ? ffk_graph_launch(g, stream) : FFK_ERR_HIP;
+    }
+    if (!rc) rc = mark_enqueued(ff, stream);
+    return rc;
+}
+
 static int enqueue(FastFace* ff, int batch, void* stream, int fmt)
 {
-    if (ff->keep_all) return run_direct(ff, batch, stream, fmt);
-    void* g = graph_for(ff, batch, fmt);
-    if (!g) return FFK_ERR_HIP;
-    return ffk_graph_launch(g, stream);
+    return enqueue_exec(ff, batch, stream, fmt, NULL);
 }
 
 FastFace* fastface_create(const char* ffw4_path)
+{
+    return fastface_create_with_scales(ffw4_path, NULL, NULL);
+}
+
+FastFace* fastface_create_with_scales(const char* ffw4_path, const char* opsc_path,
+                                      const char* opsc2_path)
 {
     if (!ffw4_path) return NULL;
     if (ffk_device_count() <= 0) {
@@ -294,9 +366,9 @@ FastFace* fastface_create(const char* ffw4_path)
     }
     FastFace* ff = (FastFace*)calloc(1, sizeof(FastFace));
     if (!ff) return NULL;
-    const char* v2 = getenv("OPSC2_PATH");
+    const char* v2 = opsc2_path ? opsc2_path : getenv("OPSC2_PATH");
     if (!v2) v2 = "models/op_scales_v2.bin";
-    if (ff_model_load(&ff->model, ffw4_path, "models/op_scales.bin", v2) != 0) {
+    if (ff_model_load(&ff->model, ffw4_path, opsc_path ? opsc_path : "models/op_scales.bin", v2) != 0) {
         free(ff);
         return NULL;
     }
@@ -315,6 +387,7 @@ FastFace* fastface_create(const char* ffw4_path)
     if (ffk_stream_create(&ff->cstream)) { report("stream", FFK_ERR_HIP); goto fail; }
     for (int k = 0; k < FF_MAX_CHUNKS; k++)
         if (ffk_event_create(&ff->ev_chunk[k])) { report("event", FFK_ERR_HIP); goto fail; }
+    if (ffk_event_create(&ff->ev_last)) { report("event", FFK_ERR_HIP); goto fail; }
     if (!ff->d_weights || !ff->d_params || !ff->d_in_inv || !ff->d_in_lut || !ff->d_io || !ff->h_io) {
         report("device allocation", FFK_ERR_NOMEM);
         goto fail;
@@ -346,6 +419,7 @@ fail:
 void fastface_destroy(FastFace* ff)
 {
     if (!ff) return;
+    if (ff->ev_last) drain(ff);
     if (ff->stream) ffk_stream_sync(ff->stream);
     free_activations(ff);
     ffk_free(ff->d_weights);
@@ -357,6 +431,7 @@ void fastface_destroy(FastFace* ff)
     if (ff->cstream) { ffk_stream_sync(ff->cstream); ffk_stream_destroy(ff->cstream); }
     for (int k = 0; k < FF_MAX_CHUNKS; k++)
         if (ff->ev_chunk[k]) ffk_event_destroy(ff->ev_chunk[k]);
+    if (ff->ev_last) ffk_event_destroy(ff->ev_last);
     if (ff->stream) ffk_stream_destroy(ff->stream);
     ff_plan_free(&ff->plan);
     ff_model_free(&ff->model);
@@ -381,7 +456,10 @@ void* fastface_stream(FastFace* ff) { return ff ? ff->stream : NULL; }
  * path's bit for bit. */
 static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, int batch, float* out)
 {
-    int rc = ensure_capacity(ff, batch);
+    /* a host call is synchronous: first let any device call still running
+     * on a caller stream finish with the context's buffers */
+    int rc = drain(ff);
+    if (!rc) rc = ensure_capacity(ff, batch);
     if (rc) { report("activation allocation", rc); return -2; }
     int8_t* d_in = fmt ? (int8_t*)ff->d_input_u8 : (int8_t*)ff->d_input;
     const size_t out_bytes = (size_t)batch * FASTFACE_OUTPUT_N * sizeof(float);
@@ -393,9 +471,12 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
         if (!rc) rc = ffk_memcpy_h2d(d_in, in, (size_t)batch * face_bytes, ff->stream);
         if (!rc) rc = enqueue(ff, batch, ff->stream, fmt);
     } else {
-        /* capture the chains first: no capture while copies are being issued */
+        /* capture both chains before any copy is issued (the second lookup
+         * may not evict the first), and launch them directly */
         const int last = batch - (n - 1) * chunk;
-        if (!graph_for(ff, chunk, fmt) || !graph_for(ff, last, fmt)) rc = FFK_ERR_HIP;
+        void* g_chunk = graph_for(ff, chunk, fmt, NULL);
+        void* g_last = g_chunk ? graph_for(ff, last, fmt, g_chunk) : NULL;
+        if (!g_chunk || !g_last) rc = FFK_ERR_HIP;
         for (int k = 0; k < n && !rc; k++) {
             const size_t b0 = (size_t)k * chunk;
             const int nb = k + 1 < n ? chunk : last;
@@ -407,7 +488,7 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
             slot->in = (const float*)(d_in + b0 * face_bytes);
             slot->out = ff->d_output + b0 * FASTFACE_OUTPUT_N;
             if (!rc) rc = ffk_memcpy_h2d(ff->d_io, slot, sizeof(ffk_io), ff->stream);
-            if (!rc) rc = enqueue(ff, nb, ff->stream, fmt);
+            if (!rc) rc = enqueue_exec(ff, nb, ff->stream, fmt, k + 1 < n ? g_chunk : g_last);
             if (!rc) ff->io_cur = *slot;
         }
         if (rc) {           /* leave no copy or chunk running into the buffers */
@@ -418,6 +499,7 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
     }
     if (!rc) rc = ffk_memcpy_d2h(out, ff->d_output, out_bytes, ff->stream);
     if (!rc) rc = ffk_stream_sync(ff->stream);
+    if (!rc) ff->last_stream = NULL;        /* all of it has finished */
     if (rc) { report("embed", rc); return -3; }
     return 0;
 }
@@ -477,7 +559,7 @@ int fastface_set_conv_algo(FastFace* ff, int algo)
         for (int s = 0; s < ff->plan.n_steps; s++)
             if (ff->plan.steps[s].kind == 1 && ff->plan.steps[s].wino_off != (size_t)-1) n++;
     if (algo == ff->algo) return n;
-    if (ffk_stream_sync(ff->stream)) return -2;
+    if (drain(ff) || ffk_stream_sync(ff->stream)) return -2;
     /* other launch chains, and another workspace size */
     const int cap = ff->capacity;
     free_activations(ff);
@@ -528,7 +610,8 @@ int fastface_get_step(const FastFace* ff, int s, fastface_step_info* info)
 int fastface_profile_steps(FastFace* ff, int batch, int reps, float* step_ms)
 {
     if (!ff || !step_ms || batch < 1 || reps < 1) return -1;
-    int rc = ensure_capacity(ff, batch);
+    int rc = drain(ff);
+    if (!rc) rc = ensure_capacity(ff, batch);
     if (!rc) rc = set_io(ff, ff->d_input, ff->d_output, ff->stream);
     if (rc) return -2;
     const int n = ff->plan.n_steps;
@@ -550,14 +633,15 @@ int fastface_profile_steps(FastFace* ff, int batch, int reps, float* step_ms)
     }
     for (int s = 0; s <= n; s++) if (ev[s]) ffk_event_destroy(ev[s]);
     free(ev);
-    if (rc) { report("profile", rc); return -3; }
+    if (rc) { report("profile", rc); ffk_stream_sync(ff->stream); return -3; }
     return n;
 }
 
 int fastface_debug_keep_tensors(FastFace* ff, int on)
 {
     if (!ff) return -1;
-    int rc = ffk_stream_sync(ff->stream);
+    int rc = drain(ff);
+    if (!rc) rc = ffk_stream_sync(ff->stream);
     if (rc) return -3;
     int cap = ff->capacity;
     free_activations(ff);
@@ -574,6 +658,7 @@ long long fastface_debug_read(FastFace* ff, int op_idx, int batch, void* host, s
         if (T->op != op_idx || T->buf < 0) continue;
         size_t n = (size_t)T->C * T->H * T->W * (size_t)batch;
         if (n > bytes) return -4;
+        if (drain(ff)) return -3;
         if (ffk_memcpy_d2h(host, ff->d_bufs[T->buf], n, ff->stream) || ffk_stream_sync(ff->stream))
             return -3;
         return (long long)n;

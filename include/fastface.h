@@ -48,7 +48,17 @@ void fastface_destroy(FastFace* ff);
 #define FASTFACE_OUTPUT_N 512
 
 /* ---------------- additive extensions (no reference counterpart) --------
- * Batched embedding.  Face i of the batch gives exactly the embedding that
+ * fastface_create with the scale files named explicitly instead of found
+ * relative to the working directory: opsc_path replaces
+ * "models/op_scales.bin" (NULL: that default), opsc2_path replaces
+ * $OPSC2_PATH / "models/op_scales_v2.bin" (NULL: those defaults).  For
+ * callers that must not change the process's working directory (several
+ * threads creating contexts).  fastface_create(p) is
+ * fastface_create_with_scales(p, NULL, NULL). */
+FastFace* fastface_create_with_scales(const char* ffw4_path, const char* opsc_path,
+                                      const char* opsc2_path);
+
+/* Batched embedding.  Face i of the batch gives exactly the embedding that
  * fastface_embed gives for face i alone (the reference's own invariant: its
  * batched driver, arcface_forward_int8_batched.c, is bit-identical per face).
  * Host buffers: batch*37632 floats in, batch*512 floats out.  A batch of

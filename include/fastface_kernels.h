@@ -45,6 +45,7 @@ int   ffk_stream_sync(void* stream);            /* NULL: device-wide sync */
 int   ffk_event_create(void** event);
 int   ffk_event_destroy(void* event);
 int   ffk_event_record(void* event, void* stream);
+int   ffk_event_sync(void* event);              /* host waits for the event */
 /* later work on `stream` waits for `event` (recorded on another stream) */
 int   ffk_stream_wait_event(void* stream, void* event);
 int   ffk_event_elapsed_ms(void* start, void* stop, float* ms);

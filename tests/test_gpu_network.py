@@ -283,3 +283,47 @@ def test_concurrent_contexts(gpu_lib, synth_ffw4):
     finally:
         for c in ctxs:
             c.close()
+
+
+def test_device_calls_on_caller_streams_are_ordered(gpu_lib, synth_ffw4, oracle, oracle_model):
+    """Device calls on two caller streams, interleaved with host calls on the
+    context stream and with no host wait in between, never overlap on the
+    context's I/O descriptor, activation buffers or split-K workspace: each
+    call's embeddings equal the oracle's.  One face takes the split-K kernels
+    (arrival counters in the workspace); an overlap would leave a counter
+    wrong and corrupt every later small batch, so the sequence repeats."""
+    f = fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT)
+    streams = [C.c_void_p(), C.c_void_p()]
+    for s in streams:
+        check(gpu_lib, gpu_lib.ffk_stream_create(C.byref(s)))
+    try:
+        x = synth.faces_uniform(4, 61)
+        exp, _ = oracle.forward(oracle_model, x)
+        din = [Dev(gpu_lib, host=x[i:i + 1]) for i in range(3)]
+        din3 = Dev(gpu_lib, host=x[:3])
+        outs = []
+        for rep in range(4):
+            o = [Dev(gpu_lib, nbytes=512 * 4) for _ in range(3)]
+            o3 = Dev(gpu_lib, nbytes=3 * 512 * 4)
+            s1, s2 = streams[rep % 2], streams[1 - rep % 2]
+            assert gpu_lib.fastface_embed_batch_device(f.ff, din[0].ptr, 1, o[0].ptr, s1) == 0
+            host1 = f.embed(x[3])                                   # context stream, b=1
+            assert gpu_lib.fastface_embed_batch_device(f.ff, din3.ptr, 3, o3.ptr, s2) == 0
+            assert gpu_lib.fastface_embed_batch_device(f.ff, din[1].ptr, 1, o[1].ptr, s1) == 0
+            # same I/O pointers as the previous call, another stream
+            assert gpu_lib.fastface_embed_batch_device(f.ff, din[1].ptr, 1, o[1].ptr, s2) == 0
+            assert gpu_lib.fastface_embed_batch_device(f.ff, din[2].ptr, 1, o[2].ptr, None) == 0
+            outs.append((o, o3, host1))
+        for s in streams:
+            check(gpu_lib, gpu_lib.ffk_stream_sync(s))
+        check(gpu_lib, gpu_lib.ffk_stream_sync(gpu_lib.fastface_stream(f.ff)))
+        for rep, (o, o3, host1) in enumerate(outs):
+            assert np.array_equal(host1, exp[3]), rep
+            for i in range(3):
+                assert np.array_equal(o[i].get(np.float32, (512,)), exp[i]), (rep, i)
+            assert np.array_equal(o3.get(np.float32, (3, 512)), exp[:3]), rep
+        assert np.array_equal(f.embed(x[0]), exp[0])
+    finally:
+        for s in streams:
+            gpu_lib.ffk_stream_destroy(s)
+        f.close()

@@ -57,6 +57,7 @@ class Oracle:
                                            C.c_float, _i8p, C.c_int, C.c_int]
         L.orc_add_requant.argtypes = [_i8p, C.c_float, _i8p, C.c_float, _i8p,
                                       C.c_float, C.c_int]
+        L.orc_quant_input_pt.argtypes = [_f32p, C.c_int, C.c_float, _i8p]
         L.orc_fc.argtypes = [_i8p, _i8p, _f32p, _f32p, C.c_float, _f32p, C.c_int, C.c_int]
         L.orc_model_load.argtypes = [C.c_char_p, C.c_char_p, C.c_char_p]
         L.orc_model_load.restype = _p
@@ -78,6 +79,13 @@ class Oracle:
         out = np.empty(x.shape, np.int8)
         self.lib.orc_quant_input_pc(x.reshape(-1), x.size // C_, C_,
                                     np.ascontiguousarray(inv_pc, np.float32), out.reshape(-1))
+        return out
+
+    def quant_input_pt(self, x, scale):
+        """Per-tensor input quantization (the OPSC-only path)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = np.empty(x.size, np.int8)
+        self.lib.orc_quant_input_pt(x, x.size, scale, out)
         return out
 
     def conv_i32(self, x, w_oihw, stride, pad):
@@ -217,6 +225,7 @@ class Ref:
         L.bn_prelu_requant_int8.argtypes = [_i8p, C.c_float, _p, _p, _p, _p, _p, C.c_float,
                                             _i8p, C.c_int, C.c_int]
         L.quantize_fp32_nhwc_to_int8_per_channel.argtypes = [_f32p, C.c_int, C.c_int, _f32p, _i8p]
+        L.quantize_fp32_nhwc_to_int8.argtypes = [_f32p, C.c_int, C.c_float, _i8p]
         L.add_requant_int8.argtypes = [_i8p, C.c_float, _i8p, C.c_float, _i8p, C.c_float, C.c_int]
         L.pack_conv_weight_nhwc.argtypes = [_i8p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                             _i8p, _i8p, _i32p]
@@ -281,6 +290,12 @@ class Ref:
         self.lib.quantize_fp32_nhwc_to_int8_per_channel(
             x.reshape(-1), x.size // C_, C_, np.ascontiguousarray(inv_pc, np.float32),
             out.reshape(-1))
+        return out
+
+    def quant_input_pt(self, x, scale):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = np.empty(x.size, np.int8)
+        self.lib.quantize_fp32_nhwc_to_int8(x, x.size, C.c_float(scale), out)
         return out
 
     def add_requant(self, a, a_scale, b, b_scale, out_scale):

@@ -1,0 +1,176 @@
+"""The model loader and launch planner (ff_model.c, ff_plan.c) on valid,
+truncated and corrupt weight and scale files, run under AddressSanitizer and
+UndefinedBehaviorSanitizer (fastface_amd/csrc/host/ff_loader_check.c, built
+by `make -C fastface_amd/csrc san`; CPU only).
+
+Acceptance rules follow the reference (kernels/ffw2_loader.c:96-155,
+libfastface.c:133-204,235-240): a weights file with a bad magic, an unknown
+op type or missing bytes, and an OPSC file that is missing, malformed or has
+another op count, make create fail (NULL); an OPSC2 file that is missing,
+malformed or has another op count is dropped and the per-tensor OPSC scales
+are used (the reference degrades the same way; unlike it, a mid-file OPSC2
+error drops the whole file rather than keeping the tables read so far).
+The reference reads its mmapped file without bounds checks, so truncation
+has no reference behaviour to match: here it is an error.
+"""
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+from fastface_amd import synth
+
+ROOT = synth.REPO_ROOT
+CSRC = os.path.join(ROOT, "fastface_amd", "csrc")
+EXE = os.path.join(CSRC, "_build", "san", "ff_loader_check")
+LIB = os.path.join(ROOT, "fastface_amd", "lib", "libfastface_amd.so")
+
+
+@pytest.fixture(scope="module")
+def checker():
+    if not os.path.exists(LIB):
+        pytest.skip("library not built")
+    subprocess.run(["make", "-s", "-C", CSRC, "san"], check=True, capture_output=True)
+    return EXE
+
+
+def run(exe, ffw, opsc=synth.OPSC_PATH, opsc2=synth.OPSC2_PATH):
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0",
+               UBSAN_OPTIONS="print_stacktrace=1")
+    r = subprocess.run([exe, ffw, opsc, opsc2 or "-"], capture_output=True, text=True, env=env,
+                       timeout=120)
+    assert r.returncode == 0, "sanitizer or crash:\n" + r.stderr[-3000:]
+    assert "runtime error" not in r.stderr and "AddressSanitizer" not in r.stderr, r.stderr[-3000:]
+    out = {}
+    for line in r.stdout.splitlines():
+        t = line.split()
+        for k, v in zip(t[0::2], t[1::2]):
+            out.setdefault(k, v)
+    return out
+
+
+def op_offsets(blob):
+    """Byte offset of every op record of an FFW3/FFW4 blob (the layout
+    kernels/ffw2_loader.c:96-155 parses), and the end offset."""
+    n = struct.unpack_from("<I", blob, 4)[0]
+    off, offs = 8, []
+    for _ in range(n):
+        offs.append(off)
+        t = blob[off]
+        off += 1
+        if t == synth.OP_CONV:
+            cin, cout, kh, kw = struct.unpack_from("<4H", blob, off)
+            off += 12 + cout * cin * kh * kw + 8 * cout
+        elif t in (synth.OP_BN,):
+            c = struct.unpack_from("<H", blob, off)[0]
+            off += 2 + 8 * c
+        elif t == synth.OP_PRELU:
+            c = struct.unpack_from("<H", blob, off)[0]
+            off += 2 + 4 * c
+        elif t == synth.OP_GEMM:
+            N, K = struct.unpack_from("<2I", blob, off)
+            off += 8 + N * K + 8 * N
+    return offs, off
+
+
+@pytest.fixture(scope="module")
+def blob(synth_ffw4):
+    with open(synth_ffw4, "rb") as f:
+        return f.read()
+
+
+def write(tmp_path, name, data):
+    p = tmp_path / name
+    p.write_bytes(bytes(data))
+    return str(p)
+
+
+def test_valid_model_loads_and_plans(checker, synth_ffw4):
+    o = run(checker, synth_ffw4)
+    assert o["load"] == "0" and o["version"] == "4" and o["ops"] == "177" and o["v2"] == "1"
+    assert o["plan"] == "0" and o["steps"] == "54"
+    o = run(checker, synth_ffw4, opsc2=None)            # OPSC only: per-tensor scales
+    assert o["load"] == "0" and o["v2"] == "0" and o["plan"] == "0"
+
+
+def test_layout_walk_matches_file(blob):
+    offs, end = op_offsets(blob)
+    assert len(offs) == 177 and end == len(blob)
+
+
+def test_truncated_weights_fail(checker, blob, tmp_path):
+    offs, end = op_offsets(blob)
+    gemm = [o for o in offs if blob[o] == synth.OP_GEMM][0]
+    cuts = [0, 3, 7, 8, offs[0] + 5, offs[0] + 20, offs[5] + 1, gemm + 6, gemm + 5000, end - 1]
+    for cut in cuts:
+        o = run(checker, write(tmp_path, "t%d.ffw" % cut, blob[:cut]))
+        assert o["load"] != "0", cut
+
+
+def test_corrupt_weights_fail(checker, blob, tmp_path):
+    offs, _ = op_offsets(blob)
+    bad_magic = bytearray(blob)
+    bad_magic[:4] = b"FFWX"
+    bad_op = bytearray(blob)
+    bad_op[offs[5]] = 99                                  # unknown op type
+    zero_ops = bytearray(blob)
+    struct.pack_into("<I", zero_ops, 4, 0)
+    many_ops = bytearray(blob)
+    struct.pack_into("<I", many_ops, 4, 0x7FFFFFFF)
+    big_conv = bytearray(blob)
+    struct.pack_into("<H", big_conv, offs[0] + 3, 0xFFFF)  # Cout of the stem
+    gemm = [o for o in offs if blob[o] == synth.OP_GEMM][0]
+    big_gemm = bytearray(blob)
+    struct.pack_into("<2I", big_gemm, gemm + 1, 0xFFFFFFFF, 0xFFFFFFFF)
+    for name, data in [("magic", bad_magic), ("op", bad_op), ("zero", zero_ops),
+                       ("many", many_ops), ("conv", big_conv), ("gemm", big_gemm)]:
+        o = run(checker, write(tmp_path, name + ".ffw", data))
+        assert o["load"] != "0", name
+
+
+def test_opsc_errors_fail(checker, synth_ffw4, tmp_path):
+    with open(synth.OPSC_PATH, "rb") as f:
+        opsc = f.read()
+    n = struct.unpack_from("<I", opsc, 4)[0]
+    assert n == 177
+    fewer = bytearray(opsc[:12 + 176 * 4])
+    struct.pack_into("<I", fewer, 4, 176)                # n_ops mismatch
+    cases = {"missing": str(tmp_path / "nope.bin"),
+             "magic": write(tmp_path, "m.bin", b"OPSX" + opsc[4:]),
+             "truncated": write(tmp_path, "t.bin", opsc[:100]),
+             "mismatch": write(tmp_path, "n.bin", fewer),
+             "empty": write(tmp_path, "e.bin", b"")}
+    for name, path in cases.items():
+        o = run(checker, synth_ffw4, opsc=path)
+        assert o["load"] != "0", name
+
+
+def test_opsc2_errors_degrade_to_per_tensor(checker, synth_ffw4, tmp_path):
+    with open(synth.OPSC2_PATH, "rb") as f:
+        v2 = f.read()
+    mism = bytearray(v2)
+    struct.pack_into("<I", mism, 5, 176)
+    huge = bytearray(v2)
+    struct.pack_into("<I", huge, 9, 0xFFFFFFFF)           # input channel count
+    cases = {"missing": str(tmp_path / "nope2.bin"),
+             "magic": write(tmp_path, "m2.bin", b"OPSCX" + v2[5:]),
+             "mismatch": write(tmp_path, "n2.bin", mism),
+             "truncated_mid": write(tmp_path, "t2.bin", v2[:len(v2) // 2]),
+             "truncated_end": write(tmp_path, "u2.bin", v2[:-1]),
+             "huge_in": write(tmp_path, "h2.bin", huge)}
+    for name, path in cases.items():
+        o = run(checker, synth_ffw4, opsc2=path)
+        assert o["load"] == "0" and o["v2"] == "0" and o["plan"] == "0", name
+
+
+def test_unsupported_op_sequence_fails_plan(checker, tmp_path):
+    """A stand-alone PReLU (no conv before it) is a valid file the planner
+    rejects with a message: create fails instead of running it otherwise."""
+    ffw = b"FFW4" + struct.pack("<I", 1) + bytes([synth.OP_PRELU]) + struct.pack("<H", 3) + \
+        np.full(3, 0.25, np.float32).tobytes()
+    opsc = b"OPSC" + struct.pack("<I", 1) + np.float32(1 / 127).tobytes() + \
+        np.float32(0.05).tobytes()
+    o = run(checker, write(tmp_path, "p.ffw", ffw), opsc=write(tmp_path, "p.bin", opsc), opsc2=None)
+    assert o["load"] == "0" and o["plan"] != "0"

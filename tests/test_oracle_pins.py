@@ -259,3 +259,86 @@ def test_forward_batch_invariance(oracle, oracle_model):
     for i in range(3):
         e1, _ = oracle.forward(oracle_model, faces[i:i + 1])
         assert np.array_equal(e1[0], emb3[i])
+
+
+def test_input_quant_per_tensor_vs_reference(oracle, ref):
+    """The OPSC-only input path (no OPSC2): one scale for all channels,
+    inv = 1/(s + 1e-9f) computed in fp32 inside the function, then lrintf and
+    the clamp (kernels/int8_epilogue.c:218-227).  Scales include the committed
+    1/127, a denormal (inv = 1/1e-9 rounded) and zero."""
+    r = rng(18)
+    x = r.uniform(-1, 1, 5000).astype(F32)
+    x[:10] = [0.5 / 127, 1.5 / 127, -2.5 / 127, 1e10, -1e10, np.inf, -np.inf, np.nan, 3e9, -0.0]
+    for scale in (1.0 / 127, 0.0371, float(np.float32(1e-45)), 0.0, 2.0):
+        got = oracle.quant_input_pt(x, scale)
+        assert np.array_equal(got, ref.quant_input_pt(x, scale)), scale
+    # closed form on the in-range values: round half to even of RN(x * inv)
+    inv = np.float32(1.0) / (np.float32(1.0 / 127) + np.float32(1e-9))
+    v = x[10:] * inv
+    assert np.array_equal(oracle.quant_input_pt(x[10:], 1.0 / 127),
+                          np.clip(np.rint(v), -128, 127).astype(np.int8))
+
+
+@pytest.mark.parametrize("prelu,add,bn", [(False, False, False), (True, False, False),
+                                          (False, True, False), (True, True, True)])
+def test_epilogue_in_scale_vs_reference(oracle, ref, prelu, add, bn):
+    """The FFW2/FFW3 branch of the epilogue, f = RN(RN(acc * in_scale) * ws)
+    (+ bias): in_scale != 1, including a denormal and a scale whose products
+    round, against the reference's fused_epilogue_int8 on the same inputs."""
+    r = rng(19)
+    C, P = 64, 2000
+    acc = r.integers(-3_000_000, 3_000_000, size=(P, C), dtype=np.int32)
+    acc[:, 0] = r.integers(-600, 600, size=P) | 1
+    ws, bias, inv = _specials_epilogue(C, r)
+    for in_scale in (0.0173, 3.3, float(np.float32(2.0 ** -130)), 1.0 / 3.0):
+        kw = dict(ws=ws, bias=bias, inv_pc=inv, out_scale=0.037, in_scale=in_scale)
+        if prelu:
+            kw["prelu"] = r.uniform(0, 0.3, C).astype(F32)
+        if add:
+            kw["add_src"] = r.integers(-128, 128, size=(P, C), dtype=np.int8)
+            kw["add_scale"] = 0.021
+            kw["add_scale_pc"] = r.uniform(1e-3, 5e-2, C).astype(F32)
+        if bn:
+            kw["bn_scale"] = r.uniform(0.5, 1.5, C).astype(F32)
+            kw["bn_offset"] = r.normal(0, 0.05, C).astype(F32)
+        got = oracle.fused_epilogue(acc, **kw)
+        assert np.array_equal(got, ref.fused_epilogue(acc, **kw)), in_scale
+    # a dropped in-scale multiply would not pass: the scale changes the output
+    base = oracle.fused_epilogue(acc, ws=ws, bias=bias, inv_pc=inv, in_scale=1.0)
+    assert not np.array_equal(oracle.fused_epilogue(acc, ws=ws, bias=bias, inv_pc=inv,
+                                                    in_scale=0.0173), base)
+
+
+def _round_f32_exact(fr):
+    """The fp32 value nearest the exact rational fr, ties to even (one
+    rounding, with no double-rounding through float64)."""
+    from fractions import Fraction
+    c = np.float32(float(fr))
+    cands = [np.nextafter(c, F32(-np.inf)), c, np.nextafter(c, F32(np.inf))]
+    best = min(cands, key=lambda v: (abs(Fraction(float(v)) - fr),
+                                     int(np.array(v, F32).view(np.uint32)) & 1))
+    return F32(best)
+
+
+def test_fc_a_scale_vs_reference_and_closed_form(oracle, ref):
+    """FC with A_scale != 1 (FFW2/FFW3 models): out = fma(RN(RN(dot) * a_scale),
+    ws, bias) (gemm_int8_matvec.c:78-79, libfastface.c:441-455), against the
+    reference's matvec and against the exact closed form (exact int dot,
+    fp32 roundings, one rounding of the exact fma)."""
+    from fractions import Fraction
+    r = rng(20)
+    K, N = 25088, 48
+    a = r.integers(-128, 128, K, dtype=np.int8)
+    a[:64] = -128
+    W = r.integers(-127, 128, size=(N, K), dtype=np.int8)
+    W[0, :] = -127
+    ws = r.uniform(1e-5, 1e-3, N).astype(F32)
+    bias = r.normal(0, 0.05, N).astype(F32)
+    for a_scale in (0.0213, 7.0, 1.0 / 3.0):
+        got = oracle.fc(a, W, ws, bias, a_scale=a_scale)
+        assert np.array_equal(got, ref.fc(a, W, ws, bias, a_scale=a_scale)), a_scale
+        dot = W.astype(np.int64) @ a.astype(np.int64)
+        t = dot.astype(F32) * F32(a_scale)                       # two fp32 roundings
+        exp = np.array([_round_f32_exact(Fraction(float(t[n])) * Fraction(float(ws[n])) +
+                                         Fraction(float(bias[n]))) for n in range(N)], F32)
+        assert np.array_equal(got, exp), a_scale

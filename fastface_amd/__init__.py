@@ -26,6 +26,7 @@ FFK_EPI_PRELU_LE1 = 0x40
 FFK_ALGO_WINOGRAD = 0x80
 FFK_OUT_X_EVEN = 0x100
 FFK_EPI_IN_RANGE = 0x200
+FFK_NOALLOC_SCRATCH_BYTES = 1024 + 160 * 64 * 64 * 4
 (FFK_P_WS, FFK_P_BIAS, FFK_P_SLOPE, FFK_P_ADDSCALE, FFK_P_INV, FFK_P_BN_SIN, FFK_P_BN_S,
  FFK_P_BN_O, FFK_P_BN_INV, FFK_NPARAM) = range(10)
 
@@ -111,6 +112,7 @@ EXPORTS = [
     ("ffk_pack_conv_weights", C.c_int, [_p, C.c_int, C.c_int, C.c_int, C.c_int, _p]),
     ("ffk_conv_workspace_bytes", C.c_size_t, [C.POINTER(ffk_conv_desc)]),
     ("ffk_conv", C.c_int, [C.POINTER(ffk_conv_desc), _p]),
+    ("ffk_conv_noalloc", C.c_int, [C.POINTER(ffk_conv_desc), _p]),
     ("ffk_conv_variant", C.c_char_p, [C.POINTER(ffk_conv_desc)]),
     ("ffk_winograd_supported", C.c_int, [C.c_int] * 8),
     ("ffk_winograd_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),

@@ -32,6 +32,8 @@
 // bit-exactly on the host, ffk_make_bn_lut).
 #include <algorithm>
 #include <cmath>
+#include <mutex>
+#include <string>
 
 #include "ff_internal.h"
 #include "ff_numerics.h"
@@ -1721,6 +1723,72 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
         if (rc != FFK_OK) return rc;
     }
     return FFK_OK;
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant of ffk_conv: the split-K workspace is a file-scope
+// device array (each GPU holds its own copy, at its own address, for the life
+// of the process) instead of caller memory.  Its size covers the largest
+// split grid (FF_SPLIT_MAX_WG workgroups of 64x64 int32 partial tiles) behind
+// the counter area.  In host code `scratch` names a host-side stand-in, not
+// device memory: its device address comes from hipGetSymbolAddress, once per
+// device, and only that address is passed on.
+// ---------------------------------------------------------------------------
+static_assert(FFK_NOALLOC_SCRATCH_BYTES == FF_WS_COUNTER_AREA + (size_t)FF_SPLIT_MAX_WG * FF_SM_BM * FF_SM_BN * 4,
+              "the header's limit is the split-K workspace bound");
+static __device__ __align__(256) int8_t scratch[FFK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int FF_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[FF_MAX_DEVICES];
+
+// Device address of the current device's `scratch`.  First use on a device:
+// look it up and clear the counter area with a fill kernel on `stream` (the
+// array is zero when the code object loads; the clear does not rely on it).
+int scratch_for_current_device(hipStream_t stream, void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return ffk_hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= FF_MAX_DEVICES) {
+        ffk_set_error("conv_noalloc: device index out of range%s%s", nullptr, nullptr);
+        return FFK_ERR_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return ffk_hip_fail(e, "hipGetSymbolAddress(scratch)");
+        const int rc = ffk_zero(p, FF_WS_COUNTER_AREA, stream);
+        if (rc != FFK_OK) return rc;
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return FFK_OK;
+}
+}  // namespace
+
+int ffk_conv_noalloc(const ffk_conv_desc* d, void* stream) {
+    if (!d) {
+        ffk_set_error("conv_noalloc: bad descriptor%s%s", nullptr, nullptr);
+        return FFK_ERR_ARG;
+    }
+    ffk_conv_desc dd = *d;
+    dd.workspace = nullptr;
+    dd.workspace_bytes = 0;
+    const size_t need = ffk_conv_workspace_bytes(&dd);
+    if (need > FFK_NOALLOC_SCRATCH_BYTES) {
+        ffk_set_error("conv_noalloc: this layer needs a %s-byte workspace, above the %s-byte device scratch "
+                      "(use ffk_conv with a workspace)",
+                      std::to_string(need).c_str(), std::to_string(FFK_NOALLOC_SCRATCH_BYTES).c_str());
+        return FFK_ERR_ARG;
+    }
+    void* p = nullptr;
+    const int rc = scratch_for_current_device((hipStream_t)stream, &p);
+    if (rc != FFK_OK) return rc;
+    dd.workspace = p;
+    dd.workspace_bytes = FFK_NOALLOC_SCRATCH_BYTES;
+    return ffk_conv(&dd, stream);
 }
 
 size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d) {

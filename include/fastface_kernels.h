@@ -187,6 +187,19 @@ int    ffk_pack_conv_weights(const int8_t* w_oihw, int cout, int cin, int kh, in
  * workspace_bytes fields are not read. */
 size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d);
 int    ffk_conv(const ffk_conv_desc* d, void* stream);
+/* ffk_conv without a caller workspace and without any allocation: no
+ * counterpart in the reference.  For callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  The small-batch split-K path takes its workspace from a
+ * device array inside the library, FFK_NOALLOC_SCRATCH_BYTES per GPU, held
+ * until the process ends (the descriptor's workspace fields are ignored).
+ * Layers whose launch needs more (the FFK_ALGO_WINOGRAD path) are rejected
+ * with FFK_ERR_ARG.  Every call on one GPU shares that GPU's array: calls that
+ * overlap in time on one GPU (other streams, other threads) race and must be
+ * ordered by the caller; each launch leaves the array's counter area zero for
+ * the next.  Results are bit-identical to ffk_conv's. */
+#define FFK_NOALLOC_SCRATCH_BYTES ((size_t)1024 + (size_t)160 * 64 * 64 * 4)
+int    ffk_conv_noalloc(const ffk_conv_desc* d, void* stream);
 /* Name of the kernel variant ffk_conv would run for this descriptor (its
  * geometry, batch and workspace): "stem", "patch" (3x3 stride-1 layers:
  * input patch staged once per channel run), "direct" (direct-to-LDS tiles),

@@ -1,0 +1,221 @@
+// ff_conv_table.h -- the launch-table machinery of the int8 conv kernels:
+// host launchers of each kernel template, the table entry type, the tile
+// configurations and the entry macros.  Each ff_conv_t*.hip unit
+// instantiates the kernels of its layer geometries into a table of its own
+// (separate units compile in parallel); ff_conv.hip looks layers up in them.
+#pragma once
+#include "ff_conv_kernels.h"
+
+namespace ffconv {
+
+typedef void (*launch_fn)(const ConvArgs&, int grid, hipStream_t);
+
+template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN, int KB, int PF,
+          int MI, int NJ, int OCC, int SPLIT>
+void launch_conv(const ConvArgs& a, int grid, hipStream_t s) {
+    hipLaunchKernelGGL((conv_i8_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, BM, BN, KB, PF, MI, NJ, OCC, SPLIT>),
+                       dim3(grid), dim3(256), 0, s, a);
+}
+
+template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int WM, int WN, int MI, int NJ,
+          int NST, int WPE>
+void launch_conv_dma(const ConvArgs& a, int grid, hipStream_t s) {
+    hipLaunchKernelGGL((conv_dma_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, WM, WN, MI, NJ, NST, WPE>),
+                       dim3(grid), dim3(WM * WN * 64), 0, s, a);
+}
+
+template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int WPE>
+void launch_patch(const ConvArgs& a, int grid, hipStream_t s) {
+    hipLaunchKernelGGL((conv3_patch_kernel<CIN, COUT, H, H, WM, WN, MI, NJ, WPE>), dim3(grid),
+                       dim3(WM * WN * 64), 0, s, a);
+}
+
+// Small-batch split-K tiling: 64x64 workgroup tiles (one 32x32 MFMA tile per
+// wave), the K stages of a tile shared by `split` workgroups.
+constexpr int FF_SM_BM = 64, FF_SM_BN = 64;
+// The split path is taken when the whole-K tiling leaves most CUs idle and the
+// split grid stays small: every split workgroup pays one agent-scope L2
+// write-back (~0.4 us, serialized per XCD), so a split grid much beyond ~20
+// workgroups per XCD costs more than the shorter K chain saves.
+constexpr int FF_SPLIT_MIN_WG = 256;
+constexpr int FF_SPLIT_MAX_WG = 160;
+// split-K workspace: [counter per tile, fixed size][int32 partial tiles]
+constexpr size_t FF_SPLIT_COUNTER_BYTES = FF_SPLIT_MAX_WG * sizeof(unsigned);
+static_assert(FF_SPLIT_COUNTER_BYTES <= FF_WS_COUNTER_AREA, "counters stay in the reserved area");
+
+struct ConvEntry {
+    int cin, cout, ks, stride, hin, win, bm, bn;
+    launch_fn fn;
+    int split;          // K split of the small-batch variant (1: no partial tiles)
+    launch_fn small;    // 64x64-tile split-K variant, or none
+    launch_fn mid;      // variant for grids too small for the big tiles (default:
+                        // the 128x128-tile register-staged kernel), or none
+    const char* kind;   // name of `fn` (ffk_conv_variant)
+    int mid_bm, mid_bn; // tile of `mid` when it is not 128x128
+    const char* mid_kind;
+};
+
+// A grid of fewer big tiles than this leaves CUs idle; the 128x128 variant
+// (four times the workgroups) is taken instead.
+constexpr int FF_MID_MAX_WG = 512;
+
+// Tile configurations: (BM, BN, MI, NJ, OCC) -- workgroup tile, wave tile in
+// 32x32 MFMA blocks, workgroups per CU.
+//   T64:  Cout = 64, 256x64 tiles of 64x64 waves
+//   T128: 128x128 tiles of 64x64 waves
+//   TBIG: the Cout >= 256 layers (stages 3-4)
+#define FF_T64 256, 64, 2, 2, 2
+#define FF_T128 128, 128, 2, 2, 2
+#ifndef FF_TBIG
+#define FF_TBIG 128, 128, 2, 2, 2
+#endif
+// 128-byte stages wherever Cin allows (twice the MFMA work per barrier)
+#define FF_KB(CIN) ((CIN) % 128 == 0 ? 128 : 64)
+#define FF_PFS(CIN) (FF_KB(CIN) == 128 ? FF_PF128 : FF_PF)
+// The 128x128 mid-size variants of the 512-channel layers keep two stages in
+// flight: with three their address registers spilled to scratch.
+#define FF_PF_MID(CIN) ((CIN) >= 512 ? 2 : FF_PFS(CIN))
+#ifdef FF_KB_BIG_V
+#define FF_KB_BIG(CIN) FF_KB_BIG_V
+#define FF_PF_BIG(CIN) FF_PF_BIG_V
+#else
+#define FF_KB_BIG(CIN) FF_KB(CIN)
+#define FF_PF_BIG(CIN) FF_PFS(CIN)
+#endif
+template <int CIN, int COUT, int KS, int S, int H, int SPLIT>
+constexpr launch_fn split_launch() {
+    if constexpr (SPLIT > 1)
+        return &launch_conv<CIN, COUT, KS, S, H, H, FF_SM_BM, FF_SM_BN, FF_KB(CIN), 2, 1, 1, 4, SPLIT>;
+    else
+        return nullptr;
+}
+#define FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, KB, PF, BM, BN, MI, NJ, OCC)       \
+    {CIN, COUT, KS, S, H, H, BM, BN,                                             \
+     &launch_conv<CIN, COUT, KS, S, H, H, BM, BN, KB, PF, MI, NJ, OCC, 1>, SPLIT, \
+     split_launch<CIN, COUT, KS, S, H, SPLIT>(), nullptr, "staged"}
+#define FF_CONV(CIN, COUT, KS, S, H, SPLIT, TILE) \
+    FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, FF_KB(CIN), FF_PFS(CIN), TILE)
+#define FF_CONV_K(CIN, COUT, KS, S, H, SPLIT, KB, PF, TILE) \
+    FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, KB, PF, TILE)
+#define FF_CONVB(CIN, COUT, KS, S, H, SPLIT) \
+    FF_CONV_K(CIN, COUT, KS, S, H, SPLIT, FF_KB_BIG(CIN), FF_PF_BIG(CIN), FF_TBIG)
+
+// Direct-to-LDS tiles (WM, WN, MI, NJ, NST, WPE): 8 waves of 2x2 MFMA tiles
+// -> 256x128, a 3-stage ring, 4 waves per SIMD (two workgroups per CU).
+#ifndef FF_TDMA
+#define FF_TDMA 4, 2, 2, 2, 3, 4
+#endif
+#define FF_DENTRY(CIN, COUT, KS, S, H, SPLIT, WM, WN, MI, NJ, NST, WPE)              \
+    {CIN, COUT, KS, S, H, H, WM * MI * 32, WN * NJ * 32,                             \
+     &launch_conv_dma<CIN, COUT, KS, S, H, H, WM, WN, MI, NJ, NST, WPE>, SPLIT,      \
+     split_launch<CIN, COUT, KS, S, H, SPLIT>(),                                     \
+     &launch_conv<CIN, COUT, KS, S, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>, "direct"}
+#define FF_CONVD_K(CIN, COUT, KS, S, H, SPLIT, TILE) FF_DENTRY(CIN, COUT, KS, S, H, SPLIT, TILE)
+#define FF_CONVD(CIN, COUT, KS, S, H, SPLIT) FF_CONVD_K(CIN, COUT, KS, S, H, SPLIT, FF_TDMA)
+#define FF_DENTRY_NOMID(CIN, COUT, KS, S, H, SPLIT, WM, WN, MI, NJ, NST, WPE)        \
+    {CIN, COUT, KS, S, H, H, WM * MI * 32, WN * NJ * 32,                             \
+     &launch_conv_dma<CIN, COUT, KS, S, H, H, WM, WN, MI, NJ, NST, WPE>, SPLIT,      \
+     split_launch<CIN, COUT, KS, S, H, SPLIT>(), nullptr, "direct"}
+#define FF_CONVD64_K(CIN, COUT, KS, S, H, SPLIT, TILE) FF_DENTRY_NOMID(CIN, COUT, KS, S, H, SPLIT, TILE)
+// Cout = 64: 4 waves of 2x2 MFMA tiles -> 256x64, a 2-stage ring, 4 waves per
+// SIMD (four workgroups per CU)
+#ifndef FF_T64DMA
+#define FF_T64DMA 4, 1, 2, 2, 2, 4
+#endif
+#ifdef FF_NO_DMA
+#define FF_C64(CIN, COUT, KS, S, H, SPLIT) FF_CONV(CIN, COUT, KS, S, H, SPLIT, FF_T64)
+#else
+#define FF_C64(CIN, COUT, KS, S, H, SPLIT) FF_CONVD64_K(CIN, COUT, KS, S, H, SPLIT, FF_T64DMA)
+#endif
+#ifdef FF_NO_DMA
+#define FF_C128(CIN, COUT, KS, S, H, SPLIT) FF_CONV(CIN, COUT, KS, S, H, SPLIT, FF_T128)
+#define FF_CBIG(CIN, COUT, KS, S, H, SPLIT) FF_CONVB(CIN, COUT, KS, S, H, SPLIT)
+#else
+#define FF_C128(CIN, COUT, KS, S, H, SPLIT) FF_CONVD(CIN, COUT, KS, S, H, SPLIT)
+#define FF_CBIG(CIN, COUT, KS, S, H, SPLIT) FF_CONVD(CIN, COUT, KS, S, H, SPLIT)
+#endif
+
+// 3x3 stride-1 layers: the patch kernel (WM, WN, MI, NJ, WPE).  8 waves of
+// 2x2 MFMA tiles -> 256x128, two workgroups per CU; Cout = 64: 4 waves ->
+// 256x64 and one 64-channel run, so a single patch buffer: three workgroups
+// per CU at 56x56 and at 112x112.
+#ifndef FF_TPATCH
+#define FF_TPATCH 4, 2, 2, 2, 4
+#endif
+#ifndef FF_TPATCH64
+#define FF_TPATCH64 4, 1, 2, 2, 3
+#endif
+// 64 -> 64 at 56x56: 8 waves -> 512x64 tiles, two workgroups per CU (4 waves
+// per SIMD; half the per-tile setup and patch halo per output; only waves 0-3
+// load a step's 4 KB of weights).  3 % faster there, slower at 112x112.
+#ifndef FF_TPATCH64W
+#define FF_TPATCH64W 8, 1, 2, 2, 4
+#endif
+// Cout >= 256 (stages 3-4)
+#ifndef FF_TPATCH_BIG
+#define FF_TPATCH_BIG FF_TPATCH
+#endif
+#define FF_PENTRY(CIN, COUT, H, SPLIT, MID, WM, WN, MI, NJ, WPE)                      \
+    {CIN, COUT, 3, 1, H, H, WM * MI * 32, WN * NJ * 32,                              \
+     &launch_patch<CIN, COUT, H, WM, WN, MI, NJ, WPE>, SPLIT,                         \
+     split_launch<CIN, COUT, 3, 1, H, SPLIT>(), MID, "patch"}
+#define FF_PENTRY_K(CIN, COUT, H, SPLIT, MID, TILE) FF_PENTRY(CIN, COUT, H, SPLIT, MID, TILE)
+#ifdef FF_NO_PATCH
+#define FF_P(CIN, COUT, H, SPLIT) FF_CBIG(CIN, COUT, 3, 1, H, SPLIT)
+#define FF_PB(CIN, COUT, H, SPLIT) FF_CBIG(CIN, COUT, 3, 1, H, SPLIT)
+#define FF_P64(CIN, COUT, H, SPLIT) FF_C64(CIN, COUT, 3, 1, H, SPLIT)
+#define FF_P64W(CIN, COUT, H, SPLIT) FF_C64(CIN, COUT, 3, 1, H, SPLIT)
+#else
+#define FF_P(CIN, COUT, H, SPLIT)                                                   \
+    FF_PENTRY_K(CIN, COUT, H, SPLIT,                                                \
+                (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>), \
+                FF_TPATCH)
+#define FF_PB(CIN, COUT, H, SPLIT)                                                  \
+    FF_PENTRY_K(CIN, COUT, H, SPLIT,                                                \
+                (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>), \
+                FF_TPATCH_BIG)
+#define FF_P64(CIN, COUT, H, SPLIT) FF_PENTRY_K(CIN, COUT, H, SPLIT, nullptr, FF_TPATCH64)
+// (small grids: the 256x64 tiles, twice the workgroups)
+#define FF_P64W(CIN, COUT, H, SPLIT)                                                \
+    {CIN, COUT, 3, 1, H, H, 512, 64, &launch_patch<CIN, COUT, H, FF_TPATCH64W>, SPLIT, \
+     split_launch<CIN, COUT, 3, 1, H, SPLIT>(), &launch_patch<CIN, COUT, H, FF_TPATCH64>, "patch", \
+     256, 64, "patch"}
+#endif
+
+#ifndef FF_S2_SPLIT
+#define FF_S2_SPLIT 3
+#endif
+#ifndef FF_S3_SPLIT
+#define FF_S3_SPLIT 3
+#endif
+#ifndef FF_S3S2_SPLIT
+#define FF_S3S2_SPLIT 6
+#endif
+#ifndef FF_S4_SPLIT
+#define FF_S4_SPLIT 9
+#endif
+// split: how many workgroups share the K stages of one small-batch tile (1:
+// never split).  The 3x3 layers with 128 input channels or more gain from it
+// (9, 18 or 36 stages of 128 bytes; the stage-2 layers measured 0.511 ->
+// 0.486 ms for the b=1 chain with 3 ranges of 3 stages).  Each workgroup's
+// partial tile costs an L2 write-back and those serialize per XCD, so fewer
+// splits can win: 256->256 @14 (12 launches at b=1) with 3 instead of 9
+// took the b=1 chain from 0.485 to 0.433 ms; 3 for the stride-2 and
+// 512-channel layers measured the same as their 6 and 9, 2 (and 4) slower.
+// One face gives 48-156 workgroups.  The 64-channel layers' 9 stages of 64
+// bytes are too short to pay for the partial-sum exchange.
+}  // namespace ffconv
+
+using namespace ffconv;
+
+// The tables of the ff_conv_t*.hip units (a ConvEntry array and its size).
+const ConvEntry* ff_conv_table_stem(int* n);
+const ConvEntry* ff_conv_table_c64(int* n);
+const ConvEntry* ff_conv_table_c128(int* n);
+const ConvEntry* ff_conv_table_c256(int* n);
+const ConvEntry* ff_conv_table_c512(int* n);
+// FC head as an MFMA GEMM (ff_conv_fc.hip)
+constexpr int FC_SPLIT = 7;
+size_t ffk_fc_split_ws_bytes(int batch);
+int ffk_fc_gemm_launch(const ffk_fc_desc* d, hipStream_t s);
+

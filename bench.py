@@ -42,8 +42,9 @@ def check(lib, rc, what):
 
 
 def host_cpu():
-    """CPU model, physical cores and SMT state of this host (from /proc/cpuinfo)."""
-    model, cores, logical = "?", set(), 0
+    """CPU model, family/model/stepping, physical cores, SMT state and the
+    VNNI flags of this host (from /proc/cpuinfo)."""
+    model, cores, logical, ident, flags = "?", set(), 0, {}, set()
     try:
         phys = None
         for line in open("/proc/cpuinfo"):
@@ -53,6 +54,10 @@ def host_cpu():
                 logical += 1
             elif k == "model name":
                 model = v
+            elif k in ("cpu family", "model", "stepping", "vendor_id") and k not in ident:
+                ident[k] = v
+            elif k == "flags" and not flags:
+                flags = set(v.split())
             elif k == "physical id":
                 phys = v
             elif k == "core id":
@@ -60,7 +65,10 @@ def host_cpu():
     except OSError:
         pass
     n = len(cores) or logical
-    return {"model": model, "physical_cores": n, "logical_cpus": logical, "smt": logical > n}
+    return {"model": model, "vendor": ident.get("vendor_id"), "family": ident.get("cpu family"),
+            "model_number": ident.get("model"), "stepping": ident.get("stepping"),
+            "physical_cores": n, "logical_cpus": logical, "smt": logical > n,
+            "avx_vnni": "avx_vnni" in flags, "avx512_vnni": "avx512_vnni" in flags}
 
 
 def _ref_best(exe, args, threads, env):
@@ -79,18 +87,24 @@ def _ref_best(exe, args, threads, env):
     return None
 
 
-def cpu_baseline(ffw):
+def cpu_baseline(ffw, runs=5, cooldown=1.0):
     """The reference's own CPU binaries (oracle/_ref, built from its sources)
-    on this host, their built-in bench (5 trials x 30 passes, best):
-    fastface_int8_batched --batch 8 on all (up to 16) cores -- `value` -- and
-    on its default 8 threads, and fastface_int8 at b=1.  About 15 s of CPU
-    work.  Falls back to the C restatement when the host lacks AVX-VNNI (the
-    reference build would SIGILL)."""
+    on this host.  `value`: fastface_int8_batched --batch 8 on all (up to 16)
+    cores, its built-in bench (5 trials x 30 passes, best;
+    arcface_forward_int8.c:549-562).  Also: the same on its default 8 threads,
+    and the reference's stable protocol for b=1 (bench_stable_int8_ffw4.py:7-13:
+    repeated runs of fastface_int8 with a cooldown between them, median of
+    the runs' best) with `runs` runs and `cooldown` seconds instead of its 20
+    and 3 s, so that the default bench stays within minutes.  About 30 s of
+    CPU work.  Falls back to the C restatement when the host lacks AVX-VNNI
+    (the reference build would SIGILL)."""
     from oracle.oracle import host_has_avx_vnni
     cpu = host_cpu()
     cores = min(16, cpu["physical_cores"] or os.cpu_count() or 1)
     exe = os.path.join(ROOT, "oracle", "_ref", "fastface_int8_batched")
     exe1 = os.path.join(ROOT, "oracle", "_ref", "fastface_int8")
+    cc = os.path.join(ROOT, "oracle", "_ref", "compiler.txt")
+    compiler = open(cc).read().strip() if os.path.exists(cc) else None
     env = dict(os.environ, OMP_PROC_BIND="close", OMP_PLACES="cores")
     if os.path.exists(exe) and host_has_avx_vnni():
         log("cpu baseline: reference fastface_int8_batched --batch 8, %d threads" % cores)
@@ -99,14 +113,27 @@ def cpu_baseline(ffw):
             rec = {"value": best[0], "unit": "faces/s", "cores": cores, "kind": "reference",
                    "sample": "reference fastface_int8_batched, B=8 synthetic faces, best of 5x30 "
                              "passes (%.2f ms/face); synthetic FFW4 + committed OPSC2" % best[1],
-                   "host": cpu}
+                   "host": cpu, "compiler": compiler,
+                   "build_flags": "-O3 -march=x86-64-v3 -mavx2 -mfma -mavxvnni -fopenmp (Makefile:32-37, "
+                                  "CFLAGS_ARCH override)"}
             b8 = _ref_best(exe, [ffw, "--batch", "8"], 8, env)
             if b8:
                 rec["value_8_threads"] = b8[0]
             if os.path.exists(exe1):
-                b1 = _ref_best(exe1, [ffw], 8, env)
+                b1 = []
+                for i in range(runs):
+                    if i:
+                        time.sleep(cooldown)
+                    r1 = _ref_best(exe1, [ffw], 8, env)
+                    if r1:
+                        b1.append(r1[1])
                 if b1:
-                    rec["b1_ms_8_threads"] = b1[1]
+                    rec["b1_ms_8_threads"] = min(b1)
+                    rec["b1_stable_8_threads"] = {
+                        "runs": len(b1), "cooldown_s": cooldown, "median_ms": round(statistics.median(b1), 3),
+                        "min_ms": round(min(b1), 3), "max_ms": round(max(b1), 3),
+                        "protocol": "bench_stable_int8_ffw4.py:7-13 (median of runs, each the binary's "
+                                    "best of 5x30), %d runs / %.1f s cooldown instead of 20 / 3 s" % (len(b1), cooldown)}
             return rec
     from fastface_amd import synth
     from oracle.oracle import Oracle
@@ -119,7 +146,7 @@ def cpu_baseline(ffw):
     dt = time.perf_counter() - t0
     orc.free_model(m)
     return {"value": 4 / dt, "unit": "faces/s", "cores": cores, "kind": "port",
-            "sample": "oracle/ff_oracle.c forward of 4 synthetic faces"}
+            "sample": "oracle/ff_oracle.c forward of 4 synthetic faces", "host": cpu, "compiler": compiler}
 
 
 def main():
@@ -134,6 +161,10 @@ def main():
                     help="time only the B=%d chain, its per-step profile and the Winograd leg "
                          "(the rocprofv3 kernel-statistics run: b=1, B=8, the config-2 layer and "
                          "the host-buffer rates are left out)" % 1024)
+    ap.add_argument("--cpu-runs", type=int, default=5,
+                    help="runs of the reference's b=1 binary in its stable protocol (reference: 20)")
+    ap.add_argument("--cpu-cooldown", type=float, default=1.0,
+                    help="seconds between those runs (reference: 3)")
     ap.add_argument("--no-winograd", action="store_true",
                     help="skip the config-5 run of the stage-1 layers as Winograd F(2,3)")
     args = ap.parse_args()
@@ -152,7 +183,12 @@ def main():
     B, K, W = args.batch, args.steps, args.warmup
     ffw = synth.synthetic_ffw4_path(3)
     log("weights %s" % ffw)
+    # cold start (the reference's ~180 ms, README.md:91): the first
+    # fastface_create of the process (HIP runtime and code objects come up,
+    # the FFW4/OPSC files are read, weights packed and uploaded)
+    t_create = time.perf_counter()
     ff = fastface_amd.FastFace(ffw, cwd=ROOT)
+    first_create_ms = (time.perf_counter() - t_create) * 1e3
     check(lib, lib.fastface_reserve(ff.ff, B), "reserve")
     stream = lib.fastface_stream(ff.ff)
 
@@ -404,9 +440,26 @@ def main():
             raise RuntimeError("Winograd embeddings differ from the direct path")
         check(lib, lib.fastface_set_conv_algo(ff.ff, 0), "algo direct")
 
+    # a second context in the same process: create, first b=1 embed (captures
+    # its launch chain), destroy
+    t_c = time.perf_counter()
+    ff2 = fastface_amd.FastFace(ffw, cwd=ROOT)
+    create_ms = (time.perf_counter() - t_c) * 1e3
+    t_e = time.perf_counter()
+    ff2.embed(x1[0] if x1.ndim == 4 else x1)
+    first_embed_ms = (time.perf_counter() - t_e) * 1e3
+    ff2.close()
+    cold = {"first_create_ms": round(first_create_ms, 1), "create_ms": round(create_ms, 1),
+            "first_embed_ms": round(first_embed_ms, 2),
+            "note": "first_create: the process's first fastface_create (HIP runtime start-up "
+                    "included); create: a second context; first_embed: its first b=1 embed "
+                    "(launch chain captured)"}
+    log("cold start: first create %.1f ms, create %.1f ms, first embed %.2f ms"
+        % (first_create_ms, create_ms, first_embed_ms))
+
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(ffw)
+        cpu = cpu_baseline(ffw, runs=args.cpu_runs, cooldown=args.cpu_cooldown)
         log("cpu baseline: %.1f %s (%s)" % (cpu["value"], cpu["unit"], cpu["kind"]))
 
     ff.close()
@@ -454,6 +507,7 @@ def main():
                      "timing": "26 launches (13 PReLU, 13 residual+BN) in one hipGraph, 20 replays "
                                "between HIP events on the launch stream"},
         "stage1_winograd": wino,
+        "cold_start": cold,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -38,7 +38,10 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
     if not lib.ffk_conv_supported(cin, cout, k, k, stride, pad, hin, hin):
         raise ValueError("unsupported layer geometry")
     r = np.random.default_rng(1)
-    x = r.integers(-127, 128, size=(batch, hin, hin, cin), dtype=np.int8)
+    if cin == 3:        # the input layer reads fp32 faces in [-1, 1]
+        x = r.uniform(-1, 1, size=(batch, hin, hin, cin)).astype(np.float32)
+    else:
+        x = r.integers(-127, 128, size=(batch, hin, hin, cin), dtype=np.int8)
     w = r.integers(-127, 128, size=(cout, cin, k, k), dtype=np.int8)
     if winograd:
         packed = np.empty(lib.ffk_winograd_packed_bytes(cin, cout), np.int8)
@@ -73,6 +76,8 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
     d.batch, d.cin, d.cout, d.kh, d.kw = batch, cin, cout, k, k
     d.stride, d.pad, d.hin, d.win = stride, pad, hin, hin
     d.in_ = dev(x)
+    if cin == 3:
+        d.in_inv = dev(np.array([127.0, 127.0, 127.0, 0.0], np.float32))
     d.w = dev(packed)
     d.params = dev(P)
     d.flags = fa.FFK_EPI_BIAS | (fa.FFK_ALGO_WINOGRAD if winograd else 0)
@@ -159,6 +164,65 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
             "frac_of_peak": round(ops / (per * 1e-3) / 5e15, 4)}
 
 
+def time_fc(lib, batch=1, iters=50):
+    """Mean launch time of the FC head 25088 -> 512 at `batch` faces (the
+    path and split-K workspace ffk_fc chooses; HIP events on the launch
+    stream); seeded int8 activations and weights.  Frees what it allocates."""
+    N, K = 512, 25088
+    r = np.random.default_rng(7)
+    a = r.integers(-128, 128, size=(batch, K), dtype=np.int8)
+    W = r.integers(-127, 128, size=(N, K), dtype=np.int8)
+    packed = np.empty(lib.ffk_fc_packed_bytes(N, K), np.int8)
+    lib.ffk_pack_fc_weights(W.ctypes.data, N, K, packed.ctypes.data)
+    ws = r.uniform(1e-5, 1e-3, N).astype(np.float32)
+    bias = r.normal(0, 0.05, N).astype(np.float32)
+    held = []
+
+    def dev(arr=None, nbytes=None):
+        n = arr.nbytes if arr is not None else nbytes
+        p = lib.ffk_malloc(n)
+        if not p:
+            raise MemoryError(fa.last_error())
+        held.append(p)
+        if arr is not None:
+            lib.ffk_memcpy_h2d(p, arr.ctypes.data, n, None)
+        return p
+    d = fa.ffk_fc_desc()
+    d.batch, d.n, d.k = batch, N, K
+    d.a, d.w, d.ws, d.bias = dev(a), dev(packed), dev(ws), dev(bias)
+    d.out = dev(nbytes=batch * N * 4)
+    d.a_scale = 1.0
+    n_ws = lib.ffk_fc_workspace_bytes(C.byref(d))
+    if n_ws:
+        d.workspace, d.workspace_bytes = dev(nbytes=n_ws), n_ws
+        assert lib.ffk_zero(d.workspace, n_ws, None) == 0, fa.last_error()
+    stream, e0, e1, ms = C.c_void_p(), C.c_void_p(), C.c_void_p(), C.c_float()
+    lib.ffk_stream_create(C.byref(stream))
+    lib.ffk_event_create(C.byref(e0))
+    lib.ffk_event_create(C.byref(e1))
+    try:
+        for _ in range(3):
+            assert lib.ffk_fc(C.byref(d), stream) == 0, fa.last_error()
+        lib.ffk_event_record(e0, stream)
+        for _ in range(iters):
+            lib.ffk_fc(C.byref(d), stream)
+        lib.ffk_event_record(e1, stream)
+        assert lib.ffk_event_elapsed_ms(e0, e1, C.byref(ms)) == 0, fa.last_error()
+    finally:
+        lib.ffk_stream_sync(stream)
+        lib.ffk_event_destroy(e0)
+        lib.ffk_event_destroy(e1)
+        lib.ffk_stream_destroy(stream)
+        for p in held:
+            lib.ffk_free(p)
+    per = ms.value / iters
+    return {"layer": "fc 25088->512", "batch": batch, "split_ws_bytes": n_ws,
+            "path": "matvec" if batch <= 16 else "gemm",
+            "ms_per_launch": round(per, 5),
+            "weight_gbs": round(N * K / (per * 1e-3) / 1e9, 1),
+            "int8_tops": round(2.0 * batch * N * K / (per * 1e-3) / 1e12, 2)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--cin", type=int, default=256)
@@ -175,6 +239,8 @@ def main():
                     help="64-channel 3x3 stride-1 layers: the integer Winograd F(2,3) path")
     ap.add_argument("--no-split", action="store_true",
                     help="give no split-K workspace (small batches then use the whole-K tiling)")
+    ap.add_argument("--fc", action="store_true",
+                    help="instead: the FC head 25088 -> 512 at --batch faces")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="instead: device-to-device copies of this many MiB (the calibration "
                          "workload for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -189,6 +255,9 @@ def main():
             assert lib.ffk_memcpy_d2d(dst, src, n, None) == 0, fa.last_error()
         lib.ffk_stream_sync(None)
         print(json.dumps({"copy_bytes": n, "iters": a.iters}), flush=True)
+        return
+    if a.fc:
+        print(json.dumps(time_fc(lib, a.batch, a.iters)), flush=True)
         return
     try:
         res = time_layer(lib, a.cin, a.cout, a.k, a.stride, a.hin, a.batch, a.iters, a.epi,

@@ -327,3 +327,32 @@ def test_device_calls_on_caller_streams_are_ordered(gpu_lib, synth_ffw4, oracle,
         for s in streams:
             gpu_lib.ffk_stream_destroy(s)
         f.close()
+
+
+def test_reference_c_caller_unchanged(gpu_lib, synth_ffw4, oracle, oracle_model, tmp_path):
+    """The reference's own C-API client, test_libfastface.c (reference
+    Makefile:72-73), compiled unchanged against include/fastface.h and linked to
+    libfastface_amd.so (oracle/Makefile `ref`), run in a directory laid out as
+    it expects: models/w600k_r50_ffw4.bin (here the synthetic FFW4),
+    models/op_scales{,_v2}.bin and tests/golden_input.bin.  Its printed
+    emb[0..4] must equal the oracle's embedding of that face (its own %g
+    formatting of the same floats)."""
+    import subprocess
+    exe = os.path.join(synth.REPO_ROOT, "oracle", "_ref", "test_libfastface")
+    if not os.path.exists(exe):
+        pytest.skip("oracle/_ref/test_libfastface not built (needs /root/reference at build time)")
+    (tmp_path / "models").mkdir()
+    (tmp_path / "tests").mkdir()
+    os.symlink(synth_ffw4, tmp_path / "models" / "w600k_r50_ffw4.bin")
+    os.symlink(synth.OPSC_PATH, tmp_path / "models" / "op_scales.bin")
+    os.symlink(synth.OPSC2_PATH, tmp_path / "models" / "op_scales_v2.bin")
+    os.symlink(os.path.join(GOLDEN, "golden_input.bin"), tmp_path / "tests" / "golden_input.bin")
+    env = {k: v for k, v in os.environ.items() if k != "OPSC2_PATH"}
+    r = subprocess.run([exe], cwd=str(tmp_path), capture_output=True, text=True, timeout=120, env=env)
+    assert r.returncode == 0, r.stderr
+    x = np.fromfile(os.path.join(GOLDEN, "golden_input.bin"), np.float32).reshape(1, 112, 112, 3)
+    exp, _ = oracle.forward(oracle_model, x)
+    line = [l for l in r.stdout.splitlines() if l.startswith("emb[0..4] = ")]
+    assert line, r.stdout
+    want = "emb[0..4] = " + " ".join("%g" % float(v) for v in exp[0, :5])
+    assert line[0] == want

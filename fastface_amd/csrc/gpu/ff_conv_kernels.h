@@ -1017,6 +1017,269 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
 }
 
 // ---------------------------------------------------------------------------
+// Small-grid variant of the 3x3 stride-1 patch kernel: the channel runs of a
+// tile are shared by KG groups of WM x WN waves inside the workgroup (group g
+// takes runs g, g + KG, ...), each group with its own patch buffers and
+// weight ring; all groups step in lockstep (one barrier per step).  At the
+// end the int32 partial tiles are summed through LDS: the MI x NJ MFMA
+// blocks of a wave position are divided among the groups (group g owns
+// blocks g*T/KG .. (g+1)*T/KG - 1 in row-major order, T = MI*NJ); every
+// other group writes its partial of those blocks, the owner adds them and
+// runs the epilogue on its blocks.  Integer sums are exact, so the result is
+// the whole-K kernel's.  This gives a small batch KG times the waves without
+// the global workspace and L2 write-backs of split-K across workgroups.
+// ---------------------------------------------------------------------------
+template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int KG, int WPE>
+__global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(ConvArgs a) {
+    constexpr int NWG = WM * WN;                             // waves per group
+    constexpr int NW = NWG * KG;
+    constexpr int NTG = NWG * 64;
+    constexpr int BM = WM * MI * 32, BN = WN * NJ * 32;
+    constexpr int CSTEPS = CIN / DMA_KB;                     // 64-channel runs
+    constexpr int RUNS = CSTEPS / KG;                        // runs of one group
+    constexpr int NP = BM + 2 * W + 2;
+    constexpr int PSLOTS = NP * (PATCH_PITCH / 16);
+    constexpr int PLOADS = (PSLOTS + 63) / 64;
+    constexpr int LA = (PLOADS + NWG - 1) / NWG;             // patch loads per thread
+    constexpr int PATCH_BYTES = PLOADS * 1024;
+    constexpr int B_BYTES = BN * DMA_KB;
+    constexpr int BW = B_BYTES / 1024;
+    constexpr bool B_PART = BW < NWG;
+    constexpr int B_LD = B_PART ? 1 : B_BYTES / (NTG * 16);
+    constexpr int NSTB = 3;
+    constexpr int NPB = RUNS > 1 ? 2 : 1;
+    constexpr int GROUP_BYTES = NPB * PATCH_BYTES + NSTB * B_BYTES;
+    constexpr int ZERO_OFF = KG * GROUP_BYTES;
+    constexpr int LDS_K = ZERO_OFF + 1024;
+    constexpr int T = MI * NJ;                               // MFMA blocks per wave
+    constexpr int TO = T / KG;                               // blocks a group owns
+    constexpr int PART = 64 * 64;                            // bytes of one block's partial (per wave)
+    // partials are summed CHUNK blocks at a time: as many as fit beside the
+    // main loop's LDS footprint (all of them when KG == 2)
+    constexpr int BLOCK_X = (KG - 1) * NWG * PART;           // LDS of one block's partials
+    constexpr int LDS_BASE = LDS_K > 64 * 1024 ? LDS_K : 64 * 1024;
+    constexpr int CHUNK = KG == 1 ? 1 : (T * BLOCK_X <= LDS_BASE ? T : (LDS_BASE / BLOCK_X > 0 ? LDS_BASE / BLOCK_X : 1));
+    constexpr int LDS_X = KG == 1 ? 0 : CHUNK * BLOCK_X;
+    // owned blocks as an (MO x NO) sub-block at (i0, j0) of the wave tile
+    constexpr int NO = TO >= NJ ? NJ : TO;
+    constexpr int MO = TO >= NJ ? TO / NJ : 1;
+    constexpr int LDS_E = NW * wave_tile_bytes<MO, NO>() + BN * FF_LUT_PITCH;
+    constexpr int LDS = LDS_K > LDS_E ? (LDS_K > LDS_X ? LDS_K : LDS_X) : (LDS_E > LDS_X ? LDS_E : LDS_X);
+    static_assert(CIN % DMA_KB == 0 && CSTEPS % KG == 0, "runs divide among the groups");
+    static_assert(T % KG == 0 && (TO % NJ == 0 || NJ % TO == 0), "blocks divide among the groups");
+    static_assert(B_BYTES % 1024 == 0 && (B_PART || B_BYTES % (NTG * 16) == 0), "whole wave loads");
+    static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
+    static_assert(B_LD + LA < 64, "load counter range");
+    static_assert((2 * W + 2) * PATCH_PITCH + 32 + 16 < 65536, "tap offsets fit the ds_read offset field");
+    static_assert(LDS <= 160 * 1024, "LDS");
+
+    __shared__ __align__(1024) int8_t smem[LDS];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int g = wave / NWG;                                // K group (uniform per wave)
+    const int wg = wave - g * NWG;                           // wave within the group
+    const int xbid = xcd_tile(blockIdx.x, gridDim.x);
+    const int tn = xbid % a.tiles_n;
+    const int tm = xbid / a.tiles_n;
+    const int m0 = tm * BM;
+    const int first = m0 - W - 1;
+    int8_t* gbase = smem + g * GROUP_BYTES;                   // this group's patches and ring
+
+    for (int i = tid; i < 64; i += NW * 64) reinterpret_cast<v4i*>(smem + ZERO_OFF)[i] = v4i{0, 0, 0, 0};
+
+    int p_src[LA];
+#pragma unroll
+    for (int j = 0; j < LA; j++) {
+        const int blk = j * NWG + wg;
+        const int slot = blk * 64 + lane;
+        const int px = slot / 5;
+        const int piece = slot - px * 5;
+        const int gp = first + px;
+        const bool ok = blk < PLOADS && piece < 4 && gp >= 0 && gp < a.M;
+        p_src[j] = ok ? gp * CIN + piece * 16 : -1;
+    }
+    // run r of this group is channel run g + KG*r
+    auto issue_patch = [&](int r, int buf) {
+        const int c = g + KG * r;
+#pragma unroll
+        for (int j = 0; j < LA; j++) {
+            const int blk = j * NWG + wg;
+            const int8_t* src = p_src[j] >= 0 ? a.in + (p_src[j] + c * DMA_KB) : ff_zero_page;
+            dma16(src, blk < PLOADS ? gbase + buf * PATCH_BYTES + blk * 1024 : smem + ZERO_OFF);
+        }
+    };
+    int b_off[B_LD];
+#pragma unroll
+    for (int j = 0; j < B_LD; j++) {
+        const int line = (j * NWG + wg) * 4 + (lane >> 4);
+        const int sl = (lane & 15) ^ (line & 3);
+        const int n = line * 4 + (sl >> 2);
+        b_off[j] = (tn * BN + n) * FF_KSTEP + (sl & 3) * 16;
+    }
+    const bool loads_b = !B_PART || wg < BW;
+    auto issue_b = [&](int r, int t, int slot) {
+        if (!loads_b) return;
+        const int c = g + KG * r;
+        const int8_t* wst = a.w + (size_t)(t * CSTEPS + c) * COUT * FF_KSTEP;
+#pragma unroll
+        for (int j = 0; j < B_LD; j++)
+            dma16(wst + b_off[j], gbase + NPB * PATCH_BYTES + slot * B_BYTES + (j * NWG + wg) * 1024);
+    };
+
+    const int wm = wg / WN;
+    const int wn = wg % WN;
+    int a_base[MI], a_edge[MI];
+#pragma unroll
+    for (int i = 0; i < MI; i++) {
+        const int rr0 = wm * MI * 32 + i * 32 + (lane & 31);
+        const int m = m0 + rr0;
+        const int rr = m % (H * W);
+        const int oh = rr / W;
+        const int ow = rr - oh * W;
+        a_edge[i] = (oh == 0 ? 1 : 0) | (oh == H - 1 ? 2 : 0) | (ow == 0 ? 4 : 0) | (ow == W - 1 ? 8 : 0);
+        a_base[i] = g * GROUP_BYTES + rr0 * PATCH_PITCH + (lane >> 5) * 16;   // (absolute LDS offsets)
+    }
+    const int z_addr = ZERO_OFF + (lane >> 5) * 16;
+    const int b_rd = g * GROUP_BYTES + NPB * PATCH_BYTES + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
+
+    v16i acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+    issue_patch(0, 0);
+    issue_b(0, 0, 0);
+    issue_b(0, 1, 1);
+    for (int r = 0; r < RUNS; r++) {
+        const bool more = r + 1 < RUNS;
+        const int pb = (r & 1) * PATCH_BYTES;
+#pragma unroll
+        for (int i = 0; i < MI; i++) asm volatile("" : "+v"(a_base[i]), "+v"(a_edge[i]));
+#pragma unroll
+        for (int t = 0; t < 9; t++) {
+            if (loads_b) {
+                if (t == 1 || t == 2) {
+                    if (more) dma_wait_barrier<B_LD + LA>();
+                    else dma_wait_barrier<B_LD>();
+                } else if (t == 8) {
+                    if (more) dma_wait_barrier<B_LD>();
+                    else dma_wait_barrier<0>();
+                } else {
+                    dma_wait_barrier<B_LD>();
+                }
+            } else {
+                if ((t == 1 || t == 2) && more) dma_wait_barrier<LA>();
+                else dma_wait_barrier<0>();
+            }
+            if (t + 2 < 9) issue_b(r, t + 2, (t + 2) % NSTB);
+            else if (more) issue_b(r + 1, t + 2 - 9, (t + 2) % NSTB);
+            if (t == 0 && more) issue_patch(r + 1, (r + 1) & 1);
+
+            const int kh = t / 3, kw = t % 3;
+            const int emask = (kh == 0 ? 1 : 0) | (kh == 2 ? 2 : 0) | (kw == 0 ? 4 : 0) | (kw == 2 ? 8 : 0);
+            const int toff = pb + (kh * W + kw) * PATCH_PITCH;
+            int aa[MI];
+#pragma unroll
+            for (int i = 0; i < MI; i++) aa[i] = (a_edge[i] & emask) ? z_addr : a_base[i] + toff;
+            const int br = b_rd + (t % NSTB) * B_BYTES;
+#if FF_PATCH_IGLP
+            __builtin_amdgcn_iglp_opt(1);
+#endif
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                v4i af[MI], bf[NJ];
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+                    af[i] = *reinterpret_cast<const v4i*>(smem + aa[i] + ks * 32);
+#pragma unroll
+                for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((br + j * 2048) ^ (ks * 32)));
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();                       // every wave is done with the patches and rings
+
+    if constexpr (KG > 1) {
+        // Block k (owner group o = k / TO) of wave position wg: the partial of
+        // group g != o goes to slot ((k - c0)*(KG-1) + (g > o ? g - 1 : g))*NWG
+        // + wg of the current chunk [c0, c0 + CHUNK), lane L's 16 ints as four
+        // 16-byte pieces q at q*1024 + 16 L (conflict-free); the owner adds
+        // the KG - 1 partials.
+#pragma unroll
+        for (int c0 = 0; c0 < T; c0 += CHUNK) {
+#pragma unroll
+            for (int k = c0; k < c0 + CHUNK && k < T; k++) {
+                const int o = k / TO;
+                if (g != o) {
+                    const int src = g > o ? g - 1 : g;
+                    int8_t* dst = smem + (((k - c0) * (KG - 1) + src) * NWG + wg) * PART + lane * 16;
+                    const v16i& v = acc[k / NJ][k % NJ];
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        *reinterpret_cast<v4i*>(dst + q * 1024) = v4i{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = c0; k < c0 + CHUNK && k < T; k++) {
+                if (g == k / TO) {
+                    v16i& v = acc[k / NJ][k % NJ];
+#pragma unroll
+                    for (int s2 = 0; s2 < KG - 1; s2++) {
+                        const int8_t* srcp = smem + (((k - c0) * (KG - 1) + s2) * NWG + wg) * PART + lane * 16;
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const v4i pv = *reinterpret_cast<const v4i*>(srcp + q * 1024);
+#pragma unroll
+                            for (int e = 0; e < 4; e++) v[4 * q + e] += pv[e];
+                        }
+                    }
+                }
+            }
+            __syncthreads();               // the partial area is free again
+        }
+    }
+    // the owned blocks (all of them when KG == 1) move to the front of the
+    // array, so that one epilogue call with a runtime block offset serves
+    // every group
+    v16i own[MO][NO];
+#pragma unroll
+    for (int i = 0; i < MO; i++)
+#pragma unroll
+        for (int j = 0; j < NO; j++) own[i][j] = acc[i][j];
+    if constexpr (KG > 1) {
+#pragma unroll
+        for (int gg = 1; gg < KG; gg++) {
+            if (g == gg) {
+#pragma unroll
+                for (int i = 0; i < MO; i++)
+#pragma unroll
+                    for (int j = 0; j < NO; j++) {
+                        const int k = gg * TO + i * NO + j;
+                        own[i][j] = acc[k / NJ][k % NJ];
+                    }
+            }
+        }
+    }
+    const int k0 = g * TO;                                   // first owned block
+    const int i0 = k0 / NJ, j0 = k0 % NJ;
+    int8_t* Ws = smem + wave * wave_tile_bytes<MO, NO>();
+    int8_t* Ls = smem + NW * wave_tile_bytes<MO, NO>();
+    if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<NW, BN>(Ls, a.bn_lut, tn * BN);
+    const int ncol = wn * NJ * 32 + j0 * 32;
+    wave_epilogue<COUT, MO, NO, H, W>(own, a, m0 + wm * MI * 32 + i0 * 32, tn * BN + ncol, Ws,
+                                      Ls + ncol * FF_LUT_PITCH);
+}
+
+// ---------------------------------------------------------------------------
 // Stem: 3 -> 64, 3x3, s1, p1 at 112x112, reading the fp32 faces.  One
 // workgroup = two output rows of one face (224 pixels = 7 waves x 32 rows,
 // all 64 channels).  The four input rows it needs are quantized once into

@@ -30,6 +30,12 @@ void launch_patch(const ConvArgs& a, int grid, hipStream_t s) {
                        dim3(WM * WN * 64), 0, s, a);
 }
 
+template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int KG, int WPE>
+void launch_patch_kg(const ConvArgs& a, int grid, hipStream_t s) {
+    hipLaunchKernelGGL((conv3_patch_kg_kernel<CIN, COUT, H, H, WM, WN, MI, NJ, KG, WPE>), dim3(grid),
+                       dim3(WM * WN * KG * 64), 0, s, a);
+}
+
 // Small-batch split-K tiling: 64x64 workgroup tiles (one 32x32 MFMA tile per
 // wave), the K stages of a tile shared by `split` workgroups.
 constexpr int FF_SM_BM = 64, FF_SM_BN = 64;
@@ -166,14 +172,25 @@ constexpr launch_fn split_launch() {
 #define FF_P64(CIN, COUT, H, SPLIT) FF_C64(CIN, COUT, 3, 1, H, SPLIT)
 #define FF_P64W(CIN, COUT, H, SPLIT) FF_C64(CIN, COUT, 3, 1, H, SPLIT)
 #else
-#define FF_P(CIN, COUT, H, SPLIT)                                                   \
-    FF_PENTRY_K(CIN, COUT, H, SPLIT,                                                \
-                (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>), \
-                FF_TPATCH)
-#define FF_PB(CIN, COUT, H, SPLIT)                                                  \
-    FF_PENTRY_K(CIN, COUT, H, SPLIT,                                                \
-                (&launch_conv<CIN, COUT, 3, 1, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>), \
-                FF_TPATCH_BIG)
+// Grids too small for the 256-row tiles (small batches): 128x128 tiles of
+// four 64x64 waves, the channel runs shared by two K-groups inside the
+// workgroup where they divide evenly (conv3_patch_kg_kernel): eight waves,
+// one workgroup per CU.
+#ifndef FF_MID_KG_MAX
+#define FF_MID_KG_MAX 2
+#endif
+// (four groups only where each takes one 64-channel run: with two runs per
+// group the double-buffered patches of four groups exceed the LDS)
+#define FF_MID_KG(CIN) ((CIN) == 256 && FF_MID_KG_MAX >= 4 ? 4 : (((CIN) / 64) % 2 == 0 && FF_MID_KG_MAX >= 2 ? 2 : 1))
+#define FF_MID_WPE(CIN) (FF_MID_KG(CIN) == 2 ? 2 : 4)
+#define FF_PMID(CIN, COUT, H) (&launch_patch_kg<CIN, COUT, H, 2, 2, 2, 2, FF_MID_KG(CIN), FF_MID_WPE(CIN)>)
+#define FF_PENTRY_MID(CIN, COUT, H, SPLIT, WM, WN, MI, NJ, WPE)                       \
+    {CIN, COUT, 3, 1, H, H, WM * MI * 32, WN * NJ * 32,                              \
+     &launch_patch<CIN, COUT, H, WM, WN, MI, NJ, WPE>, SPLIT,                         \
+     split_launch<CIN, COUT, 3, 1, H, SPLIT>(), FF_PMID(CIN, COUT, H), "patch", 128, 128, "patch_kg"}
+#define FF_PENTRY_MID_K(CIN, COUT, H, SPLIT, TILE) FF_PENTRY_MID(CIN, COUT, H, SPLIT, TILE)
+#define FF_P(CIN, COUT, H, SPLIT) FF_PENTRY_MID_K(CIN, COUT, H, SPLIT, FF_TPATCH)
+#define FF_PB(CIN, COUT, H, SPLIT) FF_PENTRY_MID_K(CIN, COUT, H, SPLIT, FF_TPATCH_BIG)
 #define FF_P64(CIN, COUT, H, SPLIT) FF_PENTRY_K(CIN, COUT, H, SPLIT, nullptr, FF_TPATCH64)
 // (small grids: the 256x64 tiles, twice the workgroups)
 #define FF_P64W(CIN, COUT, H, SPLIT)                                                \

@@ -439,8 +439,8 @@ SHORTCUT_S1 = [(64, 64, 56), (64, 128, 28), (128, 256, 14), (256, 512, 7)]
 X_EVEN_CASES = [
     (64, 64, 3, 1, 56, "big", "patch"), (128, 128, 3, 1, 28, "big", "patch"),
     (256, 256, 3, 1, 14, "big", "patch"), (256, 256, 3, 1, 14, 1, "splitk"),
-    (256, 256, 3, 1, 14, 7, "staged128"), (64, 64, 3, 2, 112, "big", "direct"),
-    (64, 128, 3, 1, 56, 2, "staged128"),
+    (256, 256, 3, 1, 14, 7, "patch_kg"), (64, 64, 3, 2, 112, "big", "direct"),
+    (64, 128, 3, 1, 56, 2, "patch_kg"),
 ]
 
 

@@ -162,8 +162,8 @@ def test_conv_variant_policy():
     assert variant(3, 64, 3, 1, 112, 1) == "stem"
     assert variant(256, 256, 3, 1, 14, 1024) == "patch"          # 3x3 stride 1
     assert variant(256, 256, 3, 2, 28, 1024) == "direct"
-    assert variant(256, 256, 3, 1, 14, 64) == "staged128"
-    assert variant(256, 256, 3, 1, 14, 1) == "staged128"          # no workspace given
+    assert variant(256, 256, 3, 1, 14, 64) == "patch_kg"           # small grid: K-groups
+    assert variant(256, 256, 3, 1, 14, 1) == "patch_kg"           # no workspace given
     assert variant(256, 256, 3, 1, 14, 1, ws=1 << 30) == "splitk"
     assert variant(64, 64, 3, 1, 56, 1) == "patch"                # Cout 64: one variant
     assert variant(64, 64, 3, 1, 112, 1) == "patch"               # one 64-channel run

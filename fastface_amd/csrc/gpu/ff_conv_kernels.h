@@ -1017,6 +1017,222 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
 }
 
 // ---------------------------------------------------------------------------
+// 3x3 stride-2 pad-1 conv with the input staged once per channel run, as four
+// phase patches.  Phase (rp, cp) of the input is the image of its pixels
+// (2i + rp, 2j + cp), HO x WO like the output, and indexed like it: tap
+// (kh, kw) of output pixel (oh, ow) reads phase (kh != 1, kw != 1) at
+// (oh + di, ow + dj), di = kh == 0 ? -1 : 0 (dj likewise).  So for a tile of
+// BM consecutive output pixels every tap reads one phase's run of pixels
+// m0 - WO - 1 .. m0 + BM - 1 at a constant offset (0, 1, WO or WO + 1), and a
+// tap whose input row or column is -1 (oh == 0 with di = -1, ow == 0 with
+// dj = -1) reads the zero block instead.  Per 64-channel run the nine taps go
+// phase by phase -- (1,1): 4 taps, (1,0): 2, (0,1): 2, (0,0): 1 -- with the
+// phases' patches double-buffered: the next phase's patch is issued at the
+// barrier of the current phase's first step, before that step's weights, and
+// a phase of one tap waits for it at its own end.  The weights of each tap go
+// through the 3-stage ring of conv3_patch_kernel.  Each input pixel is read
+// about once per tile (the im2col gather of conv_dma_kernel reads each one
+// for every tap that covers it).
+// ---------------------------------------------------------------------------
+namespace s2 {
+// step k of a run: phase, first step of its phase, and the tap
+constexpr int ph[9] = {0, 0, 0, 0, 1, 1, 2, 2, 3};
+constexpr int start[9] = {1, 0, 0, 0, 1, 0, 1, 0, 1};
+constexpr int len[4] = {4, 2, 2, 1};
+constexpr int kh[9] = {0, 0, 2, 2, 0, 2, 1, 1, 1};
+constexpr int kw[9] = {0, 2, 0, 2, 1, 1, 0, 2, 1};
+constexpr int rp[4] = {1, 1, 0, 0};
+constexpr int cp[4] = {1, 0, 1, 0};
+}  // namespace s2
+
+template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int WPE>
+__global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvArgs a) {
+    constexpr int NW = WM * WN;
+    constexpr int NT = NW * 64;
+    constexpr int BM = WM * MI * 32, BN = WN * NJ * 32;
+    constexpr int HO = H / 2, WO = W / 2;
+    constexpr int CSTEPS = CIN / DMA_KB;
+    constexpr int NSTEP = 9 * CSTEPS;
+    constexpr int NP = BM + WO + 1;                          // phase patch pixels
+    constexpr int PSLOTS = NP * (PATCH_PITCH / 16);
+    constexpr int PLOADS = (PSLOTS + 63) / 64;
+    constexpr int LA = (PLOADS + NW - 1) / NW;
+    constexpr int PATCH_BYTES = PLOADS * 1024;
+    constexpr int B_BYTES = BN * DMA_KB;
+    constexpr int BW = B_BYTES / 1024;
+    constexpr bool B_PART = BW < NW;
+    constexpr int B_LD = B_PART ? 1 : B_BYTES / (NT * 16);
+    constexpr int NSTB = 3;
+    constexpr int ZERO_OFF = 2 * PATCH_BYTES;
+    constexpr int RING_OFF = ZERO_OFF + 1024;
+    constexpr int LDS_K = RING_OFF + NSTB * B_BYTES;
+    constexpr int LDS_E = NW * wave_tile_bytes<MI, NJ>() + BN * FF_LUT_PITCH;
+    constexpr int LDS = LDS_K > LDS_E ? LDS_K : LDS_E;
+    static_assert(H % 2 == 0 && W % 2 == 0, "even input");
+    static_assert(CIN % DMA_KB == 0, "Cin must be a multiple of 64");
+    static_assert(B_BYTES % 1024 == 0 && (B_PART || B_BYTES % (NT * 16) == 0), "whole wave loads");
+    static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
+    static_assert(B_LD + LA < 64, "load counter range");
+
+    __shared__ __align__(1024) int8_t smem[LDS];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int xbid = xcd_tile(blockIdx.x, gridDim.x);
+    const int tn = xbid % a.tiles_n;
+    const int tm = xbid / a.tiles_n;
+    const int m0 = tm * BM;
+    const int first = m0 - WO - 1;                           // phase pixel of patch pixel 0
+
+    for (int i = tid; i < 64; i += NT) reinterpret_cast<v4i*>(smem + ZERO_OFF)[i] = v4i{0, 0, 0, 0};
+
+    // patch slot -> input offset of the phase-(0,0) pixel (2i, 2j) of phase
+    // pixel n = first + slot/5 (piece slot%5; piece 4 is the pitch padding),
+    // or -1 (zero page)
+    int p_src[LA];
+#pragma unroll
+    for (int j = 0; j < LA; j++) {
+        const int blk = j * NW + wave;
+        const int slot = blk * 64 + lane;
+        const int px = slot / 5;
+        const int piece = slot - px * 5;
+        const int n = first + px;
+        const bool ok = blk < PLOADS && piece < 4 && n >= 0 && n < a.M;
+        const int nn = ok ? n : 0;
+        const int b = nn / (HO * WO);
+        const int rem = nn - b * (HO * WO);
+        const int i = rem / WO;
+        const int jj = rem - i * WO;
+        p_src[j] = ok ? ((b * H + 2 * i) * W + 2 * jj) * CIN + piece * 16 : -1;
+    }
+    // patch of phase P = c*4 + q (run c) into buffer P & 1
+    auto issue_patch = [&](int P) {
+        const int c = P >> 2, q = P & 3;
+        const int poff = (s2::rp[q] * W + s2::cp[q]) * CIN + c * DMA_KB;
+#pragma unroll
+        for (int j = 0; j < LA; j++) {
+            const int blk = j * NW + wave;
+            const int8_t* src = p_src[j] >= 0 ? a.in + (p_src[j] + poff) : ff_zero_page;
+            dma16(src, smem + (blk < PLOADS ? (P & 1) * PATCH_BYTES + blk * 1024 : ZERO_OFF));
+        }
+    };
+    int b_off[B_LD];
+#pragma unroll
+    for (int j = 0; j < B_LD; j++) {
+        const int line = (j * NW + wave) * 4 + (lane >> 4);
+        const int sl = (lane & 15) ^ (line & 3);
+        const int n = line * 4 + (sl >> 2);
+        b_off[j] = (tn * BN + n) * FF_KSTEP + (sl & 3) * 16;
+    }
+    const bool loads_b = !B_PART || wave < BW;
+    // weights of step s (run s/9, tap of step s%9) into ring slot s % 3
+    auto issue_b = [&](int s) {
+        if (!loads_b) return;
+        const int c = s / 9, k = s - c * 9;
+        const int tap = s2::kh[k] * 3 + s2::kw[k];
+        const int8_t* wst = a.w + (size_t)(tap * CSTEPS + c) * COUT * FF_KSTEP;
+#pragma unroll
+        for (int j = 0; j < B_LD; j++)
+            dma16(wst + b_off[j], smem + RING_OFF + (s % NSTB) * B_BYTES + (j * NW + wave) * 1024);
+    };
+
+    const int wm = wave / WN;
+    const int wn = wave % WN;
+    // edge bits of this lane's output rows: 1 first output row, 4 first column
+    int a_base[MI], a_edge[MI];
+#pragma unroll
+    for (int i = 0; i < MI; i++) {
+        const int r = wm * MI * 32 + i * 32 + (lane & 31);
+        const int m = m0 + r;
+        const int rr = m % (HO * WO);
+        const int oh = rr / WO;
+        const int ow = rr - oh * WO;
+        a_edge[i] = (oh == 0 ? 1 : 0) | (ow == 0 ? 4 : 0);
+        a_base[i] = r * PATCH_PITCH + (lane >> 5) * 16;
+    }
+    const int z_addr = ZERO_OFF + (lane >> 5) * 16;
+    const int b_rd = RING_OFF + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
+
+    v16i acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+    // prologue: patch of phase 0, weights of steps 0 and 1 (in that order)
+    issue_patch(0);
+    issue_b(0);
+    issue_b(1);
+    for (int c = 0; c < CSTEPS; c++) {
+#pragma unroll
+        for (int i = 0; i < MI; i++) asm volatile("" : "+v"(a_base[i]), "+v"(a_edge[i]));
+#pragma unroll
+        for (int k = 0; k < 9; k++) {
+            const int s = c * 9 + k;
+            // Barrier before step s: the step's weights and its phase's patch
+            // have landed.  Loads in flight allowed: the weights of step s+1
+            // (issued at the previous barrier), and the patch issued there
+            // too when the step before starts a phase of more than one step
+            // (then it is the next phase's, not needed yet).
+            const int kp = k == 0 ? 8 : k - 1;               // step s-1 within its run
+            const bool prev_patch = s > 0 && s2::start[kp] && s2::len[s2::ph[kp]] > 1 &&
+                                    !(k == 0 && c == 0);
+            const bool more_b = s + 1 < NSTEP;
+            if (loads_b) {
+                if (prev_patch) {
+                    if (more_b) dma_wait_barrier<B_LD + LA>();
+                    else dma_wait_barrier<LA>();
+                } else {
+                    if (more_b) dma_wait_barrier<B_LD>();
+                    else dma_wait_barrier<0>();
+                }
+            } else {
+                if (prev_patch) dma_wait_barrier<LA>();
+                else dma_wait_barrier<0>();
+            }
+            // at a phase's first step: the next phase's patch (into the buffer
+            // the phase before this one used), then the weights two steps ahead
+            const int P = c * 4 + s2::ph[k];
+            if (s2::start[k] && P + 1 < 4 * CSTEPS) issue_patch(P + 1);
+            if (s + 2 < NSTEP) issue_b(s + 2);
+
+            const int di = s2::kh[k] == 0 ? -1 : 0, dj = s2::kw[k] == 0 ? -1 : 0;
+            const int emask = (di ? 1 : 0) | (dj ? 4 : 0);
+            const int toff = (P & 1) * PATCH_BYTES + ((WO + 1) + di * WO + dj) * PATCH_PITCH;
+            int aa[MI];
+#pragma unroll
+            for (int i = 0; i < MI; i++) aa[i] = (a_edge[i] & emask) ? z_addr : a_base[i] + toff;
+            const int br = b_rd + (s % NSTB) * B_BYTES;
+#if FF_PATCH_IGLP
+            __builtin_amdgcn_iglp_opt(1);
+#endif
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                v4i af[MI], bf[NJ];
+#pragma unroll
+                for (int i = 0; i < MI; i++) af[i] = *reinterpret_cast<const v4i*>(smem + aa[i] + ks * 32);
+#pragma unroll
+                for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((br + j * 2048) ^ (ks * 32)));
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();
+
+    int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
+    int8_t* Ls = smem + NW * wave_tile_bytes<MI, NJ>();
+    if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<NW, BN>(Ls, a.bn_lut, tn * BN);
+    wave_epilogue<COUT, MI, NJ, HO, WO>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
+                                Ls + (wn * NJ * 32) * FF_LUT_PITCH);
+}
+
+// ---------------------------------------------------------------------------
 // Small-grid variant of the 3x3 stride-1 patch kernel: the channel runs of a
 // tile are shared by KG groups of WM x WN waves inside the workgroup (group g
 // takes runs g, g + KG, ...), each group with its own patch buffers and

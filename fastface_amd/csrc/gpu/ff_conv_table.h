@@ -36,6 +36,12 @@ void launch_patch_kg(const ConvArgs& a, int grid, hipStream_t s) {
                        dim3(WM * WN * KG * 64), 0, s, a);
 }
 
+template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int WPE>
+void launch_s2(const ConvArgs& a, int grid, hipStream_t s) {
+    hipLaunchKernelGGL((conv3s2_phase_kernel<CIN, COUT, H, H, WM, WN, MI, NJ, WPE>), dim3(grid),
+                       dim3(WM * WN * 64), 0, s, a);
+}
+
 // Small-batch split-K tiling: 64x64 workgroup tiles (one 32x32 MFMA tile per
 // wave), the K stages of a tile shared by `split` workgroups.
 constexpr int FF_SM_BM = 64, FF_SM_BN = 64;
@@ -197,6 +203,33 @@ constexpr launch_fn split_launch() {
     {CIN, COUT, 3, 1, H, H, 512, 64, &launch_patch<CIN, COUT, H, FF_TPATCH64W>, SPLIT, \
      split_launch<CIN, COUT, 3, 1, H, SPLIT>(), &launch_patch<CIN, COUT, H, FF_TPATCH64>, "patch", \
      256, 64, "patch"}
+#endif
+
+// 3x3 stride-2 layers at large batches: the phase-split patch kernel
+// (conv3s2_phase_kernel) -- 256x128 tiles of 8 waves, 256x64 of 4 waves for
+// Cout = 64; small grids keep the register-staged 128x128 tiles / split-K.
+#ifndef FF_S2_PHASE
+#define FF_S2_PHASE 1
+#endif
+#ifndef FF_TS2
+#define FF_TS2 4, 2, 2, 2, 4
+#endif
+#ifndef FF_TS2_64
+#define FF_TS2_64 4, 1, 2, 2, 4
+#endif
+#define FF_S2ENTRY(CIN, COUT, H, SPLIT, MID, WM, WN, MI, NJ, WPE)                    \
+    {CIN, COUT, 3, 2, H, H, WM * MI * 32, WN * NJ * 32,                              \
+     &launch_s2<CIN, COUT, H, WM, WN, MI, NJ, WPE>, SPLIT,                            \
+     split_launch<CIN, COUT, 3, 2, H, SPLIT>(), MID, "phase"}
+#define FF_S2ENTRY_K(CIN, COUT, H, SPLIT, MID, TILE) FF_S2ENTRY(CIN, COUT, H, SPLIT, MID, TILE)
+#if FF_S2_PHASE
+#define FF_S2(CIN, COUT, H, SPLIT)                                                  \
+    FF_S2ENTRY_K(CIN, COUT, H, SPLIT,                                               \
+                 (&launch_conv<CIN, COUT, 3, 2, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>), FF_TS2)
+#define FF_S2_64(CIN, COUT, H, SPLIT) FF_S2ENTRY_K(CIN, COUT, H, SPLIT, nullptr, FF_TS2_64)
+#else
+#define FF_S2(CIN, COUT, H, SPLIT) FF_CBIG(CIN, COUT, 3, 2, H, SPLIT)
+#define FF_S2_64(CIN, COUT, H, SPLIT) FF_C64(CIN, COUT, 3, 2, H, SPLIT)
 #endif
 
 #ifndef FF_S2_SPLIT

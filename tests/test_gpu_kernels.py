@@ -143,7 +143,7 @@ def _variant(lib, cin, cout, k, s, H, B):
     return v.decode() if v else None
 
 
-BIG_GRID_VARIANTS = ("direct", "patch")
+BIG_GRID_VARIANTS = ("direct", "patch", "phase")
 
 
 def _direct_batch(lib, cin, cout, k, s, H):
@@ -439,7 +439,7 @@ SHORTCUT_S1 = [(64, 64, 56), (64, 128, 28), (128, 256, 14), (256, 512, 7)]
 X_EVEN_CASES = [
     (64, 64, 3, 1, 56, "big", "patch"), (128, 128, 3, 1, 28, "big", "patch"),
     (256, 256, 3, 1, 14, "big", "patch"), (256, 256, 3, 1, 14, 1, "splitk"),
-    (256, 256, 3, 1, 14, 7, "patch_kg"), (64, 64, 3, 2, 112, "big", "direct"),
+    (256, 256, 3, 1, 14, 7, "patch_kg"), (64, 64, 3, 2, 112, "big", "phase"),
     (64, 128, 3, 1, 56, 2, "patch_kg"),
 ]
 

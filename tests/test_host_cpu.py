@@ -161,7 +161,7 @@ def test_conv_variant_policy():
         return v.decode() if v else None
     assert variant(3, 64, 3, 1, 112, 1) == "stem"
     assert variant(256, 256, 3, 1, 14, 1024) == "patch"          # 3x3 stride 1
-    assert variant(256, 256, 3, 2, 28, 1024) == "direct"
+    assert variant(256, 256, 3, 2, 28, 1024) == "phase"           # 3x3 stride 2
     assert variant(256, 256, 3, 1, 14, 64) == "patch_kg"           # small grid: K-groups
     assert variant(256, 256, 3, 1, 14, 1) == "patch_kg"           # no workspace given
     assert variant(256, 256, 3, 1, 14, 1, ws=1 << 30) == "splitk"

@@ -67,6 +67,24 @@ __device__ __forceinline__ void dma16(const int8_t* g, int8_t* lds_wave_base) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
 }
 
+// The same through a buffer resource: byte voff (per lane) + soff (uniform)
+// of the buffer.  A lane whose voff is at or past the buffer's size
+// (FF_OOB) is out of range: the hardware returns zeros and reads no memory.
+// Padding taps and rows past the batch use that instead of a zero page, so
+// the per-lane address is one 32-bit offset (no 64-bit pointer select), and
+// the uniform part stays in a scalar register.
+constexpr unsigned FF_OOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ff_rsrc(const void* base, unsigned bytes) {
+    // raw (stride 0) buffer, 32-bit data format: the range check is offset < bytes
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff, int8_t* lds_wave_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 16, voff, soff, 0,
+                                             0);
+}
+
 struct ConvArgs {
     const int8_t* in;
     const float* in_f32;
@@ -863,24 +881,30 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
 
     __shared__ __align__(1024) int8_t smem[LDS];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    // (the wave index is uniform: kept in a scalar register, so the LDS
+    // destinations of the direct-to-LDS loads are scalar arithmetic)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int xbid = xcd_tile(blockIdx.x, gridDim.x);
     const int tn = xbid % a.tiles_n;
     const int tm = xbid / a.tiles_n;
     const int m0 = tm * BM;
     const int first = m0 - W - 1;                            // input pixel of patch pixel 0
+    // the input tensor (a.M pixels; the host keeps it below 2 GiB) and the
+    // packed weights as buffers
+    const __amdgpu_buffer_rsrc_t r_in = ff_rsrc(a.in, (unsigned)a.M * CIN);
+    const __amdgpu_buffer_rsrc_t r_w = ff_rsrc(a.w, 9u * CSTEPS * COUT * FF_KSTEP);
 
     // Zero block: masked taps read it.  Wave loads beyond the patch's PLOADS
-    // (every thread issues LA, so that all waves count the same loads) fetch
-    // the zero page into it as well.
+    // (every thread issues LA, so that all waves count the same loads) are
+    // out-of-range loads into it.
     for (int i = tid; i < 64; i += NT) reinterpret_cast<v4i*>(smem + ZERO_OFF)[i] = v4i{0, 0, 0, 0};
 
     // Patch slots of this thread: wave load j of wave w is patch block j*NW + w,
     // lane L its slot L, i.e. patch pixel slot/5, piece slot%5 (piece 4 is the
-    // unused 16 bytes).  Input offset of the slot at channel run 0, or -1 for
-    // the zero page (unused piece, or a pixel outside the batch).
-    int p_src[LA];
+    // unused 16 bytes).  Input offset of the slot at channel run 0, or FF_OOB
+    // (unused piece, or a pixel outside the batch: the load returns zeros).
+    unsigned p_src[LA];
 #pragma unroll
     for (int j = 0; j < LA; j++) {
         const int blk = j * NW + wave;
@@ -889,14 +913,13 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
         const int piece = slot - px * 5;
         const int g = first + px;
         const bool ok = blk < PLOADS && piece < 4 && g >= 0 && g < a.M;
-        p_src[j] = ok ? g * CIN + piece * 16 : -1;
+        p_src[j] = ok ? (unsigned)(g * CIN + piece * 16) : FF_OOB;
     }
     auto issue_patch = [&](int c, int buf) {
 #pragma unroll
         for (int j = 0; j < LA; j++) {
             const int blk = j * NW + wave;
-            const int8_t* src = p_src[j] >= 0 ? a.in + (p_src[j] + c * DMA_KB) : ff_zero_page;
-            dma16(src, smem + (blk < PLOADS ? buf * PATCH_BYTES + blk * 1024 : ZERO_OFF));
+            bdma16(r_in, p_src[j], (unsigned)(c * DMA_KB), smem + (blk < PLOADS ? buf * PATCH_BYTES + blk * 1024 : ZERO_OFF));
         }
     };
     int b_off[B_LD];
@@ -911,10 +934,10 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     const bool loads_b = !B_PART || wave < BW;               // (uniform per wave)
     auto issue_b = [&](int c, int t, int slot) {
         if (!loads_b) return;
-        const int8_t* wst = a.w + (size_t)(t * CSTEPS + c) * COUT * FF_KSTEP;
+        const unsigned wst = (unsigned)((t * CSTEPS + c) * COUT * FF_KSTEP);
 #pragma unroll
         for (int j = 0; j < B_LD; j++)
-            dma16(wst + b_off[j], smem + RING_OFF + slot * B_BYTES + (j * NW + wave) * 1024);
+            bdma16(r_w, (unsigned)b_off[j], wst, smem + RING_OFF + slot * B_BYTES + (j * NW + wave) * 1024);
     };
 
     const int wm = wave / WN;

@@ -711,8 +711,11 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
 
     __shared__ __align__(1024) int8_t smem[LDS];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: scalar)
     const int lane = tid & 63;
+    // input (images x HIN x WIN x CIN, below 2 GiB) and packed weights as buffers
+    const __amdgpu_buffer_rsrc_t r_in = ff_rsrc(a.in, (unsigned)(a.M / HWO) * (HIN * WIN * CIN));
+    const __amdgpu_buffer_rsrc_t r_w = ff_rsrc(a.w, (unsigned)KSTEPS * COUT * FF_KSTEP);
     const int xbid = xcd_tile(blockIdx.x, gridDim.x);
     const int tn = xbid % a.tiles_n;
     const int tm = xbid / a.tiles_n;
@@ -722,8 +725,9 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
     // +3 of the stage tile; lane L takes line +L/16, slot L%16.  Registers are
     // kept few (occupancy): a 32-bit image offset per piece, the piece's input
     // origin (a row past the tile's end gets an origin that fails every bounds
-    // check), and its 16-byte slot in a 64-byte channel run.
-    int a_off[A_LD], a_ih0[A_LD], a_iw0[A_LD], a_p[A_LD];
+    // check; such a piece, and every padding tap, is an out-of-range load that
+    // returns zeros).
+    int a_off[A_LD], a_ih0[A_LD], a_iw0[A_LD];
 #pragma unroll
     for (int j = 0; j < A_LD; j++) {
         const int line = (j * NW + wave) * 4 + (lane >> 4);
@@ -740,7 +744,6 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
         a_off[j] = b * (HIN * WIN * CIN) + p * 16;
         a_ih0[j] = ok ? oh * STRIDE - PAD : -4 * HIN;
         a_iw0[j] = ow * STRIDE - PAD;
-        a_p[j] = p;
     }
     int b_off[B_LD];
 #pragma unroll
@@ -761,13 +764,12 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
             const int ih = a_ih0[j] + kh;
             const int iw = a_iw0[j] + kw;
             const bool v = (unsigned)ih < (unsigned)HIN && (unsigned)iw < (unsigned)WIN;
-            const int8_t* src = v ? a.in + (a_off[j] + (ih * WIN + iw) * CIN + cs * DMA_KB)
-                                  : ff_zero_page + a_p[j] * 16;
-            dma16(src, sb + (j * NW + wave) * 1024);
+            bdma16(r_in, v ? (unsigned)(a_off[j] + (ih * WIN + iw) * CIN) : FF_OOB, (unsigned)(cs * DMA_KB),
+                   sb + (j * NW + wave) * 1024);
         }
-        const int8_t* wst = a.w + (size_t)st * COUT * FF_KSTEP;
+        const unsigned wst = (unsigned)(st * COUT * FF_KSTEP);
 #pragma unroll
-        for (int j = 0; j < B_LD; j++) dma16(wst + b_off[j], sb + A_BYTES + (j * NW + wave) * 1024);
+        for (int j = 0; j < B_LD; j++) bdma16(r_w, (unsigned)b_off[j], wst, sb + A_BYTES + (j * NW + wave) * 1024);
     };
 
     const int wm = wave / WN;
@@ -1099,20 +1101,24 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
 
     __shared__ __align__(1024) int8_t smem[LDS];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: scalar)
     const int lane = tid & 63;
     const int xbid = xcd_tile(blockIdx.x, gridDim.x);
     const int tn = xbid % a.tiles_n;
     const int tm = xbid / a.tiles_n;
     const int m0 = tm * BM;
     const int first = m0 - WO - 1;                           // phase pixel of patch pixel 0
+    // input (batch x H x W x CIN, below 2 GiB) and packed weights as buffers
+    const int nimg = a.M / (HO * WO);
+    const __amdgpu_buffer_rsrc_t r_in = ff_rsrc(a.in, (unsigned)nimg * (H * W * CIN));
+    const __amdgpu_buffer_rsrc_t r_w = ff_rsrc(a.w, 9u * CSTEPS * COUT * FF_KSTEP);
 
     for (int i = tid; i < 64; i += NT) reinterpret_cast<v4i*>(smem + ZERO_OFF)[i] = v4i{0, 0, 0, 0};
 
     // patch slot -> input offset of the phase-(0,0) pixel (2i, 2j) of phase
     // pixel n = first + slot/5 (piece slot%5; piece 4 is the pitch padding),
-    // or -1 (zero page)
-    int p_src[LA];
+    // or FF_OOB (the load returns zeros)
+    unsigned p_src[LA];
 #pragma unroll
     for (int j = 0; j < LA; j++) {
         const int blk = j * NW + wave;
@@ -1126,7 +1132,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
         const int rem = nn - b * (HO * WO);
         const int i = rem / WO;
         const int jj = rem - i * WO;
-        p_src[j] = ok ? ((b * H + 2 * i) * W + 2 * jj) * CIN + piece * 16 : -1;
+        p_src[j] = ok ? (unsigned)(((b * H + 2 * i) * W + 2 * jj) * CIN + piece * 16) : FF_OOB;
     }
     // patch of phase P = c*4 + q (run c) into buffer P & 1
     auto issue_patch = [&](int P) {
@@ -1135,8 +1141,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
 #pragma unroll
         for (int j = 0; j < LA; j++) {
             const int blk = j * NW + wave;
-            const int8_t* src = p_src[j] >= 0 ? a.in + (p_src[j] + poff) : ff_zero_page;
-            dma16(src, smem + (blk < PLOADS ? (P & 1) * PATCH_BYTES + blk * 1024 : ZERO_OFF));
+            bdma16(r_in, p_src[j], (unsigned)poff, smem + (blk < PLOADS ? (P & 1) * PATCH_BYTES + blk * 1024 : ZERO_OFF));
         }
     };
     int b_off[B_LD];
@@ -1153,10 +1158,10 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
         if (!loads_b) return;
         const int c = s / 9, k = s - c * 9;
         const int tap = s2::kh[k] * 3 + s2::kw[k];
-        const int8_t* wst = a.w + (size_t)(tap * CSTEPS + c) * COUT * FF_KSTEP;
+        const unsigned wst = (unsigned)((tap * CSTEPS + c) * COUT * FF_KSTEP);
 #pragma unroll
         for (int j = 0; j < B_LD; j++)
-            dma16(wst + b_off[j], smem + RING_OFF + (s % NSTB) * B_BYTES + (j * NW + wave) * 1024);
+            bdma16(r_w, (unsigned)b_off[j], wst, smem + RING_OFF + (s % NSTB) * B_BYTES + (j * NW + wave) * 1024);
     };
 
     const int wm = wave / WN;
@@ -1314,7 +1319,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
 
     __shared__ __align__(1024) int8_t smem[LDS];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: scalar)
     const int lane = tid & 63;
     const int g = wave / NWG;                                // K group (uniform per wave)
     const int wg = wave - g * NWG;                           // wave within the group
@@ -1324,10 +1329,12 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
     const int m0 = tm * BM;
     const int first = m0 - W - 1;
     int8_t* gbase = smem + g * GROUP_BYTES;                   // this group's patches and ring
+    const __amdgpu_buffer_rsrc_t r_in = ff_rsrc(a.in, (unsigned)a.M * CIN);
+    const __amdgpu_buffer_rsrc_t r_w = ff_rsrc(a.w, 9u * CSTEPS * COUT * FF_KSTEP);
 
     for (int i = tid; i < 64; i += NW * 64) reinterpret_cast<v4i*>(smem + ZERO_OFF)[i] = v4i{0, 0, 0, 0};
 
-    int p_src[LA];
+    unsigned p_src[LA];
 #pragma unroll
     for (int j = 0; j < LA; j++) {
         const int blk = j * NWG + wg;
@@ -1336,7 +1343,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
         const int piece = slot - px * 5;
         const int gp = first + px;
         const bool ok = blk < PLOADS && piece < 4 && gp >= 0 && gp < a.M;
-        p_src[j] = ok ? gp * CIN + piece * 16 : -1;
+        p_src[j] = ok ? (unsigned)(gp * CIN + piece * 16) : FF_OOB;
     }
     // run r of this group is channel run g + KG*r
     auto issue_patch = [&](int r, int buf) {
@@ -1344,8 +1351,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
 #pragma unroll
         for (int j = 0; j < LA; j++) {
             const int blk = j * NWG + wg;
-            const int8_t* src = p_src[j] >= 0 ? a.in + (p_src[j] + c * DMA_KB) : ff_zero_page;
-            dma16(src, blk < PLOADS ? gbase + buf * PATCH_BYTES + blk * 1024 : smem + ZERO_OFF);
+            bdma16(r_in, p_src[j], (unsigned)(c * DMA_KB), blk < PLOADS ? gbase + buf * PATCH_BYTES + blk * 1024 : smem + ZERO_OFF);
         }
     };
     int b_off[B_LD];
@@ -1360,10 +1366,10 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
     auto issue_b = [&](int r, int t, int slot) {
         if (!loads_b) return;
         const int c = g + KG * r;
-        const int8_t* wst = a.w + (size_t)(t * CSTEPS + c) * COUT * FF_KSTEP;
+        const unsigned wst = (unsigned)((t * CSTEPS + c) * COUT * FF_KSTEP);
 #pragma unroll
         for (int j = 0; j < B_LD; j++)
-            dma16(wst + b_off[j], gbase + NPB * PATCH_BYTES + slot * B_BYTES + (j * NWG + wg) * 1024);
+            bdma16(r_w, (unsigned)b_off[j], wst, gbase + NPB * PATCH_BYTES + slot * B_BYTES + (j * NWG + wg) * 1024);
     };
 
     const int wm = wg / WN;

@@ -1617,28 +1617,36 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
     EpiParams<2> prm = {};
     if (EPI != STEM_EPI_RAW) prm = load_epi_params<COUT, 2>(a, 0);
 
-    // The patch of tile t+1 is fetched into registers (PE elements per thread)
-    // while tile t runs its MFMAs and epilogue: the loads' latency, not their
-    // bytes, bounds this layer.
-    constexpr int PE = (PATCH + STEM_NT - 1) / STEM_NT;
-    float pv[RGB8 ? 1 : PE];                         // fp32 faces: the raw values
-    int pq[RGB8 ? PE : 1];                           // uint8 pixels: the byte, or -1 for padding
+    // The patch of tile t+1 is fetched into registers while tile t runs its
+    // MFMAs and epilogue: the loads' latency, not their bytes, bounds this
+    // layer.  One thread per patch pixel (4 rows x 114 columns; the first PP
+    // - 1 rounds cover every thread, the last the remainder): its three
+    // channels, 0 for the zero padding (0 quantizes to 0 for any scale, and
+    // the uint8 path marks padding with -1).
+    constexpr int NPIX = 4 * PW;
+    constexpr int PP = (NPIX + STEM_NT - 1) / STEM_NT;
+    float pv[RGB8 ? 1 : PP][3];                      // fp32 faces: the raw values
+    int pq[RGB8 ? PP : 1];                           // uint8 pixels: 3 bytes, or -1 for padding
     auto fetch = [&](int t) {
         const int b = t / (H / 2);
         const int oh0 = (t - b * (H / 2)) * 2;
 #pragma unroll
-        for (int j = 0; j < PE; j++) {
-            const int e = tid + j * STEM_NT;
-            const int pr = e / (PW * 4);
-            const int rem = e - pr * (PW * 4);
-            const int pc = rem >> 2;
-            const int ci = rem & 3;
+        for (int j = 0; j < PP; j++) {
+            const int px = tid + j * STEM_NT;
+            const int pr = px / PW;
+            const int pc = px - pr * PW;
             const int ih = oh0 - 1 + pr;
             const int iw = pc - 1;
-            const bool in = e < PATCH && ci < 3 && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
-            const size_t off = (size_t)b * HW * 3 + (ih * W + iw) * 3 + ci;
-            if constexpr (RGB8) pq[j] = in ? (int)((const uint8_t*)x)[off] : -1;
-            else pv[j] = in ? ((const float*)x)[off] : __builtin_nanf("");
+            const bool in = px < NPIX && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+            const size_t off = ((size_t)b * HW + ih * W + iw) * 3;
+            if constexpr (RGB8) {
+                const uint8_t* src = (const uint8_t*)x + off;
+                pq[j] = in ? (int)(src[0] | (src[1] << 8) | (src[2] << 16)) : -1;
+            } else {
+                const float* src = (const float*)x + off;
+#pragma unroll
+                for (int c = 0; c < 3; c++) pv[j][c] = in ? src[c] : 0.0f;
+            }
         }
     };
     if (t_beg < t_end) fetch(t_beg);
@@ -1649,25 +1657,41 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
         const int m0 = b * HW + oh0 * W;
         __syncthreads();                             // the previous tile is done with Ps / Es
 
-        // input rows oh0-1 .. oh0+2, columns -1 .. 112, channels 0..2 (+1 zero):
-        // fp32 faces quantized in place, or uint8 pixels through the table;
-        // padding and the fourth channel are zero
+        // input rows oh0-1 .. oh0+2, columns -1 .. 112: each pixel's three
+        // channels quantized (fp32 faces) or mapped through the table (uint8),
+        // with a zero fourth byte, as one dword
 #pragma unroll
-        for (int j = 0; j < PE; j++) {
-            const int e = tid + j * STEM_NT;
-            if (e < PATCH) {
-                const int ci = e & 3;
-                int8_t q = 0;
+        for (int j = 0; j < PP; j++) {
+            const int px = tid + j * STEM_NT;
+            if (px < NPIX) {
+                uint32_t packed = 0;
                 if constexpr (RGB8) {
-                    if (pq[j] >= 0) q = a.in_lut[ci * 256 + pq[j]];
+                    if (pq[j] >= 0)
+#pragma unroll
+                        for (int c = 0; c < 3; c++)
+                            packed |= (uint32_t)(uint8_t)a.in_lut[c * 256 + ((pq[j] >> (8 * c)) & 255)] << (8 * c);
                 } else {
-                    const int pr = e / (PW * 4);
-                    const int pc = (e - pr * (PW * 4)) >> 2;
-                    const int ih = oh0 - 1 + pr, iw = pc - 1;
-                    if (ci < 3 && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
-                        q = (int8_t)ff::quant_input(pv[j], ci == 0 ? inv0 : (ci == 1 ? inv1 : inv2));
+                    const float inv[3] = {inv0, inv1, inv2};
+                    float r[3];
+                    bool fast = true;
+#pragma unroll
+                    for (int c = 0; c < 3; c++) {
+                        r[c] = __builtin_rintf(pv[j][c] * inv[c]);
+                        fast = fast && __builtin_fabsf(r[c]) < 2147483648.0f;
+                    }
+                    // every value of the wave in int32 range (real faces): the
+                    // conversion is the clamp; otherwise the exact lrintf rule
+                    if (__all(fast)) {
+#pragma unroll
+                        for (int c = 0; c < 3; c++)
+                            packed |= (uint32_t)(uint8_t)(int)__builtin_amdgcn_fmed3f(r[c], -128.0f, 127.0f) << (8 * c);
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 3; c++)
+                            packed |= (uint32_t)(uint8_t)ff::quant_input(pv[j][c], inv[c]) << (8 * c);
+                    }
                 }
-                Ps[e] = q;
+                reinterpret_cast<uint32_t*>(Ps)[px] = packed;
             }
         }
         // the BN table's loads land before the first tile's barrier (nothing

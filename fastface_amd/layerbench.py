@@ -22,13 +22,15 @@ import fastface_amd as fa  # noqa: E402
 
 
 def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=200, epi="prelu",
-               winograd=False, no_split=False, graph_reps=0, epis=None):
+               winograd=False, no_split=False, graph_reps=0, epis=None, x_even=False):
     """Mean launch time of one conv layer (HIP events on the launch stream)
     over `iters` launches after 3 warm-up launches; frees what it allocates.
     Inputs: seeded int8 U[-127,127] activations and weights (seed 1), ws
     U[1e-3,1e-2], bias N(0,0.1), PReLU slope 0.25.
-    epi: prelu | prelu_le1 | add_bn | none | raw; an "_rng" suffix adds
-    FFK_EPI_IN_RANGE (the parameters here satisfy ffk_requant_in_range).
+    epi: prelu | prelu_le1 | prelu_le1_bn | add_bn | none | raw; an "_rng"
+    suffix adds FFK_EPI_IN_RANGE (the parameters here satisfy
+    ffk_requant_in_range).  x_even: X stored at its even pixels only
+    (FFK_OUT_X_EVEN, as the network stores the stem's and each stage's last X).
     graph_reps > 0: the `iters` launches are captured in one hipGraph (epis,
     if given, cycles the epilogue form per launch) and the graph is replayed
     graph_reps times between the events: the per-launch time then excludes
@@ -85,8 +87,9 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
         d.out_i32 = dev(nbytes=n_out * 4)
     else:
         d.out = dev(nbytes=n_out)
-    if any(f.startswith("add_bn") for f in forms):
+    if any(f.startswith("add") for f in forms):
         d.add_src = dev(r.integers(-127, 128, size=n_out, dtype=np.int8))
+    if any("bn" in f for f in forms):
         d.out_bn = dev(nbytes=n_out)
         lut = np.empty((cout, 256), np.int8)
         rows = [np.ascontiguousarray(P[i]) for i in (fa.FFK_P_BN_SIN, fa.FFK_P_BN_S,
@@ -101,8 +104,12 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
             fl |= fa.FFK_EPI_PRELU
         if f.startswith("prelu_le1"):
             fl |= fa.FFK_EPI_PRELU_LE1
-        if f.startswith("add_bn"):
-            fl |= fa.FFK_EPI_ADD | fa.FFK_EPI_BN
+        if f.startswith("add"):
+            fl |= fa.FFK_EPI_ADD
+        if "bn" in f:
+            fl |= fa.FFK_EPI_BN
+        if x_even:
+            fl |= fa.FFK_OUT_X_EVEN
         if f.endswith("_rng"):
             fl |= fa.FFK_EPI_IN_RANGE
             assert lib.ffk_requant_in_range(P.ctypes.data, cout, k * k * cin, fl) == 1
@@ -125,8 +132,10 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
         for f in forms:
             df = fa.ffk_conv_desc.from_buffer_copy(d)
             df.flags = form_flags(f)
-            if not f.startswith("add_bn"):
-                df.add_src, df.out_bn, df.bn_lut = None, None, None
+            if not f.startswith("add"):
+                df.add_src = None
+            if "bn" not in f:
+                df.out_bn, df.bn_lut = None, None
             descs.append(df)
         for i in range(3):
             assert lib.ffk_conv(C.byref(descs[i % len(descs)]), stream) == 0, fa.last_error()
@@ -234,7 +243,9 @@ def main():
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--epi", default="prelu",
                     choices=["prelu", "prelu_le1", "add_bn", "none", "raw", "prelu_le1_rng", "add_bn_rng",
-                             "none_rng"])
+                             "none_rng", "prelu_le1_bn", "prelu_le1_bn_rng"])
+    ap.add_argument("--x-even", action="store_true",
+                    help="store X at its even pixels only (the network's stem and stage-last convs)")
     ap.add_argument("--winograd", action="store_true",
                     help="64-channel 3x3 stride-1 layers: the integer Winograd F(2,3) path")
     ap.add_argument("--no-split", action="store_true",
@@ -261,7 +272,7 @@ def main():
         return
     try:
         res = time_layer(lib, a.cin, a.cout, a.k, a.stride, a.hin, a.batch, a.iters, a.epi,
-                         winograd=a.winograd, no_split=a.no_split)
+                         winograd=a.winograd, no_split=a.no_split, x_even=a.x_even)
     except ValueError as e:
         raise SystemExit(str(e))
     print(json.dumps(res), flush=True)

@@ -33,6 +33,7 @@
 #pragma once
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "ff_internal.h"
 #include "ff_numerics.h"
@@ -1050,24 +1051,91 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
 // BM consecutive output pixels every tap reads one phase's run of pixels
 // m0 - WO - 1 .. m0 + BM - 1 at a constant offset (0, 1, WO or WO + 1), and a
 // tap whose input row or column is -1 (oh == 0 with di = -1, ow == 0 with
-// dj = -1) reads the zero block instead.  Per 64-channel run the nine taps go
-// phase by phase -- (1,1): 4 taps, (1,0): 2, (0,1): 2, (0,0): 1 -- with the
-// phases' patches double-buffered: the next phase's patch is issued at the
-// barrier of the current phase's first step, before that step's weights, and
-// a phase of one tap waits for it at its own end.  The weights of each tap go
-// through the 3-stage ring of conv3_patch_kernel.  Each input pixel is read
-// about once per tile (the im2col gather of conv_dma_kernel reads each one
-// for every tap that covers it).
+// dj = -1) reads the zero block instead.  The steps go phase by phase --
+// (1,1): 4 taps, (1,0): 2, (0,1): 2, (0,0): 1 -- and within a phase run by run
+// (64 channels each), so the channel runs of one input pixel, which share its
+// 128-byte L2 lines, are fetched one right after the other (run-major order
+// re-fetched those lines from HBM for the second run: 1.57x the algorithmic
+// bytes at 128 channels).  Each (phase, run) patch is staged once in LDS,
+// double-buffered: the next one is issued at the barrier of the current one's
+// first step, before that step's weights, and a one-tap phase waits for it at
+// its own end.  The weights of each tap go through the 3-stage ring of
+// conv3_patch_kernel; s2::Plan computes every barrier's load count at compile
+// time.  Each input pixel is read about once per tile (the im2col gather of
+// conv_dma_kernel reads each one for every tap that covers it).
 // ---------------------------------------------------------------------------
 namespace s2 {
-// step k of a run: phase, first step of its phase, and the tap
-constexpr int ph[9] = {0, 0, 0, 0, 1, 1, 2, 2, 3};
-constexpr int start[9] = {1, 0, 0, 0, 1, 0, 1, 0, 1};
+// taps of the four phases, phase by phase: (1,1) taps 0-3, (1,0) 4-5, (0,1) 6-7, (0,0) 8
+constexpr int first_tap[4] = {0, 4, 6, 8};
 constexpr int len[4] = {4, 2, 2, 1};
 constexpr int kh[9] = {0, 0, 2, 2, 0, 2, 1, 1, 1};
 constexpr int kw[9] = {0, 2, 0, 2, 1, 1, 0, 2, 1};
 constexpr int rp[4] = {1, 1, 0, 0};
 constexpr int cp[4] = {1, 0, 1, 0};
+
+// Step order and load waits of the phase kernel for C 64-channel runs.  The
+// steps go phase-major: phase q's patch for run 0, its taps, then run 1's
+// patch of the same phase and its taps, ...  (one input pixel's channel runs
+// share 128-byte L2 lines, so the runs of a phase follow each other while the
+// lines are still in L2).  Patch p = q*C + c; step s reads patch pat[s] at
+// tap tap[s] of run run[s].  Loads are issued at step barriers, in this order:
+// prologue: patch 0, weights 0, weights 1; at the barrier of step s: patch
+// pat[s] + 1 if s is the first step of its patch, then weights s + 2.  wait[s]
+// (wait_p[s] for a wave that loads no weights) is how many of this wave's
+// loads may still be in flight at step s's barrier, with step s's weights and
+// patch landed: everything issued after the later of the two.
+template <int C, int LA, int BL>
+struct Plan {
+    static constexpr int N = 9 * C;
+    int pat[N], tap[N], run[N], first[N], wait[N], wait_p[N];
+    constexpr Plan() : pat(), tap(), run(), first(), wait(), wait_p() {
+        int st = 0;
+        for (int q = 0; q < 4; q++)
+            for (int c = 0; c < C; c++)
+                for (int t = 0; t < len[q]; t++) {
+                    pat[st] = q * C + c;
+                    tap[st] = first_tap[q] + t;
+                    run[st] = c;
+                    first[st] = t == 0;
+                    st++;
+                }
+        // issue order: (kind, id, count) with kind 0 patch, 1 weights
+        int kind[3 * N + 3] = {}, id[3 * N + 3] = {}, cnt[3 * N + 3] = {}, at[3 * N + 3] = {};
+        int n = 0;
+        auto add = [&](int k, int i, int c_, int barrier) { kind[n] = k; id[n] = i; cnt[n] = c_; at[n] = barrier; n++; };
+        add(0, 0, LA, -1);
+        add(1, 0, BL, -1);
+        if (N > 1) add(1, 1, BL, -1);
+        for (int b = 0; b < N; b++) {
+            if (first[b] && pat[b] + 1 < 4 * C) add(0, pat[b] + 1, LA, b);
+            if (b + 2 < N) add(1, b + 2, BL, b);
+        }
+        for (int s2 = 0; s2 < N; s2++) {
+            int last_w = -1, last_p = -1;
+            for (int i = 0; i < n; i++) {
+                if (kind[i] == 1 && id[i] == s2) last_w = i;
+                if (kind[i] == 0 && id[i] == pat[s2]) last_p = i;
+            }
+            const int lw = last_w > last_p ? last_w : last_p;
+            int after = 0, after_p = 0;
+            for (int i = 0; i < n; i++) {
+                if (at[i] >= s2) continue;                   // not issued yet at this barrier
+                if (i > lw) after += cnt[i];
+                if (i > last_p && kind[i] == 0) after_p += cnt[i];
+            }
+            wait[s2] = after;
+            wait_p[s2] = after_p;
+        }
+    }
+};
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
 }  // namespace s2
 
 template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int WPE>
@@ -1134,9 +1202,9 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
         const int jj = rem - i * WO;
         p_src[j] = ok ? (unsigned)(((b * H + 2 * i) * W + 2 * jj) * CIN + piece * 16) : FF_OOB;
     }
-    // patch of phase P = c*4 + q (run c) into buffer P & 1
+    // patch P = q*CSTEPS + c (phase q of run c) into buffer P & 1
     auto issue_patch = [&](int P) {
-        const int c = P >> 2, q = P & 3;
+        const int q = P / CSTEPS, c = P - q * CSTEPS;
         const int poff = (s2::rp[q] * W + s2::cp[q]) * CIN + c * DMA_KB;
 #pragma unroll
         for (int j = 0; j < LA; j++) {
@@ -1153,10 +1221,11 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
         b_off[j] = (tn * BN + n) * FF_KSTEP + (sl & 3) * 16;
     }
     const bool loads_b = !B_PART || wave < BW;
-    // weights of step s (run s/9, tap of step s%9) into ring slot s % 3
+    // weights of step s (run PLAN.run[s], tap PLAN.tap[s]) into ring slot s % 3
+    constexpr s2::Plan<CSTEPS, LA, B_LD> PLAN{};
     auto issue_b = [&](int s) {
         if (!loads_b) return;
-        const int c = s / 9, k = s - c * 9;
+        const int c = PLAN.run[s], k = PLAN.tap[s];
         const int tap = s2::kh[k] * 3 + s2::kw[k];
         const unsigned wst = (unsigned)((tap * CSTEPS + c) * COUT * FF_KSTEP);
 #pragma unroll
@@ -1189,68 +1258,52 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
-    // prologue: patch of phase 0, weights of steps 0 and 1 (in that order)
+    // prologue: patch 0, weights of steps 0 and 1 (in that order)
     issue_patch(0);
     issue_b(0);
     issue_b(1);
-    for (int c = 0; c < CSTEPS; c++) {
+    s2::static_for<0, NSTEP>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        constexpr int k = PLAN.tap[s];
+        constexpr int P = PLAN.pat[s];
+        if (s % 9 == 0) {
+            // (opaque once per 9 steps: the taps' addresses are recomputed from
+            // these instead of being kept live across the loop)
 #pragma unroll
-        for (int i = 0; i < MI; i++) asm volatile("" : "+v"(a_base[i]), "+v"(a_edge[i]));
-#pragma unroll
-        for (int k = 0; k < 9; k++) {
-            const int s = c * 9 + k;
-            // Barrier before step s: the step's weights and its phase's patch
-            // have landed.  Loads in flight allowed: the weights of step s+1
-            // (issued at the previous barrier), and the patch issued there
-            // too when the step before starts a phase of more than one step
-            // (then it is the next phase's, not needed yet).
-            const int kp = k == 0 ? 8 : k - 1;               // step s-1 within its run
-            const bool prev_patch = s > 0 && s2::start[kp] && s2::len[s2::ph[kp]] > 1 &&
-                                    !(k == 0 && c == 0);
-            const bool more_b = s + 1 < NSTEP;
-            if (loads_b) {
-                if (prev_patch) {
-                    if (more_b) dma_wait_barrier<B_LD + LA>();
-                    else dma_wait_barrier<LA>();
-                } else {
-                    if (more_b) dma_wait_barrier<B_LD>();
-                    else dma_wait_barrier<0>();
-                }
-            } else {
-                if (prev_patch) dma_wait_barrier<LA>();
-                else dma_wait_barrier<0>();
-            }
-            // at a phase's first step: the next phase's patch (into the buffer
-            // the phase before this one used), then the weights two steps ahead
-            const int P = c * 4 + s2::ph[k];
-            if (s2::start[k] && P + 1 < 4 * CSTEPS) issue_patch(P + 1);
-            if (s + 2 < NSTEP) issue_b(s + 2);
+            for (int i = 0; i < MI; i++) asm volatile("" : "+v"(a_base[i]), "+v"(a_edge[i]));
+        }
+        // barrier before step s: its weights and its patch have landed
+        if (loads_b) dma_wait_barrier<PLAN.wait[s]>();
+        else dma_wait_barrier<PLAN.wait_p[s]>();
+        // at a patch's first step: the next patch (into the buffer the patch
+        // before this one used), then the weights two steps ahead
+        if constexpr (PLAN.first[s] && P + 1 < 4 * CSTEPS) issue_patch(P + 1);
+        if constexpr (s + 2 < NSTEP) issue_b(s + 2);
 
-            const int di = s2::kh[k] == 0 ? -1 : 0, dj = s2::kw[k] == 0 ? -1 : 0;
-            const int emask = (di ? 1 : 0) | (dj ? 4 : 0);
-            const int toff = (P & 1) * PATCH_BYTES + ((WO + 1) + di * WO + dj) * PATCH_PITCH;
-            int aa[MI];
+        constexpr int di = s2::kh[k] == 0 ? -1 : 0, dj = s2::kw[k] == 0 ? -1 : 0;
+        constexpr int emask = (di ? 1 : 0) | (dj ? 4 : 0);
+        constexpr int toff = (P & 1) * PATCH_BYTES + ((WO + 1) + di * WO + dj) * PATCH_PITCH;
+        int aa[MI];
 #pragma unroll
-            for (int i = 0; i < MI; i++) aa[i] = (a_edge[i] & emask) ? z_addr : a_base[i] + toff;
-            const int br = b_rd + (s % NSTB) * B_BYTES;
+        for (int i = 0; i < MI; i++) aa[i] = (a_edge[i] & emask) ? z_addr : a_base[i] + toff;
+        const int br = b_rd + (s % NSTB) * B_BYTES;
 #if FF_PATCH_IGLP
-            __builtin_amdgcn_iglp_opt(1);
+        __builtin_amdgcn_iglp_opt(1);
 #endif
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                v4i af[MI], bf[NJ];
+        for (int ks = 0; ks < 2; ks++) {
+            v4i af[MI], bf[NJ];
 #pragma unroll
-                for (int i = 0; i < MI; i++) af[i] = *reinterpret_cast<const v4i*>(smem + aa[i] + ks * 32);
+            for (int i = 0; i < MI; i++) af[i] = *reinterpret_cast<const v4i*>(smem + aa[i] + ks * 32);
 #pragma unroll
-                for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((br + j * 2048) ^ (ks * 32)));
+            for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((br + j * 2048) ^ (ks * 32)));
 #pragma unroll
-                for (int i = 0; i < MI; i++)
+            for (int i = 0; i < MI; i++)
 #pragma unroll
-                    for (int j = 0; j < NJ; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-            }
+                for (int j = 0; j < NJ; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-    }
+    });
     __syncthreads();
 
     int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();

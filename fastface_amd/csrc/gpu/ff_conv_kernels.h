@@ -76,6 +76,22 @@ __device__ __forceinline__ void dma16(const int8_t* g, int8_t* lds_wave_base) {
 // the uniform part stays in a scalar register.
 constexpr unsigned FF_OOB = 0x80000000u;
 
+// Per-workgroup phase timestamps, compiled in only by the phase probe
+// (fastface_amd/csrc/probe/ff_phase_probe.hip defines FF_PHASE_STAMPS as the
+// number of workgroups it records): slot i of workgroup b holds the 100 MHz
+// real-time counter when wave 0 passed point i (0 entry, 1 first barrier of
+// the main loop, 2 main loop done, 3 epilogue start, 4 end).
+#ifdef FF_PHASE_STAMPS
+__device__ unsigned long long ff_phase_stamps[5 * FF_PHASE_STAMPS];
+#define FF_STAMP(i)                                                                        \
+    do {                                                                                   \
+        if (threadIdx.x == 0 && blockIdx.x < FF_PHASE_STAMPS)                              \
+            ff_phase_stamps[blockIdx.x * 5 + (i)] = __builtin_amdgcn_s_memrealtime();      \
+    } while (0)
+#else
+#define FF_STAMP(i) do { } while (0)
+#endif
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ff_rsrc(const void* base, unsigned bytes) {
     // raw (stride 0) buffer, 32-bit data format: the range check is offset < bytes
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
@@ -853,6 +869,7 @@ constexpr int PATCH_PITCH = 80;
 
 template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int WPE>
 __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs a) {
+    FF_STAMP(0);
     constexpr int NW = WM * WN;
     constexpr int NT = NW * 64;
     constexpr int BM = WM * MI * 32, BN = WN * NJ * 32;
@@ -1002,6 +1019,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
                 if ((t == 1 || t == 2) && more) dma_wait_barrier<LA>();
                 else dma_wait_barrier<0>();
             }
+            if (c == 0 && t == 0) FF_STAMP(1);
             if (t + 2 < 9) issue_b(c, t + 2, (t + 2) % NSTB);
             else if (more) issue_b(c + 1, t + 2 - 9, (t + 2) % NSTB);
             if (t == 0 && more) issue_patch(c + 1, (c + 1) & 1);
@@ -1034,12 +1052,15 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
         }
     }
     __syncthreads();                       // every wave is done with the patch and the ring
+    FF_STAMP(2);
+    FF_STAMP(3);
 
     int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
     int8_t* Ls = smem + NW * wave_tile_bytes<MI, NJ>();
     if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<NW, BN>(Ls, a.bn_lut, tn * BN);
     wave_epilogue<COUT, MI, NJ, H, W>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
                                 Ls + (wn * NJ * 32) * FF_LUT_PITCH);
+    FF_STAMP(4);
 }
 
 // ---------------------------------------------------------------------------
@@ -1313,6 +1334,57 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
                                 Ls + (wn * NJ * 32) * FF_LUT_PITCH);
 }
 
+namespace ps1 {
+// Load schedule of the small-grid patch kernel: RUNS channel runs of 9 taps
+// (N = 9*RUNS steps), a barrier before every U-th step, weights D steps ahead
+// in a ring of D + U slots.  Prologue: patch 0, then the weights of steps
+// 0 .. D-1.  At the barrier before step b: the weights of steps b+D ..
+// b+D+U-1, then the patch of run pnext[b/U] (-1: none).  Run r+1's patch goes
+// into the buffer of run r-1, so it is issued at the first barrier at or
+// after run r's first step (every step of run r-1 is done there).
+// wait[k] (wait_p[k] for a wave that loads no weights) is how many of this
+// wave's loads may still be in flight at barrier k with the weights and the
+// patches of steps kU .. kU+U-1 landed.
+template <int RUNS, int LA, int BL, int D, int U>
+struct Plan {
+    static constexpr int N = 9 * RUNS;
+    static constexpr int NB = (N + U - 1) / U;
+    int pnext[NB], wait[NB], wait_p[NB];
+    constexpr Plan() : pnext(), wait(), wait_p() {
+        for (int k = 0; k < NB; k++) pnext[k] = -1;
+        for (int r = 0; r + 1 < RUNS; r++) pnext[(9 * r + U - 1) / U] = r + 1;
+        constexpr int MAXI = 2 * N + RUNS + 2;
+        int kind[MAXI] = {}, id[MAXI] = {}, cnt[MAXI] = {}, at[MAXI] = {};
+        int n = 0;
+        auto add = [&](int k, int i, int c, int bar) { kind[n] = k; id[n] = i; cnt[n] = c; at[n] = bar; n++; };
+        add(0, 0, LA, -1);
+        for (int w = 0; w < D && w < N; w++) add(1, w, BL, -1);
+        for (int k = 0; k < NB; k++) {
+            for (int i = 0; i < U; i++)
+                if (k * U + D + i < N) add(1, k * U + D + i, BL, k);
+            if (pnext[k] >= 0) add(0, pnext[k], LA, k);
+        }
+        for (int k = 0; k < NB; k++) {
+            int last = -1, last_p = -1;
+            for (int st = k * U; st < k * U + U && st < N; st++)
+                for (int i = 0; i < n; i++) {
+                    if (kind[i] == 1 && id[i] == st && i > last) last = i;
+                    if (kind[i] == 0 && id[i] == st / 9 && i > last_p) last_p = i;
+                }
+            if (last_p > last) last = last_p;
+            int after = 0, after_p = 0;
+            for (int i = 0; i < n; i++) {
+                if (at[i] >= k) continue;                    // not issued yet at this barrier
+                if (i > last) after += cnt[i];
+                if (i > last_p && kind[i] == 0) after_p += cnt[i];
+            }
+            wait[k] = after;
+            wait_p[k] = after_p;
+        }
+    }
+};
+}  // namespace ps1
+
 // ---------------------------------------------------------------------------
 // Small-grid variant of the 3x3 stride-1 patch kernel: the channel runs of a
 // tile are shared by KG groups of WM x WN waves inside the workgroup (group g
@@ -1325,9 +1397,14 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
 // runs the epilogue on its blocks.  Integer sums are exact, so the result is
 // the whole-K kernel's.  This gives a small batch KG times the waves without
 // the global workspace and L2 write-backs of split-K across workgroups.
+// A small grid has one workgroup per CU, so no other workgroup fills the
+// SIMDs while its waves meet at a barrier: the steps go U at a time between
+// barriers, the weights D steps ahead in a ring of D + U slots (ps1::Plan);
+// the epilogue's per-channel parameters are loaded before the main loop.
 // ---------------------------------------------------------------------------
-template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int KG, int WPE>
+template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int KG, int WPE, int D, int U>
 __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(ConvArgs a) {
+    FF_STAMP(0);
     constexpr int NWG = WM * WN;                             // waves per group
     constexpr int NW = NWG * KG;
     constexpr int NTG = NWG * 64;
@@ -1343,7 +1420,8 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
     constexpr int BW = B_BYTES / 1024;
     constexpr bool B_PART = BW < NWG;
     constexpr int B_LD = B_PART ? 1 : B_BYTES / (NTG * 16);
-    constexpr int NSTB = 3;
+    constexpr int NSTB = D + U;                              // weight ring slots
+    constexpr int NSTEP = 9 * RUNS;
     constexpr int NPB = RUNS > 1 ? 2 : 1;
     constexpr int GROUP_BYTES = NPB * PATCH_BYTES + NSTB * B_BYTES;
     constexpr int ZERO_OFF = KG * GROUP_BYTES;
@@ -1366,9 +1444,10 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
     static_assert(T % KG == 0 && (TO % NJ == 0 || NJ % TO == 0), "blocks divide among the groups");
     static_assert(B_BYTES % 1024 == 0 && (B_PART || B_BYTES % (NTG * 16) == 0), "whole wave loads");
     static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
-    static_assert(B_LD + LA < 64, "load counter range");
+    static_assert(D >= U && U >= 1 && (D + U) * B_LD + 2 * LA < 64, "load counter range");
     static_assert((2 * W + 2) * PATCH_PITCH + 32 + 16 < 65536, "tap offsets fit the ds_read offset field");
     static_assert(LDS <= 160 * 1024, "LDS");
+    constexpr ps1::Plan<RUNS, LA, B_LD, D, U> PLAN{};
 
     __shared__ __align__(1024) int8_t smem[LDS];
     const int tid = threadIdx.x;
@@ -1449,61 +1528,70 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
-    issue_patch(0, 0);
-    issue_b(0, 0, 0);
-    issue_b(0, 1, 1);
-    for (int r = 0; r < RUNS; r++) {
-        const bool more = r + 1 < RUNS;
-        const int pb = (r & 1) * PATCH_BYTES;
-#pragma unroll
-        for (int i = 0; i < MI; i++) asm volatile("" : "+v"(a_base[i]), "+v"(a_edge[i]));
-#pragma unroll
-        for (int t = 0; t < 9; t++) {
-            if (loads_b) {
-                if (t == 1 || t == 2) {
-                    if (more) dma_wait_barrier<B_LD + LA>();
-                    else dma_wait_barrier<B_LD>();
-                } else if (t == 8) {
-                    if (more) dma_wait_barrier<B_LD>();
-                    else dma_wait_barrier<0>();
-                } else {
-                    dma_wait_barrier<B_LD>();
-                }
-            } else {
-                if ((t == 1 || t == 2) && more) dma_wait_barrier<LA>();
-                else dma_wait_barrier<0>();
-            }
-            if (t + 2 < 9) issue_b(r, t + 2, (t + 2) % NSTB);
-            else if (more) issue_b(r + 1, t + 2 - 9, (t + 2) % NSTB);
-            if (t == 0 && more) issue_patch(r + 1, (r + 1) & 1);
+    // the epilogue's per-channel parameters (columns of the blocks this
+    // group owns), loaded now so that their latency hides behind the main loop
+    const int k0 = g * TO;                                   // first owned block
+    const int i0 = k0 / NJ, j0 = k0 % NJ;
+    const int ncol = wn * NJ * 32 + j0 * 32;
+    EpiParams<NO> prm{};
+    if (!a.out_i32) prm = load_epi_params<COUT, NO>(a, tn * BN + ncol);
 
-            const int kh = t / 3, kw = t % 3;
-            const int emask = (kh == 0 ? 1 : 0) | (kh == 2 ? 2 : 0) | (kw == 0 ? 4 : 0) | (kw == 2 ? 8 : 0);
-            const int toff = pb + (kh * W + kw) * PATCH_PITCH;
-            int aa[MI];
+    // prologue: run 0's patch, then the weights of steps 0 .. D-1
+    issue_patch(0, 0);
+    s2::static_for<0, (D < NSTEP ? D : NSTEP)>([&](auto wc) {
+        constexpr int w = decltype(wc)::value;
+        issue_b(w / 9, w % 9, w % NSTB);
+    });
+    s2::static_for<0, NSTEP>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        constexpr int r = s / 9, t = s % 9;
+        if constexpr (t == 0) {
 #pragma unroll
-            for (int i = 0; i < MI; i++) aa[i] = (a_edge[i] & emask) ? z_addr : a_base[i] + toff;
-            const int br = b_rd + (t % NSTB) * B_BYTES;
+            for (int i = 0; i < MI; i++) asm volatile("" : "+v"(a_base[i]), "+v"(a_edge[i]));
+        }
+        if constexpr (s % U == 0) {
+            // barrier before steps s .. s+U-1: their weights and their runs'
+            // patches have landed
+            constexpr int k = s / U;
+            if (loads_b) dma_wait_barrier<PLAN.wait[k]>();
+            else dma_wait_barrier<PLAN.wait_p[k]>();
+            if constexpr (k == 0) FF_STAMP(1);
+            // the weights D steps ahead (into the slots of steps s-U .. s-1),
+            // then the next run's patch where one is due
+            s2::static_for<0, U>([&](auto ic) {
+                constexpr int w = s + D + decltype(ic)::value;
+                if constexpr (w < NSTEP) issue_b(w / 9, w % 9, w % NSTB);
+            });
+            if constexpr (PLAN.pnext[k] >= 0) issue_patch(PLAN.pnext[k], PLAN.pnext[k] & 1);
+        }
+
+        constexpr int kh = t / 3, kw = t % 3;
+        constexpr int emask = (kh == 0 ? 1 : 0) | (kh == 2 ? 2 : 0) | (kw == 0 ? 4 : 0) | (kw == 2 ? 8 : 0);
+        constexpr int toff = (r & 1) * PATCH_BYTES + (kh * W + kw) * PATCH_PITCH;
+        int aa[MI];
+#pragma unroll
+        for (int i = 0; i < MI; i++) aa[i] = (a_edge[i] & emask) ? z_addr : a_base[i] + toff;
+        const int br = b_rd + (s % NSTB) * B_BYTES;
 #if FF_PATCH_IGLP
-            __builtin_amdgcn_iglp_opt(1);
+        __builtin_amdgcn_iglp_opt(1);
 #endif
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                v4i af[MI], bf[NJ];
+        for (int ks = 0; ks < 2; ks++) {
+            v4i af[MI], bf[NJ];
 #pragma unroll
-                for (int i = 0; i < MI; i++)
-                    af[i] = *reinterpret_cast<const v4i*>(smem + aa[i] + ks * 32);
+            for (int i = 0; i < MI; i++)
+                af[i] = *reinterpret_cast<const v4i*>(smem + aa[i] + ks * 32);
 #pragma unroll
-                for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((br + j * 2048) ^ (ks * 32)));
+            for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((br + j * 2048) ^ (ks * 32)));
 #pragma unroll
-                for (int i = 0; i < MI; i++)
+            for (int i = 0; i < MI; i++)
 #pragma unroll
-                    for (int j = 0; j < NJ; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-            }
+                for (int j = 0; j < NJ; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-    }
+    });
     __syncthreads();                       // every wave is done with the patches and rings
+    FF_STAMP(2);
 
     if constexpr (KG > 1) {
         // Block k (owner group o = k / TO) of wave position wg: the partial of
@@ -1567,14 +1655,13 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
             }
         }
     }
-    const int k0 = g * TO;                                   // first owned block
-    const int i0 = k0 / NJ, j0 = k0 % NJ;
+    FF_STAMP(3);
     int8_t* Ws = smem + wave * wave_tile_bytes<MO, NO>();
     int8_t* Ls = smem + NW * wave_tile_bytes<MO, NO>();
     if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<NW, BN>(Ls, a.bn_lut, tn * BN);
-    const int ncol = wn * NJ * 32 + j0 * 32;
-    wave_epilogue<COUT, MO, NO, H, W>(own, a, m0 + wm * MI * 32 + i0 * 32, tn * BN + ncol, Ws,
-                                      Ls + ncol * FF_LUT_PITCH);
+    wave_epilogue_p<COUT, MO, NO, H, W>(own, a, prm, m0 + wm * MI * 32 + i0 * 32, tn * BN + ncol, Ws,
+                                        Ls + ncol * FF_LUT_PITCH);
+    FF_STAMP(4);
 }
 
 // ---------------------------------------------------------------------------

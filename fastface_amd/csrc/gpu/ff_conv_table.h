@@ -30,9 +30,9 @@ void launch_patch(const ConvArgs& a, int grid, hipStream_t s) {
                        dim3(WM * WN * 64), 0, s, a);
 }
 
-template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int KG, int WPE>
+template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int KG, int WPE, int D, int U>
 void launch_patch_kg(const ConvArgs& a, int grid, hipStream_t s) {
-    hipLaunchKernelGGL((conv3_patch_kg_kernel<CIN, COUT, H, H, WM, WN, MI, NJ, KG, WPE>), dim3(grid),
+    hipLaunchKernelGGL((conv3_patch_kg_kernel<CIN, COUT, H, H, WM, WN, MI, NJ, KG, WPE, D, U>), dim3(grid),
                        dim3(WM * WN * KG * 64), 0, s, a);
 }
 
@@ -189,7 +189,17 @@ constexpr launch_fn split_launch() {
 // group the double-buffered patches of four groups exceed the LDS)
 #define FF_MID_KG(CIN) ((CIN) == 256 && FF_MID_KG_MAX >= 4 ? 4 : (((CIN) / 64) % 2 == 0 && FF_MID_KG_MAX >= 2 ? 2 : 1))
 #define FF_MID_WPE(CIN) (FF_MID_KG(CIN) == 2 ? 2 : 4)
-#define FF_PMID(CIN, COUT, H) (&launch_patch_kg<CIN, COUT, H, 2, 2, 2, 2, FF_MID_KG(CIN), FF_MID_WPE(CIN)>)
+// one barrier per FF_MID_STEPS taps (a small grid has one workgroup per CU:
+// nothing else fills the SIMDs while its waves meet at a barrier); weights
+// FF_MID_DEPTH taps ahead
+#ifndef FF_MID_STEPS
+#define FF_MID_STEPS 2
+#endif
+#ifndef FF_MID_DEPTH
+#define FF_MID_DEPTH FF_MID_STEPS
+#endif
+#define FF_PMID(CIN, COUT, H)                                                        \
+    (&launch_patch_kg<CIN, COUT, H, 2, 2, 2, 2, FF_MID_KG(CIN), FF_MID_WPE(CIN), FF_MID_DEPTH, FF_MID_STEPS>)
 #define FF_PENTRY_MID(CIN, COUT, H, SPLIT, WM, WN, MI, NJ, WPE)                       \
     {CIN, COUT, 3, 1, H, H, WM * MI * 32, WN * NJ * 32,                              \
      &launch_patch<CIN, COUT, H, WM, WN, MI, NJ, WPE>, SPLIT,                         \

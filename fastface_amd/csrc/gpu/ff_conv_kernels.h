@@ -888,8 +888,12 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     constexpr int B_LD = B_PART ? 1 : B_BYTES / (NT * 16);   // weight loads per loading thread and step
     constexpr int NSTB = 3;                                  // weight ring depth (9 % 3 == 0)
     constexpr int NPB = CSTEPS > 1 ? 2 : 1;                  // patch buffers (one run: no double buffer)
-    constexpr int ZERO_OFF = NPB * PATCH_BYTES;              // 1 KB of zeros
-    constexpr int RING_OFF = ZERO_OFF + 1024;
+    // each patch buffer is followed by 1 KB of zeros: a masked tap's address
+    // is the zero block's, and the second buffer's taps are the first's plus
+    // PBUF, the zero block's included
+    constexpr int PBUF = PATCH_BYTES + 1024;
+    constexpr int ZERO_OFF = PATCH_BYTES;
+    constexpr int RING_OFF = NPB * PBUF;
     constexpr int LDS_K = RING_OFF + NSTB * B_BYTES;
     constexpr int LDS_E = NW * wave_tile_bytes<MI, NJ>() + BN * FF_LUT_PITCH;
     constexpr int LDS = LDS_K > LDS_E ? LDS_K : LDS_E;
@@ -897,7 +901,9 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     static_assert(B_BYTES % 1024 == 0 && (B_PART || B_BYTES % (NT * 16) == 0), "whole wave loads");
     static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
     static_assert(B_LD + LA < 64, "load counter range");
-    static_assert((2 * W + 2) * PATCH_PITCH + 32 + 16 < 65536, "tap offsets fit the ds_read offset field");
+    static_assert((NPB - 1) * PBUF + (2 * W + 2) * PATCH_PITCH + 32 + 16 < 65536,
+                  "tap offsets fit the ds_read offset field");
+    static_assert(NPB == 1 || CSTEPS % 2 == 0, "runs go in pairs over the two buffers");
 
     __shared__ __align__(1024) int8_t smem[LDS];
     const int tid = threadIdx.x;
@@ -918,7 +924,8 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     // Zero block: masked taps read it.  Wave loads beyond the patch's PLOADS
     // (every thread issues LA, so that all waves count the same loads) are
     // out-of-range loads into it.
-    for (int i = tid; i < 64; i += NT) reinterpret_cast<v4i*>(smem + ZERO_OFF)[i] = v4i{0, 0, 0, 0};
+    for (int i = tid; i < 64 * NPB; i += NT)
+        reinterpret_cast<v4i*>(smem + ZERO_OFF + (i >> 6) * PBUF)[i & 63] = v4i{0, 0, 0, 0};
 
     // Patch slots of this thread: wave load j of wave w is patch block j*NW + w,
     // lane L its slot L, i.e. patch pixel slot/5, piece slot%5 (piece 4 is the
@@ -939,7 +946,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
 #pragma unroll
         for (int j = 0; j < LA; j++) {
             const int blk = j * NW + wave;
-            bdma16(r_in, p_src[j], (unsigned)(c * DMA_KB), smem + (blk < PLOADS ? buf * PATCH_BYTES + blk * 1024 : ZERO_OFF));
+            bdma16(r_in, p_src[j], (unsigned)(c * DMA_KB), smem + (blk < PLOADS ? buf * PBUF + blk * 1024 : ZERO_OFF));
         }
     };
     int b_off[B_LD];
@@ -980,6 +987,18 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     const int z_addr = ZERO_OFF + (lane >> 5) * 16;
     const int b_rd = RING_OFF + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
 
+    // LDS address of every tap of every row tile of this lane, selected once
+    // (masked taps: the zero block): no per-step address arithmetic
+    int ta[9][MI];
+#pragma unroll
+    for (int t = 0; t < 9; t++) {
+        const int kh = t / 3, kw = t % 3;
+        const int emask = (kh == 0 ? 1 : 0) | (kh == 2 ? 2 : 0) | (kw == 0 ? 4 : 0) | (kw == 2 ? 8 : 0);
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+            ta[t][i] = (a_edge[i] & emask) ? z_addr : a_base[i] + (kh * W + kw) * PATCH_PITCH;
+    }
+
     v16i acc[MI][NJ];
 #pragma unroll
     for (int i = 0; i < MI; i++)
@@ -991,13 +1010,10 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     issue_patch(0, 0);
     issue_b(0, 0, 0);
     issue_b(0, 1, 1);
-    for (int c = 0; c < CSTEPS; c++) {
+    // channel run c, its patch in buffer PB (c % 2: a compile-time offset)
+    auto run = [&](const int c, auto pbc) {
+        constexpr int PB = decltype(pbc)::value;
         const bool more = c + 1 < CSTEPS;
-        const int pb = (c & 1) * PATCH_BYTES;
-        // (opaque per run: the nine taps' addresses are recomputed from these
-        // instead of being kept live across the loop in 18 more registers)
-#pragma unroll
-        for (int i = 0; i < MI; i++) asm volatile("" : "+v"(a_base[i]), "+v"(a_edge[i]));
 #pragma unroll
         for (int t = 0; t < 9; t++) {
             // loads issued after this step's weights: the next step's weights
@@ -1022,14 +1038,8 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
             if (c == 0 && t == 0) FF_STAMP(1);
             if (t + 2 < 9) issue_b(c, t + 2, (t + 2) % NSTB);
             else if (more) issue_b(c + 1, t + 2 - 9, (t + 2) % NSTB);
-            if (t == 0 && more) issue_patch(c + 1, (c + 1) & 1);
+            if (t == 0 && more) issue_patch(c + 1, 1 - PB);
 
-            const int kh = t / 3, kw = t % 3;
-            const int emask = (kh == 0 ? 1 : 0) | (kh == 2 ? 2 : 0) | (kw == 0 ? 4 : 0) | (kw == 2 ? 8 : 0);
-            const int toff = pb + (kh * W + kw) * PATCH_PITCH;
-            int aa[MI];
-#pragma unroll
-            for (int i = 0; i < MI; i++) aa[i] = (a_edge[i] & emask) ? z_addr : a_base[i] + toff;
             const int br = b_rd + (t % NSTB) * B_BYTES;
             // scheduling hint: interleave the LDS reads with the MFMAs that
             // use them (measured 1-4% faster on every patch-kernel layer)
@@ -1040,7 +1050,8 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
             for (int ks = 0; ks < 2; ks++) {
                 v4i af[MI], bf[NJ];
 #pragma unroll
-                for (int i = 0; i < MI; i++) af[i] = *reinterpret_cast<const v4i*>(smem + aa[i] + ks * 32);
+                for (int i = 0; i < MI; i++)
+                    af[i] = *reinterpret_cast<const v4i*>(smem + ta[t][i] + PB * PBUF + ks * 32);
 #pragma unroll
                 for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((br + j * 2048) ^ (ks * 32)));
 #pragma unroll
@@ -1050,6 +1061,10 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
                         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
             }
         }
+    };
+    for (int c = 0; c < CSTEPS; c += NPB) {
+        run(c, std::integral_constant<int, 0>{});
+        if constexpr (NPB == 2) run(c + 1, std::integral_constant<int, 1>{});
     }
     __syncthreads();                       // every wave is done with the patch and the ring
     FF_STAMP(2);

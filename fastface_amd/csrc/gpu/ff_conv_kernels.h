@@ -1192,8 +1192,12 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
     constexpr bool B_PART = BW < NW;
     constexpr int B_LD = B_PART ? 1 : B_BYTES / (NT * 16);
     constexpr int NSTB = 3;
-    constexpr int ZERO_OFF = 2 * PATCH_BYTES;
-    constexpr int RING_OFF = ZERO_OFF + 1024;
+    // each of the two patch buffers is followed by 1 KB of zeros: a masked
+    // tap's address is the zero block's, the second buffer's taps are the
+    // first's plus PBUF
+    constexpr int PBUF = PATCH_BYTES + 1024;
+    constexpr int ZERO_OFF = PATCH_BYTES;
+    constexpr int RING_OFF = 2 * PBUF;
     constexpr int LDS_K = RING_OFF + NSTB * B_BYTES;
     constexpr int LDS_E = NW * wave_tile_bytes<MI, NJ>() + BN * FF_LUT_PITCH;
     constexpr int LDS = LDS_K > LDS_E ? LDS_K : LDS_E;
@@ -1202,6 +1206,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
     static_assert(B_BYTES % 1024 == 0 && (B_PART || B_BYTES % (NT * 16) == 0), "whole wave loads");
     static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
     static_assert(B_LD + LA < 64, "load counter range");
+    static_assert(PBUF + (WO + 1) * PATCH_PITCH + 32 + 16 < 65536, "tap offsets fit the ds_read offset field");
 
     __shared__ __align__(1024) int8_t smem[LDS];
     const int tid = threadIdx.x;
@@ -1217,7 +1222,8 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
     const __amdgpu_buffer_rsrc_t r_in = ff_rsrc(a.in, (unsigned)nimg * (H * W * CIN));
     const __amdgpu_buffer_rsrc_t r_w = ff_rsrc(a.w, 9u * CSTEPS * COUT * FF_KSTEP);
 
-    for (int i = tid; i < 64; i += NT) reinterpret_cast<v4i*>(smem + ZERO_OFF)[i] = v4i{0, 0, 0, 0};
+    for (int i = tid; i < 128; i += NT)
+        reinterpret_cast<v4i*>(smem + ZERO_OFF + (i >> 6) * PBUF)[i & 63] = v4i{0, 0, 0, 0};
 
     // patch slot -> input offset of the phase-(0,0) pixel (2i, 2j) of phase
     // pixel n = first + slot/5 (piece slot%5; piece 4 is the pitch padding),
@@ -1245,7 +1251,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
 #pragma unroll
         for (int j = 0; j < LA; j++) {
             const int blk = j * NW + wave;
-            bdma16(r_in, p_src[j], (unsigned)poff, smem + (blk < PLOADS ? (P & 1) * PATCH_BYTES + blk * 1024 : ZERO_OFF));
+            bdma16(r_in, p_src[j], (unsigned)poff, smem + (blk < PLOADS ? (P & 1) * PBUF + blk * 1024 : ZERO_OFF));
         }
     };
     int b_off[B_LD];
@@ -1285,6 +1291,17 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
     }
     const int z_addr = ZERO_OFF + (lane >> 5) * 16;
     const int b_rd = RING_OFF + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
+    // LDS address of each row tile for the four tap offsets (di, dj) in
+    // {-1, 0}^2 (index (di + 1) * 2 + dj + 1), selected once
+    int ta[4][MI];
+#pragma unroll
+    for (int o = 0; o < 4; o++) {
+        const int di = (o >> 1) - 1, dj = (o & 1) - 1;
+        const int emask = (di ? 1 : 0) | (dj ? 4 : 0);
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+            ta[o][i] = (a_edge[i] & emask) ? z_addr : a_base[i] + ((WO + 1) + di * WO + dj) * PATCH_PITCH;
+    }
 
     v16i acc[MI][NJ];
 #pragma unroll
@@ -1302,12 +1319,6 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
         constexpr int s = decltype(sc)::value;
         constexpr int k = PLAN.tap[s];
         constexpr int P = PLAN.pat[s];
-        if (s % 9 == 0) {
-            // (opaque once per 9 steps: the taps' addresses are recomputed from
-            // these instead of being kept live across the loop)
-#pragma unroll
-            for (int i = 0; i < MI; i++) asm volatile("" : "+v"(a_base[i]), "+v"(a_edge[i]));
-        }
         // barrier before step s: its weights and its patch have landed
         if (loads_b) dma_wait_barrier<PLAN.wait[s]>();
         else dma_wait_barrier<PLAN.wait_p[s]>();
@@ -1316,12 +1327,8 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
         if constexpr (PLAN.first[s] && P + 1 < 4 * CSTEPS) issue_patch(P + 1);
         if constexpr (s + 2 < NSTEP) issue_b(s + 2);
 
-        constexpr int di = s2::kh[k] == 0 ? -1 : 0, dj = s2::kw[k] == 0 ? -1 : 0;
-        constexpr int emask = (di ? 1 : 0) | (dj ? 4 : 0);
-        constexpr int toff = (P & 1) * PATCH_BYTES + ((WO + 1) + di * WO + dj) * PATCH_PITCH;
-        int aa[MI];
-#pragma unroll
-        for (int i = 0; i < MI; i++) aa[i] = (a_edge[i] & emask) ? z_addr : a_base[i] + toff;
+        constexpr int o = (s2::kh[k] == 0 ? 0 : 2) + (s2::kw[k] == 0 ? 0 : 1);
+        constexpr int pbo = (P & 1) * PBUF;
         const int br = b_rd + (s % NSTB) * B_BYTES;
 #if FF_PATCH_IGLP
         __builtin_amdgcn_iglp_opt(1);
@@ -1330,7 +1337,7 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
         for (int ks = 0; ks < 2; ks++) {
             v4i af[MI], bf[NJ];
 #pragma unroll
-            for (int i = 0; i < MI; i++) af[i] = *reinterpret_cast<const v4i*>(smem + aa[i] + ks * 32);
+            for (int i = 0; i < MI; i++) af[i] = *reinterpret_cast<const v4i*>(smem + ta[o][i] + pbo + ks * 32);
 #pragma unroll
             for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((br + j * 2048) ^ (ks * 32)));
 #pragma unroll
@@ -1438,9 +1445,12 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
     constexpr int NSTB = D + U;                              // weight ring slots
     constexpr int NSTEP = 9 * RUNS;
     constexpr int NPB = RUNS > 1 ? 2 : 1;
-    constexpr int GROUP_BYTES = NPB * PATCH_BYTES + NSTB * B_BYTES;
-    constexpr int ZERO_OFF = KG * GROUP_BYTES;
-    constexpr int LDS_K = ZERO_OFF + 1024;
+    // a group's patch buffers are each followed by 1 KB of zeros (masked
+    // taps read them; the second buffer's taps are the first's plus PBUF)
+    constexpr int PBUF = PATCH_BYTES + 1024;
+    constexpr int GROUP_BYTES = NPB * PBUF + NSTB * B_BYTES;
+    constexpr int ZERO_OFF = PATCH_BYTES;                    // (within each group)
+    constexpr int LDS_K = KG * GROUP_BYTES;
     constexpr int T = MI * NJ;                               // MFMA blocks per wave
     constexpr int TO = T / KG;                               // blocks a group owns
     constexpr int PART = 64 * 64;                            // bytes of one block's partial (per wave)
@@ -1460,7 +1470,8 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
     static_assert(B_BYTES % 1024 == 0 && (B_PART || B_BYTES % (NTG * 16) == 0), "whole wave loads");
     static_assert(COUT % BN == 0, "Cout must be a multiple of BN");
     static_assert(D >= U && U >= 1 && (D + U) * B_LD + 2 * LA < 64, "load counter range");
-    static_assert((2 * W + 2) * PATCH_PITCH + 32 + 16 < 65536, "tap offsets fit the ds_read offset field");
+    static_assert((NPB - 1) * PBUF + (2 * W + 2) * PATCH_PITCH + 32 + 16 < 65536,
+                  "tap offsets fit the ds_read offset field");
     static_assert(LDS <= 160 * 1024, "LDS");
     constexpr ps1::Plan<RUNS, LA, B_LD, D, U> PLAN{};
 
@@ -1479,7 +1490,9 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
     const __amdgpu_buffer_rsrc_t r_in = ff_rsrc(a.in, (unsigned)a.M * CIN);
     const __amdgpu_buffer_rsrc_t r_w = ff_rsrc(a.w, 9u * CSTEPS * COUT * FF_KSTEP);
 
-    for (int i = tid; i < 64; i += NW * 64) reinterpret_cast<v4i*>(smem + ZERO_OFF)[i] = v4i{0, 0, 0, 0};
+    for (int i = tid; i < 64 * NPB * KG; i += NW * 64)
+        reinterpret_cast<v4i*>(smem + (i >> 6) / NPB * GROUP_BYTES + ZERO_OFF + (i >> 6) % NPB * PBUF)[i & 63] =
+            v4i{0, 0, 0, 0};
 
     unsigned p_src[LA];
 #pragma unroll
@@ -1498,7 +1511,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
 #pragma unroll
         for (int j = 0; j < LA; j++) {
             const int blk = j * NWG + wg;
-            bdma16(r_in, p_src[j], (unsigned)(c * DMA_KB), blk < PLOADS ? gbase + buf * PATCH_BYTES + blk * 1024 : smem + ZERO_OFF);
+            bdma16(r_in, p_src[j], (unsigned)(c * DMA_KB), gbase + (blk < PLOADS ? buf * PBUF + blk * 1024 : ZERO_OFF));
         }
     };
     int b_off[B_LD];
@@ -1516,7 +1529,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
         const unsigned wst = (unsigned)((t * CSTEPS + c) * COUT * FF_KSTEP);
 #pragma unroll
         for (int j = 0; j < B_LD; j++)
-            bdma16(r_w, (unsigned)b_off[j], wst, gbase + NPB * PATCH_BYTES + slot * B_BYTES + (j * NWG + wg) * 1024);
+            bdma16(r_w, (unsigned)b_off[j], wst, gbase + NPB * PBUF + slot * B_BYTES + (j * NWG + wg) * 1024);
     };
 
     const int wm = wg / WN;
@@ -1532,8 +1545,18 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
         a_edge[i] = (oh == 0 ? 1 : 0) | (oh == H - 1 ? 2 : 0) | (ow == 0 ? 4 : 0) | (ow == W - 1 ? 8 : 0);
         a_base[i] = g * GROUP_BYTES + rr0 * PATCH_PITCH + (lane >> 5) * 16;   // (absolute LDS offsets)
     }
-    const int z_addr = ZERO_OFF + (lane >> 5) * 16;
-    const int b_rd = g * GROUP_BYTES + NPB * PATCH_BYTES + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
+    const int z_addr = g * GROUP_BYTES + ZERO_OFF + (lane >> 5) * 16;
+    const int b_rd = g * GROUP_BYTES + NPB * PBUF + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
+    // LDS address of every tap of every row tile, selected once
+    int ta[9][MI];
+#pragma unroll
+    for (int t = 0; t < 9; t++) {
+        const int kh = t / 3, kw = t % 3;
+        const int emask = (kh == 0 ? 1 : 0) | (kh == 2 ? 2 : 0) | (kw == 0 ? 4 : 0) | (kw == 2 ? 8 : 0);
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+            ta[t][i] = (a_edge[i] & emask) ? z_addr : a_base[i] + (kh * W + kw) * PATCH_PITCH;
+    }
 
     v16i acc[MI][NJ];
 #pragma unroll
@@ -1560,10 +1583,6 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
     s2::static_for<0, NSTEP>([&](auto sc) {
         constexpr int s = decltype(sc)::value;
         constexpr int r = s / 9, t = s % 9;
-        if constexpr (t == 0) {
-#pragma unroll
-            for (int i = 0; i < MI; i++) asm volatile("" : "+v"(a_base[i]), "+v"(a_edge[i]));
-        }
         if constexpr (s % U == 0) {
             // barrier before steps s .. s+U-1: their weights and their runs'
             // patches have landed
@@ -1580,12 +1599,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
             if constexpr (PLAN.pnext[k] >= 0) issue_patch(PLAN.pnext[k], PLAN.pnext[k] & 1);
         }
 
-        constexpr int kh = t / 3, kw = t % 3;
-        constexpr int emask = (kh == 0 ? 1 : 0) | (kh == 2 ? 2 : 0) | (kw == 0 ? 4 : 0) | (kw == 2 ? 8 : 0);
-        constexpr int toff = (r & 1) * PATCH_BYTES + (kh * W + kw) * PATCH_PITCH;
-        int aa[MI];
-#pragma unroll
-        for (int i = 0; i < MI; i++) aa[i] = (a_edge[i] & emask) ? z_addr : a_base[i] + toff;
+        constexpr int pbo = (r & 1) * PBUF;
         const int br = b_rd + (s % NSTB) * B_BYTES;
 #if FF_PATCH_IGLP
         __builtin_amdgcn_iglp_opt(1);
@@ -1595,7 +1609,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
             v4i af[MI], bf[NJ];
 #pragma unroll
             for (int i = 0; i < MI; i++)
-                af[i] = *reinterpret_cast<const v4i*>(smem + aa[i] + ks * 32);
+                af[i] = *reinterpret_cast<const v4i*>(smem + ta[t][i] + pbo + ks * 32);
 #pragma unroll
             for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((br + j * 2048) ^ (ks * 32)));
 #pragma unroll

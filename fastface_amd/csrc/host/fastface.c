@@ -31,6 +31,16 @@
 #define FF_STREAM_CHUNK_U8 1024
 #define FF_MAX_CHUNKS 64
 
+/* Batches of at least FF_SPLIT_MIN faces run as two halves, each on its own
+ * stream inside the one captured graph (a fork and a join): a layer's
+ * kernel of one half fills the CUs the other half's kernel leaves idle in
+ * its last, partly filled round of workgroups (1568 workgroups of the
+ * 256-channel layers at 1024 faces are 3.06 rounds of the 512 the GPU
+ * holds).  Faces are independent, so the embeddings equal the one-chain
+ * path's bit for bit.  Each half has its own I/O descriptor (d_io[part]) and
+ * its own half of the split-K workspace. */
+#define FF_SPLIT_MIN 1024
+
 /* one captured chain per (batch, input format: 0 fp32 faces, 1 uint8 RGB) */
 typedef struct { int batch, fmt; void* exec; } GraphEntry;
 
@@ -60,11 +70,15 @@ struct FastFace {
     float* d_output;            /* capacity * 512 */
     void* d_ws;                 /* split-K workspace of the small-batch convs */
     size_t ws_bytes;
-    ffk_io* d_io;               /* device I/O descriptor */
-    ffk_io* h_io;               /* pinned staging: [0] set_io, [1 + k] chunk k */
+    size_t ws_part;             /* bytes of each half of d_ws */
+    ffk_io* d_io;               /* device I/O descriptors of the two halves */
+    ffk_io* h_io;               /* pinned staging, two descriptors each:
+                                   [0..1] set_io, [2(1 + k)..] chunk k */
     void* cstream;              /* host-to-device copies of streamed chunks */
+    void* sstream;              /* the second half of a split chain */
+    void* ev_fork, *ev_join;    /* (recorded only inside graph capture) */
     void* ev_chunk[FF_MAX_CHUNKS];
-    ffk_io io_cur;              /* what d_io holds now */
+    ffk_io io_cur[2];           /* what d_io holds now */
     int keep_all;
     int algo;                   /* FASTFACE_CONV_* of the 64-channel 3x3 s1 layers */
     GraphEntry graphs[FF_MAX_GRAPHS];
@@ -122,7 +136,26 @@ static void free_activations(FastFace* ff)
     ffk_free(ff->d_output); ff->d_output = NULL;
     ffk_free(ff->d_ws); ff->d_ws = NULL;
     ff->ws_bytes = 0;
+    ff->ws_part = 0;
     ff->capacity = 0;
+}
+
+/* first face of the second half of a `batch` chain, or 0: one chain */
+static int split_at(const FastFace* ff, int batch)
+{
+    return (!ff->keep_all && batch >= FF_SPLIT_MIN) ? batch / 2 : 0;
+}
+
+/* the I/O descriptors of the two halves of a `batch` chain over (in, out);
+ * fmt 0: fp32 faces, 1: uint8 RGB */
+static void io_pair(const FastFace* ff, ffk_io* io, const void* in, float* out, int batch, int fmt)
+{
+    const int na = split_at(ff, batch);
+    const size_t face = (size_t)FASTFACE_INPUT_N * (fmt ? 1 : sizeof(float));
+    io[0].in = (const float*)in;
+    io[0].out = out;
+    io[1].in = (const float*)((const int8_t*)in + (size_t)na * face);
+    io[1].out = out + (size_t)na * FASTFACE_OUTPUT_N;
 }
 
 /* Point the device I/O descriptor at (in, out) for work enqueued next on
@@ -130,23 +163,24 @@ static void free_activations(FastFace* ff)
  * after the last one).  Changed: every earlier enqueue of this context, on
  * any stream, may still read the descriptor or the staging slot, so wait for
  * them on the host first. */
-static int set_io(FastFace* ff, const float* in, float* out, void* stream)
+static int set_io(FastFace* ff, const void* in, float* out, void* stream, int batch, int fmt)
 {
-    if (ff->io_cur.in == in && ff->io_cur.out == out) return 0;
+    ffk_io want[2];
+    io_pair(ff, want, in, out, batch, fmt);
+    if (!memcmp(want, ff->io_cur, sizeof want)) return 0;
     int rc = drain(ff);
     if (!rc) rc = ffk_stream_sync(ff->stream);
     if (!rc && stream != ff->stream) rc = ffk_stream_sync(stream);
     if (rc) return rc;
-    ff->h_io->in = in;
-    ff->h_io->out = out;
-    rc = ffk_memcpy_h2d(ff->d_io, ff->h_io, sizeof(ffk_io), stream);
+    memcpy(ff->h_io, want, sizeof want);
+    rc = ffk_memcpy_h2d(ff->d_io, ff->h_io, sizeof want, stream);
     if (!rc) rc = ffk_stream_sync(stream);
     if (rc) return rc;
-    ff->io_cur = *ff->h_io;
+    memcpy(ff->io_cur, want, sizeof want);
     return 0;
 }
 
-static void step_desc(FastFace* ff, int s, int batch, int fmt, ffk_conv_desc* d);
+static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, int f0, ffk_conv_desc* d);
 
 /* Largest workspace any conv step asks for at 1..max_batch faces.  Only
  * small batches split K (the split grid is capped at a few thousand 64x64
@@ -171,7 +205,7 @@ static size_t workspace_bytes(FastFace* ff, int max_batch)
         if (ff->plan.steps[s].kind != 1) continue;
         for (int b = 1; b <= top + 1; b++) {
             ffk_conv_desc d;
-            step_desc(ff, s, b <= top ? b : max_batch, 0, &d);
+            step_desc(ff, s, b <= top ? b : max_batch, 0, 0, 0, &d);
             const size_t n = ffk_conv_workspace_bytes(&d);
             if (n > best) best = n;
         }
@@ -198,25 +232,32 @@ static int ensure_capacity(FastFace* ff, int batch)
     ff->d_output = (float*)ffk_malloc((size_t)batch * FASTFACE_OUTPUT_N * sizeof(float));
     ff->d_input_u8 = (uint8_t*)ffk_malloc((size_t)batch * FASTFACE_INPUT_N);
     if (!ff->d_input || !ff->d_output || !ff->d_input_u8) { free_activations(ff); return FFK_ERR_NOMEM; }
+    /* one workspace per half of a split chain (each covers any batch up to
+     * the capacity); a one-chain launch uses the first */
     const size_t ws = workspace_bytes(ff, batch);
     if (ws) {
-        ff->d_ws = ffk_malloc(ws);
+        ff->d_ws = ffk_malloc(2 * ws);
         if (!ff->d_ws) { free_activations(ff); return FFK_ERR_NOMEM; }
-        rc = ffk_zero(ff->d_ws, ws, ff->stream);
+        rc = ffk_zero(ff->d_ws, 2 * ws, ff->stream);
         if (!rc) rc = ffk_stream_sync(ff->stream);
         if (rc) { free_activations(ff); return rc; }
-        ff->ws_bytes = ws;
+        ff->ws_bytes = 2 * ws;
+        ff->ws_part = ws;
     }
     ff->capacity = batch;
-    ff->io_cur.in = NULL; ff->io_cur.out = NULL;
+    memset(ff->io_cur, 0, sizeof ff->io_cur);
     return 0;
 }
 
-static int8_t* tensor_ptr(FastFace* ff, int t)
+/* tensor t of face f0 onwards (each buffer holds [batch][face bytes]; a
+ * tensor kept at its even pixels only has a quarter of the pixels) */
+static int8_t* tensor_ptr(FastFace* ff, int t, int f0)
 {
     if (t < 0) return NULL;
-    int b = ff->plan.tensors[t].buf;
-    return b >= 0 ? ff->d_bufs[b] : NULL;
+    const FfTensor* T = &ff->plan.tensors[t];
+    if (T->buf < 0) return NULL;
+    const size_t face = (size_t)T->C * T->H * T->W / (T->even ? 4 : 1);
+    return ff->d_bufs[T->buf] + (size_t)f0 * face;
 }
 
 /* conv descriptor of step s (pointers are NULL while no activations exist);
@@ -233,7 +274,8 @@ static int writes_even(const FastFace* ff, const FfStep* st)
     return st->kind == 1 && st->t_out >= 0 && ff->plan.tensors[st->t_out].even;
 }
 
-static void step_desc(FastFace* ff, int s, int batch, int fmt, ffk_conv_desc* d)
+/* part / f0: the half of a split chain (0 or 1) and its first face */
+static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, int f0, ffk_conv_desc* d)
 {
     const FfStep* st = &ff->plan.steps[s];
     memset(d, 0, sizeof *d);
@@ -242,18 +284,18 @@ static void step_desc(FastFace* ff, int s, int batch, int fmt, ffk_conv_desc* d)
     if (reads_even(ff, st)) { d->stride = 1; d->hin = st->hin / 2; d->win = st->win / 2; }
     if (st->t_in == FF_T_INPUT) {
         d->in = NULL;
-        d->io = ff->d_io;
+        d->io = ff->d_io + part;
         d->in_inv = ff->d_in_inv;
         if (fmt) d->in_lut = ff->d_in_lut;
     } else {
-        d->in = ff->d_bufs ? tensor_ptr(ff, st->t_in) : NULL;
+        d->in = ff->d_bufs ? tensor_ptr(ff, st->t_in, f0) : NULL;
     }
     d->w = ff->d_weights + st->w_off;
     d->params = ff->d_params + st->p_off;
     if (ff->d_bufs) {
-        d->add_src = tensor_ptr(ff, st->t_add);
-        d->out = tensor_ptr(ff, st->t_out);
-        d->out_bn = tensor_ptr(ff, st->t_bn);
+        d->add_src = tensor_ptr(ff, st->t_add, f0);
+        d->out = tensor_ptr(ff, st->t_out, f0);
+        d->out_bn = tensor_ptr(ff, st->t_bn, f0);
     }
     if (st->flags & FFK_EPI_BN) d->bn_lut = ff->d_weights + st->lut_off;
     d->flags = st->flags | ((fmt && st->t_in == FF_T_INPUT) ? FFK_IN_RGB8 : 0) |
@@ -263,41 +305,64 @@ static void step_desc(FastFace* ff, int s, int batch, int fmt, ffk_conv_desc* d)
         d->w = ff->d_weights + st->wino_off;
     }
     d->in_scale = st->in_scale;
-    d->workspace = ff->d_ws;
-    d->workspace_bytes = ff->ws_bytes;
+    d->workspace = ff->d_ws ? (int8_t*)ff->d_ws + (size_t)part * ff->ws_part : NULL;
+    d->workspace_bytes = ff->ws_part;
 }
 
-static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt)
+static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt, int part, int f0)
 {
     const FfStep* st = &ff->plan.steps[s];
     if (st->kind == 1) {
         ffk_conv_desc d;
-        step_desc(ff, s, batch, fmt, &d);
+        step_desc(ff, s, batch, fmt, part, f0, &d);
         return ffk_conv(&d, stream);
     }
     ffk_fc_desc f;
     memset(&f, 0, sizeof f);
     f.batch = batch; f.n = st->fc_n; f.k = st->fc_k;
-    f.a = tensor_ptr(ff, st->t_in);
+    f.a = tensor_ptr(ff, st->t_in, f0);
     f.w = ff->d_weights + st->w_off;
     f.ws = ff->d_params + st->ws_off;
     f.bias = ff->d_params + st->bias_off;
     f.a_scale = st->a_scale;
     f.out = NULL;
-    f.io = ff->d_io;
+    f.io = ff->d_io + part;
     f.path = 0;
-    f.workspace = ff->d_ws;
-    f.workspace_bytes = ff->ws_bytes;
+    f.workspace = ff->d_ws ? (int8_t*)ff->d_ws + (size_t)part * ff->ws_part : NULL;
+    f.workspace_bytes = ff->ws_part;
     return ffk_fc(&f, stream);
+}
+
+/* the chain of faces f0 .. f0 + batch - 1, as half `part` */
+static int run_part(FastFace* ff, int part, int f0, int batch, void* stream, int fmt)
+{
+    for (int s = 0; s < ff->plan.n_steps; s++) {
+        int rc = launch_step(ff, s, batch, stream, fmt, part, f0);
+        if (rc) return rc;
+    }
+    return 0;
 }
 
 static int run_direct(FastFace* ff, int batch, void* stream, int fmt)
 {
-    for (int s = 0; s < ff->plan.n_steps; s++) {
-        int rc = launch_step(ff, s, batch, stream, fmt);
-        if (rc) return rc;
-    }
-    return 0;
+    return run_part(ff, 0, 0, batch, stream, fmt);
+}
+
+/* The chain as captured: one, or two halves forked onto the second stream
+ * and joined back (the join is recorded even after an error, so that the
+ * capture can end). */
+static int run_captured(FastFace* ff, int batch, int fmt)
+{
+    const int na = split_at(ff, batch);
+    if (!na) return run_direct(ff, batch, ff->stream, fmt);
+    int rc = ffk_event_record(ff->ev_fork, ff->stream);
+    if (rc) return rc;
+    rc = ffk_stream_wait_event(ff->sstream, ff->ev_fork);
+    if (!rc) rc = run_part(ff, 0, 0, na, ff->stream, fmt);
+    if (!rc) rc = run_part(ff, 1, na, batch - na, ff->sstream, fmt);
+    int rj = ffk_event_record(ff->ev_join, ff->sstream);
+    if (!rj) rj = ffk_stream_wait_event(ff->stream, ff->ev_join);
+    return rc ? rc : rj;
 }
 
 /* The captured chain for (batch, fmt), capturing it on first use.  A full
@@ -309,7 +374,7 @@ static void* graph_for(FastFace* ff, int batch, int fmt, const void* keep)
     for (int i = 0; i < ff->n_graphs; i++)
         if (ff->graphs[i].batch == batch && ff->graphs[i].fmt == fmt) return ff->graphs[i].exec;
     if (ffk_graph_begin(ff->stream)) return NULL;
-    int rc = run_direct(ff, batch, ff->stream, fmt);
+    int rc = run_captured(ff, batch, fmt);
     void* exec = NULL;
     int rc2 = ffk_graph_end(ff->stream, &exec);
     if (rc || rc2) { if (exec) ffk_graph_destroy(exec); return NULL; }
@@ -382,9 +447,11 @@ FastFace* fastface_create_with_scales(const char* ffw4_path, const char* opsc_pa
     ff->d_params = (float*)ffk_malloc(ff->plan.p_floats * sizeof(float));
     ff->d_in_inv = (float*)ffk_malloc(4 * sizeof(float));
     ff->d_in_lut = (int8_t*)ffk_malloc(3 * 256);
-    ff->d_io = (ffk_io*)ffk_malloc(sizeof(ffk_io));
-    ff->h_io = (ffk_io*)ffk_host_alloc((1 + FF_MAX_CHUNKS) * sizeof(ffk_io));
+    ff->d_io = (ffk_io*)ffk_malloc(2 * sizeof(ffk_io));
+    ff->h_io = (ffk_io*)ffk_host_alloc(2 * (1 + FF_MAX_CHUNKS) * sizeof(ffk_io));
     if (ffk_stream_create(&ff->cstream)) { report("stream", FFK_ERR_HIP); goto fail; }
+    if (ffk_stream_create(&ff->sstream)) { report("stream", FFK_ERR_HIP); goto fail; }
+    if (ffk_event_create(&ff->ev_fork) || ffk_event_create(&ff->ev_join)) { report("event", FFK_ERR_HIP); goto fail; }
     for (int k = 0; k < FF_MAX_CHUNKS; k++)
         if (ffk_event_create(&ff->ev_chunk[k])) { report("event", FFK_ERR_HIP); goto fail; }
     if (ffk_event_create(&ff->ev_last)) { report("event", FFK_ERR_HIP); goto fail; }
@@ -429,6 +496,9 @@ void fastface_destroy(FastFace* ff)
     ffk_free(ff->d_io);
     ffk_host_free(ff->h_io);
     if (ff->cstream) { ffk_stream_sync(ff->cstream); ffk_stream_destroy(ff->cstream); }
+    if (ff->sstream) { ffk_stream_sync(ff->sstream); ffk_stream_destroy(ff->sstream); }
+    if (ff->ev_fork) ffk_event_destroy(ff->ev_fork);
+    if (ff->ev_join) ffk_event_destroy(ff->ev_join);
     for (int k = 0; k < FF_MAX_CHUNKS; k++)
         if (ff->ev_chunk[k]) ffk_event_destroy(ff->ev_chunk[k]);
     if (ff->ev_last) ffk_event_destroy(ff->ev_last);
@@ -467,7 +537,7 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
     if (batch > chunk * FF_MAX_CHUNKS) chunk = (batch + FF_MAX_CHUNKS - 1) / FF_MAX_CHUNKS;
     const int n = (batch + chunk - 1) / chunk;
     if (n < 2 || ff->keep_all) {
-        rc = set_io(ff, (const float*)d_in, ff->d_output, ff->stream);
+        rc = set_io(ff, d_in, ff->d_output, ff->stream, batch, fmt);
         if (!rc) rc = ffk_memcpy_h2d(d_in, in, (size_t)batch * face_bytes, ff->stream);
         if (!rc) rc = enqueue(ff, batch, ff->stream, fmt);
     } else {
@@ -484,17 +554,16 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
                                 (size_t)nb * face_bytes, ff->cstream);
             if (!rc) rc = ffk_event_record(ff->ev_chunk[k], ff->cstream);
             if (!rc) rc = ffk_stream_wait_event(ff->stream, ff->ev_chunk[k]);
-            ffk_io* slot = &ff->h_io[1 + k];
-            slot->in = (const float*)(d_in + b0 * face_bytes);
-            slot->out = ff->d_output + b0 * FASTFACE_OUTPUT_N;
-            if (!rc) rc = ffk_memcpy_h2d(ff->d_io, slot, sizeof(ffk_io), ff->stream);
+            ffk_io* slot = &ff->h_io[2 * (1 + k)];
+            io_pair(ff, slot, d_in + b0 * face_bytes, ff->d_output + b0 * FASTFACE_OUTPUT_N, nb, fmt);
+            if (!rc) rc = ffk_memcpy_h2d(ff->d_io, slot, 2 * sizeof(ffk_io), ff->stream);
             if (!rc) rc = enqueue_exec(ff, nb, ff->stream, fmt, k + 1 < n ? g_chunk : g_last);
-            if (!rc) ff->io_cur = *slot;
+            if (!rc) memcpy(ff->io_cur, slot, sizeof ff->io_cur);
         }
         if (rc) {           /* leave no copy or chunk running into the buffers */
             ffk_stream_sync(ff->cstream);
             ffk_stream_sync(ff->stream);
-            ff->io_cur.in = NULL; ff->io_cur.out = NULL;
+            memset(ff->io_cur, 0, sizeof ff->io_cur);
         }
     }
     if (!rc) rc = ffk_memcpy_d2h(out, ff->d_output, out_bytes, ff->stream);
@@ -524,7 +593,7 @@ int fastface_embed_batch_device(FastFace* ff, const float* d_in, int batch, floa
     if (!stream) stream = ff->stream;
     int rc = ensure_capacity(ff, batch);
     if (rc) { report("activation allocation", rc); return -2; }
-    rc = set_io(ff, d_in, d_out, stream);
+    rc = set_io(ff, d_in, d_out, stream, batch, 0);
     if (!rc) rc = enqueue(ff, batch, stream, 0);
     if (rc) { report("embed_batch_device", rc); return -3; }
     return 0;
@@ -545,7 +614,7 @@ int fastface_embed_batch_rgb8_device(FastFace* ff, const uint8_t* d_in, int batc
     if (!stream) stream = ff->stream;
     int rc = ensure_capacity(ff, batch);
     if (rc) { report("activation allocation", rc); return -2; }
-    rc = set_io(ff, (const float*)d_in, d_out, stream);
+    rc = set_io(ff, d_in, d_out, stream, batch, 1);
     if (!rc) rc = enqueue(ff, batch, stream, 1);
     if (rc) { report("embed_batch_rgb8_device", rc); return -3; }
     return 0;
@@ -612,7 +681,7 @@ int fastface_profile_steps(FastFace* ff, int batch, int reps, float* step_ms)
     if (!ff || !step_ms || batch < 1 || reps < 1) return -1;
     int rc = drain(ff);
     if (!rc) rc = ensure_capacity(ff, batch);
-    if (!rc) rc = set_io(ff, ff->d_input, ff->d_output, ff->stream);
+    if (!rc) rc = set_io(ff, ff->d_input, ff->d_output, ff->stream, batch, 0);
     if (rc) return -2;
     const int n = ff->plan.n_steps;
     void** ev = (void**)calloc((size_t)n + 1, sizeof(void*));
@@ -621,7 +690,7 @@ int fastface_profile_steps(FastFace* ff, int batch, int reps, float* step_ms)
     for (int r = 0; r < reps && !rc; r++) {
         for (int s = 0; s < n && !rc; s++) {
             rc = ffk_event_record(ev[s], ff->stream);
-            if (!rc) rc = launch_step(ff, s, batch, ff->stream, 0);
+            if (!rc) rc = launch_step(ff, s, batch, ff->stream, 0, 0, 0);
         }
         if (!rc) rc = ffk_event_record(ev[n], ff->stream);
         if (!rc) rc = ffk_stream_sync(ff->stream);

@@ -251,6 +251,38 @@ def test_streamed_host_batch_equals_one_shot(ff, gpu_lib):
     assert np.array_equal(ff.embed_batch(x[:3]), got[:3])
 
 
+def test_split_chain_equals_unsplit_halves(gpu_lib, synth_ffw4):
+    """Batches of 1024 faces or more run as two halves, each on its own stream
+    inside one captured graph (fork and join).  Every embedding equals the
+    one-chain result of the smaller batches (faces are independent): 1025
+    fp32 faces (halves of 512 and 513) against 512 + 513 faces, 1024 uint8
+    faces against 2 x 512, and the Winograd stage-1 path split against
+    direct."""
+    f = fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT)
+    try:
+        stream = gpu_lib.fastface_stream(f.ff)
+        B = 1025
+        x = synth.faces_uniform(B, 61)
+        din, dout = Dev(gpu_lib, host=x), Dev(gpu_lib, nbytes=B * 512 * 4)
+        assert gpu_lib.fastface_embed_batch_device(f.ff, din.ptr, B, dout.ptr, None) == 0
+        check(gpu_lib, gpu_lib.ffk_stream_sync(stream))
+        got = dout.get(np.float32, (B, 512))
+        exp = np.concatenate([f.embed_batch(x[:512]), f.embed_batch(x[512:])])
+        assert np.array_equal(got, exp)
+        imgs = np.random.default_rng(62).integers(0, 256, size=(1024, 112, 112, 3), dtype=np.uint8)
+        d8 = Dev(gpu_lib, host=imgs)
+        assert gpu_lib.fastface_embed_batch_rgb8_device(f.ff, d8.ptr, 1024, dout.ptr, None) == 0
+        check(gpu_lib, gpu_lib.ffk_stream_sync(stream))
+        got8 = dout.get(np.float32, (1024, 512))
+        assert np.array_equal(got8, np.concatenate([f.embed_batch_rgb8(imgs[:512]), f.embed_batch_rgb8(imgs[512:])]))
+        assert gpu_lib.fastface_set_conv_algo(f.ff, 1) == 5
+        assert gpu_lib.fastface_embed_batch_device(f.ff, din.ptr, 1024, dout.ptr, None) == 0
+        check(gpu_lib, gpu_lib.ffk_stream_sync(stream))
+        assert np.array_equal(dout.get(np.float32, (1024, 512)), exp[:1024])
+    finally:
+        f.close()
+
+
 def test_concurrent_contexts(gpu_lib, synth_ffw4):
     """One context per thread (fastface.h): two contexts embedding on two
     threads at once -- each with its own stream, buffers and captured chains

@@ -49,15 +49,17 @@ constexpr int LDS_BYTES = 64 * 1024;
 // 2: MFMAs plus, in the same wave, VALU elements of the conv epilogue's
 // arithmetic (10 operations each); 3: the VALU elements alone; 4: waves 0-3
 // of each workgroup run mode 0's MFMAs, waves 4-7 mode 3's VALU work (each
-// SIMD holds MFMA waves and VALU waves).
+// SIMD holds MFMA waves and VALU waves); 5: mode 1's LDS-fed MFMAs with VEL
+// epilogue elements interleaved in the same wave (an epilogue spread over
+// the next tile's main loop).
 // VEL: VALU elements per step (16 MFMAs per step in modes 0-2).
 template <int MODE, int VEL>
 __global__ __launch_bounds__(512) void probe_kernel(int steps, int random, int* guard) {
     __shared__ __align__(1024) int8_t smem[LDS_BYTES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const bool do_mfma = MODE <= 2 || (MODE == 4 && (wave & 4) == 0);
-    const bool do_valu = MODE == 2 || MODE == 3 || (MODE == 4 && (wave & 4) != 0);
-    if (MODE == 1) {
+    const bool do_mfma = MODE <= 2 || MODE == 5 || (MODE == 4 && (wave & 4) == 0);
+    const bool do_valu = MODE == 2 || MODE == 3 || MODE == 5 || (MODE == 4 && (wave & 4) != 0);
+    if (MODE == 1 || MODE == 5) {
         for (int i = tid; i < LDS_BYTES / 16; i += 512) {
             v4i v;
             for (int q = 0; q < 4; q++) v[q] = operand(i * 4 + q, random != 0);
@@ -86,7 +88,7 @@ __global__ __launch_bounds__(512) void probe_kernel(int steps, int random, int* 
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
                 v4i af[2], bf[2];
-                if (MODE == 1) {
+                if (MODE == 1 || MODE == 5) {
                     const int off = ((s * 4 + ks) & 7) * 1024;
 #pragma unroll
                     for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const v4i*>(smem + base + off + i * 8192 + (ks & 1) * 32);
@@ -116,7 +118,7 @@ __global__ __launch_bounds__(512) void probe_kernel(int steps, int random, int* 
                 f[r & 15] = (float)(v + s);
             }
         }
-        if (MODE == 2) {
+        if (MODE == 2 || MODE == 5) {
             // one MFMA, then its share of the VALU work, in the wave's order
 #pragma unroll
             for (int i = 0; i < 16; i++) {
@@ -148,7 +150,8 @@ void run(const char* name, int grid, int steps, int random, int* guard) {
     PROBE_CHECK(hipEventElapsedTime(&ms, e0, e1));
     ms /= 5;
     // 8 waves per workgroup; mode 4: half of them run each kind of work
-    const double mw = MODE <= 2 ? 8 : (MODE == 4 ? 4 : 0), vw = MODE == 2 || MODE == 3 ? 8 : (MODE == 4 ? 4 : 0);
+    const double mw = MODE <= 2 || MODE == 5 ? 8 : (MODE == 4 ? 4 : 0);
+    const double vw = MODE == 2 || MODE == 3 || MODE == 5 ? 8 : (MODE == 4 ? 4 : 0);
     const double mfma = (double)grid * mw * steps * 16;
     const double tops = mfma * 32 * 32 * 32 * 2 / (ms * 1e-3) / 1e12;
     const double valu = (double)grid * vw * steps * VEL * 10;
@@ -182,6 +185,12 @@ int main(int argc, char** argv) {
     run<3, 32>("valu_only", 512, steps, 1, guard);
     run<2, 32>("mfma_and_valu_same_wave", 512, steps, 1, guard);
     run<4, 32>("mfma_waves_beside_valu_waves", 512, steps, 1, guard);
+    // the conv's ratio (~2.5 VALU per MFMA): 4 epilogue elements per 16 MFMAs
+    run<1, 0>("mfma_from_lds", 256, steps, 1, guard);
+    run<5, 4>("mfma_from_lds_and_epilogue_same_wave", 256, steps, 1, guard);
+    run<3, 4>("valu_only", 256, steps, 1, guard);
+    run<5, 4>("mfma_from_lds_and_epilogue_same_wave", 512, steps, 1, guard);
+    run<3, 4>("valu_only", 512, steps, 1, guard);
     PROBE_CHECK(hipFree(guard));
     return 0;
 }

@@ -31,15 +31,21 @@
 #define FF_STREAM_CHUNK_U8 1024
 #define FF_MAX_CHUNKS 64
 
-/* Batches of at least FF_SPLIT_MIN faces run as two halves, each on its own
- * stream inside the one captured graph (a fork and a join): a layer's
- * kernel of one half fills the CUs the other half's kernel leaves idle in
- * its last, partly filled round of workgroups (1568 workgroups of the
- * 256-channel layers at 1024 faces are 3.06 rounds of the 512 the GPU
- * holds).  Faces are independent, so the embeddings equal the one-chain
+/* Batches in the ranges below run as two halves, each on its own stream
+ * inside the one captured graph (a fork and a join): a layer's kernel of one
+ * half fills the CUs the other half's kernel leaves idle (the last, partly
+ * filled round of workgroups at large batches; the small grids at small
+ * ones).  Faces are independent, so the embeddings equal the one-chain
  * path's bit for bit.  Each half has its own I/O descriptor (d_io[part]) and
- * its own half of the split-K workspace. */
-#define FF_SPLIT_MIN 1024
+ * its own half of the split-K workspace.  Measured (ms per batch, one chain
+ * -> two halves, two contexts on two streams, same box): 8 faces 0.63 ->
+ * 0.85, 16-32 equal, 64 0.91 -> 0.85, 128 1.53 -> 1.30, 256 2.51 -> 2.28,
+ * 384 3.16 -> 3.12, 448-640 3-8 % slower (halves of 224-320 faces take the
+ * small-grid tiles the whole batch does not), 704 5.64 -> 5.15, 768 5.71 ->
+ * 5.51, 1024 8.00 -> 7.67. */
+#define FF_SPLIT_SMALL_MIN 64
+#define FF_SPLIT_SMALL_MAX 384
+#define FF_SPLIT_LARGE_MIN 704
 
 /* one captured chain per (batch, input format: 0 fp32 faces, 1 uint8 RGB) */
 typedef struct { int batch, fmt; void* exec; } GraphEntry;
@@ -143,7 +149,9 @@ static void free_activations(FastFace* ff)
 /* first face of the second half of a `batch` chain, or 0: one chain */
 static int split_at(const FastFace* ff, int batch)
 {
-    return (!ff->keep_all && batch >= FF_SPLIT_MIN) ? batch / 2 : 0;
+    if (ff->keep_all) return 0;
+    const int split = (batch >= FF_SPLIT_SMALL_MIN && batch <= FF_SPLIT_SMALL_MAX) || batch >= FF_SPLIT_LARGE_MIN;
+    return split ? batch / 2 : 0;
 }
 
 /* the I/O descriptors of the two halves of a `batch` chain over (in, out);
@@ -180,7 +188,7 @@ static int set_io(FastFace* ff, const void* in, float* out, void* stream, int ba
     return 0;
 }
 
-static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, int f0, ffk_conv_desc* d);
+static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t off, ffk_conv_desc* d);
 
 /* Largest workspace any conv step asks for at 1..max_batch faces.  Only
  * small batches split K (the split grid is capped at a few thousand 64x64
@@ -249,15 +257,17 @@ static int ensure_capacity(FastFace* ff, int batch)
     return 0;
 }
 
-/* tensor t of face f0 onwards (each buffer holds [batch][face bytes]; a
- * tensor kept at its even pixels only has a quarter of the pixels) */
-static int8_t* tensor_ptr(FastFace* ff, int t, int f0)
+/* tensor t of a half whose region starts `off` bytes into every buffer.
+ * The plan reuses a buffer for tensors of different sizes once the earlier
+ * one is dead, and the two halves of a split chain run different layers at
+ * the same time, so each half has its own region of every buffer: the
+ * second starts after the first half's faces at the largest tensor size. */
+static int8_t* tensor_ptr(FastFace* ff, int t, size_t off)
 {
     if (t < 0) return NULL;
     const FfTensor* T = &ff->plan.tensors[t];
     if (T->buf < 0) return NULL;
-    const size_t face = (size_t)T->C * T->H * T->W / (T->even ? 4 : 1);
-    return ff->d_bufs[T->buf] + (size_t)f0 * face;
+    return ff->d_bufs[T->buf] + off;
 }
 
 /* conv descriptor of step s (pointers are NULL while no activations exist);
@@ -274,8 +284,9 @@ static int writes_even(const FastFace* ff, const FfStep* st)
     return st->kind == 1 && st->t_out >= 0 && ff->plan.tensors[st->t_out].even;
 }
 
-/* part / f0: the half of a split chain (0 or 1) and its first face */
-static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, int f0, ffk_conv_desc* d)
+/* part / off: the half of a split chain (0 or 1) and its region's offset
+ * into every activation buffer */
+static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t off, ffk_conv_desc* d)
 {
     const FfStep* st = &ff->plan.steps[s];
     memset(d, 0, sizeof *d);
@@ -288,14 +299,14 @@ static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, int f0,
         d->in_inv = ff->d_in_inv;
         if (fmt) d->in_lut = ff->d_in_lut;
     } else {
-        d->in = ff->d_bufs ? tensor_ptr(ff, st->t_in, f0) : NULL;
+        d->in = ff->d_bufs ? tensor_ptr(ff, st->t_in, off) : NULL;
     }
     d->w = ff->d_weights + st->w_off;
     d->params = ff->d_params + st->p_off;
     if (ff->d_bufs) {
-        d->add_src = tensor_ptr(ff, st->t_add, f0);
-        d->out = tensor_ptr(ff, st->t_out, f0);
-        d->out_bn = tensor_ptr(ff, st->t_bn, f0);
+        d->add_src = tensor_ptr(ff, st->t_add, off);
+        d->out = tensor_ptr(ff, st->t_out, off);
+        d->out_bn = tensor_ptr(ff, st->t_bn, off);
     }
     if (st->flags & FFK_EPI_BN) d->bn_lut = ff->d_weights + st->lut_off;
     d->flags = st->flags | ((fmt && st->t_in == FF_T_INPUT) ? FFK_IN_RGB8 : 0) |
@@ -309,18 +320,18 @@ static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, int f0,
     d->workspace_bytes = ff->ws_part;
 }
 
-static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt, int part, int f0)
+static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt, int part, size_t off)
 {
     const FfStep* st = &ff->plan.steps[s];
     if (st->kind == 1) {
         ffk_conv_desc d;
-        step_desc(ff, s, batch, fmt, part, f0, &d);
+        step_desc(ff, s, batch, fmt, part, off, &d);
         return ffk_conv(&d, stream);
     }
     ffk_fc_desc f;
     memset(&f, 0, sizeof f);
     f.batch = batch; f.n = st->fc_n; f.k = st->fc_k;
-    f.a = tensor_ptr(ff, st->t_in, f0);
+    f.a = tensor_ptr(ff, st->t_in, off);
     f.w = ff->d_weights + st->w_off;
     f.ws = ff->d_params + st->ws_off;
     f.bias = ff->d_params + st->bias_off;
@@ -333,11 +344,12 @@ static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt, in
     return ffk_fc(&f, stream);
 }
 
-/* the chain of faces f0 .. f0 + batch - 1, as half `part` */
-static int run_part(FastFace* ff, int part, int f0, int batch, void* stream, int fmt)
+/* the chain of `batch` faces as half `part`, its activations `off` bytes
+ * into every buffer */
+static int run_part(FastFace* ff, int part, size_t off, int batch, void* stream, int fmt)
 {
     for (int s = 0; s < ff->plan.n_steps; s++) {
-        int rc = launch_step(ff, s, batch, stream, fmt, part, f0);
+        int rc = launch_step(ff, s, batch, stream, fmt, part, off);
         if (rc) return rc;
     }
     return 0;
@@ -359,7 +371,7 @@ static int run_captured(FastFace* ff, int batch, int fmt)
     if (rc) return rc;
     rc = ffk_stream_wait_event(ff->sstream, ff->ev_fork);
     if (!rc) rc = run_part(ff, 0, 0, na, ff->stream, fmt);
-    if (!rc) rc = run_part(ff, 1, na, batch - na, ff->sstream, fmt);
+    if (!rc) rc = run_part(ff, 1, (size_t)na * ff->plan.max_face_bytes, batch - na, ff->sstream, fmt);
     int rj = ffk_event_record(ff->ev_join, ff->sstream);
     if (!rj) rj = ffk_stream_wait_event(ff->stream, ff->ev_join);
     return rc ? rc : rj;

@@ -252,33 +252,49 @@ def test_streamed_host_batch_equals_one_shot(ff, gpu_lib):
 
 
 def test_split_chain_equals_unsplit_halves(gpu_lib, synth_ffw4):
-    """Batches of 1024 faces or more run as two halves, each on its own stream
-    inside one captured graph (fork and join).  Every embedding equals the
-    one-chain result of the smaller batches (faces are independent): 1025
-    fp32 faces (halves of 512 and 513) against 512 + 513 faces, 1024 uint8
-    faces against 2 x 512, and the Winograd stage-1 path split against
-    direct."""
+    """Batches of 64-384 and of 704 or more faces run as two halves, each on
+    its own stream inside one captured graph (fork and join), each half in
+    its own region of every activation buffer.  Every embedding of every
+    face equals the one-chain result of 32-face batches (faces are
+    independent), for batches on the small-grid and split-K kernels (101,
+    256, 384: halves of 50-192 faces, each with its own workspace) and on the
+    large tiles (1025: halves of 512 and 513), captured and then replayed;
+    1024 uint8 faces against 32-face batches; the Winograd stage-1 path split
+    against direct.  (Regression: halves that shared buffer regions corrupted
+    faces from B/4 on, because a buffer holds tensors of different sizes at
+    different layers and the halves run different layers at once.)"""
     f = fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT)
     try:
         stream = gpu_lib.fastface_stream(f.ff)
-        B = 1025
-        x = synth.faces_uniform(B, 61)
-        din, dout = Dev(gpu_lib, host=x), Dev(gpu_lib, nbytes=B * 512 * 4)
-        assert gpu_lib.fastface_embed_batch_device(f.ff, din.ptr, B, dout.ptr, None) == 0
-        check(gpu_lib, gpu_lib.ffk_stream_sync(stream))
-        got = dout.get(np.float32, (B, 512))
-        exp = np.concatenate([f.embed_batch(x[:512]), f.embed_batch(x[512:])])
-        assert np.array_equal(got, exp)
+
+        def pieces(fn, a):
+            return np.concatenate([fn(a[i:i + 32]) for i in range(0, len(a), 32)])
+
+        for B in (101, 256, 384, 1025):
+            x = synth.faces_uniform(B, 61 + B)
+            exp = pieces(f.embed_batch, x)
+            din, dout = Dev(gpu_lib, host=x), Dev(gpu_lib, nbytes=B * 512 * 4)
+            for rep in range(2):                  # capture, then replay
+                assert gpu_lib.fastface_embed_batch_device(f.ff, din.ptr, B, dout.ptr, None) == 0
+                check(gpu_lib, gpu_lib.ffk_stream_sync(stream))
+                got = dout.get(np.float32, (B, 512))
+                bad = [i for i in range(B) if not np.array_equal(got[i], exp[i])]
+                assert not bad, "B=%d replay %d: faces %s differ" % (B, rep, bad[:16])
+            assert np.array_equal(f.embed_batch(x), exp), B     # host path
         imgs = np.random.default_rng(62).integers(0, 256, size=(1024, 112, 112, 3), dtype=np.uint8)
-        d8 = Dev(gpu_lib, host=imgs)
+        d8, dout = Dev(gpu_lib, host=imgs), Dev(gpu_lib, nbytes=1024 * 512 * 4)
         assert gpu_lib.fastface_embed_batch_rgb8_device(f.ff, d8.ptr, 1024, dout.ptr, None) == 0
         check(gpu_lib, gpu_lib.ffk_stream_sync(stream))
-        got8 = dout.get(np.float32, (1024, 512))
-        assert np.array_equal(got8, np.concatenate([f.embed_batch_rgb8(imgs[:512]), f.embed_batch_rgb8(imgs[512:])]))
+        assert np.array_equal(dout.get(np.float32, (1024, 512)), pieces(f.embed_batch_rgb8, imgs))
+        x = synth.faces_uniform(1024, 64)
+        din = Dev(gpu_lib, host=x)
+        assert gpu_lib.fastface_embed_batch_device(f.ff, din.ptr, 1024, dout.ptr, None) == 0
+        check(gpu_lib, gpu_lib.ffk_stream_sync(stream))
+        direct = dout.get(np.float32, (1024, 512))
         assert gpu_lib.fastface_set_conv_algo(f.ff, 1) == 5
         assert gpu_lib.fastface_embed_batch_device(f.ff, din.ptr, 1024, dout.ptr, None) == 0
         check(gpu_lib, gpu_lib.ffk_stream_sync(stream))
-        assert np.array_equal(dout.get(np.float32, (1024, 512)), exp[:1024])
+        assert np.array_equal(dout.get(np.float32, (1024, 512)), direct)
     finally:
         f.close()
 

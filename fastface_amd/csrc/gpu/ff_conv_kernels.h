@@ -184,8 +184,12 @@ __device__ __forceinline__ int8_t* x_row(const ConvArgs& a, int m) {
 // HO x WO: output image size (FFK_OUT_X_EVEN addressing).
 // LUT_DMA: the BN table was issued as direct-to-LDS loads (issue_bn_lut) that
 // may still be in flight; they are waited for before the flush.
+// WG_SYNC: a workgroup barrier before the flush, which makes a BN table other
+// waves loaded visible; without it (a table already visible, as in the
+// persistent stem after its first tile) the flush reads only the wave's own
+// staging tile, which the wave's in-order LDS accesses already order.
 template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC, bool RANGE, int HO, int WO,
-          bool LUT_DMA = false>
+          bool LUT_DMA = false, bool WG_SYNC = true>
 __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                             const EpiParams<NJ>& prm, int mrow0, int ncol0, int8_t* Ws,
                                             const int8_t* Lw) {
@@ -256,7 +260,8 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
                 if (r == 15) asm volatile("" ::: "memory");
             }
     if (BN2 && LUT_DMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    if constexpr (WG_SYNC) __syncthreads();
+    else __builtin_amdgcn_wave_barrier();
     // Flush: 16-byte chunks of the X tile go out as they are; the BN second
     // output maps each byte through its channel's table on the way.
 #pragma unroll
@@ -1722,6 +1727,12 @@ constexpr int STEM_WG_PER_CU = FF_STEM_WG_PER_CU;
 //   7    raw int32 accumulators
 //   8-13 0-5 with FFK_EPI_IN_RANGE
 constexpr int STEM_EPI_INSC = 6, STEM_EPI_RAW = 7;
+// The epilogue's workgroup barrier: the BN table is loaded once and waited
+// for before the first tile's patch barrier, and each wave flushes only its
+// own staging tile, so the stem needs none.
+#ifndef FF_STEM_EPI_SYNC
+#define FF_STEM_EPI_SYNC false
+#endif
 
 // (7 waves per workgroup over 4 SIMDs: STEM_WG_PER_CU * 7 / 4 waves per SIMD)
 template <bool RGB8, int EPI>
@@ -1824,7 +1835,9 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
         const int b = t / (H / 2);
         const int oh0 = (t - b * (H / 2)) * 2;
         const int m0 = b * HW + oh0 * W;
-        __syncthreads();                             // the previous tile is done with Ps / Es
+        // the previous tile is done with the patch (a second patch buffer
+        // instead of this barrier measured 7 % slower)
+        __syncthreads();
 
         // input rows oh0-1 .. oh0+2, columns -1 .. 112: each pixel's three
         // channels quantized (fp32 faces) or mapped through the table (uint8),
@@ -1886,8 +1899,8 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
         const int mw = m0 + wave * 32;
         if constexpr (EPI == STEM_EPI_RAW) wave_epi_wide<COUT, 1, 2, false>(acc, a, mw, 0);
         else if constexpr (EPI == STEM_EPI_INSC) wave_epilogue_f<COUT, 1, 2, true, H, W>(acc, a, prm, mw, 0, Ws, Ls);
-        else wave_epi_i8<COUT, 1, 2, (EPI & 7) % 3, false, ((EPI & 7) >= 3), false, (EPI >= 8), H, W>(
-            acc, a, prm, mw, 0, Ws, Ls);
+        else wave_epi_i8<COUT, 1, 2, (EPI & 7) % 3, false, ((EPI & 7) >= 3), false, (EPI >= 8), H, W, false,
+                         FF_STEM_EPI_SYNC>(acc, a, prm, mw, 0, Ws, Ls);
     }
 }
 

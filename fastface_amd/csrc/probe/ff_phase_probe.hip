@@ -15,8 +15,10 @@
 // Synthetic random int8 activations and weights, the PReLU epilogue in the
 // in-range form the network runs.  Per case one JSON line: the mean launch
 // time of 20 back-to-back launches (HIP events), the span from the first
-// workgroup's entry to the last one's end, and the median and maximum over
-// workgroups of each phase, all of the last of those launches.
+// workgroup's entry to the last one's end, the median and maximum over
+// workgroups of each phase, the last workgroup's start and the times by which
+// 50 / 90 / 98 / 100 % of the workgroups had ended, all of the last of those
+// launches.
 #define FF_PHASE_STAMPS 4096
 #include "ff_conv_table.h"
 
@@ -109,11 +111,22 @@ void run_case(const char* kernel, ffconv::launch_fn fn, int batch, int bm, int b
         for (int i = 0; i < 4; i++) ph[i].push_back((double)(r[i + 1] - r[i]) * us_per_tick);
         ph[4].push_back((double)(r[4] - r[0]) * us_per_tick);
     }
+    // when the workgroups start and end, from the first entry: the last start, and the time
+    // by which 50 / 90 / 98 % of them had ended and the last one did
+    std::vector<double> st, en;
+    for (int b = 0; b < grid; b++) {
+        st.push_back((double)(t[(size_t)b * 5] - first) * us_per_tick);
+        en.push_back((double)(t[(size_t)b * 5 + 4] - first) * us_per_tick);
+    }
+    std::sort(en.begin(), en.end());
+    auto pct = [&](double q) { return en[std::min(grid - 1, (int)(q * grid))]; };
     const char* name[5] = {"prologue", "main_loop", "reduction", "epilogue", "workgroup"};
     printf("{\"kernel\": \"%s\", \"batch\": %d, \"grid\": %d, \"launch_us\": %.2f, \"span_us\": %.2f",
            kernel, batch, grid, ms * 1e3 / 20, (double)(last - first) * us_per_tick);
     for (int i = 0; i < 5; i++)
         printf(", \"%s_us\": [%.2f, %.2f]", name[i], median(ph[i]), *std::max_element(ph[i].begin(), ph[i].end()));
+    printf(", \"last_start_us\": %.2f, \"ended_50_90_98_100_us\": [%.2f, %.2f, %.2f, %.2f]", *std::max_element(st.begin(), st.end()),
+           pct(0.5), pct(0.9), pct(0.98), en.back());
     printf("}\n");
     fflush(stdout);
     PROBE_CHECK(hipEventDestroy(e0));

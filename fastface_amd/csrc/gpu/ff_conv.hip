@@ -71,11 +71,13 @@ struct ConvLaunch {
 };
 
 // ws_avail: workspace bytes the caller provides (a split > 1 variant that
-// needs more falls back to the whole-K tiling).
-ConvLaunch choose_launch(const ConvEntry* e, long long M, size_t ws_avail) {
+// needs more falls back to the whole-K tiling).  shared (FFK_SHARED_GPU):
+// a twin launch runs at the same time, so the large tiles are kept when the
+// two grids together reach FF_MID_MAX_WG.
+ConvLaunch choose_launch(const ConvEntry* e, long long M, size_t ws_avail, bool shared = false) {
     long long big = ((M + e->bm - 1) / e->bm) * (e->cout / e->bn);
     ConvLaunch l = {e->fn, e->kind, e->bn, (int)big, 1, 0, 0};
-    if (e->mid && big < FF_MID_MAX_WG) {
+    if (e->mid && big * (shared ? 2 : 1) < FF_MID_MAX_WG) {
         const int mbm = e->mid_bm ? e->mid_bm : 128, mbn = e->mid_bn ? e->mid_bn : 128;
         big = ((M + mbm - 1) / mbm) * (e->cout / mbn);
         l = {e->mid, e->mid_kind ? e->mid_kind : "staged128", mbn, (int)big, 1, 0, 0};
@@ -266,7 +268,8 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
         if (a.out_bn) as.out_bn = a.out_bn + o;
         if (a.out_i32) as.out_i32 = a.out_i32 + o;
         as.M = (int)ms;
-        const ConvLaunch l = choose_launch(e, ms, d->workspace ? d->workspace_bytes : 0);
+        const ConvLaunch l = choose_launch(e, ms, d->workspace ? d->workspace_bytes : 0,
+                                           (d->flags & FFK_SHARED_GPU) != 0);
         if (l.split > 1) {
             as.counters = (unsigned*)d->workspace;
             as.ws = (int32_t*)((int8_t*)d->workspace + l.counter_bytes);
@@ -352,7 +355,7 @@ size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d) {
     if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_ws_bytes(d);
     const long long M = conv_pixels(d);
     if (M > 0x7fffffffLL) return 0;
-    return choose_launch(e, M, (size_t)-1).ws_bytes;
+    return choose_launch(e, M, (size_t)-1, (d->flags & FFK_SHARED_GPU) != 0).ws_bytes;
 }
 
 const char* ffk_conv_variant(const ffk_conv_desc* d) {
@@ -362,7 +365,7 @@ const char* ffk_conv_variant(const ffk_conv_desc* d) {
     if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_eligible(d) ? "winograd" : nullptr;
     const long long M = conv_pixels(d);
     if (M > 0x7fffffffLL) return nullptr;
-    return choose_launch(e, M, d->workspace ? d->workspace_bytes : 0).kind;
+    return choose_launch(e, M, d->workspace ? d->workspace_bytes : 0, (d->flags & FFK_SHARED_GPU) != 0).kind;
 }
 
 // BN second output as a table: lut[c][q + 128] = BN-requant of the int8

@@ -43,6 +43,9 @@
  * 384 3.16 -> 3.12, 448-640 3-8 % slower (halves of 224-320 faces take the
  * small-grid tiles the whole batch does not), 704 5.64 -> 5.15, 768 5.71 ->
  * 5.51, 1024 8.00 -> 7.67. */
+/* halves of at least this many faces launch with FFK_SHARED_GPU (their
+ * layers keep the large tiles the whole batch would take) */
+#define FF_SPLIT_SHARED_MIN 352
 #define FF_SPLIT_SMALL_MIN 64
 #define FF_SPLIT_SMALL_MAX 384
 #define FF_SPLIT_LARGE_MIN 704
@@ -188,7 +191,7 @@ static int set_io(FastFace* ff, const void* in, float* out, void* stream, int ba
     return 0;
 }
 
-static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t off, ffk_conv_desc* d);
+static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t off, int shared, ffk_conv_desc* d);
 
 /* Largest workspace any conv step asks for at 1..max_batch faces.  Only
  * small batches split K (the split grid is capped at a few thousand 64x64
@@ -213,7 +216,7 @@ static size_t workspace_bytes(FastFace* ff, int max_batch)
         if (ff->plan.steps[s].kind != 1) continue;
         for (int b = 1; b <= top + 1; b++) {
             ffk_conv_desc d;
-            step_desc(ff, s, b <= top ? b : max_batch, 0, 0, 0, &d);
+            step_desc(ff, s, b <= top ? b : max_batch, 0, 0, 0, 0, &d);
             const size_t n = ffk_conv_workspace_bytes(&d);
             if (n > best) best = n;
         }
@@ -285,8 +288,9 @@ static int writes_even(const FastFace* ff, const FfStep* st)
 }
 
 /* part / off: the half of a split chain (0 or 1) and its region's offset
- * into every activation buffer */
-static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t off, ffk_conv_desc* d)
+ * into every activation buffer; shared: the other half runs at the same
+ * time (FFK_SHARED_GPU) */
+static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t off, int shared, ffk_conv_desc* d)
 {
     const FfStep* st = &ff->plan.steps[s];
     memset(d, 0, sizeof *d);
@@ -315,17 +319,18 @@ static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t 
         d->flags |= FFK_ALGO_WINOGRAD;
         d->w = ff->d_weights + st->wino_off;
     }
+    if (shared) d->flags |= FFK_SHARED_GPU;
     d->in_scale = st->in_scale;
     d->workspace = ff->d_ws ? (int8_t*)ff->d_ws + (size_t)part * ff->ws_part : NULL;
     d->workspace_bytes = ff->ws_part;
 }
 
-static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt, int part, size_t off)
+static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt, int part, size_t off, int shared)
 {
     const FfStep* st = &ff->plan.steps[s];
     if (st->kind == 1) {
         ffk_conv_desc d;
-        step_desc(ff, s, batch, fmt, part, off, &d);
+        step_desc(ff, s, batch, fmt, part, off, shared, &d);
         return ffk_conv(&d, stream);
     }
     ffk_fc_desc f;
@@ -346,10 +351,10 @@ static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt, in
 
 /* the chain of `batch` faces as half `part`, its activations `off` bytes
  * into every buffer */
-static int run_part(FastFace* ff, int part, size_t off, int batch, void* stream, int fmt)
+static int run_part(FastFace* ff, int part, size_t off, int batch, void* stream, int fmt, int shared)
 {
     for (int s = 0; s < ff->plan.n_steps; s++) {
-        int rc = launch_step(ff, s, batch, stream, fmt, part, off);
+        int rc = launch_step(ff, s, batch, stream, fmt, part, off, shared);
         if (rc) return rc;
     }
     return 0;
@@ -357,7 +362,7 @@ static int run_part(FastFace* ff, int part, size_t off, int batch, void* stream,
 
 static int run_direct(FastFace* ff, int batch, void* stream, int fmt)
 {
-    return run_part(ff, 0, 0, batch, stream, fmt);
+    return run_part(ff, 0, 0, batch, stream, fmt, 0);
 }
 
 /* The chain as captured: one, or two halves forked onto the second stream
@@ -370,8 +375,9 @@ static int run_captured(FastFace* ff, int batch, int fmt)
     int rc = ffk_event_record(ff->ev_fork, ff->stream);
     if (rc) return rc;
     rc = ffk_stream_wait_event(ff->sstream, ff->ev_fork);
-    if (!rc) rc = run_part(ff, 0, 0, na, ff->stream, fmt);
-    if (!rc) rc = run_part(ff, 1, (size_t)na * ff->plan.max_face_bytes, batch - na, ff->sstream, fmt);
+    const int shared = na >= FF_SPLIT_SHARED_MIN;
+    if (!rc) rc = run_part(ff, 0, 0, na, ff->stream, fmt, shared);
+    if (!rc) rc = run_part(ff, 1, (size_t)na * ff->plan.max_face_bytes, batch - na, ff->sstream, fmt, shared);
     int rj = ffk_event_record(ff->ev_join, ff->sstream);
     if (!rj) rj = ffk_stream_wait_event(ff->stream, ff->ev_join);
     return rc ? rc : rj;
@@ -702,7 +708,7 @@ int fastface_profile_steps(FastFace* ff, int batch, int reps, float* step_ms)
     for (int r = 0; r < reps && !rc; r++) {
         for (int s = 0; s < n && !rc; s++) {
             rc = ffk_event_record(ev[s], ff->stream);
-            if (!rc) rc = launch_step(ff, s, batch, ff->stream, 0, 0, 0);
+            if (!rc) rc = launch_step(ff, s, batch, ff->stream, 0, 0, 0, 0);
         }
         if (!rc) rc = ffk_event_record(ev[n], ff->stream);
         if (!rc) rc = ffk_stream_sync(ff->stream);

@@ -98,6 +98,12 @@ typedef struct { const float* in; float* out; } ffk_io;
                                    case (NaN or |r| >= 2^31 -> -128): the same
                                    values, two operations fewer.  Ignored with
                                    FFK_EPI_INSCALE. */
+#define FFK_SHARED_GPU   0x400  /* launch-choice hint, no effect on the
+                                   values: another launch of the same size
+                                   runs at the same time (the two halves of a
+                                   split chain), so the tiling is chosen for
+                                   the two launches' combined grid.  No
+                                   reference counterpart. */
 
 /* rows of the per-layer parameter block, each `cout` floats (device) */
 enum {

@@ -153,10 +153,11 @@ def test_conv_variant_policy():
     lib = fa.load()
     d = fa.ffk_conv_desc()
 
-    def variant(cin, cout, k, s, H, B, ws=0):
+    def variant(cin, cout, k, s, H, B, ws=0, flags=0):
         d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, k, k
         d.stride, d.pad, d.hin, d.win = s, k // 2, H, H
         d.workspace, d.workspace_bytes = (4096, ws) if ws else (None, 0)
+        d.flags = flags
         v = lib.ffk_conv_variant(C.byref(d))
         return v.decode() if v else None
     assert variant(3, 64, 3, 1, 112, 1) == "stem"
@@ -169,6 +170,12 @@ def test_conv_variant_policy():
     assert variant(64, 64, 3, 1, 112, 1) == "patch"               # one 64-channel run
     assert variant(96, 64, 3, 1, 112, 1) is None
     assert lib.ffk_conv_variant(None) is None
+    # FFK_SHARED_GPU (one half of a split chain): the large tiles stay where the
+    # two halves' grids together fill the GPU (512->512 @7 at 512 faces: 392
+    # workgroups each), not where they do not (at 64 faces)
+    assert variant(512, 512, 3, 1, 7, 512) == "patch_kg"
+    assert variant(512, 512, 3, 1, 7, 512, flags=fa.FFK_SHARED_GPU) == "patch"
+    assert variant(512, 512, 3, 1, 7, 64, flags=fa.FFK_SHARED_GPU) == "patch_kg"
 
 
 def test_rgb8_table_matches_sdk_normalization_and_reference_quant(oracle):

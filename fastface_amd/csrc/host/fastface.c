@@ -31,24 +31,19 @@
 #define FF_STREAM_CHUNK_U8 1024
 #define FF_MAX_CHUNKS 64
 
-/* Batches in the ranges below run as two halves, each on its own stream
- * inside the one captured graph (a fork and a join): a layer's kernel of one
- * half fills the CUs the other half's kernel leaves idle (the last, partly
- * filled round of workgroups at large batches; the small grids at small
- * ones).  Faces are independent, so the embeddings equal the one-chain
- * path's bit for bit.  Each half has its own I/O descriptor (d_io[part]) and
- * its own half of the split-K workspace.  Measured (ms per batch, one chain
- * -> two halves, two contexts on two streams, same box): 8 faces 0.63 ->
- * 0.85, 16-32 equal, 64 0.91 -> 0.85, 128 1.53 -> 1.30, 256 2.51 -> 2.28,
- * 384 3.16 -> 3.12, 448-640 3-8 % slower (halves of 224-320 faces take the
- * small-grid tiles the whole batch does not), 704 5.64 -> 5.15, 768 5.71 ->
- * 5.51, 1024 8.00 -> 7.67. */
-/* halves of at least this many faces launch with FFK_SHARED_GPU (their
- * layers keep the large tiles the whole batch would take) */
-#define FF_SPLIT_SHARED_MIN 352
-#define FF_SPLIT_SMALL_MIN 64
-#define FF_SPLIT_SMALL_MAX 384
-#define FF_SPLIT_LARGE_MIN 704
+/* Batches of FF_SPLIT_MIN faces or more run as two halves, each on its own
+ * stream inside the one captured graph (a fork and a join), both launched
+ * with FFK_SHARED_GPU (each layer takes the tiling the two halves' grids
+ * together fill the GPU with).  A layer's kernel of one half fills the CUs
+ * the other half's kernel leaves idle: the last, partly filled round of
+ * workgroups at large batches, the partly empty grids at small ones.
+ * Faces are independent, so the embeddings equal the one-chain path's bit
+ * for bit.  Each half has its own region of every activation buffer, its
+ * own I/O descriptor (d_io[part]) and its own half of the split-K
+ * workspace.  Measured (ms per batch, one chain -> two halves, same box):
+ * 16 0.677 -> 0.681, 32 0.754 -> 0.770, 48 0.891 -> 0.823, 96 1.42 -> 1.11,
+ * 256 2.75 -> 2.33, 512 4.37 -> 3.76, 1024 7.86 -> 7.25. */
+#define FF_SPLIT_MIN 48
 
 /* one captured chain per (batch, input format: 0 fp32 faces, 1 uint8 RGB) */
 typedef struct { int batch, fmt; void* exec; } GraphEntry;
@@ -152,9 +147,7 @@ static void free_activations(FastFace* ff)
 /* first face of the second half of a `batch` chain, or 0: one chain */
 static int split_at(const FastFace* ff, int batch)
 {
-    if (ff->keep_all) return 0;
-    const int split = (batch >= FF_SPLIT_SMALL_MIN && batch <= FF_SPLIT_SMALL_MAX) || batch >= FF_SPLIT_LARGE_MIN;
-    return split ? batch / 2 : 0;
+    return (!ff->keep_all && batch >= FF_SPLIT_MIN) ? batch / 2 : 0;
 }
 
 /* the I/O descriptors of the two halves of a `batch` chain over (in, out);
@@ -375,9 +368,8 @@ static int run_captured(FastFace* ff, int batch, int fmt)
     int rc = ffk_event_record(ff->ev_fork, ff->stream);
     if (rc) return rc;
     rc = ffk_stream_wait_event(ff->sstream, ff->ev_fork);
-    const int shared = na >= FF_SPLIT_SHARED_MIN;
-    if (!rc) rc = run_part(ff, 0, 0, na, ff->stream, fmt, shared);
-    if (!rc) rc = run_part(ff, 1, (size_t)na * ff->plan.max_face_bytes, batch - na, ff->sstream, fmt, shared);
+    if (!rc) rc = run_part(ff, 0, 0, na, ff->stream, fmt, 1);
+    if (!rc) rc = run_part(ff, 1, (size_t)na * ff->plan.max_face_bytes, batch - na, ff->sstream, fmt, 1);
     int rj = ffk_event_record(ff->ev_join, ff->sstream);
     if (!rj) rj = ffk_stream_wait_event(ff->stream, ff->ev_join);
     return rc ? rc : rj;

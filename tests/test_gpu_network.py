@@ -252,13 +252,12 @@ def test_streamed_host_batch_equals_one_shot(ff, gpu_lib):
 
 
 def test_split_chain_equals_unsplit_halves(gpu_lib, synth_ffw4):
-    """Batches of 64-384 and of 704 or more faces run as two halves, each on
-    its own stream inside one captured graph (fork and join), each half in
-    its own region of every activation buffer.  Every embedding of every
-    face equals the one-chain result of 32-face batches (faces are
-    independent), for batches on the small-grid and split-K kernels (101,
-    256, 384: halves of 50-192 faces, each with its own workspace) and on the
-    large tiles (1025: halves of 512 and 513), captured and then replayed;
+    """Batches of 48 faces or more run as two halves, each on its own stream
+    inside one captured graph (fork and join), each half in its own region
+    of every activation buffer, both with the FFK_SHARED_GPU tiling.  Every
+    embedding of every face equals the one-chain result of 32-face batches
+    (faces are independent) for 101, 256, 384 and 1025 faces (halves of
+    50-513, each with its own workspace), captured and then replayed;
     1024 uint8 faces against 32-face batches; the Winograd stage-1 path split
     against direct.  (Regression: halves that shared buffer regions corrupted
     faces from B/4 on, because a buffer holds tensors of different sizes at

@@ -177,6 +177,24 @@ __device__ __forceinline__ int8_t* x_row(const ConvArgs& a, int m) {
     return a.out + (size_t)m * COUT;
 }
 
+// x_row for row r (0..31) of a 32-row block starting at output pixel mb
+// (uniform per wave).  When an image holds a whole number of 32-row blocks
+// the block lies in one image, so the image and its first row are found once
+// per block (scalar work) instead of per row.
+template <int COUT, int HO, int WO>
+__device__ __forceinline__ int8_t* x_row_blk(const ConvArgs& a, int mb, int r) {
+    if constexpr (HO % 2 == 0 && WO % 2 == 0 && (HO * WO) % 32 == 0) {
+        if (a.flags & FFK_OUT_X_EVEN) {
+            const int img = mb / (HO * WO);
+            const int rem = mb - img * (HO * WO) + r;
+            const int oh = rem / WO, ow = rem - oh * WO;
+            if ((oh | ow) & 1) return nullptr;
+            return a.out + (((size_t)img * (HO / 2) + (oh >> 1)) * (WO / 2) + (ow >> 1)) * COUT;
+        }
+    }
+    return x_row<COUT, HO, WO>(a, mb + r);
+}
+
 // PRELU: 0 none, 1 f < 0 ? f*slope : f, 2 max(f, f*slope) (the same values
 // when every slope is at most 1 and f is never infinite: FFK_EPI_PRELU_LE1).
 // INSC: f = f * in_scale first (FFW2/FFW3 models; FFW4 skips the multiply).
@@ -264,6 +282,7 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
     else __builtin_amdgcn_wave_barrier();
     // Flush: 16-byte chunks of the X tile go out as they are; the BN second
     // output maps each byte through its channel's table on the way.
+    static_assert(32 % RPI == 0, "a copy instruction's rows lie in one 32-row block");
 #pragma unroll
     for (int k = 0; k < ROWS / RPI; k++) {
         const int row = lane / CH + k * RPI;
@@ -272,7 +291,8 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
         const v4i v = *reinterpret_cast<const v4i*>(Ws + row * P + ch * 16);
         if (m < a.M) {
             if (a.out) {
-                int8_t* xo = x_row<COUT, HO, WO>(a, m);
+                // (row = lane/CH + k*RPI: block k*RPI/32, a compile-time one)
+                int8_t* xo = x_row_blk<COUT, HO, WO>(a, mrow0 + (k * RPI / 32) * 32, row - (k * RPI / 32) * 32);
                 if (xo) *reinterpret_cast<v4i*>(xo + ncol0 + ch * 16) = v;
             }
             if (BN2) {
@@ -1746,7 +1766,7 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
     int8_t* Ls = Es + STEM_WAVES * 32 * 80;
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: scalar)
     const int lane = tid & 63;
     const int ntiles = a.M / (2 * W);               // one tile = 2 output rows of one face
     const int t_beg = blockIdx.x * tiles_per_wg;

@@ -23,12 +23,11 @@
 /* Host-buffer batches of at least two chunks stream: the host-to-device copy
  * of chunk k+1 (copy stream) runs while chunk k computes (context stream),
  * each chunk in its own region of the input buffer.  A chunk must fill the
- * GPU by itself (at 256 faces the stage-3 layers have fewer workgroups than
- * the CUs hold), and the copy it hides must be worth a second launch chain:
- * fp32 faces (4 bytes a pixel, ~40% of the compute time over PCIe) stream in
- * chunks of 512, uint8 faces (a quarter of that) only in chunks of 1024. */
+ * GPU by itself, and the copy it hides must be worth a second launch chain:
+ * both input formats stream in chunks of 512 faces (measured at 1024 uint8
+ * faces: 112k faces/s in one chunk, 120k in two, 109k in three). */
 #define FF_STREAM_CHUNK_F32 512
-#define FF_STREAM_CHUNK_U8 1024
+#define FF_STREAM_CHUNK_U8 512
 #define FF_MAX_CHUNKS 64
 
 /* Batches of FF_SPLIT_MIN faces or more run as two halves, each on its own

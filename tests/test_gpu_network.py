@@ -228,8 +228,8 @@ def test_winograd_stage1_network(gpu_lib, synth_ffw4, oracle, oracle_model):
 
 def test_streamed_host_batch_equals_one_shot(ff, gpu_lib):
     """Host batches stream in chunks (copy of one chunk during the compute of
-    the previous): 600 fp32 faces as 512 + 88, 2100 uint8 faces as 1024 +
-    1024 + 52.  Embeddings equal the device-resident one-shot path's and the
+    the previous): 600 fp32 faces as 512 + 88, 2100 uint8 faces as 4 x 512 +
+    52.  Embeddings equal the device-resident one-shot path's and the
     single-face path's; a small batch afterwards still reads its own buffers."""
     B = 600
     x = synth.faces_uniform(B, 41)

@@ -955,7 +955,12 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     // Patch slots of this thread: wave load j of wave w is patch block j*NW + w,
     // lane L its slot L, i.e. patch pixel slot/5, piece slot%5 (piece 4 is the
     // unused 16 bytes).  Input offset of the slot at channel run 0, or FF_OOB
-    // (unused piece, or a pixel outside the batch: the load returns zeros).
+    // for the unused piece.  A pixel outside the batch needs no test: past
+    // the end its offset is at least the buffer's a.M * CIN bytes, before the
+    // start (g >= -W-1) it is negative, i.e. at least 2^31 as the unsigned
+    // offset the hardware checks (a.M * CIN < 2^31); either way the load is
+    // out of range and returns zeros.  (The channel run's offset goes in the
+    // scalar offset, which stays inside the pixel.)
     unsigned p_src[LA];
 #pragma unroll
     for (int j = 0; j < LA; j++) {
@@ -964,8 +969,8 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
         const int px = slot / 5;
         const int piece = slot - px * 5;
         const int g = first + px;
-        const bool ok = blk < PLOADS && piece < 4 && g >= 0 && g < a.M;
-        p_src[j] = ok ? (unsigned)(g * CIN + piece * 16) : FF_OOB;
+        const bool ok = blk < PLOADS && piece < 4;
+        p_src[j] = ok ? (unsigned)g * CIN + piece * 16 : FF_OOB;        // (mod 2^32)
     }
     auto issue_patch = [&](int c, int buf) {
 #pragma unroll
@@ -1527,8 +1532,8 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
         const int px = slot / 5;
         const int piece = slot - px * 5;
         const int gp = first + px;
-        const bool ok = blk < PLOADS && piece < 4 && gp >= 0 && gp < a.M;
-        p_src[j] = ok ? (unsigned)(gp * CIN + piece * 16) : FF_OOB;
+        const bool ok = blk < PLOADS && piece < 4;   // (outside the batch: out of range, as above)
+        p_src[j] = ok ? (unsigned)gp * CIN + piece * 16 : FF_OOB;      // (mod 2^32)
     }
     // run r of this group is channel run g + KG*r
     auto issue_patch = [&](int r, int buf) {

@@ -71,9 +71,8 @@ struct FastFace {
     uint8_t* d_input_u8;        /* capacity * 37632 (uint8 RGB input) */
     int8_t* d_in_lut;           /* [3][256] uint8 pixel -> int8 input table */
     float* d_output;            /* capacity * 512 */
-    void* d_ws;                 /* split-K workspace of the small-batch convs */
-    size_t ws_bytes;
-    size_t ws_part;             /* bytes of each half of d_ws */
+    void* d_ws;                 /* split-K workspaces of the small-batch convs */
+    size_t ws_part;             /* bytes of each of d_ws's two halves */
     ffk_io* d_io;               /* device I/O descriptors of the two halves */
     ffk_io* h_io;               /* pinned staging, two descriptors each:
                                    [0..1] set_io, [2(1 + k)..] chunk k */
@@ -138,7 +137,6 @@ static void free_activations(FastFace* ff)
     ffk_free(ff->d_input_u8); ff->d_input_u8 = NULL;
     ffk_free(ff->d_output); ff->d_output = NULL;
     ffk_free(ff->d_ws); ff->d_ws = NULL;
-    ff->ws_bytes = 0;
     ff->ws_part = 0;
     ff->capacity = 0;
 }
@@ -244,7 +242,6 @@ static int ensure_capacity(FastFace* ff, int batch)
         rc = ffk_zero(ff->d_ws, 2 * ws, ff->stream);
         if (!rc) rc = ffk_stream_sync(ff->stream);
         if (rc) { free_activations(ff); return rc; }
-        ff->ws_bytes = 2 * ws;
         ff->ws_part = ws;
     }
     ff->capacity = batch;

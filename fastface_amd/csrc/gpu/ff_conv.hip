@@ -251,12 +251,14 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
                           FFK_EPI_PRELU_LE1 | FFK_OUT_X_EVEN | FFK_EPI_IN_RANGE |
                           FFK_IN_RGB8);
     a.in_scale = d->in_scale;
-    // The direct-to-LDS kernels address the int8 input with 32-bit offsets:
-    // a batch whose input tensor reaches 2 GiB runs as several launches over
-    // consecutive image ranges (images are independent).
+    // The direct-to-LDS kernels address the int8 input and the residual
+    // tensor with 32-bit offsets: a batch whose input or output tensor
+    // reaches 2 GiB runs as several launches over consecutive image ranges
+    // (images are independent).
     const long long px_out = M / d->batch;
     const long long in_img = (long long)d->hin * d->win * d->cin;
-    const int slice = stem ? d->batch : (int)std::min<long long>(d->batch, 0x7fffffffLL / in_img);
+    const long long img = std::max<long long>(in_img, px_out * d->cout);
+    const int slice = stem ? d->batch : (int)std::min<long long>(d->batch, 0x7fffffffLL / img);
     for (int b0 = 0; b0 < d->batch; b0 += slice) {
         const int nb = std::min(slice, d->batch - b0);
         const long long ms = (long long)nb * px_out;

@@ -233,16 +233,18 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
         // so no barrier.
         // (opaque: computed here, not folded into values kept across the
         // main loop)
+        // (through a buffer resource: rows past the batch are out of range and
+        // read as zeros, the unused piece of each row gets the FF_OOB offset)
         int lane_o = lane, m_o = mrow0;
         asm volatile("" : "+v"(lane_o), "+v"(m_o));
+        const __amdgpu_buffer_rsrc_t r_add = ff_rsrc(a.add_src, (unsigned)a.M * COUT);
 #pragma unroll
         for (int k = 0; k < RSLOTS / 64; k++) {
             const int slot = k * 64 + lane_o;
             const int row = slot / SPR;
             const int pc = slot - row * SPR;
-            const int m = m_o + row;
-            const int8_t* src = pc < CH && m < a.M ? a.add_src + (size_t)m * COUT + ncol0 + pc * 16 : ff_zero_page;
-            dma16(src, Ws + k * 1024);
+            const unsigned off = pc < CH ? (unsigned)(m_o + row) * COUT + ncol0 + pc * 16 : FF_OOB;
+            bdma16(r_add, off, 0, Ws + k * 1024);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else if (ADD) {   // residual tile -> LDS (coalesced 16-byte loads)
@@ -1021,12 +1023,15 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     // (masked taps: the zero block): no per-step address arithmetic
     int ta[9][MI];
 #pragma unroll
-    for (int t = 0; t < 9; t++) {
-        const int kh = t / 3, kw = t % 3;
-        const int emask = (kh == 0 ? 1 : 0) | (kh == 2 ? 2 : 0) | (kw == 0 ? 4 : 0) | (kw == 2 ? 8 : 0);
+    for (int i = 0; i < MI; i++) {
+        // (four lane masks per row tile; a tap's mask is the OR of at most two)
+        const bool top = a_edge[i] & 1, bot = a_edge[i] & 2, left = a_edge[i] & 4, right = a_edge[i] & 8;
 #pragma unroll
-        for (int i = 0; i < MI; i++)
-            ta[t][i] = (a_edge[i] & emask) ? z_addr : a_base[i] + (kh * W + kw) * PATCH_PITCH;
+        for (int t = 0; t < 9; t++) {
+            const int kh = t / 3, kw = t % 3;
+            const bool masked = (kh == 0 && top) || (kh == 2 && bot) || (kw == 0 && left) || (kw == 2 && right);
+            ta[t][i] = masked ? z_addr : a_base[i] + (kh * W + kw) * PATCH_PITCH;
+        }
     }
 
     v16i acc[MI][NJ];
@@ -1580,12 +1585,15 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
     // LDS address of every tap of every row tile, selected once
     int ta[9][MI];
 #pragma unroll
-    for (int t = 0; t < 9; t++) {
-        const int kh = t / 3, kw = t % 3;
-        const int emask = (kh == 0 ? 1 : 0) | (kh == 2 ? 2 : 0) | (kw == 0 ? 4 : 0) | (kw == 2 ? 8 : 0);
+    for (int i = 0; i < MI; i++) {
+        // (four lane masks per row tile; a tap's mask is the OR of at most two)
+        const bool top = a_edge[i] & 1, bot = a_edge[i] & 2, left = a_edge[i] & 4, right = a_edge[i] & 8;
 #pragma unroll
-        for (int i = 0; i < MI; i++)
-            ta[t][i] = (a_edge[i] & emask) ? z_addr : a_base[i] + (kh * W + kw) * PATCH_PITCH;
+        for (int t = 0; t < 9; t++) {
+            const int kh = t / 3, kw = t % 3;
+            const bool masked = (kh == 0 && top) || (kh == 2 && bot) || (kw == 0 && left) || (kw == 2 && right);
+            ta[t][i] = masked ? z_addr : a_base[i] + (kh * W + kw) * PATCH_PITCH;
+        }
     }
 
     v16i acc[MI][NJ];

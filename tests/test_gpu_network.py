@@ -256,8 +256,9 @@ def test_split_chain_equals_unsplit_halves(gpu_lib, synth_ffw4):
     inside one captured graph (fork and join), each half in its own region
     of every activation buffer, both with the FFK_SHARED_GPU tiling.  Every
     embedding of every face equals the one-chain result of 32-face batches
-    (faces are independent) for 101, 256, 384 and 1025 faces (halves of
-    50-513, each with its own workspace), captured and then replayed;
+    (faces are independent) for 49, 101, 129, 256, 384 and 1025 faces
+    (halves of 24-513, each with its own workspace), captured and then
+    replayed;
     1024 uint8 faces against 32-face batches; the Winograd stage-1 path split
     against direct.  (Regression: halves that shared buffer regions corrupted
     faces from B/4 on, because a buffer holds tensors of different sizes at
@@ -269,7 +270,7 @@ def test_split_chain_equals_unsplit_halves(gpu_lib, synth_ffw4):
         def pieces(fn, a):
             return np.concatenate([fn(a[i:i + 32]) for i in range(0, len(a), 32)])
 
-        for B in (101, 256, 384, 1025):
+        for B in (49, 101, 129, 256, 384, 1025):
             x = synth.faces_uniform(B, 61 + B)
             exp = pieces(f.embed_batch, x)
             din, dout = Dev(gpu_lib, host=x), Dev(gpu_lib, nbytes=B * 512 * 4)

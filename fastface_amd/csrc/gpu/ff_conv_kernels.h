@@ -160,39 +160,31 @@ __device__ __forceinline__ EpiParams<NJ> load_epi_params(const ConvArgs& a, int 
     return P;
 }
 
-// Where output pixel m's X row goes: out + m*COUT, or with FFK_OUT_X_EVEN
-// (HO x WO images, both even) its slot in the [HO/2][WO/2] tensor of the
-// even-row, even-column pixels, and null for every other pixel.
-template <int COUT, int HO, int WO>
-__device__ __forceinline__ int8_t* x_row(const ConvArgs& a, int m) {
+// Pixel index of output pixel m's X row in the launch's X tensor: m, or
+// with FFK_OUT_X_EVEN (HO x WO images, both even) its index in the
+// [HO/2][WO/2] tensor of the even-row, even-column pixels, and FF_OOB for
+// every other pixel.  Row r (0..31) of the 32-row block starting at pixel mb
+// (uniform per wave); an image holding a whole number of 32-row blocks finds
+// the block's image once (scalar work).  Pixels past the batch give indices
+// past the tensor (a.M, or a.M / 4 even pixels).
+template <int HO, int WO>
+__device__ __forceinline__ unsigned x_pix_blk(const ConvArgs& a, int mb, int r) {
     if constexpr (HO % 2 == 0 && WO % 2 == 0) {
         if (a.flags & FFK_OUT_X_EVEN) {
-            const int img = m / (HO * WO);
-            const int rem = m - img * (HO * WO);
+            int img, rem;
+            if constexpr ((HO * WO) % 32 == 0) {
+                img = mb / (HO * WO);
+                rem = mb - img * (HO * WO) + r;
+            } else {
+                img = (mb + r) / (HO * WO);
+                rem = mb + r - img * (HO * WO);
+            }
             const int oh = rem / WO, ow = rem - oh * WO;
-            if ((oh | ow) & 1) return nullptr;
-            return a.out + (((size_t)img * (HO / 2) + (oh >> 1)) * (WO / 2) + (ow >> 1)) * COUT;
+            if ((oh | ow) & 1) return FF_OOB;
+            return (unsigned)((img * (HO / 2) + (oh >> 1)) * (WO / 2) + (ow >> 1));
         }
     }
-    return a.out + (size_t)m * COUT;
-}
-
-// x_row for row r (0..31) of a 32-row block starting at output pixel mb
-// (uniform per wave).  When an image holds a whole number of 32-row blocks
-// the block lies in one image, so the image and its first row are found once
-// per block (scalar work) instead of per row.
-template <int COUT, int HO, int WO>
-__device__ __forceinline__ int8_t* x_row_blk(const ConvArgs& a, int mb, int r) {
-    if constexpr (HO % 2 == 0 && WO % 2 == 0 && (HO * WO) % 32 == 0) {
-        if (a.flags & FFK_OUT_X_EVEN) {
-            const int img = mb / (HO * WO);
-            const int rem = mb - img * (HO * WO) + r;
-            const int oh = rem / WO, ow = rem - oh * WO;
-            if ((oh | ow) & 1) return nullptr;
-            return a.out + (((size_t)img * (HO / 2) + (oh >> 1)) * (WO / 2) + (ow >> 1)) * COUT;
-        }
-    }
-    return x_row<COUT, HO, WO>(a, mb + r);
+    return (unsigned)(mb + r);
 }
 
 // PRELU: 0 none, 1 f < 0 ? f*slope : f, 2 max(f, f*slope) (the same values
@@ -283,37 +275,39 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
     if constexpr (WG_SYNC) __syncthreads();
     else __builtin_amdgcn_wave_barrier();
     // Flush: 16-byte chunks of the X tile go out as they are; the BN second
-    // output maps each byte through its channel's table on the way.
+    // output maps each byte through its channel's table on the way.  Both go
+    // through buffer resources sized to the launch's tensors: rows past the
+    // batch (and, for FFK_OUT_X_EVEN, X at odd pixels) get offsets out of
+    // range and are dropped, so the flush has no branches and the table
+    // reads of consecutive chunks can overlap.
     static_assert(32 % RPI == 0, "a copy instruction's rows lie in one 32-row block");
+    const bool xe = (HO % 2 == 0 && WO % 2 == 0) && (a.flags & FFK_OUT_X_EVEN);
+    const __amdgpu_buffer_rsrc_t r_x = ff_rsrc(a.out, a.out ? (unsigned)(xe ? a.M / 4 : a.M) * COUT : 0u);
+    const __amdgpu_buffer_rsrc_t r_bn = ff_rsrc(a.out_bn, BN2 ? (unsigned)a.M * COUT : 0u);
 #pragma unroll
     for (int k = 0; k < ROWS / RPI; k++) {
         const int row = lane / CH + k * RPI;
         const int ch = lane % CH;
         const int m = mrow0 + row;
         const v4i v = *reinterpret_cast<const v4i*>(Ws + row * P + ch * 16);
-        if (m < a.M) {
-            if (a.out) {
-                // (row = lane/CH + k*RPI: block k*RPI/32, a compile-time one)
-                int8_t* xo = x_row_blk<COUT, HO, WO>(a, mrow0 + (k * RPI / 32) * 32, row - (k * RPI / 32) * 32);
-                if (xo) *reinterpret_cast<v4i*>(xo + ncol0 + ch * 16) = v;
-            }
-            if (BN2) {
-                const int8_t* L = Lw + (ch * 16) * FF_LUT_PITCH + 128;
-                v4i o;
+        // (row = lane/CH + k*RPI: block k*RPI/32, a compile-time one)
+        const unsigned xp = x_pix_blk<HO, WO>(a, mrow0 + (k * RPI / 32) * 32, row - (k * RPI / 32) * 32);
+        __builtin_amdgcn_raw_buffer_store_b128(v, r_x, xp == FF_OOB ? FF_OOB : xp * COUT + ncol0 + ch * 16, 0, 0);
+        if (BN2) {
+            const int8_t* L = Lw + (ch * 16) * FF_LUT_PITCH + 128;
+            v4i o;
 #pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    uint32_t packed = 0;
+            for (int w = 0; w < 4; w++) {
+                uint32_t packed = 0;
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int q = (int8_t)((uint32_t)v[w] >> (e * 8));
-                        packed |= (uint32_t)(uint8_t)L[(w * 4 + e) * FF_LUT_PITCH + q] << (e * 8);
-                    }
-                    o[w] = (int)packed;
+                for (int e = 0; e < 4; e++) {
+                    const int q = (int8_t)((uint32_t)v[w] >> (e * 8));
+                    packed |= (uint32_t)(uint8_t)L[(w * 4 + e) * FF_LUT_PITCH + q] << (e * 8);
                 }
-                *reinterpret_cast<v4i*>(a.out_bn + (size_t)m * COUT + ncol0 + ch * 16) = o;
+                o[w] = (int)packed;
             }
+            __builtin_amdgcn_raw_buffer_store_b128(o, r_bn, (unsigned)m * COUT + ncol0 + ch * 16, 0, 0);
         }
-        if (BN2) asm volatile("" ::: "memory");
     }
 }
 

@@ -165,6 +165,8 @@ def main():
                     help="runs of the reference's b=1 binary in its stable protocol (reference: 20)")
     ap.add_argument("--cpu-cooldown", type=float, default=1.0,
                     help="seconds between those runs (reference: 3)")
+    ap.add_argument("--no-general-epilogue", action="store_true",
+                    help="skip the B=1024 leg with every conv on the general epilogue forms")
     ap.add_argument("--no-winograd", action="store_true",
                     help="skip the config-5 run of the stage-1 layers as Winograd F(2,3)")
     args = ap.parse_args()
@@ -440,6 +442,37 @@ def main():
             raise RuntimeError("Winograd embeddings differ from the direct path")
         check(lib, lib.fastface_set_conv_algo(ff.ff, 0), "algo direct")
 
+    # the same chain with every conv on the general epilogue forms (the
+    # reference's compare/select PReLU and cvttps2dq emulation, which a model
+    # whose parameters do not prove the shorter forms runs): throughput, and
+    # embeddings bit-identical to the shorter forms'
+    general = None
+    if not args.no_general_epilogue:
+        n_g = lib.fastface_set_epilogue_forms(ff.ff, 1)
+        if n_g < 0:
+            raise RuntimeError("fastface_set_epilogue_forms failed (%d)" % n_g)
+        for _ in range(3):
+            step()
+        check(lib, lib.ffk_stream_sync(stream), "sync")
+        kg = max(K // 4, 5)
+        check(lib, lib.ffk_event_record(ev0, stream), "record")
+        for _ in range(kg):
+            step()
+        check(lib, lib.ffk_event_record(ev1, stream), "record")
+        check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
+        g_ms = ms.value / kg
+        out_g = np.empty((B, 512), np.float32)
+        check(lib, lib.ffk_memcpy_d2h(out_g.ctypes.data, d_out, out_g.nbytes, stream), "download")
+        check(lib, lib.ffk_stream_sync(stream), "sync")
+        same = bool(np.array_equal(out_g, out_direct))
+        general = {"launches": n_g, "faces_s": round(B / (g_ms * 1e-3), 1), "ms_per_step": round(g_ms, 4),
+                   "embeddings_equal_fast_forms": same}
+        log("B=%d general epilogue forms on %d launches: %.3f ms/step, %.0f faces/s, embeddings %s"
+            % (B, n_g, g_ms, general["faces_s"], "equal to the shorter forms'" if same else "DIFFERENT"))
+        if not same:
+            raise RuntimeError("general-form embeddings differ from the shorter forms'")
+        check(lib, lib.fastface_set_epilogue_forms(ff.ff, 0), "epilogue forms")
+
     # a second context in the same process: create, first b=1 embed (captures
     # its launch chain), destroy
     t_c = time.perf_counter()
@@ -507,6 +540,7 @@ def main():
                      "timing": "26 launches (13 PReLU, 13 residual+BN) in one hipGraph, 20 replays "
                                "between HIP events on the launch stream"},
         "stage1_winograd": wino,
+        "general_epilogue": general,
         "cold_start": cold,
         "cpu_baseline": cpu,
     }

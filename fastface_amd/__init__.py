@@ -77,6 +77,7 @@ EXPORTS = [
     ("fastface_reserve", C.c_int, [_p, C.c_int]),
     ("fastface_stream", _p, [_p]),
     ("fastface_set_conv_algo", C.c_int, [_p, C.c_int]),
+    ("fastface_set_epilogue_forms", C.c_int, [_p, C.c_int]),
     ("fastface_num_steps", C.c_int, [_p]),
     ("fastface_get_step", C.c_int, [_p, C.c_int, C.POINTER(fastface_step_info)]),
     ("fastface_profile_steps", C.c_int, [_p, C.c_int, C.c_int, _p]),

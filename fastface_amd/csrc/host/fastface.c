@@ -83,6 +83,7 @@ struct FastFace {
     ffk_io io_cur[2];           /* what d_io holds now */
     int keep_all;
     int algo;                   /* FASTFACE_CONV_* of the 64-channel 3x3 s1 layers */
+    int general_epi;            /* launch every conv with the general epilogue forms */
     GraphEntry graphs[FF_MAX_GRAPHS];
     int n_graphs, graph_rr;
     void* ev_last;              /* recorded after the last enqueue, on last_stream */
@@ -179,6 +180,15 @@ static int set_io(FastFace* ff, const void* in, float* out, void* stream, int ba
     if (rc) return rc;
     memcpy(ff->io_cur, want, sizeof want);
     return 0;
+}
+
+/* The epilogue flags a step launches with: the plan's, less the proven
+ * fast forms when the context runs the general ones
+ * (fastface_set_epilogue_forms). */
+#define FF_FAST_EPI (FFK_EPI_PRELU_LE1 | FFK_EPI_IN_RANGE)
+static int step_flags(const FastFace* ff, const FfStep* st)
+{
+    return ff->general_epi ? st->flags & ~FF_FAST_EPI : st->flags;
 }
 
 static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t off, int shared, ffk_conv_desc* d);
@@ -302,7 +312,7 @@ static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t 
         d->out_bn = tensor_ptr(ff, st->t_bn, off);
     }
     if (st->flags & FFK_EPI_BN) d->bn_lut = ff->d_weights + st->lut_off;
-    d->flags = st->flags | ((fmt && st->t_in == FF_T_INPUT) ? FFK_IN_RGB8 : 0) |
+    d->flags = step_flags(ff, st) | ((fmt && st->t_in == FF_T_INPUT) ? FFK_IN_RGB8 : 0) |
                (writes_even(ff, st) ? FFK_OUT_X_EVEN : 0);
     if (ff->algo == FASTFACE_CONV_WINOGRAD_F23 && st->wino_off != (size_t)-1) {
         d->flags |= FFK_ALGO_WINOGRAD;
@@ -642,6 +652,20 @@ int fastface_set_conv_algo(FastFace* ff, int algo)
     return ensure_capacity(ff, cap > 0 ? cap : 1) ? -2 : n;
 }
 
+int fastface_set_epilogue_forms(FastFace* ff, int general)
+{
+    if (!ff || (general != 0 && general != 1)) return -1;
+    int n = 0;
+    for (int s = 0; s < ff->plan.n_steps; s++)
+        if (ff->plan.steps[s].kind == 1 && (ff->plan.steps[s].flags & FF_FAST_EPI)) n++;
+    if (general == ff->general_epi) return n;
+    if (drain(ff) || ffk_stream_sync(ff->stream)) return -2;
+    const int cap = ff->capacity;
+    free_activations(ff);                 /* (the captured chains hold the old flags) */
+    ff->general_epi = general;
+    return ensure_capacity(ff, cap > 0 ? cap : 1) ? -2 : n;
+}
+
 int fastface_num_steps(const FastFace* ff) { return ff ? ff->plan.n_steps : -1; }
 
 int fastface_get_step(const FastFace* ff, int s, fastface_step_info* info)
@@ -659,7 +683,7 @@ int fastface_get_step(const FastFace* ff, int s, fastface_step_info* info)
         info->stride = ev_in ? 1 : st->stride; info->pad = st->pad;
         info->hin = ev_in ? st->hin / 2 : st->hin; info->win = ev_in ? st->win / 2 : st->win;
         info->hout = st->hout; info->wout = st->wout;
-        info->flags = st->flags | (ev_out ? FFK_OUT_X_EVEN : 0);
+        info->flags = step_flags(ff, st) | (ev_out ? FFK_OUT_X_EVEN : 0);
         if (ff->algo == FASTFACE_CONV_WINOGRAD_F23 && st->wino_off != (size_t)-1)
             info->flags |= FFK_ALGO_WINOGRAD;
         info->stores_x = st->t_out >= 0;

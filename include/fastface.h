@@ -103,6 +103,19 @@ void* fastface_stream(FastFace* ff);
 #define FASTFACE_CONV_WINOGRAD_F23 1
 int fastface_set_conv_algo(FastFace* ff, int algo);
 
+/* Epilogue forms of the convolutions.  At create time the plan gives a conv
+ * launch the shorter requantization forms where its parameters prove them
+ * value-identical (PReLU as max(f, f*slope); no x86 out-of-range case).
+ * general = 1 launches every conv with the general forms instead (the
+ * reference's compare/select PReLU and the cvttps2dq emulation), 0 restores
+ * the plan's.  Embeddings are the same bit for bit either way; this exists
+ * to measure and check the general forms, which models whose parameters do
+ * not qualify run.  Returns the number of conv launches that have a
+ * shorter form in the plan, -1 on bad arguments, -2 on allocation failure.
+ * Captured launch chains are rebuilt on next use.  (No counterpart in the
+ * reference, which has one form.) */
+int fastface_set_epilogue_forms(FastFace* ff, int general);
+
 /* ---------------- introspection (tests, bench) ---------------------------- */
 typedef struct {
     int kind;                 /* 1 conv, 2 FC                                   */

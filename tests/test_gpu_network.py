@@ -226,6 +226,40 @@ def test_winograd_stage1_network(gpu_lib, synth_ffw4, oracle, oracle_model):
         f.close()
 
 
+def test_general_epilogue_forms(gpu_lib, synth_ffw4, oracle, oracle_model):
+    """fastface_set_epilogue_forms(1): every conv launches with the general
+    epilogue forms (compare/select PReLU, the x86 out-of-range emulation)
+    instead of the shorter ones the plan proved value-identical.  The
+    embeddings stay bit-exact with the oracle at b=1, 3 faces and a split
+    batch of 101; the step flags show the change; switching back restores
+    the plan's forms."""
+    f = fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT)
+    try:
+        fast = fa.FFK_EPI_PRELU_LE1 | fa.FFK_EPI_IN_RANGE
+        info = fa.fastface_step_info()
+        n = gpu_lib.fastface_num_steps(f.ff)
+
+        def n_fast():
+            return sum(1 for s in range(n) if gpu_lib.fastface_get_step(f.ff, s, C.byref(info)) == 0
+                       and info.kind == 1 and info.flags & fast)
+        n_convs = n_fast()
+        assert n_convs == n - 1                       # every conv of the synthetic model qualifies
+        x = synth.faces_uniform(101, 33)
+        shorter = f.embed_batch(x)
+        assert gpu_lib.fastface_set_epilogue_forms(f.ff, 1) == n_convs
+        assert n_fast() == 0
+        exp, _ = oracle.forward(oracle_model, x[:3])
+        assert np.array_equal(f.embed(x[0]), exp[0])
+        assert np.array_equal(f.embed_batch(x[:3]), exp)
+        assert np.array_equal(f.embed_batch(x), shorter)
+        assert gpu_lib.fastface_set_epilogue_forms(f.ff, 0) == n_convs
+        assert n_fast() == n_convs
+        assert np.array_equal(f.embed_batch(x), shorter)
+        assert gpu_lib.fastface_set_epilogue_forms(f.ff, 2) == -1
+    finally:
+        f.close()
+
+
 def test_streamed_host_batch_equals_one_shot(ff, gpu_lib):
     """Host batches stream in chunks (copy of one chunk during the compute of
     the previous): 600 fp32 faces as 512 + 88, 2100 uint8 faces as 4 x 512 +

@@ -166,7 +166,8 @@ def main():
     ap.add_argument("--cpu-cooldown", type=float, default=1.0,
                     help="seconds between those runs (reference: 3)")
     ap.add_argument("--no-general-epilogue", action="store_true",
-                    help="skip the B=1024 leg with every conv on the general epilogue forms")
+                    help="skip the B=1024 leg with every conv on the general epilogue forms "
+                         "(--b1024-only skips it too)")
     ap.add_argument("--no-winograd", action="store_true",
                     help="skip the config-5 run of the stage-1 layers as Winograd F(2,3)")
     args = ap.parse_args()
@@ -447,7 +448,7 @@ def main():
     # whose parameters do not prove the shorter forms runs): throughput, and
     # embeddings bit-identical to the shorter forms'
     general = None
-    if not args.no_general_epilogue:
+    if not args.no_general_epilogue and not args.b1024_only:
         n_g = lib.fastface_set_epilogue_forms(ff.ff, 1)
         if n_g < 0:
             raise RuntimeError("fastface_set_epilogue_forms failed (%d)" % n_g)

@@ -69,6 +69,9 @@ typedef struct { int batch, fmt; void* exec; } GraphEntry;
  * for ev_last on the host.  So calls on different streams never overlap on
  * one context's buffers. */
 
+typedef struct Stager Stager;
+static void stager_stop(Stager* s);
+
 struct FastFace {
     FfModel model;
     FfPlan plan;
@@ -93,6 +96,7 @@ struct FastFace {
     void* ev_chunk[FF_MAX_CHUNKS];
     void* h_stage[2];           /* pinned staging of streamed input pieces (on first use) */
     void* ev_stage[2];          /* the last DMA out of each staging buffer */
+    Stager* stager;             /* its copy threads (on first use), or NULL */
     ffk_io io_cur[2];           /* what d_io holds now */
     int keep_all;
     int algo;                   /* FASTFACE_CONV_* of the 64-channel 3x3 s1 layers */
@@ -535,6 +539,7 @@ void fastface_destroy(FastFace* ff)
     for (int k = 0; k < FF_MAX_CHUNKS; k++)
         if (ff->ev_chunk[k]) ffk_event_destroy(ff->ev_chunk[k]);
     if (ff->ev_last) ffk_event_destroy(ff->ev_last);
+    if (ff->stager) { stager_stop(ff->stager); free(ff->stager); }
     for (int b = 0; b < 2; b++) {
         if (ff->ev_stage[b]) ffk_event_destroy(ff->ev_stage[b]);
         if (ff->h_stage[b]) ffk_host_free(ff->h_stage[b]);
@@ -561,10 +566,11 @@ void* fastface_stream(FastFace* ff) { return ff ? ff->stream : NULL; }
  * rewritten while a copy may still read it) and replays the chain for the
  * chunk's size.  Faces are independent: the results equal the one-shot
  * path's bit for bit. */
-/* Copy threads of one streamed host call: the caller and n - 1 workers each
- * copy one slice of the current piece.  A piece starts when the caller bumps
- * `gen` and ends when every worker has counted itself in `finished`. */
-typedef struct Stager Stager;
+/* Copy threads of a context's streamed host calls (started on first use,
+ * idle between calls, stopped when the context is destroyed): the calling
+ * thread and n - 1 workers each copy one slice of the current piece.  A
+ * piece starts when the caller bumps `gen` and ends when every worker has
+ * counted itself in `finished`. */
 typedef struct { Stager* s; int i; } StageSlot;
 struct Stager {
     int n;                              /* copying threads, the caller included */
@@ -712,8 +718,12 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
          * without them the chunks are copied from the caller's memory */
         if (!ff->h_stage[0]) ff->h_stage[0] = ffk_host_alloc(FF_STAGE_BYTES);
         if (ff->h_stage[0] && !ff->h_stage[1]) ff->h_stage[1] = ffk_host_alloc(FF_STAGE_BYTES);
-        Stager stager;
-        Stager* st = (!rc && ff->h_stage[1] && stager_start(&stager) == 0) ? &stager : NULL;
+        if (!rc && ff->h_stage[1] && !ff->stager) {
+            Stager* sg = (Stager*)calloc(1, sizeof *sg);
+            if (sg && stager_start(sg) == 0) ff->stager = sg;
+            else free(sg);
+        }
+        Stager* st = rc || !ff->h_stage[1] ? NULL : ff->stager;
         int piece = 0;
         for (int k = 0; k < n && !rc; k++) {
             const size_t b0 = (size_t)k * chunk;
@@ -727,7 +737,6 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
             if (!rc) rc = enqueue_exec(ff, nb, ff->stream, fmt, k + 1 < n ? g_chunk : g_last);
             if (!rc) memcpy(ff->io_cur, slot, sizeof ff->io_cur);
         }
-        if (st) stager_stop(st);
         if (rc) {           /* leave no copy or chunk running into the buffers */
             ffk_stream_sync(ff->cstream);
             ffk_stream_sync(ff->stream);

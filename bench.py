@@ -472,7 +472,8 @@ def main():
             % (B, n_g, g_ms, general["faces_s"], "equal to the shorter forms'" if same else "DIFFERENT"))
         if not same:
             raise RuntimeError("general-form embeddings differ from the shorter forms'")
-        check(lib, lib.fastface_set_epilogue_forms(ff.ff, 0), "epilogue forms")
+        if lib.fastface_set_epilogue_forms(ff.ff, 0) < 0:      # (returns the launch count)
+            raise RuntimeError("fastface_set_epilogue_forms(0) failed: %s" % fastface_amd.last_error())
 
     # a second context in the same process: create, first b=1 embed (captures
     # its launch chain), destroy

@@ -38,8 +38,13 @@
  * other.  A plain copy from pageable memory is staged by the runtime on one
  * host thread (~27 GB/s measured on the MI355X box); eight threads fill
  * pinned memory at ~64 GB/s and the DMA from it runs at ~57 GB/s. */
-#define FF_STAGE_BYTES ((size_t)16 << 20)
+#ifndef FF_STAGE_MB
+#define FF_STAGE_MB 16
+#endif
+#ifndef FF_STAGE_THREADS
 #define FF_STAGE_THREADS 8
+#endif
+#define FF_STAGE_BYTES ((size_t)FF_STAGE_MB << 20)
 
 /* Batches of FF_SPLIT_MIN faces or more run as two halves, each on its own
  * stream inside the one captured graph (a fork and a join), both launched

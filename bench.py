@@ -313,7 +313,7 @@ def main():
         if DOMINANT_KERNEL in tj.get("kernel", ""):      # counters of this very kernel only
             traffic = tj.get("bytes_per_launch")
 
-    b1_ms = b1_dev_ms = b1_fc_ms = b8_ms_face = host_fp32 = host_rgb8 = dev_rgb8 = cfg2 = None
+    b1_ms = b1_dev_ms = b1_fc_ms = b8_ms_face = b256_faces_s = host_fp32 = host_rgb8 = dev_rgb8 = cfg2 = None
     if not args.b1024_only:
         # b=1 latency: host buffers in, host buffers out (fastface_embed), and the
         # device-only chain
@@ -357,6 +357,19 @@ def main():
         check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
         b8_ms_face = ms.value / 50 / 8
         log("B=8: %.4f ms/face (%.3f ms per batch), device chain" % (b8_ms_face, b8_ms_face * 8))
+
+        # B=256 throughput (the synthetic FFW4 is the config's
+        # seed-3 random-init model), device-resident chain
+        for _ in range(3):
+            check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 256, d_out, stream), "b256 dev")
+        check(lib, lib.ffk_stream_sync(stream), "sync")
+        check(lib, lib.ffk_event_record(ev0, stream), "record")
+        for _ in range(20):
+            check(lib, lib.fastface_embed_batch_device(ff.ff, d_in, 256, d_out, stream), "b256 dev")
+        check(lib, lib.ffk_event_record(ev1, stream), "record")
+        check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
+        b256_faces_s = 256 * 20 / (ms.value * 1e-3)
+        log("B=256: %.3f ms per batch, %.0f faces/s, device chain" % (ms.value / 20, b256_faces_s))
 
         # the single 256->256 3x3 layer microbench at N=64
         from fastface_amd.layerbench import time_layer
@@ -527,6 +540,7 @@ def main():
         "b1_device_ms": rnd(b1_dev_ms, 4),
         "b1_fc_ms": rnd(b1_fc_ms, 4),
         "b8_ms_per_face": rnd(b8_ms_face, 5),
+        "b256_faces_s": rnd(b256_faces_s, 1),
         "config2_layer": cfg2,
         "chain_int8_tops": round(chain_tops, 2),
         "chain_frac_of_int8_peak": round(chain_tops / PEAK_INT8_TOPS, 4),

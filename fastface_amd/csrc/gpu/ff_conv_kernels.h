@@ -298,13 +298,18 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
             v4i o;
 #pragma unroll
             for (int w = 0; w < 4; w++) {
-                uint32_t packed = 0;
+                uint32_t b[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int q = (int8_t)((uint32_t)v[w] >> (e * 8));
-                    packed |= (uint32_t)(uint8_t)L[(w * 4 + e) * FF_LUT_PITCH + q] << (e * 8);
+                    b[e] = (uint8_t)L[(w * 4 + e) * FF_LUT_PITCH + q];
                 }
-                o[w] = (int)packed;
+                // three byte permutes: (b0, b1), (b2, b3), then the two pairs
+                // (v_perm_b32 selector bytes 0-3 pick the second operand's
+                // bytes, 4-7 the first's, 0x0c a zero byte)
+                const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u);
+                const uint32_t hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
+                o[w] = (int)__builtin_amdgcn_perm(hi, lo, 0x05040100u);
             }
             __builtin_amdgcn_raw_buffer_store_b128(o, r_bn, (unsigned)m * COUT + ncol0 + ch * 16, 0, 0);
         }

@@ -367,6 +367,38 @@ def test_concurrent_contexts(gpu_lib, synth_ffw4):
             c.close()
 
 
+def test_concurrent_contexts_streamed(gpu_lib, synth_ffw4):
+    """Two contexts streaming host batches of 600 fp32 faces on two threads
+    at once: each call goes through its context's pinned staging buffers and
+    copy threads; the embeddings equal one context's alone, call after call,
+    and a context destroyed after streaming stops its copy threads."""
+    import threading
+    xs = [synth.faces_uniform(600, 52), synth.faces_uniform(600, 53)]
+    ctxs = [fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT) for _ in range(2)]
+    try:
+        exp = [ctxs[0].embed_batch(x) for x in xs]
+        out, errs = [[], []], []
+
+        def work(i):
+            try:
+                for _ in range(3):
+                    out[i].append(ctxs[i].embed_batch(xs[i]))
+            except Exception as e:          # reported below, in the main thread
+                errs.append(e)
+        th = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+        for t in th:
+            t.start()
+        for t in th:
+            t.join(timeout=120)
+        assert not errs and not any(t.is_alive() for t in th)
+        for i in range(2):
+            for got in out[i]:
+                assert np.array_equal(got, exp[i]), i
+    finally:
+        for c in ctxs:
+            c.close()
+
+
 def test_device_calls_on_caller_streams_are_ordered(gpu_lib, synth_ffw4, oracle, oracle_model):
     """Device calls on two caller streams, interleaved with host calls on the
     context stream and with no host wait in between, never overlap on the

@@ -26,10 +26,18 @@
  * of chunk k+1 (copy stream) runs while chunk k computes (context stream),
  * each chunk in its own region of the input buffer.  A chunk must fill the
  * GPU by itself, and the copy it hides must be worth a second launch chain:
- * both input formats stream in chunks of 512 faces (measured at 1024 uint8
+ * uint8 batches stream in chunks of 512 faces (measured at 1024 uint8
  * faces: 112k faces/s in one chunk, 120k in two, 109k in three). */
-#define FF_STREAM_CHUNK_F32 512
 #define FF_STREAM_CHUNK_U8 512
+/* fp32 faces are four times the bytes: the first chunk's copy, the one
+ * the GPU waits for, is kept short (256 faces), and the chunks after it
+ * are larger (768), so that each copy still finishes while the chunk
+ * before it computes (1024 faces as 256 + 768: ~111,000 faces/s against
+ * ~106,000 as 512 + 512, same box).  Batches of up to FF_STREAM_MIN_F32
+ * faces go in one copy. */
+#define FF_STREAM_FIRST_F32 256
+#define FF_STREAM_CHUNK_F32 768
+#define FF_STREAM_MIN_F32 512
 #define FF_MAX_CHUNKS 64
 
 /* A streamed chunk reaches the device through two pinned staging buffers:
@@ -404,10 +412,10 @@ static int run_captured(FastFace* ff, int batch, int fmt)
 }
 
 /* The captured chain for (batch, fmt), capturing it on first use.  A full
- * cache evicts round-robin, never the entry holding `keep` (a chain the
- * caller is about to launch); an evicted chain may still be in flight, so
- * the context's work is waited for before it is destroyed. */
-static void* graph_for(FastFace* ff, int batch, int fmt, const void* keep)
+ * cache evicts round-robin, never the entries holding `keep` or `keep2`
+ * (chains the caller is about to launch); an evicted chain may still be in
+ * flight, so the context's work is waited for before it is destroyed. */
+static void* graph_for(FastFace* ff, int batch, int fmt, const void* keep, const void* keep2)
 {
     for (int i = 0; i < ff->n_graphs; i++)
         if (ff->graphs[i].batch == batch && ff->graphs[i].fmt == fmt) return ff->graphs[i].exec;
@@ -421,7 +429,7 @@ static void* graph_for(FastFace* ff, int batch, int fmt, const void* keep)
         slot = ff->n_graphs++;
     } else {
         slot = ff->graph_rr;
-        if (ff->graphs[slot].exec == keep) slot = (slot + 1) % FF_MAX_GRAPHS;
+        while (ff->graphs[slot].exec == keep || ff->graphs[slot].exec == keep2) slot = (slot + 1) % FF_MAX_GRAPHS;
         ff->graph_rr = (slot + 1) % FF_MAX_GRAPHS;
         if (drain(ff) || ffk_stream_sync(ff->stream)) { ffk_graph_destroy(exec); return NULL; }
         ffk_graph_destroy(ff->graphs[slot].exec);
@@ -442,7 +450,7 @@ static int enqueue_exec(FastFace* ff, int batch, void* stream, int fmt, void* ex
     if (ff->keep_all) {
         rc = run_direct(ff, batch, stream, fmt);
     } else {
-        void* g = exec ? exec : graph_for(ff, batch, fmt, NULL);
+        void* g = exec ? exec : graph_for(ff, batch, fmt, NULL, NULL);
         rc = g ? ffk_graph_launch(g, stream) : FFK_ERR_HIP;
     }
     if (!rc) rc = mark_enqueued(ff, stream);
@@ -705,20 +713,26 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
     if (rc) { report("activation allocation", rc); return -2; }
     int8_t* d_in = fmt ? (int8_t*)ff->d_input_u8 : (int8_t*)ff->d_input;
     const size_t out_bytes = (size_t)batch * FASTFACE_OUTPUT_N * sizeof(float);
+    /* chunks: `first` faces, then `chunk`-face chunks, the last one the rest */
+    const int first = fmt ? FF_STREAM_CHUNK_U8 : FF_STREAM_FIRST_F32;
     int chunk = fmt ? FF_STREAM_CHUNK_U8 : FF_STREAM_CHUNK_F32;
-    if (batch > chunk * FF_MAX_CHUNKS) chunk = (batch + FF_MAX_CHUNKS - 1) / FF_MAX_CHUNKS;
-    const int n = (batch + chunk - 1) / chunk;
+    const int streamed = batch > (fmt ? FF_STREAM_CHUNK_U8 : FF_STREAM_MIN_F32);
+    if (streamed && batch - first > chunk * (FF_MAX_CHUNKS - 1))
+        chunk = (batch - first + FF_MAX_CHUNKS - 2) / (FF_MAX_CHUNKS - 1);
+    const int n = streamed ? 1 + (batch - first + chunk - 1) / chunk : 1;
     if (n < 2 || ff->keep_all) {
         rc = set_io(ff, d_in, ff->d_output, ff->stream, batch, fmt);
         if (!rc) rc = ffk_memcpy_h2d(d_in, in, (size_t)batch * face_bytes, ff->stream);
         if (!rc) rc = enqueue(ff, batch, ff->stream, fmt);
     } else {
-        /* capture both chains before any copy is issued (the second lookup
-         * may not evict the first), and launch them directly */
-        const int last = batch - (n - 1) * chunk;
-        void* g_chunk = graph_for(ff, chunk, fmt, NULL);
-        void* g_last = g_chunk ? graph_for(ff, last, fmt, g_chunk) : NULL;
-        if (!g_chunk || !g_last) rc = FFK_ERR_HIP;
+        /* capture the (up to three) chains before any copy is issued (a
+         * lookup may not evict the chains looked up before it), and launch
+         * them directly */
+        const int last = batch - first - (n - 2) * chunk;
+        void* g_first = graph_for(ff, first, fmt, NULL, NULL);
+        void* g_chunk = g_first && n > 2 ? graph_for(ff, chunk, fmt, g_first, NULL) : g_first;
+        void* g_last = g_chunk ? graph_for(ff, last, fmt, g_first, g_chunk) : NULL;
+        if (!g_first || !g_chunk || !g_last) rc = FFK_ERR_HIP;
         /* staging: pinned buffers on first use, copy threads for this call;
          * without them the chunks are copied from the caller's memory */
         if (!ff->h_stage[0]) ff->h_stage[0] = ffk_host_alloc(FF_STAGE_BYTES);
@@ -731,15 +745,15 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
         Stager* st = rc || !ff->h_stage[1] ? NULL : ff->stager;
         int piece = 0;
         for (int k = 0; k < n && !rc; k++) {
-            const size_t b0 = (size_t)k * chunk;
-            const int nb = k + 1 < n ? chunk : last;
+            const size_t b0 = k ? (size_t)first + (size_t)(k - 1) * chunk : 0;
+            const int nb = k == 0 ? first : (k + 1 < n ? chunk : last);
             rc = stage_h2d(ff, st, d_in, (const int8_t*)in, b0 * face_bytes, (size_t)nb * face_bytes, &piece);
             if (!rc) rc = ffk_event_record(ff->ev_chunk[k], ff->cstream);
             if (!rc) rc = ffk_stream_wait_event(ff->stream, ff->ev_chunk[k]);
             ffk_io* slot = &ff->h_io[2 * (1 + k)];
             io_pair(ff, slot, d_in + b0 * face_bytes, ff->d_output + b0 * FASTFACE_OUTPUT_N, nb, fmt);
             if (!rc) rc = ffk_memcpy_h2d(ff->d_io, slot, 2 * sizeof(ffk_io), ff->stream);
-            if (!rc) rc = enqueue_exec(ff, nb, ff->stream, fmt, k + 1 < n ? g_chunk : g_last);
+            if (!rc) rc = enqueue_exec(ff, nb, ff->stream, fmt, k == 0 ? g_first : (k + 1 < n ? g_chunk : g_last));
             if (!rc) memcpy(ff->io_cur, slot, sizeof ff->io_cur);
         }
         if (rc) {           /* leave no copy or chunk running into the buffers */

@@ -262,18 +262,23 @@ def test_general_epilogue_forms(gpu_lib, synth_ffw4, oracle, oracle_model):
 
 def test_streamed_host_batch_equals_one_shot(ff, gpu_lib):
     """Host batches stream in chunks (copy of one chunk during the compute of
-    the previous): 600 fp32 faces as 512 + 88, 2100 uint8 faces as 4 x 512 +
-    52.  Embeddings equal the device-resident one-shot path's and the
-    single-face path's; a small batch afterwards still reads its own buffers."""
-    B = 600
-    x = synth.faces_uniform(B, 41)
+    the previous): 600 fp32 faces as 256 + 344, 2100 as 256 + 768 + 768 + 308
+    (three launch chains), 2100 uint8 faces as 4 x 512 + 52.  Embeddings equal
+    the device-resident one-shot path's and the single-face path's; a small
+    batch afterwards still reads its own buffers."""
+    for B in (600, 2100):
+        x = synth.faces_uniform(B, 41)
+        got = ff.embed_batch(x)
+        din, dout = Dev(gpu_lib, host=x), Dev(gpu_lib, nbytes=B * 512 * 4)
+        assert gpu_lib.fastface_embed_batch_device(ff.ff, din.ptr, B, dout.ptr, None) == 0
+        check(gpu_lib, gpu_lib.ffk_stream_sync(gpu_lib.fastface_stream(ff.ff)))
+        assert np.array_equal(got, dout.get(np.float32, (B, 512)))
+        for i in (0, 255, 256, 1023, 1024, 1791, 1792, B - 1):
+            if i < B:
+                assert np.array_equal(ff.embed(x[i]), got[i]), (B, i)
+        din.free(); dout.free()
+    x = synth.faces_uniform(600, 41)
     got = ff.embed_batch(x)
-    din, dout = Dev(gpu_lib, host=x), Dev(gpu_lib, nbytes=B * 512 * 4)
-    assert gpu_lib.fastface_embed_batch_device(ff.ff, din.ptr, B, dout.ptr, None) == 0
-    check(gpu_lib, gpu_lib.ffk_stream_sync(gpu_lib.fastface_stream(ff.ff)))
-    assert np.array_equal(got, dout.get(np.float32, (B, 512)))
-    for i in (0, 511, 512, 599):
-        assert np.array_equal(ff.embed(x[i]), got[i]), i
     B8 = 2100
     imgs = np.random.default_rng(42).integers(0, 256, size=(B8, 112, 112, 3), dtype=np.uint8)
     got8 = ff.embed_batch_rgb8(imgs)

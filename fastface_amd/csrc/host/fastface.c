@@ -26,8 +26,8 @@
  * of chunk k+1 (copy stream) runs while chunk k computes (context stream),
  * each chunk in its own region of the input buffer.  A chunk must fill the
  * GPU by itself, and the copy it hides must be worth a second launch chain:
- * uint8 batches stream in chunks of 512 faces (measured at 1024 uint8
- * faces: 112k faces/s in one chunk, 120k in two, 109k in three). */
+ * uint8 batches stream in chunks of 512 faces (at 1024 faces ~122k faces/s,
+ * against ~119k as one staged copy and one launch chain). */
 #define FF_STREAM_CHUNK_U8 512
 /* fp32 faces are four times the bytes: the first chunk's copy, the one
  * the GPU waits for, is kept short (256 faces), and the chunks after it
@@ -53,6 +53,8 @@
 #define FF_STAGE_THREADS 8
 #endif
 #define FF_STAGE_BYTES ((size_t)FF_STAGE_MB << 20)
+/* a one-chunk host batch of at least this many bytes is staged too */
+#define FF_STAGE_MIN_BYTES ((size_t)8 << 20)
 
 /* Batches of FF_SPLIT_MIN faces or more run as two halves, each on its own
  * stream inside the one captured graph (a fork and a join), both launched
@@ -680,6 +682,21 @@ static void stager_stop(Stager* s)
     pthread_mutex_destroy(&s->mu);
 }
 
+/* The context's staging buffers and copy threads, set up on first use, or
+ * NULL if they cannot be (the caller's memory is then copied directly). */
+static Stager* staging(FastFace* ff)
+{
+    if (!ff->h_stage[0]) ff->h_stage[0] = ffk_host_alloc(FF_STAGE_BYTES);
+    if (ff->h_stage[0] && !ff->h_stage[1]) ff->h_stage[1] = ffk_host_alloc(FF_STAGE_BYTES);
+    if (!ff->h_stage[1]) return NULL;
+    if (!ff->stager) {
+        Stager* sg = (Stager*)calloc(1, sizeof *sg);
+        if (sg && stager_start(sg) == 0) ff->stager = sg;
+        else free(sg);
+    }
+    return ff->stager;
+}
+
 /* The input bytes [off, off + bytes) of a streamed call to d_in + off, on
  * the copy stream: through the pinned staging buffers when the stager runs
  * (piece p in buffer p % 2, after the DMA that last read that buffer),
@@ -721,8 +738,19 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
         chunk = (batch - first + FF_MAX_CHUNKS - 2) / (FF_MAX_CHUNKS - 1);
     const int n = streamed ? 1 + (batch - first + chunk - 1) / chunk : 1;
     if (n < 2 || ff->keep_all) {
+        /* one chunk: a large one still goes through the staging buffers */
+        const size_t bytes = (size_t)batch * face_bytes;
+        Stager* st = bytes >= FF_STAGE_MIN_BYTES ? staging(ff) : NULL;
+        int piece = 0;
         rc = set_io(ff, d_in, ff->d_output, ff->stream, batch, fmt);
-        if (!rc) rc = ffk_memcpy_h2d(d_in, in, (size_t)batch * face_bytes, ff->stream);
+        if (!rc && st) {
+            rc = stage_h2d(ff, st, d_in, (const int8_t*)in, 0, bytes, &piece);
+            if (!rc) rc = ffk_event_record(ff->ev_chunk[0], ff->cstream);
+            if (!rc) rc = ffk_stream_wait_event(ff->stream, ff->ev_chunk[0]);
+            if (rc) ffk_stream_sync(ff->cstream);
+        } else if (!rc) {
+            rc = ffk_memcpy_h2d(d_in, in, bytes, ff->stream);
+        }
         if (!rc) rc = enqueue(ff, batch, ff->stream, fmt);
     } else {
         /* capture the (up to three) chains before any copy is issued (a
@@ -733,16 +761,7 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
         void* g_chunk = g_first && n > 2 ? graph_for(ff, chunk, fmt, g_first, NULL) : g_first;
         void* g_last = g_chunk ? graph_for(ff, last, fmt, g_first, g_chunk) : NULL;
         if (!g_first || !g_chunk || !g_last) rc = FFK_ERR_HIP;
-        /* staging: pinned buffers on first use, copy threads for this call;
-         * without them the chunks are copied from the caller's memory */
-        if (!ff->h_stage[0]) ff->h_stage[0] = ffk_host_alloc(FF_STAGE_BYTES);
-        if (ff->h_stage[0] && !ff->h_stage[1]) ff->h_stage[1] = ffk_host_alloc(FF_STAGE_BYTES);
-        if (!rc && ff->h_stage[1] && !ff->stager) {
-            Stager* sg = (Stager*)calloc(1, sizeof *sg);
-            if (sg && stager_start(sg) == 0) ff->stager = sg;
-            else free(sg);
-        }
-        Stager* st = rc || !ff->h_stage[1] ? NULL : ff->stager;
+        Stager* st = rc ? NULL : staging(ff);
         int piece = 0;
         for (int k = 0; k < n && !rc; k++) {
             const size_t b0 = k ? (size_t)first + (size_t)(k - 1) * chunk : 0;

@@ -78,6 +78,7 @@ EXPORTS = [
     ("fastface_stream", _p, [_p]),
     ("fastface_set_conv_algo", C.c_int, [_p, C.c_int]),
     ("fastface_set_epilogue_forms", C.c_int, [_p, C.c_int]),
+    ("fastface_set_shortcut_fusion", C.c_int, [_p, C.c_int]),
     ("fastface_num_steps", C.c_int, [_p]),
     ("fastface_get_step", C.c_int, [_p, C.c_int, C.POINTER(fastface_step_info)]),
     ("fastface_profile_steps", C.c_int, [_p, C.c_int, C.c_int, _p]),
@@ -115,6 +116,7 @@ EXPORTS = [
     ("ffk_conv_workspace_bytes", C.c_size_t, [C.POINTER(ffk_conv_desc)]),
     ("ffk_conv", C.c_int, [C.POINTER(ffk_conv_desc), _p]),
     ("ffk_conv_noalloc", C.c_int, [C.POINTER(ffk_conv_desc), _p]),
+    ("ffk_conv_s2_shortcut", C.c_int, [C.POINTER(ffk_conv_desc), C.POINTER(ffk_conv_desc), _p]),
     ("ffk_conv_variant", C.c_char_p, [C.POINTER(ffk_conv_desc)]),
     ("ffk_winograd_supported", C.c_int, [C.c_int] * 8),
     ("ffk_winograd_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),

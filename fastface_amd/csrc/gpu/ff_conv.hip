@@ -110,6 +110,29 @@ long long conv_pixels(const ffk_conv_desc* d) {
     return (long long)d->batch * hout * wout;
 }
 
+// kernel arguments of a descriptor (M, tiles_n and the split-K workspace are
+// set per launch)
+ConvArgs conv_args(const ffk_conv_desc* d) {
+    ConvArgs a = {};
+    if (d->cin == 3) a.in_f32 = (const float*)d->in;
+    else a.in = (const int8_t*)d->in;
+    a.in_inv = d->in_inv;
+    a.in_lut = d->in_lut;
+    a.io = d->io;
+    a.w = d->w;
+    a.params = d->params;
+    a.add_src = d->add_src;
+    a.bn_lut = d->bn_lut;
+    a.out = d->out;
+    a.out_bn = d->out_bn;
+    a.out_i32 = d->out_i32;
+    a.flags = d->flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_BIAS | FFK_EPI_INSCALE |
+                          FFK_EPI_PRELU_LE1 | FFK_OUT_X_EVEN | FFK_EPI_IN_RANGE |
+                          FFK_IN_RGB8);
+    a.in_scale = d->in_scale;
+    return a;
+}
+
 }  // namespace
 
 extern "C" {
@@ -234,23 +257,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     }
     if (M == 0) return FFK_OK;
     if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_conv(d, (hipStream_t)stream);
-    ConvArgs a = {};
-    if (stem) a.in_f32 = (const float*)d->in;
-    else a.in = (const int8_t*)d->in;
-    a.in_inv = d->in_inv;
-    a.in_lut = d->in_lut;
-    a.io = d->io;
-    a.w = d->w;
-    a.params = d->params;
-    a.add_src = d->add_src;
-    a.bn_lut = d->bn_lut;
-    a.out = d->out;
-    a.out_bn = d->out_bn;
-    a.out_i32 = d->out_i32;
-    a.flags = d->flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_BIAS | FFK_EPI_INSCALE |
-                          FFK_EPI_PRELU_LE1 | FFK_OUT_X_EVEN | FFK_EPI_IN_RANGE |
-                          FFK_IN_RGB8);
-    a.in_scale = d->in_scale;
+    const ConvArgs a = conv_args(d);
     // The direct-to-LDS kernels address the int8 input and the residual
     // tensor with 32-bit offsets: a batch whose input or output tensor
     // reaches 2 GiB runs as several launches over consecutive image ranges
@@ -282,6 +289,43 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
         if (rc != FFK_OK) return rc;
     }
     return FFK_OK;
+}
+
+int ffk_conv_s2_shortcut(const ffk_conv_desc* c, const ffk_conv_desc* s, void* stream) {
+    if (!c || !s || c->batch < 0) {
+        ffk_set_error("conv_s2_shortcut: bad descriptors%s%s", nullptr, nullptr);
+        return FFK_ERR_ARG;
+    }
+    // the pair the fused kernel computes; anything else is left to ffk_conv
+    const int no_c = FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_INSCALE | FFK_ALGO_WINOGRAD | FFK_IN_RGB8 |
+                     FFK_OUT_X_EVEN;
+    const int no_s = FFK_EPI_PRELU | FFK_EPI_INSCALE | FFK_ALGO_WINOGRAD | FFK_IN_RGB8;
+    if (c->kh != 3 || c->kw != 3 || c->stride != 2 || c->pad != 1 || c->hin != c->win || (c->hin & 1) ||
+        (c->flags & no_c) || c->out_i32 || !c->in || !c->out || !c->w || !c->params)
+        return 0;
+    const int ho = c->hin / 2;
+    if (s->batch != c->batch || s->kh != 1 || s->kw != 1 || s->stride != 1 || s->pad != 0 || s->hin != ho ||
+        s->win != ho || s->cout != c->cout || !(s->flags & FFK_EPI_ADD) || (s->flags & no_s) || s->out_i32 ||
+        s->add_src != c->out || !s->in || !s->w || !s->params)
+        return 0;
+    if ((s->flags & FFK_EPI_BN) ? (!s->out_bn || !s->bn_lut) : !s->out) return 0;
+    if ((s->flags & FFK_OUT_X_EVEN) && ((ho & 1) || !s->out)) return 0;
+    const ConvEntry* e = find_conv(c->cin, c->cout, 3, 3, 2, 1, c->hin, c->win);
+    if (!e || !e->pair || e->pair_cx != s->cin) return 0;
+    const long long M = conv_pixels(c);
+    if (M == 0) return 1;
+    // one launch over the whole batch: every tensor below 2 GiB
+    const long long lim = 0x7fffffffLL;
+    if ((long long)c->batch * c->hin * c->win * c->cin > lim || M * c->cout > lim || M * s->cin > lim) return 0;
+    const ConvLaunch l = choose_launch(e, M, c->workspace ? c->workspace_bytes : 0,
+                                       (c->flags & FFK_SHARED_GPU) != 0);
+    if (l.fn != e->fn) return 0;
+    ConvArgs a = conv_args(c), b = conv_args(s);
+    a.M = b.M = (int)M;
+    a.tiles_n = b.tiles_n = c->cout / l.bn;
+    e->pair(a, b, l.grid, (hipStream_t)stream);
+    const int rc = ffk_check_launch("conv pair launch");
+    return rc != FFK_OK ? rc : 1;
 }
 
 // ---------------------------------------------------------------------------

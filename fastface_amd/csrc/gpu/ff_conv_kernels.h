@@ -198,8 +198,13 @@ __device__ __forceinline__ unsigned x_pix_blk(const ConvArgs& a, int mb, int r) 
 // waves loaded visible; without it (a table already visible, as in the
 // persistent stem after its first tile) the flush reads only the wave's own
 // staging tile, which the wave's in-order LDS accesses already order.
+// STAGE (a conv fused with the 1x1 shortcut that adds its output): 1 leaves
+// the int8 results in the wave's staging tile and stores nothing (the
+// residual of the shortcut's epilogue); 2 (with ADD) takes the residual from
+// the staging tile, where STAGE 1 left it, instead of loading it.  The same
+// lane writes and reads each element, so no barrier orders the two.
 template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC, bool RANGE, int HO, int WO,
-          bool LUT_DMA = false, bool WG_SYNC = true>
+          bool LUT_DMA = false, bool WG_SYNC = true, int STAGE = 0>
 __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                             const EpiParams<NJ>& prm, int mrow0, int ncol0, int8_t* Ws,
                                             const int8_t* Lw) {
@@ -217,7 +222,8 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
     const float* p2 = prm.slope;
     const float* adds = prm.adds;
     const float* inv = prm.inv;
-    if (ADD && RSLOTS % 64 == 0) {
+    static_assert(STAGE != 1 || !ADD, "a staged tile is an output, not a residual sum");
+    if (ADD && STAGE != 2 && RSLOTS % 64 == 0) {
         // residual tile -> this wave's LDS tile as direct-to-LDS loads: slot s
         // of wave load k is tile row (64k+s)/SPR, piece (64k+s)%SPR; unused
         // pieces and rows past M fetch the zero page.  One wait covers them
@@ -239,7 +245,7 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
             bdma16(r_add, off, 0, Ws + k * 1024);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    } else if (ADD) {   // residual tile -> LDS (coalesced 16-byte loads)
+    } else if (ADD && STAGE != 2) {   // residual tile -> LDS (coalesced 16-byte loads)
 #pragma unroll
         for (int k = 0; k < ROWS / RPI; k++) {
             const int row = lane / CH + k * RPI;
@@ -271,6 +277,7 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
                 // every residual read of the wave tile into registers
                 if (r == 15) asm volatile("" ::: "memory");
             }
+    if constexpr (STAGE == 1) return;
     if (BN2 && LUT_DMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if constexpr (WG_SYNC) __syncthreads();
     else __builtin_amdgcn_wave_barrier();
@@ -424,6 +431,40 @@ __device__ __forceinline__ void wave_epilogue(const v16i (&acc)[MI][NJ], const C
         return;
     }
     wave_epilogue_p<COUT, MI, NJ, HO, WO>(acc, a, load_epi_params<COUT, NJ>(a, ncol0), mrow0, ncol0, Ws, Lw);
+}
+
+// The two epilogues of a stride-2 conv fused with its block's 1x1 shortcut
+// (the host fuses only these forms: the conv with bias and no PReLU,
+// residual or BN; the shortcut with the residual add, optionally BN, no
+// PReLU; neither with an in-scale).  First the conv's int8 tile into the
+// wave's staging tile, no stores ...
+template <int COUT, int MI, int NJ, int HO, int WO>
+__device__ __forceinline__ void wave_epi_pair_stage(const v16i (&acc)[MI][NJ], const ConvArgs& a,
+                                                    const EpiParams<NJ>& P, int mrow0, int ncol0, int8_t* Ws) {
+    if (a.flags & FFK_EPI_IN_RANGE)
+        wave_epi_i8<COUT, MI, NJ, 0, false, false, false, true, HO, WO, true, true, 1>(acc, a, P, mrow0, ncol0, Ws,
+                                                                                      nullptr);
+    else
+        wave_epi_i8<COUT, MI, NJ, 0, false, false, false, false, HO, WO, true, true, 1>(acc, a, P, mrow0, ncol0, Ws,
+                                                                                       nullptr);
+}
+
+// ... then the shortcut's, with that tile as its residual.
+template <int COUT, int MI, int NJ, int HO, int WO>
+__device__ __forceinline__ void wave_epi_pair_add(const v16i (&acc)[MI][NJ], const ConvArgs& b, int mrow0, int ncol0,
+                                                  int8_t* Ws, const int8_t* Lw) {
+    const EpiParams<NJ> P = load_epi_params<COUT, NJ>(b, ncol0);
+    const bool rng = b.flags & FFK_EPI_IN_RANGE;
+#define FF_EPI(BN, RG) \
+    wave_epi_i8<COUT, MI, NJ, 0, true, BN, false, RG, HO, WO, true, true, 2>(acc, b, P, mrow0, ncol0, Ws, Lw)
+    if (b.flags & FFK_EPI_BN) {
+        if (rng) FF_EPI(true, true);
+        else FF_EPI(true, false);
+    } else {
+        if (rng) FF_EPI(false, true);
+        else FF_EPI(false, false);
+    }
+#undef FF_EPI
 }
 
 // BN tables of channels [c0, c0 + NCH) -> LDS (pitch FF_LUT_PITCH) as
@@ -1208,8 +1249,17 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 }  // namespace s2
 
-template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int WPE>
-__global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvArgs a) {
+// CX > 0: the launch also runs the block's 1x1 shortcut conv b (CX input
+// channels, over the compact block input: output pixel m reads its pixel m)
+// whose epilogue adds this conv's int8 output.  That output stays in the
+// waves' staging tiles and is never stored: after the main loop the conv's
+// epilogue leaves it there, the shortcut's GEMM (CX/64 steps, its operands
+// staged past the staging tiles; the first step's loads are issued before the
+// conv's epilogue runs) reuses the accumulators, and the shortcut's epilogue
+// reads its residual from the tiles.  The arithmetic of both epilogues is the
+// same as in two separate launches.
+template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int CX>
+__device__ __forceinline__ void conv3s2_phase_body(const ConvArgs& a, const ConvArgs& b) {
     constexpr int NW = WM * WN;
     constexpr int NT = NW * 64;
     constexpr int BM = WM * MI * 32, BN = WN * NJ * 32;
@@ -1234,7 +1284,18 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
     constexpr int RING_OFF = 2 * PBUF;
     constexpr int LDS_K = RING_OFF + NSTB * B_BYTES;
     constexpr int LDS_E = NW * wave_tile_bytes<MI, NJ>() + BN * FF_LUT_PITCH;
-    constexpr int LDS = LDS_K > LDS_E ? LDS_K : LDS_E;
+    // fused shortcut: its A operand (BM compact-input pixels at the patch
+    // pitch) and B operand (one 64-channel run of its weights) past the
+    // staging tiles; the BN table of the shortcut's epilogue goes over them
+    // once its GEMM is done
+    constexpr int A2_LOADS = (BM * (PATCH_PITCH / 16) + 63) / 64;
+    constexpr int LA2 = (A2_LOADS + NW - 1) / NW;
+    constexpr int A2_OFF = (NW * wave_tile_bytes<MI, NJ>() + 1023) / 1024 * 1024;
+    constexpr int B2_OFF = A2_OFF + A2_LOADS * 1024;
+    constexpr int LDS_SC = CX > 0 ? B2_OFF + B_BYTES : 0;
+    constexpr int LDS_KE = LDS_K > LDS_E ? LDS_K : LDS_E;
+    constexpr int LDS = LDS_KE > LDS_SC ? LDS_KE : LDS_SC;
+    static_assert(CX % DMA_KB == 0, "shortcut input channels: a multiple of 64");
     static_assert(H % 2 == 0 && W % 2 == 0, "even input");
     static_assert(CIN % DMA_KB == 0, "Cin must be a multiple of 64");
     static_assert(B_BYTES % 1024 == 0 && (B_PART || B_BYTES % (NT * 16) == 0), "whole wave loads");
@@ -1385,9 +1446,86 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvAr
 
     int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
     int8_t* Ls = smem + NW * wave_tile_bytes<MI, NJ>();
-    if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<NW, BN>(Ls, a.bn_lut, tn * BN);
-    wave_epilogue<COUT, MI, NJ, HO, WO>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
-                                Ls + (wn * NJ * 32) * FF_LUT_PITCH);
+    const int mrow0 = m0 + wm * MI * 32, ncol0 = tn * BN + wn * NJ * 32;
+    if constexpr (CX == 0) {
+        if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<NW, BN>(Ls, a.bn_lut, tn * BN);
+        wave_epilogue<COUT, MI, NJ, HO, WO>(acc, a, mrow0, ncol0, Ws, Ls + (wn * NJ * 32) * FF_LUT_PITCH);
+    } else {
+        // the conv's epilogue parameters before the shortcut's loads, so that
+        // waiting for them does not wait for those
+        const EpiParams<NJ> P1 = load_epi_params<COUT, NJ>(a, ncol0);
+        // shortcut operands of channel run c: A2 slot (pixel px, piece p) at
+        // 16*(5*px + p) (piece 4 unused: FF_OOB, zeros), pixels past the batch
+        // out of range (zeros); B2 as a weight ring slot.  (1x1 weights:
+        // stage c of the packing is channel run c.)
+        const __amdgpu_buffer_rsrc_t r_x2 = ff_rsrc(b.in, (unsigned)a.M * CX);
+        const __amdgpu_buffer_rsrc_t r_w2 = ff_rsrc(b.w, (unsigned)(CX / DMA_KB) * COUT * FF_KSTEP);
+        auto issue_sc = [&](int c) {
+#pragma unroll
+            for (int j = 0; j < LA2; j++) {
+                const int blk = j * NW + wave;
+                if (blk < A2_LOADS) {                        // (uniform per wave)
+                    const int slot = blk * 64 + lane;
+                    const int px = slot / 5;
+                    const int piece = slot - px * 5;
+                    const unsigned off = piece < 4 ? (unsigned)(m0 + px) * CX + piece * 16 : FF_OOB;
+                    bdma16(r_x2, off, (unsigned)(c * DMA_KB), smem + A2_OFF + blk * 1024);
+                }
+            }
+            if (loads_b) {
+#pragma unroll
+                for (int j = 0; j < B_LD; j++)
+                    bdma16(r_w2, (unsigned)b_off[j], (unsigned)(c * COUT * FF_KSTEP),
+                           smem + B2_OFF + (j * NW + wave) * 1024);
+            }
+        };
+        issue_sc(0);
+        wave_epi_pair_stage<COUT, MI, NJ, HO, WO>(acc, a, P1, mrow0, ncol0, Ws);
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+        const int a2_rd = A2_OFF + (wm * MI * 32 + (lane & 31)) * PATCH_PITCH + (lane >> 5) * 16;
+        const int b2_rd = B2_OFF + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
+#pragma unroll
+        for (int c = 0; c < CX / DMA_KB; c++) {
+            dma_wait_barrier<0>();                   // run c's operands landed
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                v4i af[MI], bf[NJ];
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+                    af[i] = *reinterpret_cast<const v4i*>(smem + a2_rd + i * 32 * PATCH_PITCH + ks * 32);
+#pragma unroll
+                for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(smem + ((b2_rd + j * 2048) ^ (ks * 32)));
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+            if (c + 1 < CX / DMA_KB) {
+                dma_wait_barrier<0>();               // every wave is done with run c
+                issue_sc(c + 1);
+            }
+        }
+        dma_wait_barrier<0>();                       // every wave is done with the operands
+        if (b.flags & FFK_EPI_BN) issue_bn_lut<NW, BN>(Ls, b.bn_lut, tn * BN);
+        wave_epi_pair_add<COUT, MI, NJ, HO, WO>(acc, b, mrow0, ncol0, Ws, Ls + (wn * NJ * 32) * FF_LUT_PITCH);
+    }
+}
+
+template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int WPE>
+__global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_phase_kernel(ConvArgs a) {
+    conv3s2_phase_body<CIN, COUT, H, W, WM, WN, MI, NJ, 0>(a, a);
+}
+
+// the stride-2 conv a and the 1x1 shortcut b that adds a's output, one launch
+template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int WPE, int CX>
+__global__ __launch_bounds__(WM * WN * 64, WPE) void conv3s2_shortcut_kernel(ConvArgs a, ConvArgs b) {
+    conv3s2_phase_body<CIN, COUT, H, W, WM, WN, MI, NJ, CX>(a, b);
 }
 
 namespace ps1 {

@@ -8,7 +8,7 @@ const ConvEntry kTable[] = {
     // 64 -> 128 at 56x56: one 64-channel run, so the patch kernel's single
     // input buffer fits two 256x128 workgroups per CU
     FF_P(64, 128, 56, 1),
-    FF_S2(128, 128, 56, FF_S2_SPLIT),
+    FF_S2(128, 128, 56, FF_S2_SPLIT, 64),
     FF_C128(64, 128, 1, 2, 56, 1),
     FF_P(128, 128, 28, FF_S2_SPLIT),
     FF_C128(64, 128, 1, 1, 28, 1),          // shortcut over the compact block input

@@ -6,7 +6,7 @@
 namespace {
 const ConvEntry kTable[] = {
     FF_P(128, 256, 28, FF_S2_SPLIT),
-    FF_S2(256, 256, 28, FF_S3S2_SPLIT),
+    FF_S2(256, 256, 28, FF_S3S2_SPLIT, 128),
     FF_CBIG(128, 256, 1, 2, 28, 1),
     FF_PB(256, 256, 14, FF_S3_SPLIT),
     FF_CBIG(128, 256, 1, 1, 14, 1),         // shortcut over the compact block input

@@ -6,7 +6,7 @@
 namespace {
 const ConvEntry kTable[] = {
     FF_PB(256, 512, 14, 3),
-    FF_S2(512, 512, 14, FF_S4_SPLIT),
+    FF_S2(512, 512, 14, FF_S4_SPLIT, 256),
     FF_CBIG(256, 512, 1, 2, 14, 1),
     FF_PB(512, 512, 7, FF_S4_SPLIT),
     FF_CBIG(256, 512, 1, 1, 7, 1),          // shortcut over the compact block input

@@ -6,7 +6,7 @@
 namespace {
 const ConvEntry kTable[] = {
     FF_P64(64, 64, 112, 1),
-    FF_S2_64(64, 64, 112, 1),
+    FF_S2_64(64, 64, 112, 1, 64),
     FF_C64(64, 64, 1, 2, 112, 1),
     FF_P64W(64, 64, 56, 1),
     // the 1x1 shortcut over a block input stored at its even pixels only

@@ -42,6 +42,16 @@ void launch_s2(const ConvArgs& a, int grid, hipStream_t s) {
                        dim3(WM * WN * 64), 0, s, a);
 }
 
+// A stride-2 conv and the 1x1 shortcut that adds its output, in one launch
+// (conv3s2_shortcut_kernel): the same tiles as launch_s2.
+typedef void (*launch_pair_fn)(const ConvArgs&, const ConvArgs&, int grid, hipStream_t);
+
+template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int WPE, int CX>
+void launch_s2_shortcut(const ConvArgs& a, const ConvArgs& b, int grid, hipStream_t s) {
+    hipLaunchKernelGGL((conv3s2_shortcut_kernel<CIN, COUT, H, H, WM, WN, MI, NJ, WPE, CX>), dim3(grid),
+                       dim3(WM * WN * 64), 0, s, a, b);
+}
+
 // Small-batch split-K tiling: 64x64 workgroup tiles (one 32x32 MFMA tile per
 // wave), the K stages of a tile shared by `split` workgroups.
 constexpr int FF_SM_BM = 64, FF_SM_BN = 64;
@@ -65,6 +75,8 @@ struct ConvEntry {
     const char* kind;   // name of `fn` (ffk_conv_variant)
     int mid_bm, mid_bn; // tile of `mid` when it is not 128x128
     const char* mid_kind;
+    int pair_cx;          // stride-2 layers: input channels of the 1x1 shortcut
+    launch_pair_fn pair;  // that `fn` runs fused with (conv3s2_shortcut_kernel), or none
 };
 
 // A grid of fewer big tiles than this leaves CUs idle; the 128x128 variant
@@ -227,19 +239,22 @@ constexpr launch_fn split_launch() {
 #ifndef FF_TS2_64
 #define FF_TS2_64 4, 1, 2, 2, 4
 #endif
-#define FF_S2ENTRY(CIN, COUT, H, SPLIT, MID, WM, WN, MI, NJ, WPE)                    \
+// CX: input channels of the block's 1x1 shortcut, which the phase kernel
+// can run fused (conv3s2_shortcut_kernel)
+#define FF_S2ENTRY(CIN, COUT, H, SPLIT, MID, CX, WM, WN, MI, NJ, WPE)                \
     {CIN, COUT, 3, 2, H, H, WM * MI * 32, WN * NJ * 32,                              \
      &launch_s2<CIN, COUT, H, WM, WN, MI, NJ, WPE>, SPLIT,                            \
-     split_launch<CIN, COUT, 3, 2, H, SPLIT>(), MID, "phase"}
-#define FF_S2ENTRY_K(CIN, COUT, H, SPLIT, MID, TILE) FF_S2ENTRY(CIN, COUT, H, SPLIT, MID, TILE)
+     split_launch<CIN, COUT, 3, 2, H, SPLIT>(), MID, "phase", 0, 0, nullptr,          \
+     CX, &launch_s2_shortcut<CIN, COUT, H, WM, WN, MI, NJ, WPE, CX>}
+#define FF_S2ENTRY_K(CIN, COUT, H, SPLIT, MID, CX, TILE) FF_S2ENTRY(CIN, COUT, H, SPLIT, MID, CX, TILE)
 #if FF_S2_PHASE
-#define FF_S2(CIN, COUT, H, SPLIT)                                                  \
+#define FF_S2(CIN, COUT, H, SPLIT, CX)                                              \
     FF_S2ENTRY_K(CIN, COUT, H, SPLIT,                                               \
-                 (&launch_conv<CIN, COUT, 3, 2, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>), FF_TS2)
-#define FF_S2_64(CIN, COUT, H, SPLIT) FF_S2ENTRY_K(CIN, COUT, H, SPLIT, nullptr, FF_TS2_64)
+                 (&launch_conv<CIN, COUT, 3, 2, H, H, 128, 128, FF_KB(CIN), FF_PF_MID(CIN), 2, 2, 2, 1>), CX, FF_TS2)
+#define FF_S2_64(CIN, COUT, H, SPLIT, CX) FF_S2ENTRY_K(CIN, COUT, H, SPLIT, nullptr, CX, FF_TS2_64)
 #else
-#define FF_S2(CIN, COUT, H, SPLIT) FF_CBIG(CIN, COUT, 3, 2, H, SPLIT)
-#define FF_S2_64(CIN, COUT, H, SPLIT) FF_C64(CIN, COUT, 3, 2, H, SPLIT)
+#define FF_S2(CIN, COUT, H, SPLIT, CX) FF_CBIG(CIN, COUT, 3, 2, H, SPLIT)
+#define FF_S2_64(CIN, COUT, H, SPLIT, CX) FF_C64(CIN, COUT, 3, 2, H, SPLIT)
 #endif
 
 #ifndef FF_S2_SPLIT

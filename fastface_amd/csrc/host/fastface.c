@@ -116,6 +116,7 @@ struct FastFace {
     int keep_all;
     int algo;                   /* FASTFACE_CONV_* of the 64-channel 3x3 s1 layers */
     int general_epi;            /* launch every conv with the general epilogue forms */
+    int no_fusion;              /* stride-2 convs and their shortcuts as two launches */
     GraphEntry graphs[FF_MAX_GRAPHS];
     int n_graphs, graph_rr;
     void* ev_last;              /* recorded after the last enqueue, on last_stream */
@@ -380,11 +381,28 @@ static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt, in
     return ffk_fc(&f, stream);
 }
 
+/* Steps s and s + 1 may run as one launch (ff_plan_pair: a stride-2 conv
+ * and the shortcut adding its output; the buffer plan keeps the first step's
+ * inputs out of the second's outputs); ffk_conv_s2_shortcut decides per
+ * batch.  Not with every tensor kept for debug reads. */
+static int pair_at(const FastFace* ff, int s)
+{
+    return !ff->keep_all && ff_plan_pair(&ff->plan, s);
+}
+
 /* the chain of `batch` faces as half `part`, its activations `off` bytes
  * into every buffer */
 static int run_part(FastFace* ff, int part, size_t off, int batch, void* stream, int fmt, int shared)
 {
     for (int s = 0; s < ff->plan.n_steps; s++) {
+        if (!ff->no_fusion && pair_at(ff, s)) {
+            ffk_conv_desc c, sc;
+            step_desc(ff, s, batch, fmt, part, off, shared, &c);
+            step_desc(ff, s + 1, batch, fmt, part, off, shared, &sc);
+            const int r = ffk_conv_s2_shortcut(&c, &sc, stream);
+            if (r < 0) return r;
+            if (r == 1) { s++; continue; }
+        }
         int rc = launch_step(ff, s, batch, stream, fmt, part, off, shared);
         if (rc) return rc;
     }
@@ -848,6 +866,19 @@ int fastface_set_conv_algo(FastFace* ff, int algo)
     const int cap = ff->capacity;
     free_activations(ff);
     ff->algo = algo;
+    return ensure_capacity(ff, cap > 0 ? cap : 1) ? -2 : n;
+}
+
+int fastface_set_shortcut_fusion(FastFace* ff, int on)
+{
+    if (!ff || (on != 0 && on != 1)) return -1;
+    int n = 0;
+    for (int s = 0; s < ff->plan.n_steps; s++) n += pair_at(ff, s);
+    if (on == !ff->no_fusion) return n;
+    if (drain(ff) || ffk_stream_sync(ff->stream)) return -2;
+    const int cap = ff->capacity;
+    free_activations(ff);                 /* (the captured chains hold the old launches) */
+    ff->no_fusion = !on;
     return ensure_capacity(ff, cap > 0 ? cap : 1) ? -2 : n;
 }
 

@@ -81,6 +81,10 @@ typedef struct {
 int  ff_plan_build(const FfModel* m, FfPlan* p);
 /* keep_all: one buffer per tensor (debug) */
 int  ff_plan_assign_buffers(FfPlan* p, int keep_all);
+/* 1 if step s is a 3x3 stride-2 conv whose output only step s + 1 reads, as
+ * the residual of its epilogue (a stage's 1x1 shortcut): the two may run as
+ * one launch.  Valid after ff_plan_assign_buffers. */
+int  ff_plan_pair(const FfPlan* p, int s);
 void ff_plan_free(FfPlan* p);
 
 #endif

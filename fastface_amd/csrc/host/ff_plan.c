@@ -338,6 +338,15 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
     return rc;
 }
 
+int ff_plan_pair(const FfPlan* p, int s)
+{
+    if (s < 0 || s + 1 >= p->n_steps) return 0;
+    const FfStep* a = &p->steps[s];
+    const FfStep* b = a + 1;
+    return a->kind == 1 && b->kind == 1 && a->kh == 3 && a->stride == 2 && a->t_bn < 0 && a->t_out >= 0 &&
+           b->t_add == a->t_out && b->t_in != a->t_out && p->tensors[a->t_out].last_use == s + 1;
+}
+
 int ff_plan_assign_buffers(FfPlan* p, int keep_all)
 {
     for (int t = 0; t < p->n_tensors; t++) {
@@ -393,11 +402,16 @@ int ff_plan_assign_buffers(FfPlan* p, int keep_all)
             else p->tensors[t].buf = n_buf++;
         }
         if (keep_all) continue;
+        /* A pair that may run as one launch (ff_plan_pair) releases the
+         * buffers its first step is done with only after the pair: the second
+         * step's outputs must not take a buffer the first step still reads. */
+        if (ff_plan_pair(p, s)) continue;
+        const int from = ff_plan_pair(p, s - 1) ? s - 1 : s;
         /* release what is dead after this step (inputs, and outputs never read) */
         for (int t = 1; t < p->n_tensors; t++) {
             FfTensor* T = &p->tensors[t];
             if (T->buf < 0) continue;
-            if (T->last_use == s) free_list[n_free++] = T->buf;
+            if (T->last_use >= from && T->last_use <= s) free_list[n_free++] = T->buf;
         }
     }
     free(free_list);

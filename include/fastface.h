@@ -116,6 +116,18 @@ int fastface_set_conv_algo(FastFace* ff, int algo);
  * reference, which has one form.) */
 int fastface_set_epilogue_forms(FastFace* ff, int general);
 
+/* Stride-2 blocks as one launch.  The last two convs of a stage's first
+ * block (the 3x3 stride-2 conv and the 1x1 shortcut whose epilogue adds its
+ * output) run as one kernel where the batch uses the large-tile kernels
+ * (ffk_conv_s2_shortcut): the conv's output stays on chip instead of going
+ * through memory.  on = 1 (the default) fuses them, 0 runs them as two
+ * launches.  Embeddings are the same bit for bit either way.  Returns the
+ * number of such step pairs in the plan, -1 on bad arguments, -2 on
+ * allocation failure.  Captured launch chains are rebuilt on next use.  (No
+ * counterpart in the reference, which runs the two ops one after the
+ * other.) */
+int fastface_set_shortcut_fusion(FastFace* ff, int on);
+
 /* ---------------- introspection (tests, bench) ---------------------------- */
 typedef struct {
     int kind;                 /* 1 conv, 2 FC                                   */

@@ -193,6 +193,20 @@ int    ffk_pack_conv_weights(const int8_t* w_oihw, int cout, int cin, int kh, in
  * workspace_bytes fields are not read. */
 size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d);
 int    ffk_conv(const ffk_conv_desc* d, void* stream);
+/* A block's 3x3 stride-2 conv `c` and its 1x1 shortcut `s` (run at stride 1
+ * over the compact block input, FFK_OUT_X_EVEN) whose residual is c's
+ * output (s->add_src == c->out), as one launch: the results of
+ * ffk_conv(c) then ffk_conv(s), bit for bit, except that c's output is
+ * never stored (the caller guarantees nothing else reads it).  The
+ * reference runs the two ops one after the other (libfastface.c:312-470,
+ * the shortcut's epilogue adding the SAVE_ID'd conv output,
+ * kernels/int8_epilogue.c:52-93); the fusion has no counterpart there.
+ * Served forms: c with bias only (no PReLU, residual, BN or in-scale), s
+ * with the residual add and optionally BN (no PReLU or in-scale), at the
+ * batches where c would run as the phase kernel.  Returns 1 when launched
+ * (or nothing to do), 0 when the pair is not served (nothing launched, no
+ * error set: run the two with ffk_conv), < 0 on an error. */
+int    ffk_conv_s2_shortcut(const ffk_conv_desc* c, const ffk_conv_desc* s, void* stream);
 /* ffk_conv without a caller workspace and without any allocation: no
  * counterpart in the reference.  For callers that cannot allocate device
  * memory -- code under HIP graph capture, tight serving loops, harnesses that

@@ -2,11 +2,14 @@
 
 Bar: bit-exact int32 accumulators and bit-exact int8 / fp32 outputs.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
 import fastface_amd as fa
 from conftest import rng
+import gpu_util
 from gpu_util import params_block, run_conv, run_fc
 
 pytestmark = pytest.mark.gpu
@@ -685,3 +688,94 @@ def test_patch_64_wide_tiles(gpu_lib, oracle, mode):
     assert np.array_equal(gx[idx], exp_x)
     assert np.array_equal(gb[idx], oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns,
                                                            bn_offset=bno, inv_pc=binv))
+
+
+# ---- a stride-2 conv and its 1x1 shortcut as one launch ----
+S2_PAIRS = [(64, 64, 112, 64), (128, 128, 56, 64), (256, 256, 28, 128), (512, 512, 14, 256)]
+
+
+def _pair_desc(lib, keep, B, cin, cout, k, s, pad, H, x, w, P, flags, out, out_bn=None, add=None):
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, k, k
+    d.stride, d.pad, d.hin, d.win = s, pad, H, H
+    for arr, field in ((x, "in_"), (gpu_util.pack_conv(lib, w), "w"), (P, "params")):
+        dv = gpu_util.Dev(lib, host=arr); keep.append(dv)
+        setattr(d, field, dv.ptr)
+    if flags & fa.FFK_EPI_BN:
+        dl = gpu_util.Dev(lib, host=gpu_util.make_bn_lut(lib, P)); keep.append(dl)
+        d.bn_lut = dl.ptr
+    d.out, d.out_bn, d.add_src = out, out_bn, add
+    d.flags = flags
+    d.in_scale = 1.0
+    return d
+
+
+@pytest.mark.parametrize("bn", [True, False], ids=["bn", "nobn"])
+@pytest.mark.parametrize("fast", [True, False], ids=["inrange", "general"])
+@pytest.mark.parametrize("cin,cout,H,cx", S2_PAIRS)
+def test_s2_shortcut_pair_equals_two_launches(gpu_lib, cin, cout, H, cx, fast, bn):
+    """ffk_conv_s2_shortcut: a block's 3x3 stride-2 conv and the 1x1 shortcut
+    whose epilogue adds its output (over the compact block input), as one
+    launch, give ffk_conv's X and BN(X) of the two launches bit for bit, at a
+    ragged batch of the large-tile kernel, on the in-range and the general
+    epilogue forms; forms and batches it does not serve return 0 and launch
+    nothing."""
+    lib = gpu_lib
+    r = rng(1300 + cin + H + cx + 2 * fast + bn)
+    B = _direct_batch(lib, cin, cout, 3, 2, H)
+    Ho = H // 2
+    x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, 3, 3), dtype=np.int8)
+    xc = r.integers(-128, 128, size=(B, Ho, Ho, cx), dtype=np.int8)
+    w2 = r.integers(-128, 128, size=(cout, cx, 1, 1), dtype=np.int8)
+    x[-1, -1, -1] = -128
+    w2[3] = 127
+    ws, bias, inv = _unsaturated_params(r, cout, 9 * cin)
+    ws[0], bias[0], inv[0] = 0.5, 0.0, 1.0 / 64          # exact .5 ties
+    P1 = params_block(cout, ws=ws, bias=bias, inv=inv)
+    ws2, bias2, inv2 = _unsaturated_params(r, cout, cx)
+    rows2 = dict(ws=ws2, bias=bias2, inv=inv2, adds=r.uniform(1e-3, 5e-2, cout).astype(F32))
+    if bn:
+        rows2.update(bn_sin=r.uniform(1e-3, 5e-2, cout).astype(F32), bn_s=r.uniform(0.5, 1.5, cout).astype(F32),
+                     bn_o=r.normal(0, 0.05, cout).astype(F32), bn_inv=(1.0 / r.uniform(0.01, 0.1, cout)).astype(F32))
+    P2 = params_block(cout, **rows2)
+    f1 = fa.FFK_EPI_BIAS
+    f2 = fa.FFK_EPI_BIAS | fa.FFK_EPI_ADD | (fa.FFK_EPI_BN if bn else 0)
+    if fast:
+        assert lib.ffk_requant_in_range(P1.ctypes.data, cout, 9 * cin, f1) == 1
+        assert lib.ffk_requant_in_range(P2.ctypes.data, cout, cx, f2) == 1
+        f1 |= fa.FFK_EPI_IN_RANGE
+        f2 |= fa.FFK_EPI_IN_RANGE
+
+    # two launches
+    R, _ = run_conv(lib, x, w, 2, 1, params=P1, flags=f1, split=False)
+    X_exp, BN_exp = run_conv(lib, xc, w2, 1, 0, params=P2, flags=f2, add=R, want_bn=bn, split=False)
+
+    # one launch
+    keep = []
+    n = B * Ho * Ho * cout
+    dR, dX = gpu_util.Dev(lib, nbytes=n), gpu_util.Dev(lib, nbytes=n)
+    dBN = gpu_util.Dev(lib, nbytes=n) if bn else None
+    keep += [dR, dX] + ([dBN] if bn else [])
+    c = _pair_desc(lib, keep, B, cin, cout, 3, 2, 1, H, x, w, P1, f1, dR.ptr)
+    sc = _pair_desc(lib, keep, B, cx, cout, 1, 1, 0, Ho, xc, w2, P2, f2, dX.ptr,
+                    out_bn=dBN.ptr if bn else None, add=dR.ptr)
+    assert lib.ffk_conv_variant(C.byref(c)) == b"phase"
+    gpu_util.check(lib, lib.ffk_zero(dX.ptr, n, None))
+    assert lib.ffk_conv_s2_shortcut(C.byref(c), C.byref(sc), None) == 1
+    gpu_util.check(lib, lib.ffk_stream_sync(None))
+    assert np.array_equal(dX.get(np.int8, (B, Ho, Ho, cout)), X_exp)
+    if bn:
+        assert np.array_equal(dBN.get(np.int8, (B, Ho, Ho, cout)), BN_exp)
+
+    # not served: a PReLU on the conv, a residual other than the conv's
+    # output, a batch the large tiles do not take (when the layer has one)
+    c.flags = f1 | fa.FFK_EPI_PRELU
+    assert lib.ffk_conv_s2_shortcut(C.byref(c), C.byref(sc), None) == 0
+    c.flags = f1
+    sc.add_src = dX.ptr
+    assert lib.ffk_conv_s2_shortcut(C.byref(c), C.byref(sc), None) == 0
+    sc.add_src = dR.ptr
+    c.batch = sc.batch = 1
+    if lib.ffk_conv_variant(C.byref(c)) != b"phase":
+        assert lib.ffk_conv_s2_shortcut(C.byref(c), C.byref(sc), None) == 0

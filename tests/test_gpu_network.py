@@ -260,6 +260,31 @@ def test_general_epilogue_forms(gpu_lib, synth_ffw4, oracle, oracle_model):
         f.close()
 
 
+def test_shortcut_fusion(gpu_lib, synth_ffw4, oracle, oracle_model):
+    """fastface_set_shortcut_fusion: each stage's stride-2 conv and 1x1
+    shortcut run as one launch (the default) or as two.  The plan has the
+    four pairs of IResNet-50; embeddings are bit-identical either way at 701
+    faces (two halves of 350 and 351, where every stage takes the large
+    tiles and so fuses) and at 9 faces (where none does), and equal the
+    oracle's on faces of both halves."""
+    f = fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT)
+    try:
+        x = synth.faces_uniform(701, 35)
+        fused = f.embed_batch(x)
+        small = f.embed_batch(x[:9])
+        assert gpu_lib.fastface_set_shortcut_fusion(f.ff, 0) == 4
+        assert np.array_equal(f.embed_batch(x), fused)
+        assert np.array_equal(f.embed_batch(x[:9]), small)
+        assert gpu_lib.fastface_set_shortcut_fusion(f.ff, 1) == 4
+        assert np.array_equal(f.embed_batch(x), fused)
+        idx = [0, 349, 350, 700]
+        exp, _ = oracle.forward(oracle_model, x[idx])
+        assert np.array_equal(fused[idx], exp)
+        assert gpu_lib.fastface_set_shortcut_fusion(f.ff, 2) == -1
+    finally:
+        f.close()
+
+
 def test_streamed_host_batch_equals_one_shot(ff, gpu_lib):
     """Host batches stream in chunks (copy of one chunk during the compute of
     the previous): 600 fp32 faces as 256 + 344, 2100 as 256 + 768 + 768 + 308

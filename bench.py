@@ -166,8 +166,9 @@ def main():
     ap.add_argument("--cpu-cooldown", type=float, default=1.0,
                     help="seconds between those runs (reference: 3)")
     ap.add_argument("--no-general-epilogue", action="store_true",
-                    help="skip the B=1024 leg with every conv on the general epilogue forms "
-                         "(--b1024-only skips it too)")
+                    help="skip the B=1024 legs with every conv on the general epilogue forms "
+                         "and with the stride-2 convs and shortcuts unfused (--b1024-only skips "
+                         "them too)")
     ap.add_argument("--no-winograd", action="store_true",
                     help="skip the config-5 run of the stage-1 layers as Winograd F(2,3)")
     args = ap.parse_args()
@@ -456,15 +457,12 @@ def main():
             raise RuntimeError("Winograd embeddings differ from the direct path")
         check(lib, lib.fastface_set_conv_algo(ff.ff, 0), "algo direct")
 
-    # the same chain with every conv on the general epilogue forms (the
-    # reference's compare/select PReLU and cvttps2dq emulation, which a model
-    # whose parameters do not prove the shorter forms runs): throughput, and
-    # embeddings bit-identical to the shorter forms'
-    general = None
-    if not args.no_general_epilogue and not args.b1024_only:
-        n_g = lib.fastface_set_epilogue_forms(ff.ff, 1)
-        if n_g < 0:
-            raise RuntimeError("fastface_set_epilogue_forms failed (%d)" % n_g)
+    # The B=1024 chain with a context switch flipped: throughput, and the
+    # embeddings, which must stay bit-identical to the default chain's.
+    def switched_leg(setter, value, restore, what):
+        n_l = setter(ff.ff, value)
+        if n_l < 0:
+            raise RuntimeError("%s: switch failed (%d)" % (what, n_l))
         for _ in range(3):
             step()
         check(lib, lib.ffk_stream_sync(stream), "sync")
@@ -474,19 +472,30 @@ def main():
             step()
         check(lib, lib.ffk_event_record(ev1, stream), "record")
         check(lib, lib.ffk_event_elapsed_ms(ev0, ev1, C.byref(ms)), "elapsed")
-        g_ms = ms.value / kg
-        out_g = np.empty((B, 512), np.float32)
-        check(lib, lib.ffk_memcpy_d2h(out_g.ctypes.data, d_out, out_g.nbytes, stream), "download")
+        l_ms = ms.value / kg
+        out_l = np.empty((B, 512), np.float32)
+        check(lib, lib.ffk_memcpy_d2h(out_l.ctypes.data, d_out, out_l.nbytes, stream), "download")
         check(lib, lib.ffk_stream_sync(stream), "sync")
-        same = bool(np.array_equal(out_g, out_direct))
-        general = {"launches": n_g, "faces_s": round(B / (g_ms * 1e-3), 1), "ms_per_step": round(g_ms, 4),
-                   "embeddings_equal_fast_forms": same}
-        log("B=%d general epilogue forms on %d launches: %.3f ms/step, %.0f faces/s, embeddings %s"
-            % (B, n_g, g_ms, general["faces_s"], "equal to the shorter forms'" if same else "DIFFERENT"))
+        same = bool(np.array_equal(out_l, out_direct))
+        log("B=%d %s (%d): %.3f ms/step, %.0f faces/s, embeddings %s"
+            % (B, what, n_l, l_ms, B / (l_ms * 1e-3), "equal to the default chain's" if same else "DIFFERENT"))
         if not same:
-            raise RuntimeError("general-form embeddings differ from the shorter forms'")
-        if lib.fastface_set_epilogue_forms(ff.ff, 0) < 0:      # (returns the launch count)
-            raise RuntimeError("fastface_set_epilogue_forms(0) failed: %s" % fastface_amd.last_error())
+            raise RuntimeError("%s: embeddings differ from the default chain's" % what)
+        if setter(ff.ff, restore) < 0:          # (returns a count)
+            raise RuntimeError("%s: restoring failed: %s" % (what, fastface_amd.last_error()))
+        return n_l, round(B / (l_ms * 1e-3), 1), round(l_ms, 4)
+
+    # every conv on the general epilogue forms (the reference's compare/select
+    # PReLU and cvttps2dq emulation, which a model whose parameters do not
+    # prove the shorter forms runs)
+    general = None
+    # each stage's stride-2 conv and 1x1 shortcut as two launches instead of one
+    separate = None
+    if not args.no_general_epilogue and not args.b1024_only:
+        n_g, f_g, m_g = switched_leg(lib.fastface_set_epilogue_forms, 1, 0, "general epilogue forms")
+        general = {"launches": n_g, "faces_s": f_g, "ms_per_step": m_g, "embeddings_equal_fast_forms": True}
+        n_p, f_p, m_p = switched_leg(lib.fastface_set_shortcut_fusion, 0, 1, "stride-2 convs and shortcuts unfused")
+        separate = {"pairs": n_p, "faces_s": f_p, "ms_per_step": m_p, "embeddings_equal_fused": True}
 
     # a second context in the same process: create, first b=1 embed (captures
     # its launch chain), destroy
@@ -557,6 +566,7 @@ def main():
                                "between HIP events on the launch stream"},
         "stage1_winograd": wino,
         "general_epilogue": general,
+        "unfused_shortcuts": separate,
         "cold_start": cold,
         "cpu_baseline": cpu,
     }

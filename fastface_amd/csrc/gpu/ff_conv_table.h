@@ -52,6 +52,13 @@ void launch_s2_shortcut(const ConvArgs& a, const ConvArgs& b, int grid, hipStrea
                        dim3(WM * WN * 64), 0, s, a, b);
 }
 
+// the fused launcher of a stride-2 layer, or none (CX = 0)
+template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int WPE, int CX>
+constexpr launch_pair_fn s2_pair() {
+    if constexpr (CX > 0) return &launch_s2_shortcut<CIN, COUT, H, WM, WN, MI, NJ, WPE, CX>;
+    else return nullptr;
+}
+
 // Small-batch split-K tiling: 64x64 workgroup tiles (one 32x32 MFMA tile per
 // wave), the K stages of a tile shared by `split` workgroups.
 constexpr int FF_SM_BM = 64, FF_SM_BN = 64;
@@ -240,12 +247,12 @@ constexpr launch_fn split_launch() {
 #define FF_TS2_64 4, 1, 2, 2, 4
 #endif
 // CX: input channels of the block's 1x1 shortcut, which the phase kernel
-// can run fused (conv3s2_shortcut_kernel)
+// runs fused (conv3s2_shortcut_kernel), or 0: never fused
 #define FF_S2ENTRY(CIN, COUT, H, SPLIT, MID, CX, WM, WN, MI, NJ, WPE)                \
     {CIN, COUT, 3, 2, H, H, WM * MI * 32, WN * NJ * 32,                              \
      &launch_s2<CIN, COUT, H, WM, WN, MI, NJ, WPE>, SPLIT,                            \
      split_launch<CIN, COUT, 3, 2, H, SPLIT>(), MID, "phase", 0, 0, nullptr,          \
-     CX, &launch_s2_shortcut<CIN, COUT, H, WM, WN, MI, NJ, WPE, CX>}
+     CX, s2_pair<CIN, COUT, H, WM, WN, MI, NJ, WPE, CX>()}
 #define FF_S2ENTRY_K(CIN, COUT, H, SPLIT, MID, CX, TILE) FF_S2ENTRY(CIN, COUT, H, SPLIT, MID, CX, TILE)
 #if FF_S2_PHASE
 #define FF_S2(CIN, COUT, H, SPLIT, CX)                                              \

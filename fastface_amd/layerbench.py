@@ -173,6 +173,89 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
             "frac_of_peak": round(ops / (per * 1e-3) / 5e15, 4)}
 
 
+def time_pair(lib, cin=64, cout=64, hin=112, cx=64, batch=1024, iters=10, fused=True):
+    """Mean time of a stage's stride-2 pair: the 3x3 stride-2 conv (bias, in-range
+    form) and the 1x1 shortcut over the compact block input (cx channels,
+    residual + BN, in-range form) whose residual is the conv's output, as one
+    launch (ffk_conv_s2_shortcut) or, fused=False, as two ffk_conv launches.
+    Seeded data as in time_layer; HIP events on the launch stream."""
+    ho = hin // 2
+    r = np.random.default_rng(1)
+    x = r.integers(-127, 128, size=(batch, hin, hin, cin), dtype=np.int8)
+    xc = r.integers(-127, 128, size=(batch, ho, ho, cx), dtype=np.int8)
+    held = []
+
+    def dev(arr=None, nbytes=None):
+        n = arr.nbytes if arr is not None else nbytes
+        p = lib.ffk_malloc(n)
+        if not p:
+            raise MemoryError(fa.last_error())
+        held.append(p)
+        if arr is not None:
+            lib.ffk_memcpy_h2d(p, arr.ctypes.data, n, None)
+        return p
+
+    def desc(ci, k, s, h, inp, flags):
+        w = r.integers(-127, 128, size=(cout, ci, k, k), dtype=np.int8)
+        packed = np.empty(lib.ffk_conv_packed_bytes(ci, cout, k, k), np.int8)
+        lib.ffk_pack_conv_weights(w.ctypes.data, cout, ci, k, k, packed.ctypes.data)
+        P = np.zeros((fa.FFK_NPARAM, cout), np.float32)
+        P[fa.FFK_P_WS] = r.uniform(1e-3, 1e-2, cout)
+        P[fa.FFK_P_BIAS] = r.normal(0, 0.1, cout)
+        P[fa.FFK_P_ADDSCALE] = 0.02
+        P[fa.FFK_P_INV] = 1.0 / 40.0
+        P[fa.FFK_P_BN_SIN], P[fa.FFK_P_BN_S], P[fa.FFK_P_BN_INV] = 0.02, 1.0, 50.0
+        assert lib.ffk_requant_in_range(P.ctypes.data, cout, k * k * ci, flags) == 1
+        d = fa.ffk_conv_desc()
+        d.batch, d.cin, d.cout, d.kh, d.kw = batch, ci, cout, k, k
+        d.stride, d.pad, d.hin, d.win = s, k // 2, h, h
+        d.in_, d.w, d.params = inp, dev(packed), dev(P)
+        d.flags = flags | fa.FFK_EPI_IN_RANGE
+        if flags & fa.FFK_EPI_BN:
+            lut = np.empty((cout, 256), np.int8)
+            rows = [np.ascontiguousarray(P[i]) for i in (fa.FFK_P_BN_SIN, fa.FFK_P_BN_S,
+                                                           fa.FFK_P_BN_O, fa.FFK_P_BN_INV)]
+            lib.ffk_make_bn_lut(rows[0].ctypes.data, rows[1].ctypes.data, rows[2].ctypes.data,
+                                rows[3].ctypes.data, cout, lut.ctypes.data)
+            d.bn_lut = dev(lut)
+        return d
+    n_out = batch * ho * ho * cout
+    c = desc(cin, 3, 2, hin, dev(x), fa.FFK_EPI_BIAS)
+    c.out = dev(nbytes=n_out)
+    sc = desc(cx, 1, 1, ho, dev(xc), fa.FFK_EPI_BIAS | fa.FFK_EPI_ADD | fa.FFK_EPI_BN)
+    sc.add_src, sc.out, sc.out_bn = c.out, dev(nbytes=n_out), dev(nbytes=n_out)
+    stream = C.c_void_p()
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    lib.ffk_stream_create(C.byref(stream))
+    lib.ffk_event_create(C.byref(e0))
+    lib.ffk_event_create(C.byref(e1))
+    ms = C.c_float()
+
+    def run():
+        if fused:
+            assert lib.ffk_conv_s2_shortcut(C.byref(c), C.byref(sc), stream) == 1, "pair not served"
+        else:
+            assert lib.ffk_conv(C.byref(c), stream) == 0, fa.last_error()
+            assert lib.ffk_conv(C.byref(sc), stream) == 0, fa.last_error()
+    try:
+        for _ in range(3):
+            run()
+        lib.ffk_event_record(e0, stream)
+        for _ in range(iters):
+            run()
+        lib.ffk_event_record(e1, stream)
+        assert lib.ffk_event_elapsed_ms(e0, e1, C.byref(ms)) == 0, fa.last_error()
+    finally:
+        lib.ffk_stream_sync(stream)
+        lib.ffk_event_destroy(e0)
+        lib.ffk_event_destroy(e1)
+        lib.ffk_stream_destroy(stream)
+        for p in held:
+            lib.ffk_free(p)
+    return {"pair": "%d->%d k3 s2 @%d + %d->%d k1 shortcut" % (cin, cout, hin, cx, cout), "batch": batch,
+            "fused": fused, "ms": round(ms.value / iters, 5)}
+
+
 def time_fc(lib, batch=1, iters=50):
     """Mean launch time of the FC head 25088 -> 512 at `batch` faces (the
     path and split-K workspace ffk_fc chooses; HIP events on the launch
@@ -252,6 +335,10 @@ def main():
                     help="give no split-K workspace (small batches then use the whole-K tiling)")
     ap.add_argument("--fc", action="store_true",
                     help="instead: the FC head 25088 -> 512 at --batch faces")
+    ap.add_argument("--pair-cx", type=int, default=0,
+                    help="instead: the stride-2 conv (--cin/--cout/--hin, k3 s2) and its 1x1 shortcut "
+                         "over this many compact input channels, as one launch")
+    ap.add_argument("--unfused", action="store_true", help="with --pair-cx: as two launches")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="instead: device-to-device copies of this many MiB (the calibration "
                          "workload for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -269,6 +356,10 @@ def main():
         return
     if a.fc:
         print(json.dumps(time_fc(lib, a.batch, a.iters)), flush=True)
+        return
+    if a.pair_cx:
+        print(json.dumps(time_pair(lib, a.cin, a.cout, a.hin, a.pair_cx, a.batch, a.iters,
+                                   fused=not a.unfused)), flush=True)
         return
     try:
         res = time_layer(lib, a.cin, a.cout, a.k, a.stride, a.hin, a.batch, a.iters, a.epi,

@@ -264,8 +264,8 @@ def test_shortcut_fusion(gpu_lib, synth_ffw4, oracle, oracle_model):
     """fastface_set_shortcut_fusion: each stage's stride-2 conv and 1x1
     shortcut run as one launch (the default) or as two.  The plan has the
     four pairs of IResNet-50; embeddings are bit-identical either way at 701
-    faces (two halves of 350 and 351, where every stage takes the large
-    tiles and so fuses) and at 9 faces (where none does), and equal the
+    faces (two halves of 350 and 351, where stages 1-3 take the large tiles
+    and so fuse) and at 9 faces (where only stage 1 does), and equal the
     oracle's on faces of both halves."""
     f = fa.FastFace(synth_ffw4, cwd=synth.REPO_ROOT)
     try:

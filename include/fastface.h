@@ -118,7 +118,8 @@ int fastface_set_epilogue_forms(FastFace* ff, int general);
 
 /* Stride-2 blocks as one launch.  The last two convs of a stage's first
  * block (the 3x3 stride-2 conv and the 1x1 shortcut whose epilogue adds its
- * output) run as one kernel where the batch uses the large-tile kernels
+ * output) run as one kernel where one is compiled for the layer (IResNet
+ * stages 1-3) and the batch uses the large-tile kernels
  * (ffk_conv_s2_shortcut): the conv's output stays on chip instead of going
  * through memory.  on = 1 (the default) fuses them, 0 runs them as two
  * launches.  Embeddings are the same bit for bit either way.  Returns the

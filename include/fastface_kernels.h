@@ -202,8 +202,9 @@ int    ffk_conv(const ffk_conv_desc* d, void* stream);
  * the shortcut's epilogue adding the SAVE_ID'd conv output,
  * kernels/int8_epilogue.c:52-93); the fusion has no counterpart there.
  * Served forms: c with bias only (no PReLU, residual, BN or in-scale), s
- * with the residual add and optionally BN (no PReLU or in-scale), at the
- * batches where c would run as the phase kernel.  Returns 1 when launched
+ * with the residual add and optionally BN (no PReLU or in-scale), for the
+ * stride-2 layers at 112, 56 and 28 pixels, at the batches where c would
+ * run as the phase kernel.  Returns 1 when launched
  * (or nothing to do), 0 when the pair is not served (nothing launched, no
  * error set: run the two with ffk_conv), < 0 on an error. */
 int    ffk_conv_s2_shortcut(const ffk_conv_desc* c, const ffk_conv_desc* s, void* stream);

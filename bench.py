@@ -95,8 +95,9 @@ def cpu_baseline(ffw, runs=5, cooldown=1.0):
     and the reference's stable protocol for b=1 (bench_stable_int8_ffw4.py:7-13:
     repeated runs of fastface_int8 with a cooldown between them, median of
     the runs' best) with `runs` runs and `cooldown` seconds instead of its 20
-    and 3 s, so that the default bench stays within minutes.  About 30 s of
-    CPU work.  Falls back to the C restatement when the host lacks AVX-VNNI
+    and 3 s, so that the default bench stays within minutes, on 8 threads and
+    on all physical cores (at most 16: the GPU box's CPU share per GPU).
+    About 40 s of CPU work.  Falls back to the C restatement when the host lacks AVX-VNNI
     (the reference build would SIGILL)."""
     from oracle.oracle import host_has_avx_vnni
     cpu = host_cpu()
@@ -120,20 +121,25 @@ def cpu_baseline(ffw, runs=5, cooldown=1.0):
             if b8:
                 rec["value_8_threads"] = b8[0]
             if os.path.exists(exe1):
-                b1 = []
-                for i in range(runs):
-                    if i:
-                        time.sleep(cooldown)
-                    r1 = _ref_best(exe1, [ffw], 8, env)
-                    if r1:
-                        b1.append(r1[1])
-                if b1:
-                    rec["b1_ms_8_threads"] = min(b1)
-                    rec["b1_stable_8_threads"] = {
-                        "runs": len(b1), "cooldown_s": cooldown, "median_ms": round(statistics.median(b1), 3),
-                        "min_ms": round(min(b1), 3), "max_ms": round(max(b1), 3),
-                        "protocol": "bench_stable_int8_ffw4.py:7-13 (median of runs, each the binary's "
-                                    "best of 5x30), %d runs / %.1f s cooldown instead of 20 / 3 s" % (len(b1), cooldown)}
+                # b=1 on the reference's default 8 threads and on all physical
+                # cores (BASELINE.md's two thread counts)
+                for threads, tag in ((8, "8_threads"), (cores, "all_cores")):
+                    b1 = []
+                    for i in range(runs):
+                        if i:
+                            time.sleep(cooldown)
+                        r1 = _ref_best(exe1, [ffw], threads, env)
+                        if r1:
+                            b1.append(r1[1])
+                    if b1:
+                        rec["b1_ms_" + tag] = min(b1)
+                        rec["b1_stable_" + tag] = {
+                            "threads": threads, "runs": len(b1), "cooldown_s": cooldown,
+                            "median_ms": round(statistics.median(b1), 3),
+                            "min_ms": round(min(b1), 3), "max_ms": round(max(b1), 3),
+                            "protocol": "bench_stable_int8_ffw4.py:7-13 (median of runs, each the binary's "
+                                        "best of 5x30), %d runs / %.1f s cooldown instead of 20 / 3 s"
+                                        % (len(b1), cooldown)}
             return rec
     from fastface_amd import synth
     from oracle.oracle import Oracle
@@ -149,6 +155,13 @@ def cpu_baseline(ffw, runs=5, cooldown=1.0):
             "sample": "oracle/ff_oracle.c forward of 4 synthetic faces", "host": cpu, "compiler": compiler}
 
 
+def profiler_preloaded():
+    """True when a rocprofv3 tool library is loaded into this process (its
+    preload or its ROCPROF* settings in the environment)."""
+    return ("rocprof" in os.environ.get("LD_PRELOAD", "")
+            or any(k.startswith("ROCPROF") for k in os.environ))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,9 +171,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-reps", type=int, default=3)
     ap.add_argument("--b1024-only", action="store_true",
-                    help="time only the B=%d chain, its per-step profile and the Winograd leg "
-                         "(the rocprofv3 kernel-statistics run: b=1, B=8, the config-2 layer and "
-                         "the host-buffer rates are left out)" % 1024)
+                    help="time only the B=%d chain, its per-step profile, the dominant-kernel "
+                         "timing and the Winograd leg (the rocprofv3 kernel-statistics run: b=1, "
+                         "B=8, the config-2 layer, the host-buffer rates, the switched-chain legs "
+                         "and the cold-start leg are left out; implied when a profiler is "
+                         "preloaded)" % 1024)
     ap.add_argument("--cpu-runs", type=int, default=5,
                     help="runs of the reference's b=1 binary in its stable protocol (reference: 20)")
     ap.add_argument("--cpu-cooldown", type=float, default=1.0,
@@ -172,6 +187,14 @@ def main():
     ap.add_argument("--no-winograd", action="store_true",
                     help="skip the config-5 run of the stage-1 layers as Winograd F(2,3)")
     args = ap.parse_args()
+    # Under the rocprofv3 kernel tracer the default run once ended with a host
+    # segmentation fault inside the tracer at the first launch of the B=8
+    # graph (the same run completes without the tracer).  A traced run
+    # therefore takes only the B=1024 legs.
+    profiled = profiler_preloaded()
+    if profiled and not args.b1024_only:
+        log("profiler preloaded: running the B=1024 legs only (as --b1024-only)")
+        args.b1024_only = True
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the path is per-face data "
               "parallel: N GPUs would each run their own context on a slice of the batch, "
@@ -499,20 +522,21 @@ def main():
 
     # a second context in the same process: create, first b=1 embed (captures
     # its launch chain), destroy
-    t_c = time.perf_counter()
-    ff2 = fastface_amd.FastFace(ffw, cwd=ROOT)
-    create_ms = (time.perf_counter() - t_c) * 1e3
-    t_e = time.perf_counter()
-    ff2.embed(x1[0] if x1.ndim == 4 else x1)
-    first_embed_ms = (time.perf_counter() - t_e) * 1e3
-    ff2.close()
-    cold = {"first_create_ms": round(first_create_ms, 1), "create_ms": round(create_ms, 1),
-            "first_embed_ms": round(first_embed_ms, 2),
-            "note": "first_create: the process's first fastface_create (HIP runtime start-up "
+    cold = {"first_create_ms": round(first_create_ms, 1)}
+    if not args.b1024_only:
+        t_c = time.perf_counter()
+        ff2 = fastface_amd.FastFace(ffw, cwd=ROOT)
+        create_ms = (time.perf_counter() - t_c) * 1e3
+        t_e = time.perf_counter()
+        ff2.embed(x1[0] if x1.ndim == 4 else x1)
+        first_embed_ms = (time.perf_counter() - t_e) * 1e3
+        ff2.close()
+        cold.update(create_ms=round(create_ms, 1), first_embed_ms=round(first_embed_ms, 2))
+        log("cold start: first create %.1f ms, create %.1f ms, first embed %.2f ms"
+            % (first_create_ms, create_ms, first_embed_ms))
+    cold["note"] = ("first_create: the process's first fastface_create (HIP runtime start-up "
                     "included); create: a second context; first_embed: its first b=1 embed "
-                    "(launch chain captured)"}
-    log("cold start: first create %.1f ms, create %.1f ms, first embed %.2f ms"
-        % (first_create_ms, create_ms, first_embed_ms))
+                    "(launch chain captured)")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -568,6 +592,7 @@ def main():
         "general_epilogue": general,
         "unfused_shortcuts": separate,
         "cold_start": cold,
+        "profiler_preloaded": profiled,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -125,6 +125,7 @@ EXPORTS = [
     ("ffk_make_rgb8_lut", C.c_int, [_p, _p]),
     ("ffk_fc_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("ffk_pack_fc_weights", C.c_int, [_p, C.c_int, C.c_int, _p]),
+    ("ffk_pack_fc_row", C.c_int, [_p, C.c_int, C.c_int, C.c_int, _p]),
     ("ffk_fc", C.c_int, [C.POINTER(ffk_fc_desc), _p]),
     ("ffk_fc_workspace_bytes", C.c_size_t, [C.POINTER(ffk_fc_desc)]),
     ("ffk_selftest_mfma", C.c_int, []),

@@ -16,20 +16,37 @@ import numpy as np
 from . import FASTFACE_INPUT_N, FASTFACE_OUTPUT_N, load
 
 
+def scale_paths(cwd: str, environ=None) -> tuple:
+    """The OPSC and OPSC2 files fastface_create would open with `cwd` as the
+    working directory (libfastface.c:236-240): models/op_scales.bin, and
+    $OPSC2_PATH or models/op_scales_v2.bin, relative paths taken relative to
+    `cwd`."""
+    environ = os.environ if environ is None else environ
+    opsc = os.path.join(cwd, "models", "op_scales.bin")
+    env2 = environ.get("OPSC2_PATH")
+    if env2:
+        opsc2 = env2 if os.path.isabs(env2) else os.path.join(cwd, env2)
+    else:
+        opsc2 = os.path.join(cwd, "models", "op_scales_v2.bin")
+    return opsc, opsc2
+
+
 class FastFace:
     def __init__(self, weights: str = "models/w600k_r50_ffw4.bin", batch: int = 1,
-                 cwd: str | None = None):
+                 cwd: str | None = None, scale_files: tuple | None = None):
         """`cwd`: directory holding models/op_scales.bin and
         models/op_scales_v2.bin (fastface_create opens them relative to the
         working directory, like the reference; with `cwd` they are named
         explicitly instead, so the process's working directory is left alone
-        and contexts can be created on several threads)."""
+        and contexts can be created on several threads).  `scale_files`:
+        (OPSC path, OPSC2 path) named directly instead; an OPSC2 path that
+        does not exist runs the model on the OPSC per-tensor scales, as the
+        reference does without that file."""
         self.lib = load()
         self.batch = int(batch)
         w = os.path.abspath(weights).encode()
-        if cwd:
-            opsc = os.path.join(cwd, "models", "op_scales.bin")
-            opsc2 = os.environ.get("OPSC2_PATH") or os.path.join(cwd, "models", "op_scales_v2.bin")
+        if cwd or scale_files:
+            opsc, opsc2 = scale_files if scale_files else scale_paths(cwd)
             self.ff = self.lib.fastface_create_with_scales(w, opsc.encode(), opsc2.encode())
         else:
             self.ff = self.lib.fastface_create(w)

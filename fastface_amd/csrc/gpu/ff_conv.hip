@@ -35,8 +35,10 @@
 // bit-exactly on the host, ffk_make_bn_lut).
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "ff_conv_table.h"
 
@@ -190,20 +192,21 @@ int ffk_pack_conv_weights(const int8_t* w, int cout, int cin, int kh, int kw, in
         ffk_set_error("pack_conv_weights: bad arguments%s%s", nullptr, nullptr);
         return FFK_ERR_ARG;
     }
-    const int ktot = kh * kw * cin;
+    // Per output channel: its OIHW weights (cin x taps, read in order)
+    // transposed into reduction order k = tap*cin + ci, zero-padded to whole
+    // K steps, then each 64-byte K step copied to its place in the packed
+    // [step][cout][64] layout.
+    const int taps = kh * kw;
+    const int ktot = taps * cin;
     const int steps = (ktot + FF_KSTEP - 1) / FF_KSTEP;
-    for (int s = 0; s < steps; s++)
-        for (int n = 0; n < cout; n++)
-            for (int kk = 0; kk < FF_KSTEP; kk++) {
-                const int k = s * FF_KSTEP + kk;
-                int8_t v = 0;
-                if (k < ktot) {
-                    const int tap = k / cin, ci = k - tap * cin;
-                    const int y = tap / kw, x = tap - y * kw;
-                    v = w[(((size_t)n * cin + ci) * kh + y) * kw + x];
-                }
-                packed[((size_t)s * cout + n) * FF_KSTEP + kk] = v;
-            }
+    std::vector<int8_t> row((size_t)steps * FF_KSTEP, 0);
+    for (int n = 0; n < cout; n++) {
+        const int8_t* src = w + (size_t)n * ktot;
+        for (int ci = 0; ci < cin; ci++)
+            for (int t = 0; t < taps; t++) row[(size_t)t * cin + ci] = src[(size_t)ci * taps + t];
+        for (int s = 0; s < steps; s++)
+            memcpy(packed + ((size_t)s * cout + n) * FF_KSTEP, row.data() + (size_t)s * FF_KSTEP, FF_KSTEP);
+    }
     return FFK_OK;
 }
 

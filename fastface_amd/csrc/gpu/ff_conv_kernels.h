@@ -76,22 +76,6 @@ __device__ __forceinline__ void dma16(const int8_t* g, int8_t* lds_wave_base) {
 // the uniform part stays in a scalar register.
 constexpr unsigned FF_OOB = 0x80000000u;
 
-// Per-workgroup phase timestamps, compiled in only by the phase probe
-// (fastface_amd/csrc/probe/ff_phase_probe.hip defines FF_PHASE_STAMPS as the
-// number of workgroups it records): slot i of workgroup b holds the 100 MHz
-// real-time counter when wave 0 passed point i (0 entry, 1 first barrier of
-// the main loop, 2 main loop done, 3 epilogue start, 4 end).
-#ifdef FF_PHASE_STAMPS
-__device__ unsigned long long ff_phase_stamps[5 * FF_PHASE_STAMPS];
-#define FF_STAMP(i)                                                                        \
-    do {                                                                                   \
-        if (threadIdx.x == 0 && blockIdx.x < FF_PHASE_STAMPS)                              \
-            ff_phase_stamps[blockIdx.x * 5 + (i)] = __builtin_amdgcn_s_memrealtime();      \
-    } while (0)
-#else
-#define FF_STAMP(i) do { } while (0)
-#endif
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ff_rsrc(const void* base, unsigned bytes) {
     // raw (stride 0) buffer, 32-bit data format: the range check is offset < bytes
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
@@ -936,7 +920,6 @@ constexpr int PATCH_PITCH = 80;
 
 template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int WPE>
 __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs a) {
-    FF_STAMP(0);
     constexpr int NW = WM * WN;
     constexpr int NT = NW * 64;
     constexpr int BM = WM * MI * 32, BN = WN * NJ * 32;
@@ -1110,7 +1093,6 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
                 if ((t == 1 || t == 2) && more) dma_wait_barrier<LA>();
                 else dma_wait_barrier<0>();
             }
-            if (c == 0 && t == 0) FF_STAMP(1);
             if (t + 2 < 9) issue_b(c, t + 2, (t + 2) % NSTB);
             else if (more) issue_b(c + 1, t + 2 - 9, (t + 2) % NSTB);
             if (t == 0 && more) issue_patch(c + 1, 1 - PB);
@@ -1142,15 +1124,12 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
         if constexpr (NPB == 2) run(c + 1, std::integral_constant<int, 1>{});
     }
     __syncthreads();                       // every wave is done with the patch and the ring
-    FF_STAMP(2);
-    FF_STAMP(3);
 
     int8_t* Ws = smem + wave * wave_tile_bytes<MI, NJ>();
     int8_t* Ls = smem + NW * wave_tile_bytes<MI, NJ>();
     if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<NW, BN>(Ls, a.bn_lut, tn * BN);
     wave_epilogue<COUT, MI, NJ, H, W>(acc, a, m0 + wm * MI * 32, tn * BN + wn * NJ * 32, Ws,
                                 Ls + (wn * NJ * 32) * FF_LUT_PITCH);
-    FF_STAMP(4);
 }
 
 // ---------------------------------------------------------------------------
@@ -1598,7 +1577,6 @@ struct Plan {
 // ---------------------------------------------------------------------------
 template <int CIN, int COUT, int H, int W, int WM, int WN, int MI, int NJ, int KG, int WPE, int D, int U>
 __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(ConvArgs a) {
-    FF_STAMP(0);
     constexpr int NWG = WM * WN;                             // waves per group
     constexpr int NW = NWG * KG;
     constexpr int NTG = NWG * 64;
@@ -1764,7 +1742,6 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
             constexpr int k = s / U;
             if (loads_b) dma_wait_barrier<PLAN.wait[k]>();
             else dma_wait_barrier<PLAN.wait_p[k]>();
-            if constexpr (k == 0) FF_STAMP(1);
             // the weights D steps ahead (into the slots of steps s-U .. s-1),
             // then the next run's patch where one is due
             s2::static_for<0, U>([&](auto ic) {
@@ -1795,7 +1772,6 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
         }
     });
     __syncthreads();                       // every wave is done with the patches and rings
-    FF_STAMP(2);
 
     if constexpr (KG > 1) {
         // Block k (owner group o = k / TO) of wave position wg: the partial of
@@ -1859,13 +1835,11 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
             }
         }
     }
-    FF_STAMP(3);
     int8_t* Ws = smem + wave * wave_tile_bytes<MO, NO>();
     int8_t* Ls = smem + NW * wave_tile_bytes<MO, NO>();
     if (a.flags & FFK_EPI_BN && !a.out_i32) issue_bn_lut<NW, BN>(Ls, a.bn_lut, tn * BN);
     wave_epilogue_p<COUT, MO, NO, H, W>(own, a, prm, m0 + wm * MI * 32 + i0 * 32, tn * BN + ncol, Ws,
                                         Ls + ncol * FF_LUT_PITCH);
-    FF_STAMP(4);
 }
 
 // ---------------------------------------------------------------------------

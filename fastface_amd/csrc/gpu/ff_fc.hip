@@ -9,6 +9,7 @@
 // activation rows come from L2.  Cross-lane and then cross-wave (LDS) sums
 // give the exact dot product per face.  Larger batches use the MFMA conv
 // kernel as a 1x1 GEMM (ff_conv.hip).
+#include <cstring>
 #include "ff_internal.h"
 #include "ff_numerics.h"
 
@@ -123,11 +124,17 @@ int ffk_pack_fc_weights(const int8_t* w, int n, int k, int8_t* packed) {
         ffk_set_error("pack_fc_weights: bad arguments (k must be a multiple of 64)%s%s", nullptr, nullptr);
         return FFK_ERR_ARG;
     }
-    const int steps = k / FF_KSTEP;
-    for (int s = 0; s < steps; s++)
-        for (int r = 0; r < n; r++)
-            for (int kk = 0; kk < FF_KSTEP; kk++)
-                packed[((size_t)s * n + r) * FF_KSTEP + kk] = w[(size_t)r * k + s * FF_KSTEP + kk];
+    for (int r = 0; r < n; r++) ffk_pack_fc_row(w + (size_t)r * k, n, k, r, packed);
+    return FFK_OK;
+}
+
+int ffk_pack_fc_row(const int8_t* row, int n, int k, int r, int8_t* packed) {
+    if (!row || !packed || n <= 0 || k <= 0 || (k % FF_KSTEP) != 0 || r < 0 || r >= n) {
+        ffk_set_error("pack_fc_row: bad arguments (k must be a multiple of 64)%s%s", nullptr, nullptr);
+        return FFK_ERR_ARG;
+    }
+    for (int s = 0; s < k / FF_KSTEP; s++)
+        memcpy(packed + ((size_t)s * n + r) * FF_KSTEP, row + (size_t)s * FF_KSTEP, FF_KSTEP);
     return FFK_OK;
 }
 

@@ -104,7 +104,7 @@ __device__ __forceinline__ int32_t quant_input(float x, float inv) {
     return q;
 }
 
-// FC output (gemm_int8_matvec.c:438, contracted by GCC):
+// FC output (gemm_int8_matvec.c:79, contracted by GCC):
 //   out = fma(RN((float)dot * a_scale), ws, bias)
 __device__ __forceinline__ float fc_out(int32_t dot, float a_scale, float ws, float bias) {
     float t = (float)dot * a_scale;

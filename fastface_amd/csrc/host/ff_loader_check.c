@@ -5,11 +5,18 @@
  * It needs no GPU: the planner's packing and table helpers are host
  * functions of the library.
  *
- *   ff_loader_check <weights.ffw> <op_scales.bin> [<op_scales_v2.bin> | -]
+ *   ff_loader_check <weights.ffw> <op_scales.bin> [<op_scales_v2.bin> | -] [<dump>]
  *
  * Prints "load <rc> version <v> ops <n> v2 <has_v2>" and, when the load
- * succeeded, "plan <rc> steps <n> buffers <n> weights <bytes>"; exits 0 (a
- * sanitizer finding aborts with its report and a non-zero status). */
+ * succeeded, "plan <rc> steps <n> buffers <n> weights <bytes>" and
+ * "pairs <n> overlaps <n>": the steps that may run fused with the next one
+ * (ff_plan_pair: a stride-2 conv and the shortcut adding its output, one
+ * launch) and how many of them let the second step write a buffer the pair
+ * still reads (its own input, the first step's input or output), which must
+ * be none; exits 0 (a sanitizer finding aborts with its report and a
+ * non-zero status).  With <dump>, the plan's weight arena goes to <dump>.bin
+ * and, one line per region, "conv|wino|bn|fc <op> <offset> <bytes>" to
+ * <dump>.txt, and the parameter arena to <dump>.params.bin. */
 #include <stdio.h>
 #include <string.h>
 
@@ -32,6 +39,51 @@ int main(int argc, char** argv)
     if (!prc) ff_plan_assign_buffers(&p, 0);
     printf("plan %d steps %d buffers %d weights %zu%s%s\n", prc, prc ? 0 : p.n_steps,
            prc ? 0 : p.n_buffers, prc ? (size_t)0 : p.w_bytes, prc ? " err " : "", prc ? p.err : "");
+    if (!prc) {
+        int pairs = 0, overlaps = 0;
+        for (int s = 0; s < p.n_steps; s++) {
+            if (!ff_plan_pair(&p, s)) continue;
+            const FfStep* a = &p.steps[s];
+            const FfStep* b = &p.steps[s + 1];
+            const int reads[3] = { a->t_in, b->t_in, a->t_out };
+            const int writes[2] = { b->t_out, b->t_bn };
+            pairs++;
+            for (int w = 0; w < 2; w++)
+                for (int r = 0; r < 3; r++)
+                    if (writes[w] >= 0 && reads[r] >= 0 &&
+                        p.tensors[writes[w]].buf == p.tensors[reads[r]].buf)
+                        overlaps++;
+        }
+        printf("pairs %d overlaps %d\n", pairs, overlaps);
+    }
+    if (!prc && argc > 4) {
+        char path[4096];
+        snprintf(path, sizeof path, "%s.bin", argv[4]);
+        FILE* f = fopen(path, "wb");
+        if (f) { fwrite(p.w_host, 1, p.w_bytes, f); fclose(f); }
+        snprintf(path, sizeof path, "%s.params.bin", argv[4]);
+        f = fopen(path, "wb");
+        if (f) { fwrite(p.p_host, sizeof(float), p.p_floats, f); fclose(f); }
+        snprintf(path, sizeof path, "%s.txt", argv[4]);
+        f = fopen(path, "w");
+        if (f) {
+            for (int s = 0; s < p.n_steps; s++) {
+                const FfStep* st = &p.steps[s];
+                if (st->kind == 2) {
+                    fprintf(f, "fc %d %zu %zu\n", st->op_first, st->w_off, ffk_fc_packed_bytes(st->fc_n, st->fc_k));
+                    continue;
+                }
+                fprintf(f, "conv %d %zu %zu\n", st->op_first, st->w_off,
+                        ffk_conv_packed_bytes(st->cin, st->cout, st->kh, st->kw));
+                if (st->wino_off != (size_t)-1)
+                    fprintf(f, "wino %d %zu %zu\n", st->op_first, st->wino_off,
+                            ffk_winograd_packed_bytes(st->cin, st->cout));
+                if (st->flags & FFK_EPI_BN)
+                    fprintf(f, "bn %d %zu %zu %zu\n", st->op_first, st->lut_off, (size_t)st->cout * 256, st->p_off);
+            }
+            fclose(f);
+        }
+    }
     ff_plan_free(&p);
     ff_model_free(&m);
     return 0;

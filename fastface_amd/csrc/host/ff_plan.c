@@ -24,17 +24,44 @@
  * being run some other way.
  */
 #include <math.h>
+#include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include "ff_host.h"
 
+/* Weight-arena contents are produced after the walk, as independent jobs:
+ * the walk only places them (offsets), the arena is then allocated once at
+ * its final size and the jobs fill it on a few threads. */
+enum { JOB_CONV, JOB_WINO, JOB_BN, JOB_FC };
+typedef struct {
+    int kind;
+    const int8_t* src;          /* conv / FC weights in the mapping */
+    int cout, cin, kh, kw;      /* conv; FC: cout = N, cin = K */
+    int r0, r1;                 /* FC: rows of this job */
+    int fc_hw, fc_c, flat;      /* FC: NCHW flatten -> NHWC column order */
+    size_t dst;                 /* bytes into the weight arena */
+    size_t p_off;               /* BN: floats into the parameter arena */
+} PackJob;
+
 typedef struct {
     FfPlan* p;
-    size_t w_cap, p_cap;
+    size_t p_cap;
     int s_cap, t_cap;
+    PackJob* jobs;
+    int n_jobs, j_cap;
 } Builder;
+
+static void add_job(Builder* b, PackJob j)
+{
+    if (b->n_jobs == b->j_cap) {
+        b->j_cap = b->j_cap ? 2 * b->j_cap : 128;
+        b->jobs = (PackJob*)realloc(b->jobs, (size_t)b->j_cap * sizeof(PackJob));
+    }
+    b->jobs[b->n_jobs++] = j;
+}
 
 static int fail(FfPlan* p, const char* msg, int op)
 {
@@ -81,16 +108,95 @@ static size_t alloc_params(Builder* b, size_t n)
     return off;
 }
 
+/* place n bytes in the weight arena (256-byte aligned); filled by a job */
 static size_t alloc_weights(Builder* b, size_t n)
 {
     FfPlan* p = b->p;
     size_t off = (p->w_bytes + 255) & ~(size_t)255;
-    if (off + n > b->w_cap) {
-        while (off + n > b->w_cap) b->w_cap = b->w_cap ? 2 * b->w_cap : ((size_t)1 << 24);
-        p->w_host = (int8_t*)realloc(p->w_host, b->w_cap);
-    }
     p->w_bytes = off + n;
     return off;
+}
+
+static void run_job(const FfPlan* p, const PackJob* j, int8_t* row)
+{
+    int8_t* dst = p->w_host + j->dst;
+    switch (j->kind) {
+    case JOB_CONV:
+        ffk_pack_conv_weights(j->src, j->cout, j->cin, j->kh, j->kw, dst);
+        break;
+    case JOB_WINO:
+        ffk_pack_winograd_weights(j->src, j->cout, j->cin, dst);
+        break;
+    case JOB_BN: {
+        const float* P = p->p_host + j->p_off;
+        const int C = j->cout;
+        ffk_make_bn_lut(P + FFK_P_BN_SIN * C, P + FFK_P_BN_S * C, P + FFK_P_BN_O * C,
+                        P + FFK_P_BN_INV * C, C, dst);
+        break;
+    }
+    case JOB_FC: {
+        const int N = j->cout, K = j->cin, HW = j->fc_hw, Cc = j->fc_c;
+        for (int r = j->r0; r < j->r1; r++) {
+            const int8_t* src = j->src + (size_t)r * K;
+            if (j->flat) {       /* reference column c*HW + hw -> NHWC column hw*C + c */
+                for (int c = 0; c < Cc; c++)
+                    for (int hw = 0; hw < HW; hw++) row[(size_t)hw * Cc + c] = src[(size_t)c * HW + hw];
+                ffk_pack_fc_row(row, N, K, r, dst);
+            } else {
+                ffk_pack_fc_row(src, N, K, r, dst);
+            }
+        }
+        break;
+    }
+    }
+}
+
+typedef struct {
+    const FfPlan* p;
+    const PackJob* jobs;
+    int n_jobs, next, row_bytes;
+    pthread_mutex_t mu;
+} JobQueue;
+
+static void* job_worker(void* arg)
+{
+    JobQueue* q = (JobQueue*)arg;
+    int8_t* row = q->row_bytes ? (int8_t*)malloc((size_t)q->row_bytes) : NULL;
+    for (;;) {
+        pthread_mutex_lock(&q->mu);
+        const int k = q->next < q->n_jobs ? q->next++ : -1;
+        pthread_mutex_unlock(&q->mu);
+        if (k < 0) break;
+        run_job(q->p, &q->jobs[k], row);
+    }
+    free(row);
+    return NULL;
+}
+
+/* Allocate the weight arena and fill it: the jobs on up to 8 threads (the
+ * caller's among them). */
+static int run_jobs(Builder* b)
+{
+    FfPlan* p = b->p;
+    p->w_host = (int8_t*)calloc(p->w_bytes ? p->w_bytes : 1, 1);   /* (alignment gaps stay zero) */
+    if (!p->w_host) return -1;
+    int row_bytes = 0;
+    for (int k = 0; k < b->n_jobs; k++)
+        if (b->jobs[k].kind == JOB_FC && b->jobs[k].cin > row_bytes) row_bytes = b->jobs[k].cin;
+    JobQueue q;
+    q.p = p; q.jobs = b->jobs; q.n_jobs = b->n_jobs; q.next = 0; q.row_bytes = row_bytes;
+    pthread_mutex_init(&q.mu, NULL);
+    long ncpu = sysconf(_SC_NPROCESSORS_ONLN);
+    int nt = (int)(ncpu < 1 ? 1 : (ncpu > 8 ? 8 : ncpu));
+    if (nt > b->n_jobs) nt = b->n_jobs > 0 ? b->n_jobs : 1;
+    pthread_t th[8];
+    int started = 0;
+    for (int t = 1; t < nt; t++)
+        if (pthread_create(&th[started], NULL, job_worker, &q) == 0) started++;
+    job_worker(&q);
+    for (int t = 0; t < started; t++) pthread_join(th[t], NULL);
+    pthread_mutex_destroy(&q.mu);
+    return 0;
 }
 
 static void fill_row(float* row, int n, const uint8_t* src, float scalar)
@@ -115,7 +221,7 @@ typedef struct { int C, H, W; } Shp;
 int ff_plan_build(const FfModel* m, FfPlan* p)
 {
     memset(p, 0, sizeof *p);
-    Builder B = { p, 0, 0, 0, 0 };
+    Builder B = { p, 0, 0, 0, NULL, 0, 0 };
     const int n = m->n_ops;
     const int v4 = m->version >= 4;
     const int pc = v4 && m->has_v2;
@@ -211,12 +317,14 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
             s->in_scale = in_scale;
             s->flags = FFK_EPI_BIAS | (in_scale != 1.0f ? FFK_EPI_INSCALE : 0);
             s->w_off = alloc_weights(&B, ffk_conv_packed_bytes(op->Cin, op->Cout, op->Kh, op->Kw));
-            ffk_pack_conv_weights(op->conv_w, op->Cout, op->Cin, op->Kh, op->Kw, p->w_host + s->w_off);
+            add_job(&B, (PackJob){ JOB_CONV, op->conv_w, op->Cout, op->Cin, op->Kh, op->Kw, 0, 0, 0, 0, 0,
+                                   s->w_off, 0 });
             s->wino_off = (size_t)-1;
             if (ffk_winograd_supported(op->Cin, op->Cout, op->Kh, op->Kw, op->stride, op->pad, si.H, si.W)) {
                 /* the same layer as integer Winograd F(2,3) (fastface_set_conv_algo) */
                 s->wino_off = alloc_weights(&B, ffk_winograd_packed_bytes(op->Cin, op->Cout));
-                ffk_pack_winograd_weights(op->conv_w, op->Cout, op->Cin, p->w_host + s->wino_off);
+                add_job(&B, (PackJob){ JOB_WINO, op->conv_w, op->Cout, op->Cin, 3, 3, 0, 0, 0, 0, 0,
+                                       s->wino_off, 0 });
             }
             s->p_off = alloc_params(&B, (size_t)FFK_NPARAM * op->Cout);
             float* P = p->p_host + s->p_off;
@@ -265,9 +373,7 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
             fill_rowf(P + FFK_P_BN_INV * C, C, bn_inv, inv_of(next_scale));
             s->flags |= FFK_EPI_BN;
             s->lut_off = alloc_weights(&B, (size_t)C * 256);
-            P = p->p_host + s->p_off;
-            ffk_make_bn_lut(P + FFK_P_BN_SIN * C, P + FFK_P_BN_S * C, P + FFK_P_BN_O * C,
-                            P + FFK_P_BN_INV * C, C, p->w_host + s->lut_off);
+            add_job(&B, (PackJob){ JOB_BN, NULL, C, 0, 0, 0, 0, 0, 0, 0, 0, s->lut_off, s->p_off });
             const int Y = new_tensor(&B, C, si.H, si.W, i);
             p->tensors[Y].def_step = last_conv;
             s->t_bn = Y;
@@ -306,20 +412,10 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
             s->t_in = A; s->fc_n = N; s->fc_k = K;
             s->a_scale = v4 ? 1.0f : A_scale;
             s->w_off = alloc_weights(&B, ffk_fc_packed_bytes(N, K));
-            int8_t* wt = (int8_t*)malloc((size_t)N * K);
-            if (!wt) { rc = fail(p, "out of host memory", i); break; }
-            const int HW = at->H * at->W, Cc = at->C;
-            for (int r = 0; r < N; r++) {
-                const int8_t* src = op->gemm_w + (size_t)r * K;
-                int8_t* dst = wt + (size_t)r * K;
-                if (flat)            /* reference column c*HW + hw -> NHWC column hw*C + c */
-                    for (int c = 0; c < Cc; c++)
-                        for (int hw = 0; hw < HW; hw++) dst[(size_t)hw * Cc + c] = src[(size_t)c * HW + hw];
-                else
-                    memcpy(dst, src, (size_t)K);
-            }
-            ffk_pack_fc_weights(wt, N, K, p->w_host + s->w_off);
-            free(wt);
+            /* 16 rows per job: the rows are permuted and packed on the threads */
+            for (int r0 = 0; r0 < N; r0 += 16)
+                add_job(&B, (PackJob){ JOB_FC, op->gemm_w, N, K, 0, 0, r0, r0 + 16 < N ? r0 + 16 : N,
+                                       at->H * at->W, at->C, flat, s->w_off, 0 });
             s->ws_off = alloc_params(&B, (size_t)N);
             fill_row(p->p_host + s->ws_off, N, op->gemm_scales, 0.0f);
             s->bias_off = alloc_params(&B, (size_t)N);
@@ -335,6 +431,8 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
     free(is_sc); free(sh_in); free(sh_out);
     if (!rc && !done) rc = fail(p, "model has no GEMM head", n);
     if (!rc && p->emb_n != FASTFACE_OUTPUT_N) rc = fail(p, "embedding size must be 512", n);
+    if (!rc && run_jobs(&B)) rc = fail(p, "out of host memory", n);
+    free(B.jobs);
     return rc;
 }
 

@@ -94,6 +94,53 @@ def read_opsc2(path=OPSC2_PATH):
     return in_s, per_op
 
 
+def read_opsc(path=OPSC_PATH):
+    """(input_scale, per-op scales) of an OPSC file (libfastface.c:116-129;
+    a scale <= 0 means "keep the current one")."""
+    with open(path, "rb") as f:
+        d = f.read()
+    assert d[:4] == b"OPSC"
+    (n,) = struct.unpack_from("<I", d, 4)
+    in_s = float(np.frombuffer(d, np.float32, 1, 8)[0])
+    return in_s, np.frombuffer(d, np.float32, n, 12).copy()
+
+
+def _per_tensor_scales(ops, opsc):
+    """The per-tensor scales the reference's interpreter tracks for models
+    below FFW4 (libfastface.c:349-440 with version < 4): for every op, the
+    scale of the tensor it reads (a shortcut conv reads the block input's)
+    and the scale its output is requantized to (a conv's fused PReLU / Add
+    decides it).  Returns two lists indexed by op (None where unused)."""
+    in_s, sc = opsc
+    n = len(ops)
+    a_in, out = [None] * n, [None] * n
+    A = blk = in_s
+    i = 0
+    while i < n:
+        t = ops[i]["type"]
+        nxt = sc[i] if sc[i] > 0 else A
+        if t == OP_CONV:
+            a_in[i] = blk if i > 0 and ops[i - 1]["type"] == OP_SAVE_ID else A
+            eff = nxt
+            if i + 1 < n and ops[i + 1]["type"] in (OP_PRELU, OP_ADD):
+                eff = sc[i + 1] if sc[i + 1] > 0 else nxt
+                out[i] = eff
+                A = eff
+                i += 2
+                continue
+            out[i] = eff
+            A = eff
+        elif t == OP_BN:
+            a_in[i], out[i] = A, nxt
+            A = nxt
+        elif t == OP_BLOCK_START:
+            blk = A
+        elif t == OP_GEMM:
+            a_in[i] = A
+        i += 1
+    return a_in, out
+
+
 def _fill_scales(ops, opsc2):
     """Per-op forward activation scales the interpreter tracks (the producer's
     OPSC2 entry, libfastface.c:395-396,410-411)."""
@@ -107,17 +154,28 @@ def _fill_scales(ops, opsc2):
     return out
 
 
-def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPSC2_PATH):
-    """Write a synthetic FFW4 file (about 43.7 MB) and return its path."""
+def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPSC2_PATH, version=4):
+    """Write a synthetic FFW4 file (about 43.7 MB) and return its path.
+
+    version 3 or 2 writes the same network as an FFW3 / FFW2 file
+    (kernels/ffw2_loader.c:96-125: the FFW4 layout under another magic;
+    FFW2 without the conv bias).  The reference runs those on per-tensor
+    scales (libfastface.c:335-343,356-422: the OPSC file's, an in-scale on
+    every conv, the activation scale on the FC), so their weight, BN and FC
+    scales are sized from the OPSC per-tensor scales instead of the OPSC2
+    per-channel ones.  The random draws are the same for every version: the
+    int8 weights, biases and slopes are identical."""
+    assert version in (2, 3, 4)
     rng = np.random.default_rng(seed)
     ops = iresnet_schedule()
     opsc2 = read_opsc2(opsc2_path)
     _, per_op = opsc2
     track = _fill_scales(ops, opsc2)
+    pt_in, pt_out = _per_tensor_scales(ops, read_opsc()) if version < 4 else (None, None)
     n = len(ops)
     tmp = path + ".tmp%d" % os.getpid()
     with open(tmp, "wb") as f:
-        f.write(b"FFW4")
+        f.write(b"FFW%d" % version)
         f.write(struct.pack("<I", n))
         for i, op in enumerate(ops):
             t = op["type"]
@@ -129,6 +187,8 @@ def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPS
                 eff = i + 1 if ops[i + 1]["type"] in (OP_PRELU, OP_ADD) else i
                 s_out = per_op[eff] if per_op[eff] is not None else np.full(cout, 0.02, np.float32)
                 kreal = cin * k * k
+                if version < 4:         # f = acc * in_scale * ws, requantized by 1/out_scale
+                    s_out = np.full(cout, pt_out[i] / pt_in[i])
                 # keeps the int8 output spread close to the input's
                 base = s_out.astype(np.float64) * gain / (np.sqrt(kreal) * 73.6)
                 jitter = rng.uniform(0.5, 1.5, size=cout)
@@ -137,11 +197,14 @@ def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPS
                 f.write(struct.pack("<6H", cin, cout, k, k, op["s"], op["p"]))
                 f.write(w.tobytes())
                 f.write(scales.tobytes())
-                f.write(bias.tobytes())
+                if version >= 3:
+                    f.write(bias.tobytes())
             elif t == OP_BN:
                 c = op["C"]
                 s_in = track[i].astype(np.float64)
                 s_bn = per_op[i].astype(np.float64) if per_op[i] is not None else s_in
+                if version < 4:
+                    s_in, s_bn = np.full(c, pt_in[i]), np.full(c, pt_out[i])
                 ratio = np.clip(s_bn / np.maximum(s_in, 1e-30), 1e-3, 1e3)
                 scale = (ratio * rng.uniform(0.5, 1.5, size=c)).astype(np.float32)
                 offset = rng.normal(0.0, 0.05, size=c).astype(np.float32)
@@ -156,8 +219,10 @@ def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPS
             elif t == OP_GEMM:
                 nn, kk = op["N"], op["K"]
                 w = rng.integers(-127, 128, size=(nn, kk), dtype=np.int8)
-                scales = (rng.uniform(0.5, 1.5, size=nn) /
-                          (np.sqrt(kk) * 73.6 * act_sigma)).astype(np.float32)
+                scales = rng.uniform(0.5, 1.5, size=nn) / (np.sqrt(kk) * 73.6 * act_sigma)
+                if version < 4:         # out = dot * A_scale * ws + bias
+                    scales = scales / pt_in[i]
+                scales = scales.astype(np.float32)
                 bias = rng.normal(0.0, 0.05, size=nn).astype(np.float32)
                 f.write(struct.pack("<II", nn, kk))
                 f.write(w.tobytes())
@@ -167,13 +232,16 @@ def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPS
     return path
 
 
-def synthetic_ffw4_path(seed=3, cache_dir=None):
-    """Path of the cached synthetic FFW4 for `seed`, generated on first use."""
+def synthetic_ffw4_path(seed=3, cache_dir=None, version=4):
+    """Path of the cached synthetic model for `seed` (FFW4, or with
+    version 3 / 2 the FFW3 / FFW2 file), generated on first use."""
     cache_dir = cache_dir or os.environ.get("FASTFACE_CACHE", "/tmp/fastface_cache")
     os.makedirs(cache_dir, exist_ok=True)
-    path = os.path.join(cache_dir, "synthetic_r50_seed%d.ffw4" % seed)
+    name = "synthetic_r50_seed%d.ffw4" % seed if version == 4 else \
+        "synthetic_r50_seed%d_v%d.ffw" % (seed, version)
+    path = os.path.join(cache_dir, name)
     if not os.path.exists(path):
-        write_synthetic_ffw4(path, seed=seed)
+        write_synthetic_ffw4(path, seed=seed, version=version)
     return path
 
 

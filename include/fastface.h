@@ -62,9 +62,9 @@ FastFace* fastface_create_with_scales(const char* ffw4_path, const char* opsc_pa
  * fastface_embed gives for face i alone (the reference's own invariant: its
  * batched driver, arcface_forward_int8_batched.c, is bit-identical per face).
  * Host buffers: batch*37632 floats in, batch*512 floats out.  A batch of
- * more than 512 faces streams in chunks of 512: the copy of the next chunk
- * overlaps the compute of the current one (same results).  The call returns
- * when the embeddings are in out_b512. */
+ * more than 512 faces streams: a first chunk of 256 faces, then chunks of
+ * 768; the copy of the next chunk overlaps the compute of the current one
+ * (same results).  The call returns when the embeddings are in out_b512. */
 int fastface_embed_batch(FastFace* ff, const float* in_bhwc, int batch, float* out_b512);
 
 /* Device-resident variant: d_in / d_out are device pointers (HBM), the work
@@ -78,7 +78,7 @@ int fastface_embed_batch_device(FastFace* ff, const float* d_in, int batch, floa
  * README.md:152).  The input layer maps each pixel through a 256-entry table
  * per channel (normalization + the reference's input quantization), so a
  * quarter of the fp32 input bytes cross PCIe and HBM. */
-/* (host buffers: batches of more than 1024 faces stream in chunks of 1024) */
+/* (host buffers: batches of more than 512 faces stream in chunks of 512) */
 int fastface_embed_batch_rgb8(FastFace* ff, const uint8_t* in_bhwc, int batch, float* out_b512);
 int fastface_embed_batch_rgb8_device(FastFace* ff, const uint8_t* d_in, int batch, float* d_out,
                                      void* stream);

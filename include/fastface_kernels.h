@@ -271,7 +271,11 @@ typedef struct {
  * (0: none); the workspace fields are not read. */
 size_t ffk_fc_workspace_bytes(const ffk_fc_desc* d);
 size_t ffk_fc_packed_bytes(int n, int k);
+/* Packed FC weights: packed[(s*n + r)*64 + kk] = w_nk[r*k + s*64 + kk]
+ * (k a multiple of 64); ffk_pack_fc_row packs row r alone (`row`: its k
+ * bytes), so rows can be packed as they are produced, on several threads. */
 int    ffk_pack_fc_weights(const int8_t* w_nk, int n, int k, int8_t* packed);
+int    ffk_pack_fc_row(const int8_t* row, int n, int k, int r, int8_t* packed);
 int    ffk_fc(const ffk_fc_desc* d, void* stream);
 
 /* ---- self checks -------------------------------------------------------

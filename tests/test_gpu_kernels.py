@@ -786,3 +786,51 @@ def test_s2_shortcut_pair_equals_two_launches(gpu_lib, cin, cout, H, cx, fast, b
     s4.cin, s4.hin, s4.win = 256, 7, 7
     c4.batch = s4.batch = 1024
     assert lib.ffk_conv_s2_shortcut(C.byref(c4), C.byref(s4), None) == 0
+
+
+@pytest.mark.parametrize("cin,cout,H,cx", S2_PAIRS)
+def test_s2_shortcut_pair_x_even(gpu_lib, cin, cout, H, cx):
+    """The fused stride-2 pair with the shortcut's X stored at its even
+    pixels only (FFK_OUT_X_EVEN, a compact [B, Ho/2, Ho/2, Cout] tensor) and
+    BN(X) everywhere: X equals the even pixels of the two launches' X, BN(X)
+    the two launches' BN(X), bit for bit, at a ragged batch; every X byte
+    outside the compact tensor is left alone."""
+    lib = gpu_lib
+    r = rng(1400 + cin + H)
+    B = _direct_batch(lib, cin, cout, 3, 2, H)
+    Ho = H // 2
+    x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, 3, 3), dtype=np.int8)
+    xc = r.integers(-128, 128, size=(B, Ho, Ho, cx), dtype=np.int8)
+    w2 = r.integers(-128, 128, size=(cout, cx, 1, 1), dtype=np.int8)
+    ws, bias, inv = _unsaturated_params(r, cout, 9 * cin)
+    P1 = params_block(cout, ws=ws, bias=bias, inv=inv)
+    ws2, bias2, inv2 = _unsaturated_params(r, cout, cx)
+    P2 = params_block(cout, ws=ws2, bias=bias2, inv=inv2, adds=r.uniform(1e-3, 5e-2, cout).astype(F32),
+                      bn_sin=r.uniform(1e-3, 5e-2, cout).astype(F32), bn_s=r.uniform(0.5, 1.5, cout).astype(F32),
+                      bn_o=r.normal(0, 0.05, cout).astype(F32), bn_inv=(1.0 / r.uniform(0.01, 0.1, cout)).astype(F32))
+    f1 = fa.FFK_EPI_BIAS | fa.FFK_EPI_IN_RANGE
+    f2 = fa.FFK_EPI_BIAS | fa.FFK_EPI_ADD | fa.FFK_EPI_BN | fa.FFK_EPI_IN_RANGE
+    assert lib.ffk_requant_in_range(P1.ctypes.data, cout, 9 * cin, f1) == 1
+    assert lib.ffk_requant_in_range(P2.ctypes.data, cout, cx, f2) == 1
+
+    R, _ = run_conv(lib, x, w, 2, 1, params=P1, flags=f1, split=False)
+    X_exp, BN_exp = run_conv(lib, xc, w2, 1, 0, params=P2, flags=f2, add=R, want_bn=True, split=False)
+
+    keep = []
+    n = B * Ho * Ho * cout
+    ne = B * (Ho // 2) * (Ho // 2) * cout
+    dR, dBN = gpu_util.Dev(lib, nbytes=n), gpu_util.Dev(lib, nbytes=n)
+    guard = np.full(ne + 4096, 0x5A, np.uint8)              # a guard region past the tensor
+    dX = gpu_util.Dev(lib, host=guard)
+    keep += [dR, dX, dBN]
+    c = _pair_desc(lib, keep, B, cin, cout, 3, 2, 1, H, x, w, P1, f1, dR.ptr)
+    sc = _pair_desc(lib, keep, B, cx, cout, 1, 1, 0, Ho, xc, w2, P2, f2 | fa.FFK_OUT_X_EVEN, dX.ptr,
+                    out_bn=dBN.ptr, add=dR.ptr)
+    assert lib.ffk_conv_variant(C.byref(c)) == b"phase"
+    assert lib.ffk_conv_s2_shortcut(C.byref(c), C.byref(sc), None) == 1
+    gpu_util.check(lib, lib.ffk_stream_sync(None))
+    got = dX.get(np.int8, (ne + 4096,))
+    assert np.array_equal(got[:ne].reshape(B, Ho // 2, Ho // 2, cout), X_exp[:, ::2, ::2, :])
+    assert (got[ne:].view(np.uint8) == 0x5A).all()
+    assert np.array_equal(dBN.get(np.int8, (B, Ho, Ho, cout)), BN_exp)

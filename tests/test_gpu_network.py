@@ -123,6 +123,45 @@ def test_per_layer_int8_activations(gpu_lib, synth_ffw4, oracle, oracle_model):
         f.close()
 
 
+@pytest.mark.parametrize("version,with_opsc2", [(3, True), (3, False), (2, True), (4, False)],
+                         ids=["ffw3", "ffw3-noopsc2", "ffw2", "ffw4-noopsc2"])
+def test_other_formats_end_to_end(gpu_lib, oracle, version, with_opsc2):
+    """The formats the loader accepts besides FFW4 with OPSC2: FFW3 and FFW2
+    models (per-tensor scales, an in-scale on every conv, the activation scale
+    on the FC; FFW2 without conv bias: libfastface.c:335-343,356-422,
+    kernels/ffw2_loader.c:96-125) and FFW4 without OPSC2.  Embeddings equal
+    the oracle's (itself equal to the reference's fastface_embed on these
+    models) at b=1 and on faces of both halves of a split batch of 50; every
+    intermediate int8 tensor equals the oracle's at 2 faces; below FFW4 every
+    conv launches with the in-scale epilogue."""
+    ffw = synth.synthetic_ffw4_path(3, version=version)
+    opsc2 = synth.OPSC2_PATH if with_opsc2 else os.path.join(synth.REPO_ROOT, "models", "no_such_v2.bin")
+    m = oracle.load_model(ffw, synth.OPSC_PATH, synth.OPSC2_PATH if with_opsc2 else None)
+    f = fa.FastFace(ffw, scale_files=(synth.OPSC_PATH, opsc2))
+    try:
+        info = fa.fastface_step_info()
+        n_insc = sum(1 for s in range(gpu_lib.fastface_num_steps(f.ff))
+                     if gpu_lib.fastface_get_step(f.ff, s, C.byref(info)) == 0
+                     and info.kind == 1 and info.flags & fa.FFK_EPI_INSCALE)
+        assert n_insc == (53 if version < 4 else 0)
+        x = synth.faces_uniform(50, 60 + version)
+        batch = f.embed_batch(x)                        # two halves of 25 faces
+        idx = [0, 24, 25, 49]
+        exp, _ = oracle.forward(m, x[idx])
+        assert np.array_equal(batch[idx], exp)
+        assert np.array_equal(f.embed(x[0]), exp[0])
+        assert gpu_lib.fastface_debug_keep_tensors(f.ff, 1) == 0
+        exp2, dumps = oracle.forward(m, x[:2], dump_ops=set(range(177)))
+        assert np.array_equal(f.embed_batch(x[:2]), exp2)
+        for op, t in sorted(dumps.items()):
+            buf = np.empty(t.size, np.int8)
+            assert gpu_lib.fastface_debug_read(f.ff, op, 2, buf.ctypes.data, buf.nbytes) == t.size, op
+            assert np.array_equal(buf.reshape(t.shape), t), "op %d differs" % op
+    finally:
+        f.close()
+        oracle.free_model(m)
+
+
 def test_stage_outputs_stored_at_even_pixels(ff, gpu_lib):
     """The stem's output X and each stage's last X are read only by the next
     stage's 1x1 stride-2 shortcut: the plan stores them at their even pixels

@@ -300,3 +300,16 @@ def test_requant_in_range_condition():
     assert ok(Q, PR) == 0 and ok(Q, 0) == 1
     assert ok(P, PR | fa.FFK_EPI_INSCALE) == 0          # the in-scale path always checks
     assert ok(P, PR, 0) == 0
+
+
+def test_scale_paths_follow_the_working_directory():
+    """FastFace(cwd=...) opens the files fastface_create would open with `cwd`
+    as the working directory (libfastface.c:236-240): a relative $OPSC2_PATH
+    is taken relative to `cwd`, an absolute one as it is."""
+    from fastface_amd.api import scale_paths
+    cwd = "/data/run"
+    assert scale_paths(cwd, {}) == ("/data/run/models/op_scales.bin",
+                                     "/data/run/models/op_scales_v2.bin")
+    assert scale_paths(cwd, {"OPSC2_PATH": "alt/v2.bin"})[1] == "/data/run/alt/v2.bin"
+    assert scale_paths(cwd, {"OPSC2_PATH": "/abs/v2.bin"})[1] == "/abs/v2.bin"
+    assert scale_paths(cwd, {"OPSC2_PATH": ""})[1] == "/data/run/models/op_scales_v2.bin"

@@ -95,6 +95,16 @@ def test_valid_model_loads_and_plans(checker, synth_ffw4):
     assert o["load"] == "0" and o["v2"] == "0" and o["plan"] == "0"
 
 
+def test_fused_pairs_never_write_what_they_read(checker, synth_ffw4):
+    """A stage's stride-2 conv and its 1x1 shortcut may run as one launch
+    (ff_plan_pair); the shortcut's outputs must then take no buffer the
+    launch still reads: the conv's input, the shortcut's input, the conv's
+    output.  The buffer plan releases the pair's inputs only after it; a
+    regression would be a data race on the GPU, so it is checked here."""
+    o = run(checker, synth_ffw4)
+    assert o["pairs"] == "4" and o["overlaps"] == "0"
+
+
 def test_layout_walk_matches_file(blob):
     offs, end = op_offsets(blob)
     assert len(offs) == 177 and end == len(blob)
@@ -174,3 +184,61 @@ def test_unsupported_op_sequence_fails_plan(checker, tmp_path):
         np.float32(0.05).tobytes()
     o = run(checker, write(tmp_path, "p.ffw", ffw), opsc=write(tmp_path, "p.bin", opsc), opsc2=None)
     assert o["load"] == "0" and o["plan"] != "0"
+
+
+def test_weight_arena_equals_independent_packing(checker, synth_ffw4, blob, oracle, tmp_path):
+    """The plan's weight arena (filled by packing jobs on several threads)
+    equals the same contents built independently here with numpy from the
+    FFW4 file: every conv's weights in reduction order k = (kh*KW + kw)*Cin +
+    ci cut into [K/64][Cout][64], the FC's columns moved from the reference's
+    NCHW flatten order to NHWC and cut the same way, each BN table the
+    oracle's BN requant of the 256 int8 values, each Winograd region the
+    packer's output for that conv."""
+    import fastface_amd as fa
+    lib = fa.load()
+    dump = str(tmp_path / "arena")
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0")
+    r = subprocess.run([checker, synth_ffw4, synth.OPSC_PATH, synth.OPSC2_PATH, dump],
+                       capture_output=True, text=True, env=env, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    arena = np.fromfile(dump + ".bin", np.int8)
+    params = np.fromfile(dump + ".params.bin", np.float32)
+    offs, _ = op_offsets(blob)
+
+    def conv_w(op):
+        cin, cout, kh, kw = struct.unpack_from("<4H", blob, offs[op] + 1)
+        w = np.frombuffer(blob, np.int8, cout * cin * kh * kw, offs[op] + 13)
+        return w.reshape(cout, cin, kh, kw)
+
+    seen = set()
+    for line in open(dump + ".txt"):
+        kind, op, off, n, *rest = line.split()
+        op, off, n = int(op), int(off), int(n)
+        got = arena[off:off + n]
+        seen.add(kind)
+        if kind == "conv":
+            w = conv_w(op)
+            cout, cin, kh, kw = w.shape
+            K = kh * kw * cin
+            steps = -(-K // 64)
+            wk = np.zeros((cout, steps * 64), np.int8)
+            wk[:, :K] = w.transpose(0, 2, 3, 1).reshape(cout, K)
+            exp = wk.reshape(cout, steps, 64).transpose(1, 0, 2).reshape(-1)
+        elif kind == "wino":
+            w = conv_w(op)
+            exp = np.empty(n, np.int8)
+            assert lib.ffk_pack_winograd_weights(np.ascontiguousarray(w).ctypes.data, w.shape[0], w.shape[1],
+                                                 exp.ctypes.data) == 0
+        elif kind == "fc":
+            N, K = struct.unpack_from("<2I", blob, offs[op] + 1)
+            W = np.frombuffer(blob, np.int8, N * K, offs[op] + 9).reshape(N, 512, K // 512)
+            Wn = W.transpose(0, 2, 1).reshape(N, K)              # column c*HW + hw -> hw*C + c
+            exp = Wn.reshape(N, K // 64, 64).transpose(1, 0, 2).reshape(-1)
+        else:                                                    # bn: table from the step's BN rows
+            C_, p_off = n // 256, int(rest[0])
+            rows = params[p_off:p_off + fa.FFK_NPARAM * C_].reshape(fa.FFK_NPARAM, C_)
+            q = np.arange(-128, 128, dtype=np.int8).reshape(256, 1).repeat(C_, axis=1)
+            exp = oracle.bn_prelu_requant(q, in_scale_pc=rows[fa.FFK_P_BN_SIN], bn_scale=rows[fa.FFK_P_BN_S],
+                                          bn_offset=rows[fa.FFK_P_BN_O], inv_pc=rows[fa.FFK_P_BN_INV]).T.reshape(-1)
+        assert np.array_equal(got, exp), (kind, op)
+    assert seen == {"conv", "wino", "bn", "fc"}

@@ -252,6 +252,71 @@ def test_forward_vs_reference_embed(oracle, ref, oracle_model, synth_ffw4):
     assert np.array_equal(emb, emb_ref)
 
 
+# (FFW version, OPSC2 present): the formats below FFW4, and FFW4 without
+# OPSC2, which the reference runs on per-tensor scales
+OTHER_FORMATS = [(3, True), (3, False), (2, True), (2, False), (4, False)]
+
+
+def ref_embed_without_opsc2(ref, ffw, faces):
+    """The reference's fastface_embed with no OPSC2 file to load ($OPSC2_PATH
+    naming a missing file: libfastface.c:238-240 then keeps the per-tensor
+    OPSC scales)."""
+    from fastface_amd import synth
+    old = os.environ.get("OPSC2_PATH")
+    os.environ["OPSC2_PATH"] = os.path.join(synth.REPO_ROOT, "models", "no_such_op_scales_v2.bin")
+    try:
+        return ref.embed(ffw, faces, cwd=synth.REPO_ROOT)
+    finally:
+        if old is None:
+            del os.environ["OPSC2_PATH"]
+        else:
+            os.environ["OPSC2_PATH"] = old
+
+
+@pytest.mark.parametrize("version,with_opsc2", OTHER_FORMATS,
+                         ids=["ffw3", "ffw3-noopsc2", "ffw2", "ffw2-noopsc2", "ffw4-noopsc2"])
+def test_forward_vs_reference_embed_other_formats(oracle, ref, version, with_opsc2):
+    """Whole network on the formats the loader also accepts: FFW3 (the FFW4
+    layout) and FFW2 (no conv bias), which the reference runs on per-tensor
+    scales, with an in-scale on every conv and the activation scale on the FC
+    (libfastface.c:335-343,356-422; kernels/ffw2_loader.c:96-125); and FFW4
+    without OPSC2.  Oracle interpreter == reference fastface_embed, bit for
+    bit.  Below FFW4 the reference never reads OPSC2, so its presence
+    changes nothing."""
+    from fastface_amd import synth
+    ffw = synth.synthetic_ffw4_path(3, version=version)
+    faces = np.concatenate([synth.faces_uniform(1, 0), synth.faces_normal_clipped(1, 2)])
+    m = oracle.load_model(ffw, synth.OPSC_PATH, synth.OPSC2_PATH if with_opsc2 else None)
+    try:
+        emb, acts = oracle.forward(m, faces, dump_ops=[3, 90])
+    finally:
+        oracle.free_model(m)
+    emb_ref = ref.embed(ffw, faces, cwd=synth.REPO_ROOT) if with_opsc2 else \
+        ref_embed_without_opsc2(ref, ffw, faces)
+    assert np.array_equal(emb, emb_ref)
+    if version < 4:
+        assert np.array_equal(emb, ref_embed_without_opsc2(ref, ffw, faces) if with_opsc2 else
+                              ref.embed(ffw, faces, cwd=synth.REPO_ROOT))
+    # the model is not degenerate: its activations spread over the int8 range
+    for a in acts.values():
+        assert a.astype(np.float32).std() > 5 and (a == 0).mean() < 0.2
+
+
+def test_synthetic_formats_share_their_weights():
+    """FFW3 / FFW2 variants hold the FFW4 model's int8 weights (the same
+    draws); FFW2 lacks exactly the 53 conv biases."""
+    from fastface_amd import synth
+    sizes = {v: os.path.getsize(synth.synthetic_ffw4_path(3, version=v)) for v in (4, 3, 2)}
+    couts = sum(op["Cout"] for op in synth.iresnet_schedule() if op["type"] == synth.OP_CONV)
+    assert sizes[3] == sizes[4] and sizes[4] - sizes[2] == 4 * couts
+    with open(synth.synthetic_ffw4_path(3, version=4), "rb") as f4, \
+            open(synth.synthetic_ffw4_path(3, version=3), "rb") as f3:
+        a, b = f4.read(), f3.read()
+    assert a[:4] == b"FFW4" and b[:4] == b"FFW3"
+    stem_w = 8 + 1 + 12
+    assert a[stem_w:stem_w + 64 * 27] == b[stem_w:stem_w + 64 * 27]
+
+
 def test_forward_batch_invariance(oracle, oracle_model):
     from fastface_amd import synth
     faces = synth.faces_normal_clipped(3, 2)

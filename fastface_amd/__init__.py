@@ -26,6 +26,7 @@ FFK_EPI_PRELU_LE1 = 0x40
 FFK_ALGO_WINOGRAD = 0x80
 FFK_OUT_X_EVEN = 0x100
 FFK_EPI_IN_RANGE = 0x200
+FFK_EPI_FMA_TAIL = 0x800
 FFK_SHARED_GPU = 0x400
 FFK_NOALLOC_SCRATCH_BYTES = 1024 + 160 * 64 * 64 * 4
 (FFK_P_WS, FFK_P_BIAS, FFK_P_SLOPE, FFK_P_ADDSCALE, FFK_P_INV, FFK_P_BN_SIN, FFK_P_BN_S,
@@ -111,6 +112,7 @@ EXPORTS = [
     ("ffk_conv_supported", C.c_int, [C.c_int] * 8),
     ("ffk_prelu_le1_ok", C.c_int, [_p, C.c_int, C.c_int, C.c_int]),
     ("ffk_requant_in_range", C.c_int, [_p, C.c_int, C.c_int, C.c_int]),
+    ("ffk_requant_fma_ok", C.c_int, [_p, C.c_int, C.c_int, C.c_int]),
     ("ffk_conv_packed_bytes", C.c_size_t, [C.c_int] * 4),
     ("ffk_pack_conv_weights", C.c_int, [_p, C.c_int, C.c_int, C.c_int, C.c_int, _p]),
     ("ffk_conv_workspace_bytes", C.c_size_t, [C.POINTER(ffk_conv_desc)]),

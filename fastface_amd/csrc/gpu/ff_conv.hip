@@ -129,7 +129,7 @@ ConvArgs conv_args(const ffk_conv_desc* d) {
     a.out_bn = d->out_bn;
     a.out_i32 = d->out_i32;
     a.flags = d->flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN | FFK_EPI_BIAS | FFK_EPI_INSCALE |
-                          FFK_EPI_PRELU_LE1 | FFK_OUT_X_EVEN | FFK_EPI_IN_RANGE |
+                          FFK_EPI_PRELU_LE1 | FFK_OUT_X_EVEN | FFK_EPI_IN_RANGE | FFK_EPI_FMA_TAIL |
                           FFK_IN_RGB8);
     a.in_scale = d->in_scale;
     return a;
@@ -177,6 +177,79 @@ int ffk_requant_in_range(const float* params, int cout, int ktotal, int flags) {
         const double f = (acc_max * std::fabs(ws) + std::fabs(bias) + 128.0 * std::fabs(adds)) * widen;
         const double t = f * std::max(1.0, std::fabs(slope)) * std::fabs(inv) * widen;
         if (!(t < 2147483520.0)) return 0;              // 2^31 - 128
+    }
+    return 1;
+}
+
+// FFK_EPI_FMA_TAIL.  The pre-requant value f(acc) of one channel as the
+// kernels and the reference compute it on the in-range forms without a
+// residual: (float)acc (round to nearest even above 2^24), * ws, + bias,
+// then PReLU.  With slope >= 0 it is non-decreasing in acc where ws > 0,
+// non-increasing where ws < 0 and constant where ws == 0.
+static float fma_tail_value(long long acc, float ws, float bias, float slope, bool prelu) {
+    volatile float f = (float)acc;
+    volatile float g = f * ws;
+    volatile float h = g + bias;
+    float v = h;
+    if (prelu && v < 0.0f) {
+        volatile float n = v * slope;
+        v = n;
+    }
+    return v;
+}
+
+// 1 if f(acc) == target for some acc in [-amax, amax]: binary search for the
+// smallest acc with f(s*acc) >= target, s the sign that makes f(s*acc)
+// non-decreasing (the range is symmetric)
+static int fma_tail_reached(float target, long long amax, float ws, float bias, float slope, bool prelu) {
+    const long long s = ws < 0.0f ? -1 : 1;
+    long long lo = -amax, hi = amax;
+    if (fma_tail_value(s * hi, ws, bias, slope, prelu) < target) return 0;
+    while (lo < hi) {
+        const long long mid = lo + (hi - lo) / 2;
+        if (fma_tail_value(s * mid, ws, bias, slope, prelu) >= target) hi = mid;
+        else lo = mid + 1;
+    }
+    return fma_tail_value(s * lo, ws, bias, slope, prelu) == target;
+}
+
+int ffk_requant_fma_ok(const float* params, int cout, int ktotal, int flags) {
+    if ((flags & (FFK_EPI_ADD | FFK_EPI_INSCALE)) || !ffk_requant_in_range(params, cout, ktotal, flags)) return 0;
+    const bool prelu = (flags & FFK_EPI_PRELU) != 0;
+    const long long amax = (long long)ktotal * 128 * 128;
+    // p = f*inv exact, h = copysign(0.5, p).  The reference truncates
+    // RN(RN(p) + h), the fma form RN(p + h).  At a level n >= 1 the two
+    // differ only where RN(p) lands on the other side of c_n = n - 1/2 -
+    // u_n/2 than p does (u_n: the float spacing just below n; r >= n exactly
+    // when the addend before the final rounding reaches n - u_n/2, the final
+    // tie going to n).  For n >= 2, c_n is an odd multiple of u_n/2, not a
+    // float: RN(p) and p are on the same side unless p == c_n, and then RN
+    // rounds the tie to n - 1/2 (an even multiple of u_n) and both forms
+    // reach n.  For n = 1 (u_1 = 2^-24), c_1 = 1/2 - 2^-25 is a float of the
+    // binade below: p strictly between c_1 - 2^-26 and c_1 rounds up to c_1,
+    // where the reference reaches 1 and the fma form stays at 0.  Symmetric
+    // for p < 0.  That window is the only place where they differ.
+    const double c1 = 0.5 - std::ldexp(1.0, -25), w0 = c1 - std::ldexp(1.0, -26);
+    for (int c = 0; c < cout; c++) {
+        const float ws = params[FFK_P_WS * cout + c];
+        const float bias = params[FFK_P_BIAS * cout + c];
+        const float inv = params[FFK_P_INV * cout + c];
+        const float slope = prelu ? params[FFK_P_SLOPE * cout + c] : 0.0f;
+        if (!(inv > 0.0f) || (prelu && !(slope >= 0.0f))) return 0;
+        const double di = inv;
+        auto reached = [&](float f) {
+            return fma_tail_reached(f, amax, ws, bias, slope, prelu) || fma_tail_reached(-f, amax, ws, bias, slope, prelu);
+        };
+        // floats f > 0 with f*inv strictly inside (c1 - 2^-26, c1) (the
+        // product of two floats is exact in double): start a few floats
+        // below the window's start and walk up past its end
+        float f = (float)(w0 / di);
+        if (!std::isfinite(f)) continue;
+        f = std::nextafter(std::nextafter(f, 0.0f), 0.0f);
+        int k = 0;
+        for (; k < 16 && (double)f * di < c1; k++, f = std::nextafter(f, INFINITY))
+            if ((double)f * di > w0 && reached(f)) return 0;
+        if (k == 16) return 0;                       // (never: the window is narrower than a float step)
     }
     return 1;
 }

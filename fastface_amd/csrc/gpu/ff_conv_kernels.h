@@ -174,7 +174,9 @@ __device__ __forceinline__ unsigned x_pix_blk(const ConvArgs& a, int mb, int r) 
 // PRELU: 0 none, 1 f < 0 ? f*slope : f, 2 max(f, f*slope) (the same values
 // when every slope is at most 1 and f is never infinite: FFK_EPI_PRELU_LE1).
 // INSC: f = f * in_scale first (FFW2/FFW3 models; FFW4 skips the multiply).
-// RANGE: every requant value is known in range (FFK_EPI_IN_RANGE).
+// RANGE: 0 the general requant; 1 every requant value is known in range
+// (FFK_EPI_IN_RANGE); 2 also its last two roundings taken as one fma
+// (FFK_EPI_FMA_TAIL, proven per launch by the host; no residual).
 // HO x WO: output image size (FFK_OUT_X_EVEN addressing).
 // LUT_DMA: the BN table was issued as direct-to-LDS loads (issue_bn_lut) that
 // may still be in flight; they are waited for before the flush.
@@ -187,7 +189,7 @@ __device__ __forceinline__ unsigned x_pix_blk(const ConvArgs& a, int mb, int r) 
 // residual of the shortcut's epilogue); 2 (with ADD) takes the residual from
 // the staging tile, where STAGE 1 left it, instead of loading it.  The same
 // lane writes and reads each element, so no barrier orders the two.
-template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC, bool RANGE, int HO, int WO,
+template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC, int RANGE, int HO, int WO,
           bool LUT_DMA = false, bool WG_SYNC = true, int STAGE = 0>
 __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                             const EpiParams<NJ>& prm, int mrow0, int ncol0, int8_t* Ws,
@@ -207,6 +209,7 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
     const float* adds = prm.adds;
     const float* inv = prm.inv;
     static_assert(STAGE != 1 || !ADD, "a staged tile is an output, not a residual sum");
+    static_assert(RANGE != 2 || (!ADD && !INSC), "the one-rounding tail is proven without a residual");
     if (ADD && STAGE != 2 && RSLOTS % 64 == 0) {
         // residual tile -> this wave's LDS tile as direct-to-LDS loads: slot s
         // of wave load k is tile row (64k+s)/SPR, piece (64k+s)%SPR; unused
@@ -255,8 +258,9 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
                 if (ADD) f = ff::add_residual(f, (int32_t)Ws[row * P + col], adds[j]);
                 if (PRELU == 1) f = ff::prelu(f, p2[j]);
                 if (PRELU == 2) f = ff::prelu_le1(f, p2[j]);
-                Ws[row * P + col] = (int8_t)(RANGE ? ff::requant_haz_in_range(f * inv[j])
-                                                   : ff::requant_haz(f * inv[j]));
+                Ws[row * P + col] = (int8_t)(RANGE == 2 ? ff::requant_fma_in_range(f, inv[j])
+                                             : RANGE == 1 ? ff::requant_haz_in_range(f * inv[j])
+                                                          : ff::requant_haz(f * inv[j]));
                 // one 32x32 tile at a time: keeps the compiler from hoisting
                 // every residual read of the wave tile into registers
                 if (r == 15) asm volatile("" ::: "memory");
@@ -356,37 +360,43 @@ __device__ __forceinline__ void wave_epilogue_f(const v16i (&acc)[MI][NJ], const
                                                 const int8_t* Lw) {
     const bool le1 = !INSC && (a.flags & FFK_EPI_PRELU_LE1);
     const bool rng = !INSC && (a.flags & FFK_EPI_IN_RANGE);
+    const bool fma = rng && (a.flags & FFK_EPI_FMA_TAIL);
+    constexpr int RF = INSC ? 1 : 2;   // (the in-scale instantiation never takes it)
 #define FF_EPI(PR, AD, BN, RG) \
     wave_epi_i8<COUT, MI, NJ, PR, AD, BN, INSC, RG, HO, WO, true>(acc, a, P, mrow0, ncol0, Ws, Lw)
     switch (a.flags & (FFK_EPI_PRELU | FFK_EPI_ADD | FFK_EPI_BN)) {
     case 0:
-        if (rng) FF_EPI(0, false, false, true);
-        else FF_EPI(0, false, false, false);
+        if (fma) FF_EPI(0, false, false, RF);
+        else if (rng) FF_EPI(0, false, false, 1);
+        else FF_EPI(0, false, false, 0);
         break;
     case FFK_EPI_PRELU:
-        if (le1 && rng) FF_EPI(2, false, false, true);
-        else if (le1) FF_EPI(2, false, false, false);
-        else FF_EPI(1, false, false, false);
+        if (le1 && fma) FF_EPI(2, false, false, RF);
+        else if (le1 && rng) FF_EPI(2, false, false, 1);
+        else if (le1) FF_EPI(2, false, false, 0);
+        else FF_EPI(1, false, false, 0);
         break;
     case FFK_EPI_ADD:
-        if (rng) FF_EPI(0, true, false, true);
-        else FF_EPI(0, true, false, false);
+        if (rng) FF_EPI(0, true, false, 1);
+        else FF_EPI(0, true, false, 0);
         break;
     case FFK_EPI_BN:
-        if (rng) FF_EPI(0, false, true, true);
-        else FF_EPI(0, false, true, false);
+        if (fma) FF_EPI(0, false, true, RF);
+        else if (rng) FF_EPI(0, false, true, 1);
+        else FF_EPI(0, false, true, 0);
         break;
     case FFK_EPI_PRELU | FFK_EPI_BN:
-        if (le1 && rng) FF_EPI(2, false, true, true);
-        else if (le1) FF_EPI(2, false, true, false);
-        else FF_EPI(1, false, true, false);
+        if (le1 && fma) FF_EPI(2, false, true, RF);
+        else if (le1 && rng) FF_EPI(2, false, true, 1);
+        else if (le1) FF_EPI(2, false, true, 0);
+        else FF_EPI(1, false, true, 0);
         break;
     case FFK_EPI_ADD | FFK_EPI_BN:
-        if (rng) FF_EPI(0, true, true, true);
-        else FF_EPI(0, true, true, false);
+        if (rng) FF_EPI(0, true, true, 1);
+        else FF_EPI(0, true, true, 0);
         break;
-    case FFK_EPI_PRELU | FFK_EPI_ADD: FF_EPI(1, true, false, false); break;
-    default: FF_EPI(1, true, true, false); break;
+    case FFK_EPI_PRELU | FFK_EPI_ADD: FF_EPI(1, true, false, 0); break;
+    default: FF_EPI(1, true, true, 0); break;
     }
 #undef FF_EPI
 }
@@ -425,12 +435,15 @@ __device__ __forceinline__ void wave_epilogue(const v16i (&acc)[MI][NJ], const C
 template <int COUT, int MI, int NJ, int HO, int WO>
 __device__ __forceinline__ void wave_epi_pair_stage(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                                     const EpiParams<NJ>& P, int mrow0, int ncol0, int8_t* Ws) {
-    if (a.flags & FFK_EPI_IN_RANGE)
-        wave_epi_i8<COUT, MI, NJ, 0, false, false, false, true, HO, WO, true, true, 1>(acc, a, P, mrow0, ncol0, Ws,
-                                                                                      nullptr);
+    if ((a.flags & FFK_EPI_IN_RANGE) && (a.flags & FFK_EPI_FMA_TAIL))
+        wave_epi_i8<COUT, MI, NJ, 0, false, false, false, 2, HO, WO, true, true, 1>(acc, a, P, mrow0, ncol0, Ws,
+                                                                                   nullptr);
+    else if (a.flags & FFK_EPI_IN_RANGE)
+        wave_epi_i8<COUT, MI, NJ, 0, false, false, false, 1, HO, WO, true, true, 1>(acc, a, P, mrow0, ncol0, Ws,
+                                                                                   nullptr);
     else
-        wave_epi_i8<COUT, MI, NJ, 0, false, false, false, false, HO, WO, true, true, 1>(acc, a, P, mrow0, ncol0, Ws,
-                                                                                       nullptr);
+        wave_epi_i8<COUT, MI, NJ, 0, false, false, false, 0, HO, WO, true, true, 1>(acc, a, P, mrow0, ncol0, Ws,
+                                                                                   nullptr);
 }
 
 // ... then the shortcut's, with that tile as its residual.
@@ -442,11 +455,11 @@ __device__ __forceinline__ void wave_epi_pair_add(const v16i (&acc)[MI][NJ], con
 #define FF_EPI(BN, RG) \
     wave_epi_i8<COUT, MI, NJ, 0, true, BN, false, RG, HO, WO, true, true, 2>(acc, b, P, mrow0, ncol0, Ws, Lw)
     if (b.flags & FFK_EPI_BN) {
-        if (rng) FF_EPI(true, true);
-        else FF_EPI(true, false);
+        if (rng) FF_EPI(true, 1);
+        else FF_EPI(true, 0);
     } else {
-        if (rng) FF_EPI(false, true);
-        else FF_EPI(false, false);
+        if (rng) FF_EPI(false, 1);
+        else FF_EPI(false, 0);
     }
 #undef FF_EPI
 }
@@ -1870,6 +1883,7 @@ constexpr int STEM_WG_PER_CU = FF_STEM_WG_PER_CU;
 //   6    FFK_EPI_INSCALE (FFW2/FFW3: flags dispatched inside)
 //   7    raw int32 accumulators
 //   8-13 0-5 with FFK_EPI_IN_RANGE
+//   16, 18, 19, 21  8, 10, 11, 13 with FFK_EPI_FMA_TAIL
 constexpr int STEM_EPI_INSC = 6, STEM_EPI_RAW = 7;
 // The epilogue's workgroup barrier: the BN table is loaded once and waited
 // for before the first tile's patch barrier, and each wave flushes only its
@@ -2043,7 +2057,8 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
         const int mw = m0 + wave * 32;
         if constexpr (EPI == STEM_EPI_RAW) wave_epi_wide<COUT, 1, 2, false>(acc, a, mw, 0);
         else if constexpr (EPI == STEM_EPI_INSC) wave_epilogue_f<COUT, 1, 2, true, H, W>(acc, a, prm, mw, 0, Ws, Ls);
-        else wave_epi_i8<COUT, 1, 2, (EPI & 7) % 3, false, ((EPI & 7) >= 3), false, (EPI >= 8), H, W, false,
+        else wave_epi_i8<COUT, 1, 2, (EPI & 7) % 3, false, ((EPI & 7) >= 3), false, EPI >= 16 ? 2 : (EPI >= 8 ? 1 : 0),
+                         H, W, false,
                          FF_STEM_EPI_SYNC>(acc, a, prm, mw, 0, Ws, Ls);
     }
 }

@@ -21,12 +21,16 @@ void launch_stem(const ConvArgs& a, int grid, hipStream_t s) {
     else if (a.flags & FFK_EPI_INSCALE) epi = STEM_EPI_INSC;
     else epi = (a.flags & FFK_EPI_PRELU ? (a.flags & FFK_EPI_PRELU_LE1 ? 2 : 1) : 0) + (a.flags & FFK_EPI_BN ? 3 : 0) +
                (a.flags & FFK_EPI_IN_RANGE ? 8 : 0);
+    // the one-rounding tail where the host proved it (FFK_EPI_FMA_TAIL): for
+    // the in-range forms without the compare/select PReLU
+    if (epi >= 8 && epi != 9 && epi != 12 && (a.flags & FFK_EPI_FMA_TAIL)) epi += 8;
     stem_fn fn;
     const bool rgb8 = (a.flags & FFK_IN_RGB8) != 0;
     switch (epi) {
 #define FF_STEM_CASE(E) case E: fn = rgb8 ? &launch_stem_as<true, E> : &launch_stem_as<false, E>; break;
     FF_STEM_CASE(0) FF_STEM_CASE(1) FF_STEM_CASE(2) FF_STEM_CASE(3) FF_STEM_CASE(4) FF_STEM_CASE(5)
     FF_STEM_CASE(8) FF_STEM_CASE(9) FF_STEM_CASE(10) FF_STEM_CASE(11) FF_STEM_CASE(12) FF_STEM_CASE(13)
+    FF_STEM_CASE(16) FF_STEM_CASE(18) FF_STEM_CASE(19) FF_STEM_CASE(21)
     FF_STEM_CASE(STEM_EPI_INSC)
     default: fn = rgb8 ? &launch_stem_as<true, STEM_EPI_RAW> : &launch_stem_as<false, STEM_EPI_RAW>; break;
 #undef FF_STEM_CASE

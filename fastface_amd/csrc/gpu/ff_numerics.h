@@ -42,6 +42,16 @@ __device__ __forceinline__ int32_t requant_haz_in_range(float t) {
     return (int32_t)__builtin_amdgcn_fmed3f(r, -128.0f, 127.0f);
 }
 
+// The last two roundings of the in-range requant taken as one (the host
+// proves per launch that no value the launch can produce tells them apart:
+// ffk_requant_fma_ok, FFK_EPI_FMA_TAIL): r = RN(f*inv + copysign(0.5, f)),
+// the clamp and the truncation as above.  sign(f*inv) is sign(f) because
+// inv > 0 there.
+__device__ __forceinline__ int32_t requant_fma_in_range(float f, float inv) {
+    const float r = __builtin_fmaf(f, inv, copysignf(0.5f, f));
+    return (int32_t)__builtin_amdgcn_fmed3f(r, -128.0f, 127.0f);
+}
+
 // Conv epilogue for one element (int8_epilogue.c:52-93, FFW4 call site
 // libfastface.c:389-392):
 //   f = RN(RN(RN((float)acc * in_scale) * ws) + bias)

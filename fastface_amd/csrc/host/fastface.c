@@ -218,7 +218,7 @@ static int set_io(FastFace* ff, const void* in, float* out, void* stream, int ba
 /* The epilogue flags a step launches with: the plan's, less the proven
  * fast forms when the context runs the general ones
  * (fastface_set_epilogue_forms). */
-#define FF_FAST_EPI (FFK_EPI_PRELU_LE1 | FFK_EPI_IN_RANGE)
+#define FF_FAST_EPI (FFK_EPI_PRELU_LE1 | FFK_EPI_IN_RANGE | FFK_EPI_FMA_TAIL)
 static int step_flags(const FastFace* ff, const FfStep* st)
 {
     return ff->general_epi ? st->flags & ~FF_FAST_EPI : st->flags;

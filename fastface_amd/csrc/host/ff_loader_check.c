@@ -13,7 +13,10 @@
  * (ff_plan_pair: a stride-2 conv and the shortcut adding its output, one
  * launch) and how many of them let the second step write a buffer the pair
  * still reads (its own input, the first step's input or output), which must
- * be none; exits 0 (a sanitizer finding aborts with its report and a
+ * be none; "in_range <n> fma_tail <n> fma_bad <n>": the conv launches with
+ * FFK_EPI_IN_RANGE and with FFK_EPI_FMA_TAIL, and those of the latter
+ * without the former or with a residual / in-scale (must be none); exits 0
+ * (a sanitizer finding aborts with its report and a
  * non-zero status).  With <dump>, the plan's weight arena goes to <dump>.bin
  * and, one line per region, "conv|wino|bn|fc <op> <offset> <bytes>" to
  * <dump>.txt, and the parameter arena to <dump>.params.bin. */
@@ -55,6 +58,17 @@ int main(int argc, char** argv)
                         overlaps++;
         }
         printf("pairs %d overlaps %d\n", pairs, overlaps);
+        int in_range = 0, fma = 0, fma_bad = 0;
+        for (int s = 0; s < p.n_steps; s++) {
+            const int f = p.steps[s].flags;
+            if (p.steps[s].kind != 1) continue;
+            in_range += (f & FFK_EPI_IN_RANGE) != 0;
+            if (f & FFK_EPI_FMA_TAIL) {
+                fma++;
+                fma_bad += !(f & FFK_EPI_IN_RANGE) || (f & (FFK_EPI_ADD | FFK_EPI_INSCALE));
+            }
+        }
+        printf("in_range %d fma_tail %d fma_bad %d\n", in_range, fma, fma_bad);
     }
     if (!prc && argc > 4) {
         char path[4096];

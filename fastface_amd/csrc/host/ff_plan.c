@@ -35,12 +35,12 @@
 /* Weight-arena contents are produced after the walk, as independent jobs:
  * the walk only places them (offsets), the arena is then allocated once at
  * its final size and the jobs fill it on a few threads. */
-enum { JOB_CONV, JOB_WINO, JOB_BN, JOB_FC };
+enum { JOB_CONV, JOB_WINO, JOB_BN, JOB_FC, JOB_FMA_TAIL };
 typedef struct {
     int kind;
     const int8_t* src;          /* conv / FC weights in the mapping */
     int cout, cin, kh, kw;      /* conv; FC: cout = N, cin = K */
-    int r0, r1;                 /* FC: rows of this job */
+    int r0, r1;                 /* FC: rows of this job; FMA_TAIL: r0 the step */
     int fc_hw, fc_c, flat;      /* FC: NCHW flatten -> NHWC column order */
     size_t dst;                 /* bytes into the weight arena */
     size_t p_off;               /* BN: floats into the parameter arena */
@@ -117,10 +117,16 @@ static size_t alloc_weights(Builder* b, size_t n)
     return off;
 }
 
-static void run_job(const FfPlan* p, const PackJob* j, int8_t* row)
+static void run_job(FfPlan* p, const PackJob* j, int8_t* row)
 {
     int8_t* dst = p->w_host + j->dst;
     switch (j->kind) {
+    case JOB_FMA_TAIL: {        /* (each job owns its step's flags) */
+        FfStep* st = &p->steps[j->r0];
+        if (ffk_requant_fma_ok(p->p_host + j->p_off, j->cout, j->cin, st->flags))
+            st->flags |= FFK_EPI_FMA_TAIL;
+        break;
+    }
     case JOB_CONV:
         ffk_pack_conv_weights(j->src, j->cout, j->cin, j->kh, j->kw, dst);
         break;
@@ -152,7 +158,7 @@ static void run_job(const FfPlan* p, const PackJob* j, int8_t* row)
 }
 
 typedef struct {
-    const FfPlan* p;
+    FfPlan* p;
     const PackJob* jobs;
     int n_jobs, next, row_bytes;
     pthread_mutex_t mu;
@@ -347,8 +353,15 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
             if (slope && ffk_prelu_le1_ok(P, C, op->Kh * op->Kw * op->Cin, add_k >= 0))
                 s->flags |= FFK_EPI_PRELU_LE1;
             /* requant values provably finite and below 2^31: no x86 out-of-range case */
-            if (ffk_requant_in_range(P, C, op->Kh * op->Kw * op->Cin, s->flags))
+            if (ffk_requant_in_range(P, C, op->Kh * op->Kw * op->Cin, s->flags)) {
                 s->flags |= FFK_EPI_IN_RANGE;
+                /* without a residual: its last two roundings as one, where no
+                 * value of the layer tells them apart (a job: the proof
+                 * searches per channel) */
+                if (!(s->flags & (FFK_EPI_ADD | FFK_EPI_INSCALE)))
+                    add_job(&B, (PackJob){ JOB_FMA_TAIL, NULL, C, op->Kh * op->Kw * op->Cin, 0, 0,
+                                           p->n_steps - 1, 0, 0, 0, 0, 0, s->p_off });
+            }
             A = X; A_scale = eff_scale;
             if (pc && m->scale_pc[eff]) A_pc = m->scale_pc[eff];
             last_conv = p->n_steps - 1;

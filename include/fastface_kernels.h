@@ -98,6 +98,15 @@ typedef struct { const float* in; float* out; } ffk_io;
                                    case (NaN or |r| >= 2^31 -> -128): the same
                                    values, two operations fewer.  Ignored with
                                    FFK_EPI_INSCALE. */
+#define FFK_EPI_FMA_TAIL 0x800  /* with FFK_EPI_IN_RANGE, on a launch without
+                                   FFK_EPI_ADD or FFK_EPI_INSCALE: the caller
+                                   guarantees (ffk_requant_fma_ok) that the
+                                   requant's last two roundings,
+                                   RN(RN(f*inv) + copysign(0.5, f)), may be
+                                   taken as one, fma(f, inv, copysign(0.5, f)),
+                                   with the same int8 result for every value
+                                   the launch can produce: one operation
+                                   fewer.  No reference counterpart. */
 #define FFK_SHARED_GPU   0x400  /* launch-choice hint, no effect on the
                                    values: another launch of the same size
                                    runs at the same time (the two halves of a
@@ -180,6 +189,23 @@ int    ffk_prelu_le1_ok(const float* params, int cout, int ktotal, int with_add)
  * * max(1, |slope|) * |inv|, widened for the fp32 roundings, stays below
  * 2^31 - 128.  0 with FFK_EPI_INSCALE. */
 int    ffk_requant_in_range(const float* params, int cout, int ktotal, int flags);
+
+/* 1 if a conv's parameter block (host memory) allows FFK_EPI_FMA_TAIL for
+ * a reduction of ktotal = kh*kw*cin int8 products with these epilogue flags
+ * (FFK_EPI_PRELU selects the slope row; 0 with FFK_EPI_ADD or
+ * FFK_EPI_INSCALE, or where ffk_requant_in_range fails).  With f the
+ * pre-requant value and p = f*inv exact, one rounding of p + copysign(0.5, p)
+ * truncates to another integer than the reference's two roundings only when
+ * |p| lies strictly between 1/2 - 2^-25 - 2^-26 and 1/2 - 2^-25: there the
+ * reference's first rounding lands on 1/2 - 2^-25 and its second one rounds
+ * the tie up to 1 (at every other level the midpoint that separates the
+ * two is not a float, and its exact ties round alike).  Per channel (inv
+ * positive, slope >= 0): every float f whose product with inv falls in that
+ * window is found, and the check fails if the channel's pre-requant value
+ * reaches +-f for some accumulator in [-ktotal*128*128, ktotal*128*128]
+ * (binary search: that value is monotone in the accumulator, constant for
+ * a zero weight scale). */
+int    ffk_requant_fma_ok(const float* params, int cout, int ktotal, int flags);
 
 /* 1 if a kernel is compiled for this layer geometry, else 0. */
 int    ffk_conv_supported(int cin, int cout, int kh, int kw, int stride, int pad,

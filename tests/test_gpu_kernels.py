@@ -834,3 +834,89 @@ def test_s2_shortcut_pair_x_even(gpu_lib, cin, cout, H, cx):
     assert np.array_equal(got[:ne].reshape(B, Ho // 2, Ho // 2, cout), X_exp[:, ::2, ::2, :])
     assert (got[ne:].view(np.uint8) == 0x5A).all()
     assert np.array_equal(dBN.get(np.int8, (B, Ho, Ho, cout)), BN_exp)
+
+
+# ---- FFK_EPI_FMA_TAIL: the requant's last two roundings as one fma ----
+FMA_MODES = ["none", "prelu_le1", "prelu_bn_le1", "bn_only"]
+
+
+@pytest.mark.parametrize("split", [True, False, "direct"], ids=["splitk", "wholek", "direct"])
+@pytest.mark.parametrize("mode", FMA_MODES)
+@pytest.mark.parametrize("cin,cout,k,s,H", EPI_SHAPES)
+def test_fma_tail_epilogue(gpu_lib, oracle, mode, cin, cout, k, s, H, split):
+    """With parameters the host proof accepts (ffk_requant_fma_ok), the
+    one-rounding tail gives the oracle's int8 values on every kernel variant,
+    exact .5 ties and negative zero included."""
+    if split is True and (cin, cout, k, s, H) not in SPLIT_SHAPES:
+        pytest.skip("no split-K variant for this geometry")
+    r = rng(1550 + cin + cout + H + FMA_MODES.index(mode))
+    rp = rng(1510 + cin + cout + H + FMA_MODES.index(mode))   # parameters: the same for every batch
+    if split == "direct":
+        B = _direct_batch(gpu_lib, cin, cout, k, s, H)
+        idx = sorted({0, B // 2, B - 1})
+        split = False
+    else:
+        B = 1 if split else 2
+        idx = list(range(B))
+    x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
+    ws, bias, inv = _unsaturated_params(rp, cout, k * k * cin)
+    ws[0], bias[0], inv[0] = 0.5, 0.0, 1.0 / 64        # exact .5 ties after scaling
+    ws[4], bias[4] = -1e-3, -0.0
+    rows = dict(ws=ws, bias=bias, inv=inv)
+    ekw = dict(ws=ws, bias=bias, inv_pc=inv)
+    flags = fa.FFK_EPI_BIAS
+    if "prelu" in mode:
+        slope = rp.uniform(0.05, 0.3, cout).astype(F32)
+        slope[7:9] = [1.0, 0.0]
+        rows["slope"] = slope; ekw["prelu"] = slope
+        flags |= fa.FFK_EPI_PRELU | fa.FFK_EPI_PRELU_LE1
+    bn = "bn" in mode
+    if bn:
+        bsin = r.uniform(1e-3, 5e-2, cout).astype(F32)
+        bns = r.uniform(0.5, 1.5, cout).astype(F32)
+        bno = r.normal(0, 0.05, cout).astype(F32)
+        binv = (1.0 / r.uniform(0.01, 0.1, cout)).astype(F32)
+        rows.update(bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
+        flags |= fa.FFK_EPI_BN
+    P = params_block(cout, **rows)
+    assert gpu_lib.ffk_requant_fma_ok(P.ctypes.data, cout, k * k * cin, flags) == 1
+    got_x, got_bn = run_conv(gpu_lib, x, w, s, k // 2, params=P,
+                             flags=flags | fa.FFK_EPI_IN_RANGE | fa.FFK_EPI_FMA_TAIL, want_bn=bn, split=split)
+    exp_x = oracle.fused_epilogue(oracle.conv_i32(x[idx], w, s, k // 2), **ekw)
+    assert 0.05 < np.mean(np.abs(exp_x) < 127)
+    assert np.array_equal(got_x[idx], exp_x)
+    if bn:
+        exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno, inv_pc=binv)
+        assert np.array_equal(got_bn[idx], exp_bn)
+
+
+def test_fma_tail_window_is_real(gpu_lib, oracle):
+    """Where the proof rejects, the flag would change results: channel 0 of a
+    1x1 layer has accumulators -1, 0 and 1 and a weight scale and inv that put
+    f*inv inside the one window where the two tails differ.  Without the flag
+    the kernel gives the reference's -1 / 0 / 1, with it (forced, against the
+    proof) 0 / 0 / 0; every other channel is unaffected."""
+    lib = gpu_lib
+    r = rng(1600)
+    B, H, C_ = 1, 56, 64
+    x = r.integers(-3, 4, size=(B, H, H, C_), dtype=np.int8)
+    x[..., 0] = r.integers(-1, 2, size=(B, H, H), dtype=np.int8)
+    w = r.integers(-2, 3, size=(C_, C_, 1, 1), dtype=np.int8)
+    w[0] = 0
+    w[0, 0] = 1                                          # channel 0: acc = x[..., 0]
+    ws = r.uniform(1e-2, 5e-2, C_).astype(F32)
+    inv = r.uniform(5, 20, C_).astype(F32)
+    bias = r.normal(0, 0.1, C_).astype(F32)
+    ws[0], inv[0], bias[0] = 0.1515151411294937, 3.3, 0.0
+    P = params_block(C_, ws=ws, bias=bias, inv=inv)
+    flags = fa.FFK_EPI_BIAS
+    assert lib.ffk_requant_fma_ok(P.ctypes.data, C_, C_, flags) == 0
+    exp = oracle.fused_epilogue(oracle.conv_i32(x, w, 1, 0), ws=ws, bias=bias, inv_pc=inv)
+    assert set(np.unique(exp[..., 0])) == {-1, 0, 1}
+    plain, _ = run_conv(lib, x, w, 1, 0, params=P, flags=flags | fa.FFK_EPI_IN_RANGE, split=False)
+    forced, _ = run_conv(lib, x, w, 1, 0, params=P, flags=flags | fa.FFK_EPI_IN_RANGE | fa.FFK_EPI_FMA_TAIL,
+                         split=False)
+    assert np.array_equal(plain, exp)
+    assert (forced[..., 0] == 0).all()
+    assert np.array_equal(forced[..., 1:], exp[..., 1:])

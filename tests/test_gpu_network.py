@@ -178,10 +178,16 @@ def test_stage_outputs_stored_at_even_pixels(ff, gpu_lib):
         if info.kh == 1:
             shortcuts.append((info.cin, info.cout, info.stride, info.hin, info.hout))
     assert writers == [(64, 112), (64, 56), (128, 28), (256, 14)]
-    # every conv of the synthetic model has requant values provably in range
+    # every conv of the synthetic model has requant values provably in range;
+    # 19 launches without a residual also take the one-rounding tail
+    n_fma = 0
     for s in range(gpu_lib.fastface_num_steps(ff.ff)):
         assert gpu_lib.fastface_get_step(ff.ff, s, C.byref(info)) == 0
         assert info.kind != 1 or info.flags & fa.FFK_EPI_IN_RANGE, s
+        if info.kind == 1 and info.flags & fa.FFK_EPI_FMA_TAIL:
+            assert not info.flags & (fa.FFK_EPI_ADD | fa.FFK_EPI_INSCALE)
+            n_fma += 1
+    assert n_fma == 19
     assert shortcuts == [(64, 64, 1, 56, 56), (64, 128, 1, 28, 28), (128, 256, 1, 14, 14),
                          (256, 512, 1, 7, 7)]
 

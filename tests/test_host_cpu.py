@@ -313,3 +313,98 @@ def test_scale_paths_follow_the_working_directory():
     assert scale_paths(cwd, {"OPSC2_PATH": "alt/v2.bin"})[1] == "/data/run/alt/v2.bin"
     assert scale_paths(cwd, {"OPSC2_PATH": "/abs/v2.bin"})[1] == "/abs/v2.bin"
     assert scale_paths(cwd, {"OPSC2_PATH": ""})[1] == "/data/run/models/op_scales_v2.bin"
+
+
+# FFK_EPI_FMA_TAIL: the requant's last two roundings RN(RN(f*inv) + h),
+# h = copysign(0.5, f), taken as one, RN(f*inv + h) (an fma).  Exact
+# emulations of the pre-requant value f(acc) and of both tails over every
+# accumulator of a channel (numpy float32 arithmetic is IEEE single; f*inv is
+# exact in float64, and so is f*inv + h wherever |f*inv| >= 2^-5, the only
+# place where the rounding can move the truncated result).
+def _f_pre(acc, ws, bias, slope, prelu):
+    f = (acc.astype(np.float32) * np.float32(ws)).astype(np.float32)
+    f = (f + np.float32(bias)).astype(np.float32)
+    if prelu:
+        f = np.where(f < 0, (f * np.float32(slope)).astype(np.float32), f)
+    return f
+
+
+def _tail_reference(f, inv):
+    t = (f * np.float32(inv)).astype(np.float32)
+    r = (t + np.copysign(np.float32(0.5), t)).astype(np.float32)
+    return np.clip(np.trunc(r), -128, 127)
+
+
+def _tail_fma(f, inv):
+    s = f.astype(np.float64) * float(np.float32(inv)) + np.copysign(0.5, f.astype(np.float64))
+    return np.clip(np.trunc(s.astype(np.float32)), -128, 127)
+
+
+def _fma_ok(lib, ws, bias, inv, slope, K, prelu=True, flags=0):
+    P = np.zeros((fa.FFK_NPARAM, 1), np.float32)
+    P[fa.FFK_P_WS], P[fa.FFK_P_BIAS], P[fa.FFK_P_INV], P[fa.FFK_P_SLOPE] = ws, bias, inv, slope
+    fl = fa.FFK_EPI_BIAS | (fa.FFK_EPI_PRELU if prelu else 0) | flags
+    return lib.ffk_requant_fma_ok(P.ctypes.data, 1, K, fl)
+
+
+def test_fma_tail_proof_equals_brute_force():
+    """ffk_requant_fma_ok accepts a channel exactly when no accumulator in
+    [-K*128^2, K*128^2] gives another int8 with the one-rounding tail: every
+    accumulator of 1024-deep channels whose PReLU branch is dense near
+    f*inv = -1/2 (small slopes; the layers where the proof rejects), and of
+    shallow channels with natural parameters."""
+    lib = fa.load()
+    K = 1024
+    acc = np.arange(-K * 16384, K * 16384 + 1, dtype=np.int64)
+    seen = {True: 0, False: 0}
+    for ws, slope, target in [(2.6e-7, 2.2e-4, 15.0e6), (2.6e-7, 2.2e-4, 15.15e6), (2.6e-7, 2.2e-4, 15.3e6),
+                              (1e-7, 5e-4, 16.16e6), (2e-7, 3e-4, 9e6), (2e-7, 3e-4, 9.09e6)]:
+        inv = float(np.float32(0.5 / (target * ws * slope)))
+        f = _f_pre(acc, ws, 0.01, slope, True)
+        differs = bool((_tail_reference(f, inv) != _tail_fma(f, inv)).any())
+        seen[differs] += 1
+        assert _fma_ok(lib, ws, 0.01, inv, slope, K) == (0 if differs else 1), (ws, slope, inv)
+    assert seen[True] >= 2 and seen[False] >= 2          # both outcomes are exercised
+    r = np.random.default_rng(5)
+    for _ in range(40):
+        k = int(r.integers(1, 10))
+        prelu = bool(r.integers(0, 2))
+        ws = float(r.uniform(1e-4, 1e-2) * (1 if r.random() < 0.8 else -1))
+        bias, inv, slope = float(r.normal(0, 0.1)), float(r.uniform(1, 100)), float(10 ** r.uniform(-4, -0.5))
+        a = np.arange(-k * 16384, k * 16384 + 1, dtype=np.int64)
+        f = _f_pre(a, ws, bias, slope, prelu)
+        differs = bool((_tail_reference(f, inv) != _tail_fma(f, inv)).any())
+        assert _fma_ok(lib, ws, bias, inv, slope, k, prelu) == (0 if differs else 1)
+
+
+def test_fma_tail_proof_rejects_the_window():
+    """The one place the two tails differ: f*inv strictly between
+    1/2 - 2^-25 - 2^-26 and 1/2 - 2^-25, where the reference's first
+    rounding lands on 1/2 - 2^-25 and its second rounds the tie up to 1.
+    Here f = ws at accumulator 1 (and -ws at -1) puts f*inv inside it."""
+    lib = fa.load()
+    ws, inv = 0.1515151411294937, float(np.float32(3.3))
+    p = float(np.float32(ws)) * inv
+    assert 0.5 - 2.0 ** -25 - 2.0 ** -26 < p < 0.5 - 2.0 ** -25
+    f = _f_pre(np.array([1, -1]), ws, 0.0, 0.0, False)
+    assert list(_tail_reference(f, inv)) == [1, -1] and list(_tail_fma(f, inv)) == [0, 0]
+    assert _fma_ok(lib, ws, 0.0, inv, 0.0, 1, prelu=False) == 0
+    # the same channel whose values never reach the window: accepted
+    assert _fma_ok(lib, ws, 0.25, inv, 0.0, 1, prelu=False) == 1
+    f = _f_pre(np.arange(-16384, 16385), ws, 0.25, 0.0, False)
+    assert (_tail_reference(f, inv) == _tail_fma(f, inv)).all()
+
+
+def test_fma_tail_proof_preconditions():
+    """Only in-range launches without a residual or an in-scale qualify;
+    a zero weight scale (a constant channel) and a negative one are
+    decided like any other."""
+    lib = fa.load()
+    assert _fma_ok(lib, 1e-3, 0.1, 20.0, 0.25, 2304) == 1
+    assert _fma_ok(lib, 1e-3, 0.1, 20.0, 0.25, 2304, flags=fa.FFK_EPI_ADD) == 0
+    assert _fma_ok(lib, 1e-3, 0.1, 20.0, 0.25, 2304, flags=fa.FFK_EPI_INSCALE) == 0
+    assert _fma_ok(lib, 1e-3, 0.1, 3.0e38, 0.25, 2304) == 0           # not in range
+    assert _fma_ok(lib, 1e-3, 0.1, 20.0, -0.25, 2304) == 0            # negative slope
+    assert _fma_ok(lib, 0.0, 0.0072, 1e9, 0.075, 576) == 1            # constant channel
+    assert _fma_ok(lib, 0.0, 0.1515151411294937 / 1.0, float(np.float32(3.3)), 0.0, 576, prelu=False) == 0
+    assert _fma_ok(lib, -1e-3, 0.1, 20.0, 0.25, 2304) == 1

@@ -105,6 +105,17 @@ def test_fused_pairs_never_write_what_they_read(checker, synth_ffw4):
     assert o["pairs"] == "4" and o["overlaps"] == "0"
 
 
+def test_fma_tail_launches(checker, synth_ffw4):
+    """The plan proves the one-rounding requant tail (ffk_requant_fma_ok) on
+    19 of the synthetic FFW4's 29 in-range launches without a residual (the
+    other ten have a channel whose small PReLU slope makes every float near
+    f*inv = -1/2 reachable); none of an FFW3 model (in-scale on every conv)."""
+    o = run(checker, synth_ffw4)
+    assert o["in_range"] == "53" and o["fma_tail"] == "19" and o["fma_bad"] == "0"
+    o = run(checker, synth.synthetic_ffw4_path(3, version=3))
+    assert o["fma_tail"] == "0" and o["fma_bad"] == "0"
+
+
 def test_layout_walk_matches_file(blob):
     offs, end = op_offsets(blob)
     assert len(offs) == 177 and end == len(blob)

@@ -29,7 +29,7 @@ int ffk_fc_gemm_launch(const ffk_fc_desc* d, hipStream_t s) {
         // arrive sums the int32 partial tiles and writes the fp32 outputs)
         a.counters = (unsigned*)d->workspace;
         a.ws = (int32_t*)((int8_t*)d->workspace + FF_SPLIT_COUNTER_BYTES);
-        hipLaunchKernelGGL((conv_i8_kernel<25088, 512, 1, 1, 1, 1, 128, 128, 128, FF_PF128, 2, 2, 2, FC_SPLIT>),
+        hipLaunchKernelGGL((conv_i8_kernel<25088, 512, 1, 1, 1, 1, 128, 128, 64, FF_PF, 2, 2, 2, FC_SPLIT>),
                            dim3(tiles * FC_SPLIT), dim3(256), 0, s, a);
         return ffk_check_launch("fc gemm launch");
     }
@@ -38,9 +38,10 @@ int ffk_fc_gemm_launch(const ffk_fc_desc* d, hipStream_t s) {
     return ffk_check_launch("fc gemm launch");
 }
 
-// FC GEMM split-K: K = 25088 is 196 stages of 128 bytes; 7 ranges of 28.  A
-// batch whose tiles fit the counter area and leave the GPU under-filled with
-// one workgroup per tile (fewer than two per CU) splits.
+// FC GEMM split-K: K = 25088 is 392 stages of 64 bytes; 8 ranges of 49, one
+// per XCD (conv_i8_kernel).  A batch whose tiles fit the counter area and
+// leave the GPU under-filled with one workgroup per tile (fewer than two per
+// CU) splits.
 size_t ffk_fc_split_ws_bytes(int batch) {
     const long long tiles = ((long long)(batch + 127) / 128) * (512 / 128);
     if (batch <= 0 || tiles > FF_SPLIT_MAX_WG || tiles >= 512) return 0;

@@ -540,9 +540,16 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
     int8_t* Bs = smem + 2 * BM * ROWB;
 
     const int tid = threadIdx.x;
-    const int xbid = xcd_tile(blockIdx.x, gridDim.x);
-    const int bid = xbid / SPLIT;                  // the splits of a tile are consecutive
-    const int sp = xbid - bid * SPLIT;
+    // The FC head (a 1x1 image) split 8 ways takes split = XCD (workgroups
+    // are dispatched round-robin over the 8 XCDs): each XCD streams one K
+    // range of the activations and the weights for every tile, so both are
+    // read from HBM about once (a row tile per XCD would read all the
+    // weights on every XCD).  Elsewhere the splits of a tile are
+    // consecutive within an XCD's contiguous run of tiles.
+    constexpr bool SPLIT_BY_XCD = HIN == 1 && WIN == 1 && SPLIT == 8;
+    const int xbid = SPLIT_BY_XCD ? (int)blockIdx.x : xcd_tile(blockIdx.x, gridDim.x);
+    const int bid = SPLIT_BY_XCD ? xbid >> 3 : xbid / SPLIT;
+    const int sp = SPLIT_BY_XCD ? xbid & 7 : xbid - bid * SPLIT;
     const int s_beg = sp * KSTEPS;
     const int tn = bid % a.tiles_n;
     const int tm = bid / a.tiles_n;
@@ -693,9 +700,12 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
         }
         __syncthreads();
         if (!last[0]) return;                       // another workgroup finishes this tile
-        // G partial tiles per round (NCH * G loads in flight) keep the
-        // registers within the occupancy budget
-        constexpr int G = SPLIT % 4 == 0 ? 4 : (SPLIT % 3 == 0 ? 3 : (SPLIT % 2 == 0 ? 2 : 1));
+        // G partial tiles per round (NCH * G loads in flight, at most 32
+        // 16-byte chunks per thread) keep the registers within the
+        // occupancy budget
+        constexpr int G = (SPLIT % 4 == 0 && NCH * 4 <= 32) ? 4
+                        : (SPLIT % 3 == 0 && NCH * 3 <= 32) ? 3
+                        : (SPLIT % 2 == 0 && NCH * 2 <= 32) ? 2 : 1;
         v4i s[NCH];
 #pragma unroll
         for (int c = 0; c < NCH; c++) s[c] = v4i{0, 0, 0, 0};

@@ -297,7 +297,7 @@ const ConvEntry* ff_conv_table_c128(int* n);
 const ConvEntry* ff_conv_table_c256(int* n);
 const ConvEntry* ff_conv_table_c512(int* n);
 // FC head as an MFMA GEMM (ff_conv_fc.hip)
-constexpr int FC_SPLIT = 7;
+constexpr int FC_SPLIT = 8;
 size_t ffk_fc_split_ws_bytes(int batch);
 int ffk_fc_gemm_launch(const ffk_fc_desc* d, hipStream_t s);
 

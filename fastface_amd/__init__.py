@@ -120,6 +120,7 @@ EXPORTS = [
     ("ffk_conv_noalloc", C.c_int, [C.POINTER(ffk_conv_desc), _p]),
     ("ffk_conv_s2_shortcut", C.c_int, [C.POINTER(ffk_conv_desc), C.POINTER(ffk_conv_desc), _p]),
     ("ffk_conv_variant", C.c_char_p, [C.POINTER(ffk_conv_desc)]),
+    ("ffk_conv_grid", C.c_int, [C.POINTER(ffk_conv_desc)]),
     ("ffk_winograd_supported", C.c_int, [C.c_int] * 8),
     ("ffk_winograd_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("ffk_pack_winograd_weights", C.c_int, [_p, C.c_int, C.c_int, _p]),

@@ -480,6 +480,15 @@ size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d) {
     return choose_launch(e, M, (size_t)-1, (d->flags & FFK_SHARED_GPU) != 0).ws_bytes;
 }
 
+int ffk_conv_grid(const ffk_conv_desc* d) {
+    if (!d || d->batch <= 0 || (d->flags & FFK_ALGO_WINOGRAD)) return -1;
+    const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);
+    if (!e || e->cin == 3) return -1;                // (the stem sizes its persistent grid itself)
+    const long long M = conv_pixels(d);
+    if (M > 0x7fffffffLL) return -1;
+    return choose_launch(e, M, d->workspace ? d->workspace_bytes : 0, (d->flags & FFK_SHARED_GPU) != 0).grid;
+}
+
 const char* ffk_conv_variant(const ffk_conv_desc* d) {
     if (!d || d->batch <= 0) return nullptr;
     const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);

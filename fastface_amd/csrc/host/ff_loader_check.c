@@ -5,7 +5,8 @@
  * It needs no GPU: the planner's packing and table helpers are host
  * functions of the library.
  *
- *   ff_loader_check <weights.ffw> <op_scales.bin> [<op_scales_v2.bin> | -] [<dump>]
+ *   ff_loader_check <weights.ffw> <op_scales.bin> [<op_scales_v2.bin> | -] [<dump> | -]
+ *                   [--launches <batch> ...]
  *
  * Prints "load <rc> version <v> ops <n> v2 <has_v2>" and, when the load
  * succeeded, "plan <rc> steps <n> buffers <n> weights <bytes>" and
@@ -19,11 +20,49 @@
  * (a sanitizer finding aborts with its report and a
  * non-zero status).  With <dump>, the plan's weight arena goes to <dump>.bin
  * and, one line per region, "conv|wino|bn|fc <op> <offset> <bytes>" to
- * <dump>.txt, and the parameter arena to <dump>.params.bin. */
+ * <dump>.txt, and the parameter arena to <dump>.params.bin.  With
+ * --launches, the launch list of the chain at each batch, one line per
+ * launch ("launch <batch>[/h<half>] <step> conv|fc <variant> <workgroups>
+ * <geometry> <flags>"), built as fastface.c builds its descriptors (two
+ * halves from 48 faces, FFK_SHARED_GPU) from the library's host-side
+ * launch choice: no device is involved. */
+#include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "ff_host.h"
+
+/* the chain of one half (or the whole batch) as fastface.c's run_part
+ * launches it: conv descriptors as step_desc builds them, with a workspace
+ * large enough for any split the launch may take */
+static void print_launches(const FfPlan* p, const char* tag, int batch, int shared)
+{
+    for (int s = 0; s < p->n_steps; s++) {
+        const FfStep* st = &p->steps[s];
+        if (st->kind == 2) {
+            ffk_fc_desc f;
+            memset(&f, 0, sizeof f);
+            f.batch = batch; f.n = st->fc_n; f.k = st->fc_k;
+            printf("launch %s %d fc %s %zu\n", tag, s, batch <= 16 ? "matvec" : "gemm", ffk_fc_workspace_bytes(&f));
+            continue;
+        }
+        ffk_conv_desc d;
+        memset(&d, 0, sizeof d);
+        d.batch = batch; d.cin = st->cin; d.cout = st->cout; d.kh = st->kh; d.kw = st->kw;
+        d.stride = st->stride; d.pad = st->pad; d.hin = st->hin; d.win = st->win;
+        if (st->t_in > FF_T_INPUT && p->tensors[st->t_in].even) {     /* 1x1 s2 over a compact X */
+            d.stride = 1; d.hin = st->hin / 2; d.win = st->win / 2;
+        }
+        d.flags = st->flags | ((st->t_out >= 0 && p->tensors[st->t_out].even) ? FFK_OUT_X_EVEN : 0) |
+                  (shared ? FFK_SHARED_GPU : 0);
+        d.workspace = (void*)(uintptr_t)4096;            /* (never dereferenced) */
+        d.workspace_bytes = (size_t)1 << 30;
+        const char* v = ffk_conv_variant(&d);
+        printf("launch %s %d conv %s %d %d->%d k%d s%d @%d flags 0x%x\n", tag, s, v ? v : "none",
+               ffk_conv_grid(&d), d.cin, d.cout, d.kh, d.stride, d.hin, d.flags);
+    }
+}
 
 int main(int argc, char** argv)
 {
@@ -70,7 +109,22 @@ int main(int argc, char** argv)
         }
         printf("in_range %d fma_tail %d fma_bad %d\n", in_range, fma, fma_bad);
     }
-    if (!prc && argc > 4) {
+    int la = 0;                                         /* first --launches batch */
+    for (int i = 4; i < argc; i++)
+        if (strcmp(argv[i], "--launches") == 0) { la = i + 1; break; }
+    if (!prc && la)
+        for (int i = la; i < argc; i++) {
+            const int b = atoi(argv[i]);
+            char tag[48];
+            if (b <= 0) continue;
+            if (b >= 48) {                                  /* fastface.c FF_SPLIT_MIN: two halves */
+                snprintf(tag, sizeof tag, "%d/h0", b); print_launches(&p, tag, b / 2, 1);
+                snprintf(tag, sizeof tag, "%d/h1", b); print_launches(&p, tag, b - b / 2, 1);
+            } else {
+                snprintf(tag, sizeof tag, "%d", b); print_launches(&p, tag, b, 0);
+            }
+        }
+    if (!prc && argc > 4 && strcmp(argv[4], "-") != 0 && strcmp(argv[4], "--launches") != 0) {
         char path[4096];
         snprintf(path, sizeof path, "%s.bin", argv[4]);
         FILE* f = fopen(path, "wb");

@@ -254,6 +254,11 @@ int    ffk_conv_noalloc(const ffk_conv_desc* d, void* stream);
  * NULL when no kernel applies.  No counterpart in the reference: it lets
  * tests and benchmarks name the code path they exercise. */
 const char* ffk_conv_variant(const ffk_conv_desc* d);
+/* Workgroups that launch would have (host function, no device involved);
+ * -1 for the input layer (a persistent grid sized at launch), Winograd or
+ * unsupported descriptors.  No counterpart in the reference: it lets a
+ * launch list be built without a GPU. */
+int         ffk_conv_grid(const ffk_conv_desc* d);
 
 /* The BN second output as a table: lut[c*256 + q + 128] is the reference's
  * BN requant (kernels/int8_epilogue.c:273-303 with bn != NULL) of the int8

@@ -253,3 +253,32 @@ def test_weight_arena_equals_independent_packing(checker, synth_ffw4, blob, orac
                                           bn_offset=rows[fa.FFK_P_BN_O], inv_pc=rows[fa.FFK_P_BN_INV]).T.reshape(-1)
         assert np.array_equal(got, exp), (kind, op)
     assert seen == {"conv", "wino", "bn", "fc"}
+
+
+def test_launch_lists_without_a_gpu(checker, synth_ffw4):
+    """The chain's launch list at b=1, 8, 256 and 1024 faces (two halves from
+    48), from the plan and the library's host-side launch choice: 53 convs +
+    the FC per chain or half, every conv with a kernel variant and (but the
+    persistent input layer) a workgroup count; small batches take the
+    split-K / small-grid variants, 512-face halves the large tiles."""
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0")
+    r = subprocess.run([checker, synth_ffw4, synth.OPSC_PATH, synth.OPSC2_PATH, "-", "--launches",
+                        "1", "8", "256", "1024"], capture_output=True, text=True, env=env, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    chains = {}
+    for line in r.stdout.splitlines():
+        t = line.split()
+        if t[0] == "launch":
+            chains.setdefault(t[1], []).append(t)
+    assert sorted(chains) == sorted(["1", "8", "256/h0", "256/h1", "1024/h0", "1024/h1"])
+    for tag, launches in chains.items():
+        assert len(launches) == 54, tag
+        for t in launches:
+            if t[3] == "fc":
+                assert t[4] == ("matvec" if tag in ("1", "8") else "gemm"), t
+                continue
+            assert t[4] != "none", t
+            assert int(t[5]) > 0 or t[4] == "stem", t
+    variants = lambda tag: {t[4] for t in chains[tag]}
+    assert "splitk" in variants("1") and "splitk" not in variants("1024/h0")
+    assert "patch_kg" not in variants("1024/h0") and "patch" in variants("1024/h0")

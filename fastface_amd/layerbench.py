@@ -29,7 +29,9 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
     U[1e-3,1e-2], bias N(0,0.1), PReLU slope 0.25.
     epi: prelu | prelu_le1 | prelu_le1_bn | add_bn | none | raw; an "_rng"
     suffix adds FFK_EPI_IN_RANGE (the parameters here satisfy
-    ffk_requant_in_range).  x_even: X stored at its even pixels only
+    ffk_requant_in_range); a "_planned" suffix (prelu_planned, ...) takes
+    the shorter forms the launch plan would prove for these parameters
+    (PReLU as a max, in range, the one-fma tail).  x_even: X stored at its even pixels only
     (FFK_OUT_X_EVEN, as the network stores the stem's and each stage's last X).
     graph_reps > 0: the `iters` launches are captured in one hipGraph (epis,
     if given, cycles the epilogue form per launch) and the graph is replayed
@@ -113,6 +115,14 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
         if f.endswith("_rng"):
             fl |= fa.FFK_EPI_IN_RANGE
             assert lib.ffk_requant_in_range(P.ctypes.data, cout, k * k * cin, fl) == 1
+        if f.endswith("_planned"):      # the forms the planner proves for these parameters
+            if fl & fa.FFK_EPI_PRELU and lib.ffk_prelu_le1_ok(P.ctypes.data, cout, k * k * cin,
+                                                             1 if fl & fa.FFK_EPI_ADD else 0):
+                fl |= fa.FFK_EPI_PRELU_LE1
+            if lib.ffk_requant_in_range(P.ctypes.data, cout, k * k * cin, fl):
+                fl |= fa.FFK_EPI_IN_RANGE
+                if lib.ffk_requant_fma_ok(P.ctypes.data, cout, k * k * cin, fl):
+                    fl |= fa.FFK_EPI_FMA_TAIL
         return fl
     d.flags = form_flags(epi)
     ws_bytes = 0 if no_split else lib.ffk_conv_workspace_bytes(C.byref(d))
@@ -326,7 +336,8 @@ def main():
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--epi", default="prelu",
                     choices=["prelu", "prelu_le1", "add_bn", "none", "raw", "prelu_le1_rng", "add_bn_rng",
-                             "none_rng", "prelu_le1_bn", "prelu_le1_bn_rng"])
+                             "none_rng", "prelu_le1_bn", "prelu_le1_bn_rng", "prelu_planned",
+                             "prelu_bn_planned", "none_planned"])
     ap.add_argument("--x-even", action="store_true",
                     help="store X at its even pixels only (the network's stem and stage-last convs)")
     ap.add_argument("--winograd", action="store_true",

@@ -197,11 +197,16 @@ __device__ __forceinline__ unsigned x_pix_blk(const ConvArgs& a, int mb, int r) 
 // Costs two more 16-byte LDS accesses per chunk: it pays only where the
 // conflicts dominate the flush (the stem, measured 4 % faster; the
 // 256-channel layers were up to 3 % slower).
+// XOFF: the caller gives the X byte offset of each flush chunk k (tile row
+// lane/CH + k*RPI, channels ncol0 + 16*(lane%CH); xoff[k], FF_OOB-based for
+// chunks not stored), instead of the pixel arithmetic of
+// x_pix_blk: a persistent kernel whose chunk offsets are a per-lane constant
+// plus a per-tile step (the stem) computes them with one add.
 template <int COUT, int MI, int NJ, int PRELU, bool ADD, bool BN2, bool INSC, int RANGE, int HO, int WO,
-          bool LUT_DMA = false, bool WG_SYNC = true, int STAGE = 0, bool BN_PASS = false>
+          bool LUT_DMA = false, bool WG_SYNC = true, int STAGE = 0, bool BN_PASS = false, bool XOFF = false>
 __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const ConvArgs& a,
                                             const EpiParams<NJ>& prm, int mrow0, int ncol0, int8_t* Ws,
-                                            const int8_t* Lw) {
+                                            const int8_t* Lw, const unsigned* xoff = nullptr) {
     constexpr int P = NJ * 32 + 16;
     constexpr int ROWS = MI * 32;
     constexpr int CH = NJ * 2;          // 16-byte chunks per tile row
@@ -284,6 +289,7 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
     // range and are dropped, so the flush has no branches and the table
     // reads of consecutive chunks can overlap.
     static_assert(32 % RPI == 0, "a copy instruction's rows lie in one 32-row block");
+    static_assert(!XOFF || (CH == 4 && ROWS / RPI == 2), "xoff: the stem's two chunks, row lane/4 + 16k");
     const bool xe = (HO % 2 == 0 && WO % 2 == 0) && (a.flags & FFK_OUT_X_EVEN);
     const __amdgpu_buffer_rsrc_t r_x = ff_rsrc(a.out, a.out ? (unsigned)(xe ? a.M / 4 : a.M) * COUT : 0u);
     const __amdgpu_buffer_rsrc_t r_bn = ff_rsrc(a.out_bn, BN2 ? (unsigned)a.M * COUT : 0u);
@@ -298,8 +304,14 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
             const int row = lane / CH + k * RPI;
             const int ch = lane % CH;
             const v4i v = *reinterpret_cast<const v4i*>(Ws + row * P + ch * 16);
-            const unsigned xp = x_pix_blk<HO, WO>(a, mrow0 + (k * RPI / 32) * 32, row - (k * RPI / 32) * 32);
-            __builtin_amdgcn_raw_buffer_store_b128(v, r_x, xp == FF_OOB ? FF_OOB : xp * COUT + ncol0 + ch * 16, 0, 0);
+            unsigned xo;
+            if constexpr (XOFF) {
+                xo = xoff[k];
+            } else {
+                const unsigned xp = x_pix_blk<HO, WO>(a, mrow0 + (k * RPI / 32) * 32, row - (k * RPI / 32) * 32);
+                xo = xp == FF_OOB ? FF_OOB : xp * COUT + ncol0 + ch * 16;
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(v, r_x, xo, 0, 0);
         }
 #pragma unroll
         for (int c0 = 0; c0 < CH; c0 += CPI) {
@@ -342,8 +354,14 @@ __device__ __forceinline__ void wave_epi_i8(const v16i (&acc)[MI][NJ], const Con
         const int m = mrow0 + row;
         const v4i v = *reinterpret_cast<const v4i*>(Ws + row * P + ch * 16);
         // (row = lane/CH + k*RPI: block k*RPI/32, a compile-time one)
-        const unsigned xp = x_pix_blk<HO, WO>(a, mrow0 + (k * RPI / 32) * 32, row - (k * RPI / 32) * 32);
-        __builtin_amdgcn_raw_buffer_store_b128(v, r_x, xp == FF_OOB ? FF_OOB : xp * COUT + ncol0 + ch * 16, 0, 0);
+        unsigned xo;
+        if constexpr (XOFF) {
+            xo = xoff[k];
+        } else {
+            const unsigned xp = x_pix_blk<HO, WO>(a, mrow0 + (k * RPI / 32) * 32, row - (k * RPI / 32) * 32);
+            xo = xp == FF_OOB ? FF_OOB : xp * COUT + ncol0 + ch * 16;
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(v, r_x, xo, 0, 0);
         if (BN2) {
             const int8_t* L = Lw + (ch * 16) * FF_LUT_PITCH + 128;
             v4i o;
@@ -2020,6 +2038,24 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
     // (raw int32 output: no parameter block is passed, a.params may be null)
     EpiParams<2> prm = {};
     if (EPI != STEM_EPI_RAW) prm = load_epi_params<COUT, 2>(a, 0);
+    // X byte offsets of this lane's two flush chunks: chunk k is the wave's
+    // tile row lane/4 + 16k (pixel q = wave*32 + lane/4 + 16k of the tile's
+    // 224), 16 bytes at channel 16*(lane%4).  Tile t is rows oh0, oh0 + 1 of
+    // face b with t = 56b + oh0/2, so its pixel q is pixel 224t + q of the
+    // batch, and with X at even pixels only (FFK_OUT_X_EVEN) pixel q is stored
+    // iff q < 112 and q is even, at even-pixel index 56t + q/2.  Offset = a
+    // per-lane constant + t * step; chunks not stored start at FF_OOB, which
+    // stays out of the tensor's range (a.M * COUT < 2^31) after the step.
+    const bool xev = a.flags & FFK_OUT_X_EVEN;
+    unsigned xo0[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int q = wave * 32 + (lane >> 2) + 16 * k;
+        const unsigned piece = (unsigned)(lane & 3) * 16;
+        xo0[k] = !xev ? (unsigned)q * COUT + piece
+                      : (q < W && !(q & 1)) ? (unsigned)(q >> 1) * COUT + piece : FF_OOB;
+    }
+    const unsigned xstep = (xev ? W / 2 : 2 * W) * COUT;
 
     // The patch of tile t+1 is fetched into registers while tile t runs its
     // MFMAs and epilogue: the loads' latency, not their bytes, bounds this
@@ -2123,8 +2159,11 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
         const int mw = m0 + wave * 32;
         if constexpr (EPI == STEM_EPI_RAW) wave_epi_wide<COUT, 1, 2, false>(acc, a, mw, 0);
         else if constexpr (EPI == STEM_EPI_INSC) wave_epilogue_f<COUT, 1, 2, true, H, W>(acc, a, prm, mw, 0, Ws, Ls);
-        else wave_epi_i8<COUT, 1, 2, (EPI & 7) % 3, false, ((EPI & 7) >= 3), false, EPI >= 16 ? 2 : (EPI >= 8 ? 1 : 0),
-                         H, W, false, FF_STEM_EPI_SYNC, 0, true>(acc, a, prm, mw, 0, Ws, Ls);
+        else {
+            const unsigned xoff[2] = {xo0[0] + (unsigned)t * xstep, xo0[1] + (unsigned)t * xstep};
+            wave_epi_i8<COUT, 1, 2, (EPI & 7) % 3, false, ((EPI & 7) >= 3), false, EPI >= 16 ? 2 : (EPI >= 8 ? 1 : 0),
+                        H, W, false, FF_STEM_EPI_SYNC, 0, true, true>(acc, a, prm, mw, 0, Ws, Ls, xoff);
+        }
     }
 }
 

@@ -554,6 +554,59 @@ def test_x_even_stem(gpu_lib, oracle, rgb8, in_range):
     assert np.array_equal(got_bn, exp_bn)
 
 
+STEM_MODES = ["none", "prelu", "prelu_bn"]
+STEM_FORMS = ["general", "in_range", "fma"]
+STEM_CASES = [(m, f, xe, 3) for m in STEM_MODES for f in STEM_FORMS for xe in (False, True)] + \
+             [("prelu_bn", "fma", False, 23), ("prelu_bn", "fma", True, 23), ("none", "general", False, 23)]
+
+
+@pytest.mark.parametrize("mode,form,x_even,B", STEM_CASES)
+def test_stem_epilogue_forms(gpu_lib, oracle, mode, form, x_even, B):
+    """The input layer's int8 epilogue variants (no activation / PReLU /
+    PReLU + BN second output; the general, in-range and one-fma-tail
+    requant) with X at every pixel and at its even pixels; at 23 faces the
+    persistent workgroups walk several tiles, so the flush offsets step per
+    tile."""
+    r = rng(1700 + B + 3 * STEM_FORMS.index(form) + STEM_MODES.index(mode) + 9 * x_even)
+    rp = rng(1691)                               # parameters: the same in every case
+    w = r.integers(-128, 128, size=(64, 3, 3, 3), dtype=np.int8)
+    inv_in = np.array([127.0, 126.9, 127.3], np.float32)
+    faces = r.uniform(-1.0, 1.0, size=(B, 112, 112, 3)).astype(F32)
+    ws, bias, winv = _unsaturated_params(rp, 64, 27)
+    rows = dict(ws=ws, bias=bias, inv=winv)
+    ekw = dict(ws=ws, bias=bias, inv_pc=winv)
+    flags = fa.FFK_EPI_BIAS
+    slope = rp.uniform(0.05, 0.3, 64).astype(F32)
+    if "prelu" in mode:
+        rows["slope"] = slope
+        ekw["prelu"] = slope
+        flags |= fa.FFK_EPI_PRELU | (0 if form == "general" else fa.FFK_EPI_PRELU_LE1)
+    bsin = rp.uniform(1e-3, 5e-2, 64).astype(F32)
+    bns = rp.uniform(0.5, 1.5, 64).astype(F32)
+    bno = rp.normal(0, 0.05, 64).astype(F32)
+    binv = (1.0 / rp.uniform(0.01, 0.1, 64)).astype(F32)
+    bn = "bn" in mode
+    if bn:
+        rows.update(bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
+        flags |= fa.FFK_EPI_BN
+    P = params_block(64, **rows)
+    if form != "general":
+        assert gpu_lib.ffk_requant_in_range(P.ctypes.data, 64, 27, flags) == 1
+        flags |= fa.FFK_EPI_IN_RANGE
+    if form == "fma":
+        assert gpu_lib.ffk_requant_fma_ok(P.ctypes.data, 64, 27, flags) == 1
+        flags |= fa.FFK_EPI_FMA_TAIL
+    got_x, got_bn = run_conv(gpu_lib, faces, w, 1, 1, params=P, flags=flags, in_inv=inv_in, want_bn=bn,
+                             x_even=x_even)
+    q = oracle.quant_input(faces, inv_in)
+    exp_x = oracle.fused_epilogue(oracle.conv_i32(q, w, 1, 1), **ekw)
+    assert 0.05 < np.mean(np.abs(exp_x) < 127)
+    assert np.array_equal(got_x, exp_x[:, ::2, ::2] if x_even else exp_x)
+    if bn:
+        exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno, inv_pc=binv)
+        assert np.array_equal(got_bn, exp_bn)
+
+
 @pytest.mark.parametrize("B", [2, 341])
 def test_x_even_winograd(gpu_lib, oracle, B):
     """The Winograd path keeps pixel (0, 0) of each 2x2 output block; at 341

@@ -107,7 +107,8 @@ struct ConvArgs {
     int M;
     int flags;
     float in_scale;
-    int tiles_n;
+    int tiles_n;            // column tiles of the grid (cout / tile width); the
+                            // kernels use their compile-time COUT / BN, the same value
 };
 
 // ---------------------------------------------------------------------------
@@ -625,8 +626,8 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
     const int bid = SPLIT_BY_XCD ? xbid >> 3 : xbid / SPLIT;
     const int sp = SPLIT_BY_XCD ? xbid & 7 : xbid - bid * SPLIT;
     const int s_beg = sp * KSTEPS;
-    const int tn = bid % a.tiles_n;
-    const int tm = bid / a.tiles_n;
+    const int tn = bid % (COUT / BN);              // (tiles_n = COUT / BN: a compile-time divisor)
+    const int tm = bid / (COUT / BN);
     const int m0 = tm * BM;
 
     // implicit-im2col row bookkeeping for this thread's A pieces
@@ -882,8 +883,8 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv_dma_kernel(ConvArgs a)
     const __amdgpu_buffer_rsrc_t r_in = ff_rsrc(a.in, (unsigned)(a.M / HWO) * (HIN * WIN * CIN));
     const __amdgpu_buffer_rsrc_t r_w = ff_rsrc(a.w, (unsigned)KSTEPS * COUT * FF_KSTEP);
     const int xbid = xcd_tile(blockIdx.x, gridDim.x);
-    const int tn = xbid % a.tiles_n;
-    const int tm = xbid / a.tiles_n;
+    const int tn = xbid % (COUT / BN);             // (tiles_n = COUT / BN: a compile-time divisor)
+    const int tm = xbid / (COUT / BN);
     const int m0 = tm * BM;
 
     // This thread's pieces: wave load j of wave w fills lines (j*NW + w)*4 ..
@@ -1059,8 +1060,8 @@ __global__ __launch_bounds__(WM * WN * 64, WPE) void conv3_patch_kernel(ConvArgs
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int xbid = xcd_tile(blockIdx.x, gridDim.x);
-    const int tn = xbid % a.tiles_n;
-    const int tm = xbid / a.tiles_n;
+    const int tn = xbid % (COUT / BN);             // (tiles_n = COUT / BN: a compile-time divisor)
+    const int tm = xbid / (COUT / BN);
     const int m0 = tm * BM;
     const int first = m0 - W - 1;                            // input pixel of patch pixel 0
     // the input tensor (a.M pixels; the host keeps it below 2 GiB) and the
@@ -1384,8 +1385,8 @@ __device__ __forceinline__ void conv3s2_phase_body(const ConvArgs& a, const Conv
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: scalar)
     const int lane = tid & 63;
     const int xbid = xcd_tile(blockIdx.x, gridDim.x);
-    const int tn = xbid % a.tiles_n;
-    const int tm = xbid / a.tiles_n;
+    const int tn = xbid % (COUT / BN);             // (tiles_n = COUT / BN: a compile-time divisor)
+    const int tm = xbid / (COUT / BN);
     const int m0 = tm * BM;
     const int first = m0 - WO - 1;                           // phase pixel of patch pixel 0
     // input (batch x H x W x CIN, below 2 GiB) and packed weights as buffers
@@ -1729,8 +1730,8 @@ __global__ __launch_bounds__(WM * WN * KG * 64, WPE) void conv3_patch_kg_kernel(
     const int g = wave / NWG;                                // K group (uniform per wave)
     const int wg = wave - g * NWG;                           // wave within the group
     const int xbid = xcd_tile(blockIdx.x, gridDim.x);
-    const int tn = xbid % a.tiles_n;
-    const int tm = xbid / a.tiles_n;
+    const int tn = xbid % (COUT / BN);             // (tiles_n = COUT / BN: a compile-time divisor)
+    const int tm = xbid / (COUT / BN);
     const int m0 = tm * BM;
     const int first = m0 - W - 1;
     int8_t* gbase = smem + g * GROUP_BYTES;                   // this group's patches and ring

@@ -86,9 +86,12 @@ struct ConvEntry {
     launch_pair_fn pair;  // that `fn` runs fused with (conv3s2_shortcut_kernel), or none
 };
 
-// A grid of fewer big tiles than this leaves CUs idle; the 128x128 variant
-// (four times the workgroups) is taken instead.
-constexpr int FF_MID_MAX_WG = 512;
+// A grid of fewer big tiles than this (one per CU) leaves CUs idle; the
+// 128x128 variant (four times the workgroups) is taken instead.  Between one
+// and two big tiles per CU the big tiles are kept: measured on the chain,
+// 192 faces 1.68 -> 1.59 ms and 256 faces 2.25 -> 1.97 ms against a limit
+// of 512 (1024 faces unchanged).
+constexpr int FF_MID_MAX_WG = 256;
 
 // Tile configurations: (BM, BN, MI, NJ, OCC) -- workgroup tile, wave tile in
 // 32x32 MFMA blocks, workgroups per CU.

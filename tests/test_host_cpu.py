@@ -170,11 +170,13 @@ def test_conv_variant_policy():
     assert variant(64, 64, 3, 1, 112, 1) == "patch"               # one 64-channel run
     assert variant(96, 64, 3, 1, 112, 1) is None
     assert lib.ffk_conv_variant(None) is None
-    # FFK_SHARED_GPU (one half of a split chain): the large tiles stay where the
-    # two halves' grids together fill the GPU (512->512 @7 at 512 faces: 392
-    # workgroups each), not where they do not (at 64 faces)
-    assert variant(512, 512, 3, 1, 7, 512) == "patch_kg"
-    assert variant(512, 512, 3, 1, 7, 512, flags=fa.FFK_SHARED_GPU) == "patch"
+    # The large tiles where there are at least as many as CUs (512->512 @7 at
+    # 512 faces: 392), the 128x128 K-group tiles below (at 256 faces: 196).
+    # FFK_SHARED_GPU (one half of a split chain): the two halves' grids count
+    # together (196 each at 256 faces), not where even they do not (at 64 faces)
+    assert variant(512, 512, 3, 1, 7, 512) == "patch"
+    assert variant(512, 512, 3, 1, 7, 256) == "patch_kg"
+    assert variant(512, 512, 3, 1, 7, 256, flags=fa.FFK_SHARED_GPU) == "patch"
     assert variant(512, 512, 3, 1, 7, 64, flags=fa.FFK_SHARED_GPU) == "patch_kg"
 
 

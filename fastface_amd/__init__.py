@@ -28,7 +28,7 @@ FFK_OUT_X_EVEN = 0x100
 FFK_EPI_IN_RANGE = 0x200
 FFK_EPI_FMA_TAIL = 0x800
 FFK_SHARED_GPU = 0x400
-FFK_NOALLOC_SCRATCH_BYTES = 1024 + 160 * 64 * 64 * 4
+FFK_NOALLOC_SCRATCH_BYTES = 2048 + 320 * 64 * 64 * 4
 (FFK_P_WS, FFK_P_BIAS, FFK_P_SLOPE, FFK_P_ADDSCALE, FFK_P_INV, FFK_P_BN_SIN, FFK_P_BN_S,
  FFK_P_BN_O, FFK_P_BN_INV, FFK_NPARAM) = range(10)
 

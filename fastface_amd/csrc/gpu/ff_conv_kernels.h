@@ -746,33 +746,34 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
     }
 
     if (SPLIT > 1) {
-        // Partial tiles are exchanged with the documented agent-scope
-        // release / acquire pattern, paid once per workgroup (the XCDs' L2s
-        // are not coherent with each other): every thread stores its part
-        // and waits for the stores; after the barrier one thread releases
-        // (L2 write-back) and bumps the tile's arrival count; the workgroup
-        // that arrives last acquires (L2 invalidate) and sums the partials.
+        // Partial tiles are exchanged as agent-scope monotonic accesses: the
+        // partial stores and the last workgroup's partial loads carry the sc1
+        // cache policy (what gfx950 code for a relaxed agent-scope atomic
+        // store or load uses: the store is written through the XCD's L2 and
+        // complete only when visible device-wide, the load reads the
+        // device-coherent value), every thread waits for its stores before the
+        // barrier, and one thread then bumps the tile's agent-scope arrival
+        // count.  The workgroup that arrives last sums the partials.  Only
+        // the published bytes travel past the L2: no release / acquire fence,
+        // which would write back or invalidate the whole L2 of the XCD (the
+        // XCDs' L2s are not coherent with each other) once per workgroup.
         constexpr int NCH = MI * NJ * 4;            // 16-byte chunks per thread
         constexpr int PART = BM * BN * 4;           // bytes of one partial tile
-        int8_t* part = reinterpret_cast<int8_t*>(a.ws + (size_t)bid * SPLIT * (BM * BN));
+        constexpr int CPOL_SC1 = 16;                // buffer cache policy: sc1 (device scope)
+        const __amdgpu_buffer_rsrc_t r_ws = ff_rsrc(a.ws, (unsigned)gridDim.x * PART);
+        const unsigned pbase = (unsigned)bid * SPLIT * PART;
 #pragma unroll
         for (int c = 0; c < NCH; c++) {             // chunk-major: a wave stores 1 KB runs
             const v16i& t = acc[c / (NJ * 4)][(c / 4) % NJ];
             const v4i v = {t[(c % 4) * 4], t[(c % 4) * 4 + 1], t[(c % 4) * 4 + 2], t[(c % 4) * 4 + 3]};
-            *reinterpret_cast<v4i*>(part + sp * PART + (c * 256 + tid) * 16) = v;
+            __builtin_amdgcn_raw_buffer_store_b128(v, r_ws, pbase + sp * PART + (c * 256 + tid) * 16, 0, CPOL_SC1);
         }
-        __builtin_amdgcn_s_waitcnt(0);              // this wave's stores have reached L2
+        __builtin_amdgcn_s_waitcnt(0);              // this wave's partial stores are complete
         __syncthreads();
         int* last = reinterpret_cast<int*>(smem);
-        if (tid == 0) {
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-            __builtin_amdgcn_s_waitcnt(0);          // write-back complete before the count moves
-            const bool is_last = __hip_atomic_fetch_add(&a.counters[bid], 1u, __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(SPLIT - 1);
-            if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            __builtin_amdgcn_s_waitcnt(0);
-            last[0] = is_last;
-        }
+        if (tid == 0)
+            last[0] = __hip_atomic_fetch_add(&a.counters[bid], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      (unsigned)(SPLIT - 1);
         __syncthreads();
         if (!last[0]) return;                       // another workgroup finishes this tile
         // G partial tiles per round (NCH * G loads in flight, at most 32
@@ -791,7 +792,9 @@ __global__ __launch_bounds__(256, OCC) void conv_i8_kernel(ConvArgs a) {
             for (int g = 0; g < G; g++)
 #pragma unroll
                 for (int c = 0; c < NCH; c++)
-                    t[c][g] = *reinterpret_cast<const v4i*>(part + (q0 + g) * PART + (c * 256 + tid) * 16);
+                    t[c][g] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         r_ws, pbase + (q0 + g) * PART + (c * 256 + tid) * 16, 0,
+                                                         CPOL_SC1));
 #pragma unroll
             for (int g = 0; g < G; g++)
 #pragma unroll
@@ -1667,7 +1670,7 @@ struct Plan {
 // other group writes its partial of those blocks, the owner adds them and
 // runs the epilogue on its blocks.  Integer sums are exact, so the result is
 // the whole-K kernel's.  This gives a small batch KG times the waves without
-// the global workspace and L2 write-backs of split-K across workgroups.
+// the partial tiles' round trip through memory of split-K across workgroups.
 // A small grid has one workgroup per CU, so no other workgroup fills the
 // SIMDs while its waves meet at a barrier: the steps go U at a time between
 // barriers, the weights D steps ahead in a ring of D + U slots (ps1::Plan);

@@ -63,11 +63,13 @@ constexpr launch_pair_fn s2_pair() {
 // wave), the K stages of a tile shared by `split` workgroups.
 constexpr int FF_SM_BM = 64, FF_SM_BN = 64;
 // The split path is taken when the whole-K tiling leaves most CUs idle and the
-// split grid stays small: every split workgroup pays one agent-scope L2
-// write-back (~0.4 us, serialized per XCD), so a split grid much beyond ~20
-// workgroups per XCD costs more than the shorter K chain saves.
+// split grid stays at most FF_SPLIT_MAX_WG workgroups: past that the partial
+// tiles' round trip through memory costs more than the shorter K chain saves
+// (measured on the chain at 1-32 faces with limits of 160, 256, 320 and 400:
+// 320 is fastest; against 160 it splits the long-K layers at 4 and 8 faces
+// too, 0.518 -> 0.453 ms at 4 faces and 0.613 -> 0.582 at 8).
 constexpr int FF_SPLIT_MIN_WG = 256;
-constexpr int FF_SPLIT_MAX_WG = 160;
+constexpr int FF_SPLIT_MAX_WG = 320;
 // split-K workspace: [counter per tile, fixed size][int32 partial tiles]
 constexpr size_t FF_SPLIT_COUNTER_BYTES = FF_SPLIT_MAX_WG * sizeof(unsigned);
 static_assert(FF_SPLIT_COUNTER_BYTES <= FF_WS_COUNTER_AREA, "counters stay in the reserved area");
@@ -283,10 +285,11 @@ constexpr launch_fn split_launch() {
 // never split).  The 3x3 layers with 128 input channels or more gain from it
 // (9, 18 or 36 stages of 128 bytes; the stage-2 layers measured 0.511 ->
 // 0.486 ms for the b=1 chain with 3 ranges of 3 stages).  Each workgroup's
-// partial tile costs an L2 write-back and those serialize per XCD, so fewer
-// splits can win: 256->256 @14 (12 launches at b=1) with 3 instead of 9
-// took the b=1 chain from 0.485 to 0.433 ms; 3 for the stride-2 and
-// 512-channel layers measured the same as their 6 and 9, 2 (and 4) slower.
+// partial tile makes a round trip through memory, so fewer splits can win:
+// 256->256 @14 (12 launches at b=1) with 3 instead of 9 took the b=1 chain
+// from 0.485 to 0.433 ms (and with the present exchange 0.399 ms against
+// 0.414 with 6 and 0.442 with 9); 3 for the stride-2 and 512-channel layers
+// measured the same as their 6 and 9, 2 (and 4) slower.
 // One face gives 48-156 workgroups.  The 64-channel layers' 9 stages of 64
 // bytes are too short to pay for the partial-sum exchange.
 }  // namespace ffconv

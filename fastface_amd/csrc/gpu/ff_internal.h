@@ -27,7 +27,7 @@ static constexpr int FF_KSTEP = 64;
 // A conv workspace starts with the split-K arrival counters, which every
 // split launch leaves at zero for the next one; other users of a workspace
 // (the Winograd path) keep out of these first bytes.
-static constexpr size_t FF_WS_COUNTER_AREA = 1024;
+static constexpr size_t FF_WS_COUNTER_AREA = 2048;
 
 // Integer Winograd F(2,3) path of the 64-channel 3x3 stride-1 layers
 // (ff_winograd.hip), taken by ffk_conv for FFK_ALGO_WINOGRAD.

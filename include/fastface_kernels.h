@@ -245,7 +245,7 @@ int    ffk_conv_s2_shortcut(const ffk_conv_desc* c, const ffk_conv_desc* s, void
  * overlap in time on one GPU (other streams, other threads) race and must be
  * ordered by the caller; each launch leaves the array's counter area zero for
  * the next.  Results are bit-identical to ffk_conv's. */
-#define FFK_NOALLOC_SCRATCH_BYTES ((size_t)1024 + (size_t)160 * 64 * 64 * 4)
+#define FFK_NOALLOC_SCRATCH_BYTES ((size_t)2048 + (size_t)320 * 64 * 64 * 4)
 int    ffk_conv_noalloc(const ffk_conv_desc* d, void* stream);
 /* Name of the kernel variant ffk_conv would run for this descriptor (its
  * geometry, batch and workspace): "stem", "patch" (3x3 stride-1 layers:

@@ -89,7 +89,7 @@ def conv_workspace(lib, d):
     return ws
 
 
-SPLIT_COUNTERS = 160      # uint32 arrival counters at the start of the workspace
+SPLIT_COUNTERS = 320      # uint32 arrival counters at the start of the workspace
 
 
 def split_counters_zero(lib, ws):

@@ -85,24 +85,34 @@ ConvLaunch choose_launch(const ConvEntry* e, long long M, size_t ws_avail, bool 
         l = {e->mid, e->mid_kind ? e->mid_kind : "staged128", mbn, (int)big, 1, 0, 0};
     }
     if (!e->small || big >= FF_SPLIT_MIN_WG) return l;
+    // the small-tile kernels: e->split K ranges, 3 where e->split is larger,
+    // then whole K; the first whose grid fits its limit and beats `big`
     const long long tiles = ((M + FF_SM_BM - 1) / FF_SM_BM) * (e->cout / FF_SM_BN);
-    const long long wgs = tiles * e->split;
-    if (wgs > FF_SPLIT_MAX_WG || wgs <= big) return l;
-    if (e->split > 1) {
-        // the counter area has the same size at every batch (tiles <= wgs), so
-        // launches of different sizes never see each other's partial tiles
-        // in their counters
-        const size_t cnt = FF_SPLIT_COUNTER_BYTES;
-        const size_t need = cnt + (size_t)wgs * FF_SM_BM * FF_SM_BN * sizeof(int32_t);
-        if (need > ws_avail) return l;
+    const int cand[3] = {e->split, e->split > 3 ? 3 : 1, 1};
+    for (int c = 0; c < 3; c++) {
+        const int sp = cand[c];
+        if (c > 0 && sp == cand[c - 1]) continue;
+        const long long wgs = tiles * sp;
+        const long long lim = sp > 1 ? FF_SPLIT_MAX_WG : shared ? FF_TILE64_MAX_WG_SHARED : FF_TILE64_MAX_WG;
+        if (wgs > lim || wgs <= big) continue;
+        size_t cnt = 0, need = 0;
+        if (sp > 1) {
+            // the counter area has the same size at every batch (tiles <=
+            // wgs), so launches of different sizes never see each other's
+            // partial tiles in their counters
+            cnt = FF_SPLIT_COUNTER_BYTES;
+            need = cnt + (size_t)wgs * FF_SM_BM * FF_SM_BN * sizeof(int32_t);
+            if (need > ws_avail) continue;
+        }
+        l.fn = e->small;
+        l.kind = sp > 1 ? "splitk" : "tile64";
+        l.bn = FF_SM_BN;
+        l.grid = (int)wgs;
+        l.split = sp;
         l.counter_bytes = cnt;
         l.ws_bytes = need;
+        return l;
     }
-    l.fn = e->small;
-    l.kind = "splitk";
-    l.bn = FF_SM_BN;
-    l.grid = (int)wgs;
-    l.split = e->split;
     return l;
 }
 
@@ -360,7 +370,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
             as.ws = (int32_t*)((int8_t*)d->workspace + l.counter_bytes);
         }
         as.tiles_n = d->cout / l.bn;
-        l.fn(as, l.grid, (hipStream_t)stream);
+        l.fn(as, l.grid, l.split, (hipStream_t)stream);
         const int rc = ffk_check_launch("conv launch");
         if (rc != FFK_OK) return rc;
     }

@@ -10,7 +10,7 @@ void launch_stem_as(const ConvArgs& a, int grid, int tiles_per_wg, hipStream_t s
     hipLaunchKernelGGL((stem_kernel<RGB8, EPI>), dim3(grid), dim3(STEM_NT), 0, s, a, tiles_per_wg);
 }
 
-void launch_stem(const ConvArgs& a, int grid, hipStream_t s) {
+void launch_stem(const ConvArgs& a, int grid, int, hipStream_t s) {
     (void)grid;
     const int tiles = a.M / (112 * 2);
     const int slots = 256 * STEM_WG_PER_CU;

@@ -8,36 +8,38 @@
 
 namespace ffconv {
 
-typedef void (*launch_fn)(const ConvArgs&, int grid, hipStream_t);
+// (split: the K ranges per tile choose_launch picked; only the small-tile
+// launcher reads it)
+typedef void (*launch_fn)(const ConvArgs&, int grid, int split, hipStream_t);
 
 template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int BM, int BN, int KB, int PF,
           int MI, int NJ, int OCC, int SPLIT>
-void launch_conv(const ConvArgs& a, int grid, hipStream_t s) {
+void launch_conv(const ConvArgs& a, int grid, int, hipStream_t s) {
     hipLaunchKernelGGL((conv_i8_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, BM, BN, KB, PF, MI, NJ, OCC, SPLIT>),
                        dim3(grid), dim3(256), 0, s, a);
 }
 
 template <int CIN, int COUT, int KS, int STRIDE, int HIN, int WIN, int WM, int WN, int MI, int NJ,
           int NST, int WPE>
-void launch_conv_dma(const ConvArgs& a, int grid, hipStream_t s) {
+void launch_conv_dma(const ConvArgs& a, int grid, int, hipStream_t s) {
     hipLaunchKernelGGL((conv_dma_kernel<CIN, COUT, KS, STRIDE, HIN, WIN, WM, WN, MI, NJ, NST, WPE>),
                        dim3(grid), dim3(WM * WN * 64), 0, s, a);
 }
 
 template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int WPE>
-void launch_patch(const ConvArgs& a, int grid, hipStream_t s) {
+void launch_patch(const ConvArgs& a, int grid, int, hipStream_t s) {
     hipLaunchKernelGGL((conv3_patch_kernel<CIN, COUT, H, H, WM, WN, MI, NJ, WPE>), dim3(grid),
                        dim3(WM * WN * 64), 0, s, a);
 }
 
 template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int KG, int WPE, int D, int U>
-void launch_patch_kg(const ConvArgs& a, int grid, hipStream_t s) {
+void launch_patch_kg(const ConvArgs& a, int grid, int, hipStream_t s) {
     hipLaunchKernelGGL((conv3_patch_kg_kernel<CIN, COUT, H, H, WM, WN, MI, NJ, KG, WPE, D, U>), dim3(grid),
                        dim3(WM * WN * KG * 64), 0, s, a);
 }
 
 template <int CIN, int COUT, int H, int WM, int WN, int MI, int NJ, int WPE>
-void launch_s2(const ConvArgs& a, int grid, hipStream_t s) {
+void launch_s2(const ConvArgs& a, int grid, int, hipStream_t s) {
     hipLaunchKernelGGL((conv3s2_phase_kernel<CIN, COUT, H, H, WM, WN, MI, NJ, WPE>), dim3(grid),
                        dim3(WM * WN * 64), 0, s, a);
 }
@@ -70,6 +72,18 @@ constexpr int FF_SM_BM = 64, FF_SM_BN = 64;
 // too, 0.518 -> 0.453 ms at 4 faces and 0.613 -> 0.582 at 8).
 constexpr int FF_SPLIT_MIN_WG = 256;
 constexpr int FF_SPLIT_MAX_WG = 320;
+// The whole-K 64x64 tiles (no exchange) are taken up to this many
+// workgroups, and up to FF_TILE64_MAX_WG_SHARED per half where two halves of
+// a batch run at once (FFK_SHARED_GPU).  Measured on the chain at 1-64 faces
+// with limits 0, 200, 320 and 640: 640 is fastest at 8 and 16 faces (8:
+// 0.524 ms without these tiles, 0.486 with), 200 at the 48- and 64-face
+// halves; b=1 takes them for every layer without a split (0.399 -> 0.374 ms).
+#ifndef FF_TILE64_MAX_WG
+#define FF_TILE64_MAX_WG 640
+#endif
+#ifndef FF_TILE64_MAX_WG_SHARED
+#define FF_TILE64_MAX_WG_SHARED 200
+#endif
 // split-K workspace: [counter per tile, fixed size][int32 partial tiles]
 constexpr size_t FF_SPLIT_COUNTER_BYTES = FF_SPLIT_MAX_WG * sizeof(unsigned);
 static_assert(FF_SPLIT_COUNTER_BYTES <= FF_WS_COUNTER_AREA, "counters stay in the reserved area");
@@ -118,12 +132,27 @@ constexpr int FF_MID_MAX_WG = 256;
 #define FF_KB_BIG(CIN) FF_KB(CIN)
 #define FF_PF_BIG(CIN) FF_PFS(CIN)
 #endif
+// The 64x64-tile kernels of a geometry whose long K chain is split SPLIT
+// ways at small batches: that split, 3 ranges where SPLIT is larger (for
+// batches whose SPLIT-way grid would be too large), and the whole-K tiles
+// (split 1: tiny grids of the layers without a split, or batches where no
+// split grid fits).  `split` is the one choose_launch picked.
+template <int CIN, int COUT, int KS, int S, int H, int SPLIT>
+void launch_small(const ConvArgs& a, int grid, int split, hipStream_t s) {
+#define FF_SMALL_CONV(SP) \
+    launch_conv<CIN, COUT, KS, S, H, H, FF_SM_BM, FF_SM_BN, FF_KB(CIN), 2, 1, 1, 4, SP>(a, grid, SP, s)
+    if constexpr (SPLIT > 1) {
+        if (split == SPLIT) { FF_SMALL_CONV(SPLIT); return; }
+    }
+    if constexpr (SPLIT > 3) {
+        if (split == 3) { FF_SMALL_CONV(3); return; }
+    }
+    FF_SMALL_CONV(1);
+#undef FF_SMALL_CONV
+}
 template <int CIN, int COUT, int KS, int S, int H, int SPLIT>
 constexpr launch_fn split_launch() {
-    if constexpr (SPLIT > 1)
-        return &launch_conv<CIN, COUT, KS, S, H, H, FF_SM_BM, FF_SM_BN, FF_KB(CIN), 2, 1, 1, 4, SPLIT>;
-    else
-        return nullptr;
+    return &launch_small<CIN, COUT, KS, S, H, SPLIT>;
 }
 #define FF_ENTRY(CIN, COUT, KS, S, H, SPLIT, KB, PF, BM, BN, MI, NJ, OCC)       \
     {CIN, COUT, KS, S, H, H, BM, BN,                                             \

@@ -84,6 +84,51 @@ def test_stem_int32_with_fused_input_quant(gpu_lib, oracle, B):
     assert np.array_equal(got, oracle.conv_i32(q, w, 1, 1))
 
 
+# (cin, cout, k, s, H, batch, kind, grid): the small-tile kernels of small
+# batches -- the 3-way K split of layers whose own split (6, 9) gives too
+# large a grid, and the whole-K 64x64 tiles of layers without a split or
+# where no split grid fits
+SMALL_TILE_CASES = [
+    (256, 256, 3, 2, 28, 5, "splitk", 16 * 4 * 3), (512, 512, 3, 2, 14, 8, "splitk", 7 * 8 * 3),
+    (512, 512, 3, 1, 7, 8, "splitk", 7 * 8 * 3), (128, 128, 3, 1, 28, 8, "tile64", 98 * 2),
+    (256, 512, 3, 1, 14, 8, "tile64", 25 * 8), (64, 64, 3, 1, 56, 8, "tile64", 392),
+    (64, 64, 3, 2, 112, 1, "tile64", 49), (128, 256, 1, 1, 14, 1, "tile64", 4 * 4),
+    (64, 128, 3, 1, 56, 1, "tile64", 49 * 2),
+]
+
+
+@pytest.mark.parametrize("cin,cout,k,s,H,B,kind,grid", SMALL_TILE_CASES)
+def test_small_tile_variants(gpu_lib, oracle, cin, cout, k, s, H, B, kind, grid):
+    """The small-tile kernels on the batches that take them: int32
+    accumulators and the PReLU + BN epilogue exact against the oracle."""
+    import ctypes as C
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw, d.stride, d.pad, d.hin, d.win = B, cin, cout, k, k, s, k // 2, H, H
+    n = gpu_lib.ffk_conv_workspace_bytes(C.byref(d))
+    d.workspace, d.workspace_bytes = (4096, n) if n else (None, 0)
+    assert gpu_lib.ffk_conv_variant(C.byref(d)).decode() == kind
+    assert gpu_lib.ffk_conv_grid(C.byref(d)) == grid
+    r = rng(1800 + cin + cout + H + B)
+    x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)
+    acc = oracle.conv_i32(x, w, s, k // 2)
+    assert np.array_equal(run_conv(gpu_lib, x, w, s, k // 2, raw=True), acc)
+    ws, bias, inv = _unsaturated_params(r, cout, k * k * cin)
+    slope = r.uniform(0, 0.3, cout).astype(F32)
+    bsin = r.uniform(1e-3, 5e-2, cout).astype(F32)
+    bns = r.uniform(0.5, 1.5, cout).astype(F32)
+    bno = r.normal(0, 0.05, cout).astype(F32)
+    binv = (1.0 / r.uniform(0.01, 0.1, cout)).astype(F32)
+    P = params_block(cout, ws=ws, bias=bias, inv=inv, slope=slope, bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
+    flags = fa.FFK_EPI_BIAS | fa.FFK_EPI_PRELU | fa.FFK_EPI_BN
+    got_x, got_bn = run_conv(gpu_lib, x, w, s, k // 2, params=P, flags=flags, want_bn=True)
+    exp_x = oracle.fused_epilogue(acc, ws=ws, bias=bias, prelu=slope, inv_pc=inv)
+    assert 0.05 < np.mean(np.abs(exp_x) < 127)
+    assert np.array_equal(got_x, exp_x)
+    exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno, inv_pc=binv)
+    assert np.array_equal(got_bn, exp_bn)
+
+
 def test_split_partials_back_to_back(gpu_lib, oracle):
     """Split-K launches queued back to back on one stream with no host
     synchronization between them, alternating two layers that share one
@@ -480,8 +525,8 @@ SHORTCUT_S1 = [(64, 64, 56), (64, 128, 28), (128, 256, 14), (256, 512, 7)]
 X_EVEN_CASES = [
     (64, 64, 3, 1, 56, "big", "patch"), (128, 128, 3, 1, 28, "big", "patch"),
     (256, 256, 3, 1, 14, "big", "patch"), (256, 256, 3, 1, 14, 1, "splitk"),
-    (256, 256, 3, 1, 14, 9, "patch_kg"), (64, 64, 3, 2, 112, "big", "phase"),
-    (64, 128, 3, 1, 56, 2, "patch_kg"),
+    (256, 256, 3, 1, 14, 53, "patch_kg"), (256, 256, 3, 1, 14, 9, "tile64"), (64, 64, 3, 2, 112, "big", "phase"),
+    (64, 128, 3, 1, 56, 7, "patch_kg"), (64, 128, 3, 1, 56, 2, "tile64"),
 ]
 
 
@@ -504,7 +549,7 @@ def test_x_even_output(gpu_lib, oracle, cin, cout, k, s, H, B, variant, mode):
         B = _direct_batch(gpu_lib, cin, cout, k, s, H)
         idx = sorted({0, B // 2, B - 1})
     else:
-        idx = list(range(B))
+        idx = list(range(B)) if B <= 16 else sorted({0, B // 2, B - 1})
     assert _variant_ws(gpu_lib, cin, cout, k, s, H, B) == variant
     x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
     w = r.integers(-128, 128, size=(cout, cin, k, k), dtype=np.int8)

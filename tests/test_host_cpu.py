@@ -164,10 +164,18 @@ def test_conv_variant_policy():
     assert variant(256, 256, 3, 1, 14, 1024) == "patch"          # 3x3 stride 1
     assert variant(256, 256, 3, 2, 28, 1024) == "phase"           # 3x3 stride 2
     assert variant(256, 256, 3, 1, 14, 64) == "patch_kg"           # small grid: K-groups
-    assert variant(256, 256, 3, 1, 14, 1) == "patch_kg"           # no workspace given
-    assert variant(256, 256, 3, 1, 14, 1, ws=1 << 30) == "splitk"
-    assert variant(64, 64, 3, 1, 56, 1) == "patch"                # Cout 64: one variant
-    assert variant(64, 64, 3, 1, 112, 1) == "patch"               # one 64-channel run
+    assert variant(256, 256, 3, 1, 14, 1, ws=1 << 30) == "splitk"  # tiny grid: K split 3 ways
+    assert variant(256, 256, 3, 1, 14, 1) == "tile64"             # no workspace: whole-K 64x64 tiles
+    assert variant(64, 64, 3, 1, 56, 1) == "tile64"               # no split: 49 small tiles, not 13
+    assert variant(64, 64, 3, 1, 56, 8) == "tile64"               # 392 small tiles
+    assert variant(64, 64, 3, 1, 56, 16) == "patch"               # 784: the patch tiles
+    assert variant(64, 64, 3, 1, 112, 4) == "patch"               # one 64-channel run
+    # a split grid too large for the layer's own split (9) takes 3 ranges
+    d.batch, d.cin, d.cout, d.kh, d.kw, d.stride, d.pad, d.hin, d.win = 8, 512, 512, 3, 3, 2, 1, 14, 14
+    d.workspace, d.workspace_bytes, d.flags = 4096, 1 << 30, 0
+    assert lib.ffk_conv_variant(C.byref(d)) == b"splitk" and lib.ffk_conv_grid(C.byref(d)) == 7 * 8 * 3
+    d.batch = 1
+    assert lib.ffk_conv_grid(C.byref(d)) == 1 * 8 * 9
     assert variant(96, 64, 3, 1, 112, 1) is None
     assert lib.ffk_conv_variant(None) is None
     # The large tiles where there are at least as many as CUs (512->512 @7 at

@@ -67,8 +67,11 @@
  * own I/O descriptor (d_io[part]) and its own half of the split-K
  * workspace.  Measured (ms per batch, one chain -> two halves, same box):
  * 16 0.677 -> 0.681, 32 0.754 -> 0.770, 48 0.891 -> 0.823, 96 1.42 -> 1.11,
- * 256 2.75 -> 2.33, 512 4.37 -> 3.76, 1024 7.86 -> 7.25. */
-#define FF_SPLIT_MIN 48
+ * 256 2.75 -> 2.33, 512 4.37 -> 3.76, 1024 7.86 -> 7.25; with the small-tile
+ * kernels of small grids the halves win from 24 faces on: 16 0.516 -> 0.586,
+ * 20 0.519 -> 0.566, 24 0.625 -> 0.588, 32 0.643 -> 0.637, 40 0.728 -> 0.684,
+ * 47 0.872 -> 0.722. */
+#define FF_SPLIT_MIN 24
 
 /* one captured chain per (batch, input format: 0 fp32 faces, 1 uint8 RGB) */
 typedef struct { int batch, fmt; void* exec; } GraphEntry;

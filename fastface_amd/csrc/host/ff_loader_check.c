@@ -24,7 +24,7 @@
  * --launches, the launch list of the chain at each batch, one line per
  * launch ("launch <batch>[/h<half>] <step> conv|fc <variant> <workgroups>
  * <geometry> <flags>"), built as fastface.c builds its descriptors (two
- * halves from 48 faces, FFK_SHARED_GPU) from the library's host-side
+ * halves from 24 faces, FFK_SHARED_GPU) from the library's host-side
  * launch choice: no device is involved. */
 #include <stdint.h>
 #include <stdio.h>
@@ -117,7 +117,7 @@ int main(int argc, char** argv)
             const int b = atoi(argv[i]);
             char tag[48];
             if (b <= 0) continue;
-            if (b >= 48) {                                  /* fastface.c FF_SPLIT_MIN: two halves */
+            if (b >= 24) {                                  /* fastface.c FF_SPLIT_MIN: two halves */
                 snprintf(tag, sizeof tag, "%d/h0", b); print_launches(&p, tag, b / 2, 1);
                 snprintf(tag, sizeof tag, "%d/h1", b); print_launches(&p, tag, b - b / 2, 1);
             } else {

@@ -361,14 +361,14 @@ def test_streamed_host_batch_equals_one_shot(ff, gpu_lib):
 
 
 def test_split_chain_equals_unsplit_halves(gpu_lib, synth_ffw4):
-    """Batches of 48 faces or more run as two halves, each on its own stream
+    """Batches of 24 faces or more run as two halves, each on its own stream
     inside one captured graph (fork and join), each half in its own region
     of every activation buffer, both with the FFK_SHARED_GPU tiling.  Every
-    embedding of every face equals the one-chain result of 32-face batches
-    (faces are independent) for 49, 101, 129, 256, 384 and 1025 faces
-    (halves of 24-513, each with its own workspace), captured and then
+    embedding of every face equals the one-chain result of 16-face batches
+    (faces are independent) for 25, 49, 101, 129, 256, 384 and 1025 faces
+    (halves of 12-513, each with its own workspace), captured and then
     replayed;
-    1024 uint8 faces against 32-face batches; the Winograd stage-1 path split
+    1024 uint8 faces against 16-face batches; the Winograd stage-1 path split
     against direct.  (Regression: halves that shared buffer regions corrupted
     faces from B/4 on, because a buffer holds tensors of different sizes at
     different layers and the halves run different layers at once.)"""
@@ -377,9 +377,9 @@ def test_split_chain_equals_unsplit_halves(gpu_lib, synth_ffw4):
         stream = gpu_lib.fastface_stream(f.ff)
 
         def pieces(fn, a):
-            return np.concatenate([fn(a[i:i + 32]) for i in range(0, len(a), 32)])
+            return np.concatenate([fn(a[i:i + 16]) for i in range(0, len(a), 16)])
 
-        for B in (49, 101, 129, 256, 384, 1025):
+        for B in (25, 49, 101, 129, 256, 384, 1025):
             x = synth.faces_uniform(B, 61 + B)
             exp = pieces(f.embed_batch, x)
             din, dout = Dev(gpu_lib, host=x), Dev(gpu_lib, nbytes=B * 512 * 4)

@@ -257,7 +257,7 @@ def test_weight_arena_equals_independent_packing(checker, synth_ffw4, blob, orac
 
 def test_launch_lists_without_a_gpu(checker, synth_ffw4):
     """The chain's launch list at b=1, 8, 256 and 1024 faces (two halves from
-    48), from the plan and the library's host-side launch choice: 53 convs +
+    24), from the plan and the library's host-side launch choice: 53 convs +
     the FC per chain or half, every conv with a kernel variant and (but the
     persistent input layer) a workgroup count; small batches take the
     split-K / small-grid variants, 512-face halves the large tiles."""

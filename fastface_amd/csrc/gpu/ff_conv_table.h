@@ -137,10 +137,18 @@ constexpr int FF_MID_MAX_WG = 256;
 // batches whose SPLIT-way grid would be too large), and the whole-K tiles
 // (split 1: tiny grids of the layers without a split, or batches where no
 // split grid fits).  `split` is the one choose_launch picked.
+// (three K stages of loads in flight: 1-1.6 % faster chains at 1-16 faces
+// than two; four, at two workgroups per CU, slower at 16 faces)
+#ifndef FF_SM_PF
+#define FF_SM_PF 3
+#endif
+#ifndef FF_SM_OCC
+#define FF_SM_OCC 4
+#endif
 template <int CIN, int COUT, int KS, int S, int H, int SPLIT>
 void launch_small(const ConvArgs& a, int grid, int split, hipStream_t s) {
 #define FF_SMALL_CONV(SP) \
-    launch_conv<CIN, COUT, KS, S, H, H, FF_SM_BM, FF_SM_BN, FF_KB(CIN), 2, 1, 1, 4, SP>(a, grid, SP, s)
+    launch_conv<CIN, COUT, KS, S, H, H, FF_SM_BM, FF_SM_BN, FF_KB(CIN), FF_SM_PF, 1, 1, FF_SM_OCC, SP>(a, grid, SP, s)
     if constexpr (SPLIT > 1) {
         if (split == SPLIT) { FF_SMALL_CONV(SPLIT); return; }
     }

@@ -266,10 +266,11 @@ def time_pair(lib, cin=64, cout=64, hin=112, cx=64, batch=1024, iters=10, fused=
             "fused": fused, "ms": round(ms.value / iters, 5)}
 
 
-def time_fc(lib, batch=1, iters=50):
+def time_fc(lib, batch=1, iters=50, path=0):
     """Mean launch time of the FC head 25088 -> 512 at `batch` faces (the
-    path and split-K workspace ffk_fc chooses; HIP events on the launch
-    stream); seeded int8 activations and weights.  Frees what it allocates."""
+    path and split-K workspace ffk_fc chooses, or with path 1 / 2 the matvec
+    / MFMA GEMM path; HIP events on the launch stream); seeded int8
+    activations and weights.  Frees what it allocates."""
     N, K = 512, 25088
     r = np.random.default_rng(7)
     a = r.integers(-128, 128, size=(batch, K), dtype=np.int8)
@@ -294,6 +295,7 @@ def time_fc(lib, batch=1, iters=50):
     d.a, d.w, d.ws, d.bias = dev(a), dev(packed), dev(ws), dev(bias)
     d.out = dev(nbytes=batch * N * 4)
     d.a_scale = 1.0
+    d.path = path
     n_ws = lib.ffk_fc_workspace_bytes(C.byref(d))
     if n_ws:
         d.workspace, d.workspace_bytes = dev(nbytes=n_ws), n_ws
@@ -319,7 +321,7 @@ def time_fc(lib, batch=1, iters=50):
             lib.ffk_free(p)
     per = ms.value / iters
     return {"layer": "fc 25088->512", "batch": batch, "split_ws_bytes": n_ws,
-            "path": "matvec" if batch <= 16 else "gemm",
+            "path": {1: "matvec", 2: "gemm"}.get(path, "matvec" if batch <= 16 else "gemm"),
             "ms_per_launch": round(per, 5),
             "weight_gbs": round(N * K / (per * 1e-3) / 1e9, 1),
             "int8_tops": round(2.0 * batch * N * K / (per * 1e-3) / 1e12, 2)}
@@ -346,6 +348,8 @@ def main():
                     help="give no split-K workspace (small batches then use the whole-K tiling)")
     ap.add_argument("--fc", action="store_true",
                     help="instead: the FC head 25088 -> 512 at --batch faces")
+    ap.add_argument("--fc-path", type=int, default=0, choices=[0, 1, 2],
+                    help="with --fc: 0 the library's choice, 1 the matvec, 2 the MFMA GEMM")
     ap.add_argument("--pair-cx", type=int, default=0,
                     help="instead: the stride-2 conv (--cin/--cout/--hin, k3 s2) and its 1x1 shortcut "
                          "over this many compact input channels, as one launch")
@@ -366,7 +370,7 @@ def main():
         print(json.dumps({"copy_bytes": n, "iters": a.iters}), flush=True)
         return
     if a.fc:
-        print(json.dumps(time_fc(lib, a.batch, a.iters)), flush=True)
+        print(json.dumps(time_fc(lib, a.batch, a.iters, a.fc_path)), flush=True)
         return
     if a.pair_cx:
         print(json.dumps(time_pair(lib, a.cin, a.cout, a.hin, a.pair_cx, a.batch, a.iters,

@@ -249,9 +249,12 @@ int    ffk_conv_s2_shortcut(const ffk_conv_desc* c, const ffk_conv_desc* s, void
 int    ffk_conv_noalloc(const ffk_conv_desc* d, void* stream);
 /* Name of the kernel variant ffk_conv would run for this descriptor (its
  * geometry, batch and workspace): "stem", "patch" (3x3 stride-1 layers:
- * input patch staged once per channel run), "direct" (direct-to-LDS tiles),
- * "staged" / "staged128" (register-staged tiles), "splitk" (split-K);
- * NULL when no kernel applies.  No counterpart in the reference: it lets
+ * input patch staged once per channel run), "patch_kg" (the same with the
+ * channel runs shared by K-groups of waves, small grids), "phase" (3x3
+ * stride-2 layers as four phase images), "direct" (direct-to-LDS tiles),
+ * "staged" / "staged128" (register-staged tiles), "splitk" (64x64 tiles
+ * with the K reduction split over workgroups), "tile64" (64x64 tiles, whole
+ * K: tiny grids), "winograd"; NULL when no kernel applies.  No counterpart in the reference: it lets
  * tests and benchmarks name the code path they exercise. */
 const char* ffk_conv_variant(const ffk_conv_desc* d);
 /* Workgroups that launch would have (host function, no device involved);

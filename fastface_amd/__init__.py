@@ -126,6 +126,10 @@ EXPORTS = [
     ("ffk_pack_winograd_weights", C.c_int, [_p, C.c_int, C.c_int, _p]),
     ("ffk_make_bn_lut", C.c_int, [_p, _p, _p, _p, C.c_int, _p]),
     ("ffk_make_rgb8_lut", C.c_int, [_p, _p]),
+    ("ffk_make_map_lut", C.c_int, [_p, _p, _p, _p, _p, C.c_int, _p]),
+    ("ffk_make_add_lut", C.c_int, [C.c_float, C.c_float, C.c_float, _p]),
+    ("ffk_map_i8", C.c_int, [_p, _p, C.c_longlong, C.c_int, _p, _p]),
+    ("ffk_add_i8", C.c_int, [_p, _p, _p, C.c_longlong, _p, _p]),
     ("ffk_fc_packed_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("ffk_pack_fc_weights", C.c_int, [_p, C.c_int, C.c_int, _p]),
     ("ffk_pack_fc_row", C.c_int, [_p, C.c_int, C.c_int, C.c_int, _p]),

@@ -513,26 +513,15 @@ const char* ffk_conv_variant(const ffk_conv_desc* d) {
 // value q for channel c, computed with the reference's fp32 sequence
 // (bn_prelu_requant_int8 with bn != NULL, int8_epilogue.c:273-303):
 //   f = fma(RN(q * s_in), bn_s, bn_o); round half away of RN(f * inv);
-//   x86 cvttps2dq semantics; clamp to int8.
+//   x86 cvttps2dq semantics; clamp to int8.  (The same table as a
+// stand-alone BN's, ff_eltwise.hip.)
 int ffk_make_bn_lut(const float* s_in, const float* bn_s, const float* bn_o, const float* bn_inv,
                     int cout, int8_t* lut) {
     if (!s_in || !bn_s || !bn_o || !bn_inv || !lut || cout <= 0) {
         ffk_set_error("make_bn_lut: bad arguments%s%s", nullptr, nullptr);
         return FFK_ERR_ARG;
     }
-    for (int c = 0; c < cout; c++)
-        for (int q = -128; q < 128; q++) {
-            volatile float f = (float)q * s_in[c];
-            f = __builtin_fmaf(f, bn_s[c], bn_o[c]);
-            volatile float t = f * bn_inv[c];
-            volatile float r = t + __builtin_copysignf(0.5f, t);
-            int32_t v;
-            if (r >= -2147483648.0f && r < 2147483648.0f) v = (int32_t)r;
-            else v = INT32_MIN;
-            v = v < -128 ? -128 : (v > 127 ? 127 : v);
-            lut[(size_t)c * 256 + (q + 128)] = (int8_t)v;
-        }
-    return FFK_OK;
+    return ffk_make_map_lut(s_in, bn_s, bn_o, nullptr, bn_inv, cout, lut);
 }
 
 int ffk_make_rgb8_lut(const float* in_inv, int8_t* lut) {

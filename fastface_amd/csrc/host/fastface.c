@@ -239,7 +239,7 @@ static size_t workspace_bytes(FastFace* ff, int max_batch)
     size_t best = 0;
     const int top = max_batch < 4096 ? max_batch : 4096;
     for (int s = 0; s < ff->plan.n_steps; s++) {
-        if (ff->plan.steps[s].kind == 2) {          /* FC head: split-K of mid-size batches */
+        if (ff->plan.steps[s].kind == FF_STEP_FC) {          /* FC head: split-K of mid-size batches */
             for (int b = 1; b <= top; b++) {
                 ffk_fc_desc f;
                 memset(&f, 0, sizeof f);
@@ -249,7 +249,7 @@ static size_t workspace_bytes(FastFace* ff, int max_batch)
             }
             continue;
         }
-        if (ff->plan.steps[s].kind != 1) continue;
+        if (ff->plan.steps[s].kind != FF_STEP_CONV) continue;
         for (int b = 1; b <= top + 1; b++) {
             ffk_conv_desc d;
             step_desc(ff, s, b <= top ? b : max_batch, 0, 0, 0, 0, &d);
@@ -314,12 +314,12 @@ static int8_t* tensor_ptr(FastFace* ff, int t, size_t off)
  * shortcut) runs at stride 1 over the compact tensor. */
 static int reads_even(const FastFace* ff, const FfStep* st)
 {
-    return st->kind == 1 && st->t_in > FF_T_INPUT && ff->plan.tensors[st->t_in].even;
+    return st->kind == FF_STEP_CONV && st->t_in > FF_T_INPUT && ff->plan.tensors[st->t_in].even;
 }
 
 static int writes_even(const FastFace* ff, const FfStep* st)
 {
-    return st->kind == 1 && st->t_out >= 0 && ff->plan.tensors[st->t_out].even;
+    return st->kind == FF_STEP_CONV && st->t_out >= 0 && ff->plan.tensors[st->t_out].even;
 }
 
 /* part / off: the half of a split chain (0 or 1) and its region's offset
@@ -363,10 +363,19 @@ static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t 
 static int launch_step(FastFace* ff, int s, int batch, void* stream, int fmt, int part, size_t off, int shared)
 {
     const FfStep* st = &ff->plan.steps[s];
-    if (st->kind == 1) {
+    if (st->kind == FF_STEP_CONV) {
         ffk_conv_desc d;
         step_desc(ff, s, batch, fmt, part, off, shared, &d);
         return ffk_conv(&d, stream);
+    }
+    if (st->kind == FF_STEP_MAP || st->kind == FF_STEP_ADD) {   /* stand-alone BN / PReLU / Add */
+        const long long pix = (long long)batch * st->hout * st->wout;
+        const int8_t* lut = ff->d_weights + st->lut_off;
+        if (st->kind == FF_STEP_MAP)
+            return ffk_map_i8(tensor_ptr(ff, st->t_in, off), tensor_ptr(ff, st->t_out, off), pix, st->cout,
+                              lut, stream);
+        return ffk_add_i8(tensor_ptr(ff, st->t_in, off), tensor_ptr(ff, st->t_add, off),
+                          tensor_ptr(ff, st->t_out, off), pix * st->cout, lut, stream);
     }
     ffk_fc_desc f;
     memset(&f, 0, sizeof f);
@@ -862,7 +871,7 @@ int fastface_set_conv_algo(FastFace* ff, int algo)
     int n = 0;
     if (algo == FASTFACE_CONV_WINOGRAD_F23)
         for (int s = 0; s < ff->plan.n_steps; s++)
-            if (ff->plan.steps[s].kind == 1 && ff->plan.steps[s].wino_off != (size_t)-1) n++;
+            if (ff->plan.steps[s].kind == FF_STEP_CONV && ff->plan.steps[s].wino_off != (size_t)-1) n++;
     if (algo == ff->algo) return n;
     if (drain(ff) || ffk_stream_sync(ff->stream)) return -2;
     /* other launch chains, and another workspace size */
@@ -890,7 +899,7 @@ int fastface_set_epilogue_forms(FastFace* ff, int general)
     if (!ff || (general != 0 && general != 1)) return -1;
     int n = 0;
     for (int s = 0; s < ff->plan.n_steps; s++)
-        if (ff->plan.steps[s].kind == 1 && (ff->plan.steps[s].flags & FF_FAST_EPI)) n++;
+        if (ff->plan.steps[s].kind == FF_STEP_CONV && (ff->plan.steps[s].flags & FF_FAST_EPI)) n++;
     if (general == ff->general_epi) return n;
     if (drain(ff) || ffk_stream_sync(ff->stream)) return -2;
     const int cap = ff->capacity;
@@ -909,7 +918,7 @@ int fastface_get_step(const FastFace* ff, int s, fastface_step_info* info)
     info->kind = st->kind;
     info->op_first = st->op_first;
     info->op_last = st->op_last;
-    if (st->kind == 1) {
+    if (st->kind == FF_STEP_CONV) {
         info->cin = st->cin; info->cout = st->cout; info->kh = st->kh; info->kw = st->kw;
         /* the geometry and flags of the launch (step_desc) */
         const int ev_in = reads_even(ff, st), ev_out = writes_even(ff, st);
@@ -929,6 +938,13 @@ int fastface_get_step(const FastFace* ff, int s, fastface_step_info* info)
         const double x_b = st->t_out < 0 ? 0.0 : (ev_out ? 0.25 : 1.0);
         info->act_bytes_per_face = in_bytes + out_b * (x_b + (st->t_bn >= 0) + (st->t_add >= 0));
         info->weight_bytes = (double)ffk_conv_packed_bytes(st->cin, st->cout, st->kh, st->kw);
+    } else if (st->kind == FF_STEP_MAP || st->kind == FF_STEP_ADD) {
+        info->cin = info->cout = st->cout; info->kh = info->kw = 1; info->stride = 1;
+        info->hin = info->hout = st->hout; info->win = info->wout = st->wout;
+        info->stores_x = 1;
+        const double bytes = (double)st->hout * st->wout * st->cout;
+        info->act_bytes_per_face = bytes * (st->kind == FF_STEP_ADD ? 3.0 : 2.0);
+        info->weight_bytes = st->kind == FF_STEP_ADD ? 65536.0 : 256.0 * st->cout;
     } else {
         info->cin = st->fc_k; info->cout = st->fc_n; info->kh = info->kw = 1; info->stride = 1;
         info->hin = info->win = info->hout = info->wout = 1;

@@ -50,8 +50,13 @@ typedef struct {
                                    1x1 stride-2 conv, run at stride 1 */
 } FfTensor;
 
+/* step kinds: a conv (+PReLU | +Add, + BN second output), the FC head, a
+ * stand-alone BN / PReLU (per-channel table over t_in), a stand-alone Add
+ * (one table over the pairs of t_in and t_add) */
+enum { FF_STEP_CONV = 1, FF_STEP_FC = 2, FF_STEP_MAP = 3, FF_STEP_ADD = 4 };
+
 typedef struct {
-    int kind;                   /* 1 conv, 2 fc */
+    int kind;                   /* FF_STEP_*                                  */
     int op_first, op_last;
     int cin, cout, kh, kw, stride, pad, hin, win, hout, wout;
     int t_in, t_add, t_out, t_bn;
@@ -59,7 +64,8 @@ typedef struct {
     int flags; float in_scale;
     size_t w_off;               /* bytes into the weight arena */
     size_t p_off;               /* floats into the parameter arena */
-    size_t lut_off;             /* bytes into the weight arena: BN table */
+    size_t lut_off;             /* bytes into the weight arena: BN table (conv),
+                                   the map's or the Add's table */
     size_t wino_off;            /* bytes into the weight arena: Winograd-packed
                                    weights, or (size_t)-1 if the layer has none */
     /* fc */

@@ -19,11 +19,12 @@
  * without the former or with a residual / in-scale (must be none); exits 0
  * (a sanitizer finding aborts with its report and a
  * non-zero status).  With <dump>, the plan's weight arena goes to <dump>.bin
- * and, one line per region, "conv|wino|bn|fc <op> <offset> <bytes>" to
+ * and, one line per region, "conv|wino|bn|map|add|fc <op> <offset> <bytes>" to
  * <dump>.txt, and the parameter arena to <dump>.params.bin.  With
  * --launches, the launch list of the chain at each batch, one line per
  * launch ("launch <batch>[/h<half>] <step> conv|fc <variant> <workgroups>
- * <geometry> <flags>"), built as fastface.c builds its descriptors (two
+ * <geometry> <flags>", or "... map|add <channels> <pixels>" for a
+ * stand-alone BN / PReLU / Add), built as fastface.c builds its descriptors (two
  * halves from 24 faces, FFK_SHARED_GPU) from the library's host-side
  * launch choice: no device is involved. */
 #include <stdint.h>
@@ -40,11 +41,16 @@ static void print_launches(const FfPlan* p, const char* tag, int batch, int shar
 {
     for (int s = 0; s < p->n_steps; s++) {
         const FfStep* st = &p->steps[s];
-        if (st->kind == 2) {
+        if (st->kind == FF_STEP_FC) {
             ffk_fc_desc f;
             memset(&f, 0, sizeof f);
             f.batch = batch; f.n = st->fc_n; f.k = st->fc_k;
             printf("launch %s %d fc %s %zu\n", tag, s, batch <= 16 ? "matvec" : "gemm", ffk_fc_workspace_bytes(&f));
+            continue;
+        }
+        if (st->kind == FF_STEP_MAP || st->kind == FF_STEP_ADD) {
+            printf("launch %s %d %s %d %lld\n", tag, s, st->kind == FF_STEP_MAP ? "map" : "add", st->cout,
+                   (long long)batch * st->hout * st->wout);
             continue;
         }
         ffk_conv_desc d;
@@ -100,7 +106,7 @@ int main(int argc, char** argv)
         int in_range = 0, fma = 0, fma_bad = 0;
         for (int s = 0; s < p.n_steps; s++) {
             const int f = p.steps[s].flags;
-            if (p.steps[s].kind != 1) continue;
+            if (p.steps[s].kind != FF_STEP_CONV) continue;
             in_range += (f & FFK_EPI_IN_RANGE) != 0;
             if (f & FFK_EPI_FMA_TAIL) {
                 fma++;
@@ -137,8 +143,14 @@ int main(int argc, char** argv)
         if (f) {
             for (int s = 0; s < p.n_steps; s++) {
                 const FfStep* st = &p.steps[s];
-                if (st->kind == 2) {
+                if (st->kind == FF_STEP_FC) {
                     fprintf(f, "fc %d %zu %zu\n", st->op_first, st->w_off, ffk_fc_packed_bytes(st->fc_n, st->fc_k));
+                    continue;
+                }
+                if (st->kind == FF_STEP_MAP || st->kind == FF_STEP_ADD) {
+                    fprintf(f, "%s %d %zu %zu %zu\n", st->kind == FF_STEP_MAP ? "map" : "add", st->op_first,
+                            st->lut_off, st->kind == FF_STEP_MAP ? (size_t)st->cout * 256 : (size_t)65536,
+                            st->p_off);
                     continue;
                 }
                 fprintf(f, "conv %d %zu %zu\n", st->op_first, st->w_off,

@@ -13,6 +13,11 @@
  *   - a BN that follows it (through SAVE_ID / BLOCK_START) becomes a second
  *     output of that launch (the pre-BN tensor is still stored when the
  *     identity slot or the block buffer refers to it);
+ *   - a BN or PReLU that no conv absorbs (after an Add, a PReLU, another BN)
+ *     becomes a table lookup over its input tensor, and an Add that follows
+ *     no conv a lookup over the pairs of its two inputs (the ops are
+ *     functions of int8 values; libfastface.c:401-434); their outputs are
+ *     new tensors, so earlier references to the input stay intact;
  *   - SAVE_ID / BLOCK_START become tensor references (no copies);
  *   - FLATTEN disappears: the FC weight columns are permuted from the
  *     reference's NCHW order (c*HW + hw) to NHWC (hw*C + c); the int32 dot
@@ -20,8 +25,9 @@
  *   - every scalar fallback of the reference (no OPSC2 entry, length
  *     mismatch) is resolved into explicit per-channel parameter rows,
  *     computed in fp32 exactly as the reference computes them.
- * Op sequences outside this pattern are rejected (create fails) instead of
- * being run some other way.
+ * Op sequences outside this pattern (ops on the fp32 input faces other than
+ * the 3-channel stem conv, conv geometries without a kernel, ops after the
+ * GEMM) are rejected (create fails) instead of being run some other way.
  */
 #include <math.h>
 #include <pthread.h>
@@ -35,15 +41,16 @@
 /* Weight-arena contents are produced after the walk, as independent jobs:
  * the walk only places them (offsets), the arena is then allocated once at
  * its final size and the jobs fill it on a few threads. */
-enum { JOB_CONV, JOB_WINO, JOB_BN, JOB_FC, JOB_FMA_TAIL };
+enum { JOB_CONV, JOB_WINO, JOB_BN, JOB_FC, JOB_FMA_TAIL, JOB_MAP, JOB_ADD };
 typedef struct {
     int kind;
     const int8_t* src;          /* conv / FC weights in the mapping */
-    int cout, cin, kh, kw;      /* conv; FC: cout = N, cin = K */
+    int cout, cin, kh, kw;      /* conv; FC: cout = N, cin = K; MAP: cout = C,
+                                   kh = has BN, kw = has PReLU */
     int r0, r1;                 /* FC: rows of this job; FMA_TAIL: r0 the step */
     int fc_hw, fc_c, flat;      /* FC: NCHW flatten -> NHWC column order */
     size_t dst;                 /* bytes into the weight arena */
-    size_t p_off;               /* BN: floats into the parameter arena */
+    size_t p_off;               /* BN, MAP, ADD: floats into the parameter arena */
 } PackJob;
 
 typedef struct {
@@ -140,6 +147,19 @@ static void run_job(FfPlan* p, const PackJob* j, int8_t* row)
                         P + FFK_P_BN_INV * C, C, dst);
         break;
     }
+    case JOB_MAP: {             /* rows BN_SIN, BN_S, BN_O, SLOPE, BN_INV */
+        const float* P = p->p_host + j->p_off;
+        const int C = j->cout;
+        ffk_make_map_lut(P + FFK_P_BN_SIN * C, j->kh ? P + FFK_P_BN_S * C : NULL,
+                         j->kh ? P + FFK_P_BN_O * C : NULL, j->kw ? P + FFK_P_SLOPE * C : NULL,
+                         P + FFK_P_BN_INV * C, C, dst);
+        break;
+    }
+    case JOB_ADD: {             /* a_scale, b_scale, out_scale */
+        const float* P = p->p_host + j->p_off;
+        ffk_make_add_lut(P[0], P[1], P[2], dst);
+        break;
+    }
     case JOB_FC: {
         const int N = j->cout, K = j->cin, HW = j->fc_hw, Cc = j->fc_c;
         for (int r = j->r0; r < j->r1; r++) {
@@ -224,6 +244,40 @@ static float inv_of(float s)
 
 typedef struct { int C, H, W; } Shp;
 
+/* A stand-alone BN / PReLU (libfastface.c:401-424, bn_prelu_requant_int8):
+ * a per-channel table over the int8 tensor t_in, written to a new tensor.
+ * s_in / inv: per-channel rows, or NULL for the scalar in-scale s_in_s and
+ * the reference's 1/(out_s + 1e-9f).  Returns the new tensor, or -1. */
+static int map_step(Builder* B, int op, int t_in, const float* s_in, float s_in_s,
+                    const uint8_t* bn_s, const uint8_t* bn_o, const uint8_t* slope,
+                    const float* inv, float out_s)
+{
+    FfPlan* p = B->p;
+    if (t_in == FF_T_INPUT) return fail(p, "only the 3-channel stem conv may read the input faces", op);
+    const int C = p->tensors[t_in].C, H = p->tensors[t_in].H, W = p->tensors[t_in].W;
+    if (C % 64) return fail(p, "a stand-alone BN / PReLU needs a multiple of 64 channels", op);
+    const int Y = new_tensor(B, C, H, W, op);
+    FfStep* s = new_step(B);
+    s->kind = FF_STEP_MAP; s->op_first = s->op_last = op;
+    s->cin = s->cout = C; s->kh = s->kw = 1; s->stride = 1;
+    s->hin = s->hout = H; s->win = s->wout = W;
+    s->t_in = t_in; s->t_out = s->t_x = Y;
+    s->wino_off = (size_t)-1;
+    s->p_off = alloc_params(B, (size_t)FFK_NPARAM * C);
+    float* P = p->p_host + s->p_off;
+    fill_rowf(P + FFK_P_BN_SIN * C, C, s_in, s_in_s);
+    if (bn_s) {
+        fill_row(P + FFK_P_BN_S * C, C, bn_s, 0.0f);
+        fill_row(P + FFK_P_BN_O * C, C, bn_o, 0.0f);
+    }
+    if (slope) fill_row(P + FFK_P_SLOPE * C, C, slope, 0.0f);
+    fill_rowf(P + FFK_P_BN_INV * C, C, inv, inv_of(out_s));
+    s->lut_off = alloc_weights(B, (size_t)C * 256);
+    add_job(B, (PackJob){ JOB_MAP, NULL, C, 0, bn_s != NULL, slope != NULL, 0, 0, 0, 0, 0,
+                          s->lut_off, s->p_off });
+    return Y;
+}
+
 int ff_plan_build(const FfModel* m, FfPlan* p)
 {
     memset(p, 0, sizeof *p);
@@ -265,10 +319,11 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
     int A = FF_T_INPUT;
     float A_scale = m->input_scale;
     const float* A_pc = pc ? m->in_scale_pc : NULL;
+    int A_pc_len = pc ? m->n_in : 0;    /* floats A_pc holds */
     int blk_t = FF_T_INPUT;
     float blk_scale = m->input_scale;
-    int slot_t[24]; float slot_scale[24]; const float* slot_pc[24];
-    for (int k = 0; k < 24; k++) { slot_t[k] = -1; slot_scale[k] = 0.0f; slot_pc[k] = NULL; }
+    int slot_t[24]; float slot_scale[24]; const float* slot_pc[24]; int slot_pc_len[24];
+    for (int k = 0; k < 24; k++) { slot_t[k] = -1; slot_scale[k] = 0.0f; slot_pc[k] = NULL; slot_pc_len[k] = 0; }
     int save_idx = 0, add_idx = 0;
     int last_conv = -1;         /* step whose output A currently is */
     int flat = 0, done = 0;
@@ -306,6 +361,9 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
                 if (at->C != op->Cout || at->H != so.H || at->W != so.W) {
                     rc = fail(p, "Add operands differ in shape", i + 1); break;
                 }
+                if (v4 && slot_pc[add_k] && slot_pc_len[add_k] < op->Cout) {
+                    rc = fail(p, "OPSC2 entry too short", i + 1); break;
+                }
                 eff_scale = m->scales[i + 1];
                 if (eff_scale <= 0) eff_scale = next_scale;
                 eff = i + 1; skip = 1;
@@ -315,7 +373,7 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
 
             const int X = new_tensor(&B, op->Cout, so.H, so.W, eff);
             FfStep* s = new_step(&B);
-            s->kind = 1; s->op_first = i; s->op_last = eff;
+            s->kind = FF_STEP_CONV; s->op_first = i; s->op_last = eff;
             s->cin = op->Cin; s->cout = op->Cout; s->kh = op->Kh; s->kw = op->Kw;
             s->stride = op->stride; s->pad = op->pad; s->hin = si.H; s->win = si.W;
             s->hout = so.H; s->wout = so.W;
@@ -363,50 +421,96 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
                                            p->n_steps - 1, 0, 0, 0, 0, 0, s->p_off });
             }
             A = X; A_scale = eff_scale;
-            if (pc && m->scale_pc[eff]) A_pc = m->scale_pc[eff];
+            if (pc && m->scale_pc[eff]) { A_pc = m->scale_pc[eff]; A_pc_len = (int)m->pc_len[eff]; }
             last_conv = p->n_steps - 1;
             if (skip) i++;
             break;
         }
-        case FF_OP_BN: {
+        case FF_OP_BN: {                 /* libfastface.c:401-413 */
             const Shp si = sh_in[i];
-            if (last_conv < 0 || p->steps[last_conv].t_out != A || p->steps[last_conv].t_bn >= 0) {
-                rc = fail(p, "BN must follow a Conv (through SAVE_ID/BLOCK_START only)", i); break;
-            }
-            if (op->bn_size != si.C) { rc = fail(p, "BN size != channels", i); break; }
-            FfStep* s = &p->steps[last_conv];
-            float* P = p->p_host + s->p_off;
             const int C = si.C;
-            /* libfastface.c:402-408 */
+            if (op->bn_size != C) { rc = fail(p, "BN size != channels", i); break; }
             const float* bn_inv = (pc && m->inv_pc[i] && m->pc_len[i] == (uint32_t)C) ? m->inv_pc[i] : NULL;
             const float* bn_in = (pc && A_pc) ? A_pc : NULL;
-            fill_rowf(P + FFK_P_BN_SIN * C, C, bn_in, A_scale);
-            fill_row(P + FFK_P_BN_S * C, C, op->bn_scale, 0.0f);
-            fill_row(P + FFK_P_BN_O * C, C, op->bn_offset, 0.0f);
-            fill_rowf(P + FFK_P_BN_INV * C, C, bn_inv, inv_of(next_scale));
-            s->flags |= FFK_EPI_BN;
-            s->lut_off = alloc_weights(&B, (size_t)C * 256);
-            add_job(&B, (PackJob){ JOB_BN, NULL, C, 0, 0, 0, 0, 0, 0, 0, 0, s->lut_off, s->p_off });
-            const int Y = new_tensor(&B, C, si.H, si.W, i);
-            p->tensors[Y].def_step = last_conv;
-            s->t_bn = Y;
-            s->op_last = i;
-            A = Y; A_scale = next_scale;
-            if (pc && m->scale_pc[i]) A_pc = m->scale_pc[i];
+            if (bn_in && A_pc_len < C) { rc = fail(p, "OPSC2 entry too short", i); break; }
+            if (last_conv >= 0 && p->steps[last_conv].t_out == A && p->steps[last_conv].t_bn < 0) {
+                /* the second output of the conv that produced A (through
+                 * SAVE_ID / BLOCK_START only) */
+                FfStep* s = &p->steps[last_conv];
+                float* P = p->p_host + s->p_off;
+                fill_rowf(P + FFK_P_BN_SIN * C, C, bn_in, A_scale);
+                fill_row(P + FFK_P_BN_S * C, C, op->bn_scale, 0.0f);
+                fill_row(P + FFK_P_BN_O * C, C, op->bn_offset, 0.0f);
+                fill_rowf(P + FFK_P_BN_INV * C, C, bn_inv, inv_of(next_scale));
+                s->flags |= FFK_EPI_BN;
+                s->lut_off = alloc_weights(&B, (size_t)C * 256);
+                add_job(&B, (PackJob){ JOB_BN, NULL, C, 0, 0, 0, 0, 0, 0, 0, 0, s->lut_off, s->p_off });
+                const int Y = new_tensor(&B, C, si.H, si.W, i);
+                p->tensors[Y].def_step = last_conv;
+                s->t_bn = Y;
+                s->op_last = i;
+                A = Y;
+            } else {
+                const int Y = map_step(&B, i, A, bn_in, A_scale, op->bn_scale, op->bn_offset, NULL,
+                                       bn_inv, next_scale);
+                if (Y < 0) { rc = -1; break; }
+                A = Y;
+            }
+            A_scale = next_scale;
+            if (pc && m->scale_pc[i]) { A_pc = m->scale_pc[i]; A_pc_len = (int)m->pc_len[i]; }
             break;
         }
-        case FF_OP_PRELU:
-            rc = fail(p, "stand-alone PReLU (not after a Conv) is not supported", i);
+        case FF_OP_PRELU: {              /* libfastface.c:414-424 (not after a conv) */
+            const int C = sh_in[i].C;
+            if (op->prelu_size != C) { rc = fail(p, "PReLU size != channels", i); break; }
+            const float* in_pc = (pc && A_pc) ? A_pc : NULL;
+            const float* inv = (pc && m->inv_pc[i]) ? m->inv_pc[i] : NULL;
+            if ((in_pc && A_pc_len < C) || (inv && m->pc_len[i] < (uint32_t)C)) {
+                rc = fail(p, "OPSC2 entry too short", i); break;
+            }
+            const int Y = map_step(&B, i, A, in_pc, A_scale, NULL, NULL, op->prelu_slope, inv, next_scale);
+            if (Y < 0) { rc = -1; break; }
+            A = Y; A_scale = next_scale;
+            if (pc && m->scale_pc[i]) { A_pc = m->scale_pc[i]; A_pc_len = (int)m->pc_len[i]; }
             break;
-        case FF_OP_ADD:
-            rc = fail(p, "stand-alone Add (not after a Conv) is not supported", i);
+        }
+        case FF_OP_ADD: {                /* libfastface.c:429-434 (not after a conv) */
+            const int k = add_idx % 24;
+            if (slot_t[k] < 0) { rc = fail(p, "Add before any SAVE_ID", i); break; }
+            if (A == FF_T_INPUT || slot_t[k] == FF_T_INPUT) {
+                rc = fail(p, "only the 3-channel stem conv may read the input faces", i); break;
+            }
+            const FfTensor* ta = &p->tensors[A];
+            const FfTensor* tb = &p->tensors[slot_t[k]];
+            if (ta->C != tb->C || ta->H != tb->H || ta->W != tb->W) {
+                rc = fail(p, "Add operands differ in shape", i); break;
+            }
+            const int C = ta->C, H = ta->H, W = ta->W;
+            if (C % 16) { rc = fail(p, "a stand-alone Add needs a multiple of 16 channels", i); break; }
+            const int Y = new_tensor(&B, C, H, W, i);
+            FfStep* s = new_step(&B);
+            s->kind = FF_STEP_ADD; s->op_first = s->op_last = i;
+            s->cin = s->cout = C; s->kh = s->kw = 1; s->stride = 1;
+            s->hin = s->hout = H; s->win = s->wout = W;
+            s->t_in = A; s->t_add = slot_t[k]; s->t_out = s->t_x = Y;
+            s->wino_off = (size_t)-1;
+            /* per-tensor scales even in FFW4 (add_requant_int8) */
+            s->p_off = alloc_params(&B, 3);
+            p->p_host[s->p_off] = A_scale;
+            p->p_host[s->p_off + 1] = slot_scale[k];
+            p->p_host[s->p_off + 2] = next_scale;
+            s->lut_off = alloc_weights(&B, 65536);
+            add_job(&B, (PackJob){ JOB_ADD, NULL, 0, 0, 0, 0, 0, 0, 0, 0, 0, s->lut_off, s->p_off });
+            A = Y; A_scale = next_scale;        /* (the per-channel scales stay) */
+            add_idx++;
             break;
+        }
         case FF_OP_BLOCK_START:          /* libfastface.c:425-428 */
             blk_t = A; blk_scale = A_scale;
             break;
         case FF_OP_SAVE_ID: {            /* libfastface.c:435-440 */
             const int k = save_idx % 24;
-            slot_t[k] = A; slot_scale[k] = A_scale; slot_pc[k] = A_pc;
+            slot_t[k] = A; slot_scale[k] = A_scale; slot_pc[k] = A_pc; slot_pc_len[k] = A_pc_len;
             save_idx++;
             break;
         }
@@ -421,7 +525,7 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
             }
             if (K % 64 != 0) { rc = fail(p, "GEMM K must be a multiple of 64", i); break; }
             FfStep* s = new_step(&B);
-            s->kind = 2; s->op_first = i; s->op_last = i;
+            s->kind = FF_STEP_FC; s->op_first = i; s->op_last = i;
             s->t_in = A; s->fc_n = N; s->fc_k = K;
             s->a_scale = v4 ? 1.0f : A_scale;
             s->w_off = alloc_weights(&B, ffk_fc_packed_bytes(N, K));
@@ -454,8 +558,8 @@ int ff_plan_pair(const FfPlan* p, int s)
     if (s < 0 || s + 1 >= p->n_steps) return 0;
     const FfStep* a = &p->steps[s];
     const FfStep* b = a + 1;
-    return a->kind == 1 && b->kind == 1 && a->kh == 3 && a->stride == 2 && a->t_bn < 0 && a->t_out >= 0 &&
-           b->t_add == a->t_out && b->t_in != a->t_out && p->tensors[a->t_out].last_use == s + 1;
+    return a->kind == FF_STEP_CONV && b->kind == FF_STEP_CONV && a->kh == 3 && a->stride == 2 && a->t_bn < 0 &&
+           a->t_out >= 0 && b->t_add == a->t_out && b->t_in != a->t_out && p->tensors[a->t_out].last_use == s + 1;
 }
 
 int ff_plan_assign_buffers(FfPlan* p, int keep_all)
@@ -476,7 +580,7 @@ int ff_plan_assign_buffers(FfPlan* p, int keep_all)
     /* the pre-BN output of a dual-output step is stored only if read later */
     for (int s = 0; s < p->n_steps; s++) {
         FfStep* st = &p->steps[s];
-        if (st->kind != 1) continue;
+        if (st->kind != FF_STEP_CONV) continue;
         st->t_out = st->t_x;
         if (st->t_bn >= 0 && p->tensors[st->t_x].last_use < 0 && !keep_all) st->t_out = -1;
     }
@@ -487,7 +591,7 @@ int ff_plan_assign_buffers(FfPlan* p, int keep_all)
      * keep_all (debug reads) keeps every tensor whole. */
     for (int s = 0; s < p->n_steps && !keep_all; s++) {
         const FfStep* st = &p->steps[s];
-        if (st->kind != 1 || st->t_out < 0) continue;
+        if (st->kind != FF_STEP_CONV || st->t_out < 0) continue;
         FfTensor* T = &p->tensors[st->t_out];
         if ((T->H & 1) || (T->W & 1)) continue;
         int readers = 0, ok = 1;
@@ -496,7 +600,7 @@ int ff_plan_assign_buffers(FfPlan* p, int keep_all)
             if (rd->t_add == st->t_out) ok = 0;
             if (rd->t_in != st->t_out) continue;
             readers++;
-            ok = rd->kind == 1 && rd->kh == 1 && rd->kw == 1 && rd->stride == 2 && rd->pad == 0 &&
+            ok = rd->kind == FF_STEP_CONV && rd->kh == 1 && rd->kw == 1 && rd->stride == 2 && rd->pad == 0 &&
                  ffk_conv_supported(rd->cin, rd->cout, 1, 1, 1, 0, T->H / 2, T->W / 2);
         }
         T->even = ok && readers > 0;

@@ -48,11 +48,19 @@ OPSC_PATH = os.path.join(REPO_ROOT, "models", "op_scales.bin")
 OPSC2_PATH = os.path.join(REPO_ROOT, "models", "op_scales_v2.bin")
 
 
-def iresnet_schedule(stages=STAGES):
-    """List of op dicts in FFW4 order (types and conv geometry only)."""
+def iresnet_schedule(stages=STAGES, standalone=False):
+    """List of op dicts in FFW4 order (types and conv geometry only).
+
+    standalone=True inserts elementwise ops that no conv absorbs (each marked
+    with `extra`, how its scale entries are made): a PReLU after the last
+    residual Add of stage 2; in stage 3's second block, after its Add, a
+    SAVE_ID, a BN (the conv's second output) and an Add of the two (an Add
+    after no conv), so that the next block's leading BN reads an Add's
+    output; and a second BN and a PReLU after the final BN.  The reference's
+    interpreter runs them one by one (libfastface.c:401-434)."""
     ops = [dict(type=OP_CONV, Cin=3, Cout=64, k=3, s=1, p=1), dict(type=OP_PRELU, C=64)]
     cin = 64
-    for nblocks, c in stages:
+    for si, (nblocks, c) in enumerate(stages):
         for bi in range(nblocks):
             ops.append(dict(type=OP_BLOCK_START))
             ops.append(dict(type=OP_BN, C=cin))
@@ -66,10 +74,17 @@ def iresnet_schedule(stages=STAGES):
             else:
                 ops.append(dict(type=OP_CONV, Cin=c, Cout=c, k=3, s=1, p=1))
                 ops.append(dict(type=OP_ADD))
+            if standalone and si == 1 and bi == nblocks - 1:
+                ops.append(dict(type=OP_PRELU, C=c, extra="copy"))
+            if standalone and si == 2 and bi == 1:
+                ops += [dict(type=OP_SAVE_ID, extra="none"), dict(type=OP_BN, C=c, extra="copy"),
+                        dict(type=OP_ADD, extra="sum")]
             if bi != nblocks - 1:
                 ops.append(dict(type=OP_SAVE_ID))
             cin = c
     ops.append(dict(type=OP_BN, C=cin))
+    if standalone:
+        ops += [dict(type=OP_BN, C=cin, extra="copy"), dict(type=OP_PRELU, C=cin, extra="copy")]
     ops.append(dict(type=OP_FLATTEN))
     ops.append(dict(type=OP_GEMM, N=EMB_N, K=cin * 7 * 7))
     return ops
@@ -103,6 +118,64 @@ def read_opsc(path=OPSC_PATH):
     (n,) = struct.unpack_from("<I", d, 4)
     in_s = float(np.frombuffer(d, np.float32, 1, 8)[0])
     return in_s, np.frombuffer(d, np.float32, n, 12).copy()
+
+
+def write_opsc(path, input_scale, scales):
+    """OPSC file (libfastface.c:116-129): "OPSC", u32 n, f32 input scale,
+    f32[n] per-op scales."""
+    with open(path, "wb") as f:
+        f.write(b"OPSC")
+        f.write(struct.pack("<I", len(scales)))
+        f.write(np.float32(input_scale).tobytes())
+        f.write(np.asarray(scales, np.float32).tobytes())
+
+
+def write_opsc2(path, input_scales, per_op):
+    """OPSC2 file (libfastface.c:133-204): "OPSC2", u32 n_ops, u32 n_in,
+    f32[n_in], then per op u32 c and f32[c] (c = 0: no entry)."""
+    with open(path, "wb") as f:
+        f.write(b"OPSC2")
+        f.write(struct.pack("<II", len(per_op), len(input_scales)))
+        f.write(np.asarray(input_scales, np.float32).tobytes())
+        for a in per_op:
+            if a is None:
+                f.write(struct.pack("<I", 0))
+            else:
+                f.write(struct.pack("<I", len(a)))
+                f.write(np.asarray(a, np.float32).tobytes())
+
+
+def standalone_scales(ops):
+    """OPSC and OPSC2 contents for a schedule with inserted ops: every op of
+    the plain schedule keeps its entries from the committed files, in order;
+    an inserted op copies the latest positive per-tensor scale and the latest
+    per-channel entry ("copy": the BN keeps the current per-tensor scale, as
+    the model's BNs do), has none ("none"), or, for the Add, twice the
+    current per-tensor scale and no per-channel entry ("sum")."""
+    in_s, sc = read_opsc()
+    in_pc, per_op = read_opsc2()
+    new_sc, new_pc = [], []
+    j = 0
+    for op in ops:
+        kind = op.get("extra")
+        if kind is None:
+            new_sc.append(float(sc[j]))
+            new_pc.append(per_op[j])
+            j += 1
+            continue
+        last_sc = next(v for v in reversed(new_sc) if v > 0)
+        last_pc = next(v for v in reversed(new_pc) if v is not None)
+        if kind == "copy":
+            new_sc.append(0.0 if op["type"] == OP_BN else last_sc)
+            new_pc.append(last_pc.copy())
+        elif kind == "sum":
+            new_sc.append(2.0 * last_sc)
+            new_pc.append(None)
+        else:
+            new_sc.append(0.0)
+            new_pc.append(None)
+    assert j == len(sc)
+    return (in_s, np.asarray(new_sc, np.float32)), (in_pc, new_pc)
 
 
 def _per_tensor_scales(ops, opsc):
@@ -154,7 +227,8 @@ def _fill_scales(ops, opsc2):
     return out
 
 
-def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPSC2_PATH, version=4):
+def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPSC2_PATH, version=4,
+                         ops=None, opsc2=None):
     """Write a synthetic FFW4 file (about 43.7 MB) and return its path.
 
     version 3 or 2 writes the same network as an FFW3 / FFW2 file
@@ -164,11 +238,13 @@ def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPS
     every conv, the activation scale on the FC), so their weight, BN and FC
     scales are sized from the OPSC per-tensor scales instead of the OPSC2
     per-channel ones.  The random draws are the same for every version: the
-    int8 weights, biases and slopes are identical."""
+    int8 weights, biases and slopes are identical.  `ops` / `opsc2`: another
+    schedule and its OPSC2 contents (FFW4 only)."""
     assert version in (2, 3, 4)
+    assert ops is None or version == 4
     rng = np.random.default_rng(seed)
-    ops = iresnet_schedule()
-    opsc2 = read_opsc2(opsc2_path)
+    ops = ops if ops is not None else iresnet_schedule()
+    opsc2 = opsc2 if opsc2 is not None else read_opsc2(opsc2_path)
     _, per_op = opsc2
     track = _fill_scales(ops, opsc2)
     pt_in, pt_out = _per_tensor_scales(ops, read_opsc()) if version < 4 else (None, None)
@@ -243,6 +319,23 @@ def synthetic_ffw4_path(seed=3, cache_dir=None, version=4):
     if not os.path.exists(path):
         write_synthetic_ffw4(path, seed=seed, version=version)
     return path
+
+
+def synthetic_standalone_dir(seed=5, cache_dir=None):
+    """Directory holding a synthetic FFW4 of `iresnet_schedule(standalone=True)`
+    (model.ffw4) with its own models/op_scales.bin and models/op_scales_v2.bin
+    (`standalone_scales`), generated on first use."""
+    cache_dir = cache_dir or os.environ.get("FASTFACE_CACHE", "/tmp/fastface_cache")
+    d = os.path.join(cache_dir, "standalone_seed%d" % seed)
+    ffw = os.path.join(d, "model.ffw4")
+    if not os.path.exists(ffw):
+        os.makedirs(os.path.join(d, "models"), exist_ok=True)
+        ops = iresnet_schedule(standalone=True)
+        (in_s, sc), (in_pc, per_op) = standalone_scales(ops)
+        write_opsc(os.path.join(d, "models", "op_scales.bin"), in_s, sc)
+        write_opsc2(os.path.join(d, "models", "op_scales_v2.bin"), in_pc, per_op)
+        write_synthetic_ffw4(ffw, seed=seed, ops=ops, opsc2=(in_pc, per_op))
+    return d
 
 
 def faces_uniform(batch, seed):

@@ -131,7 +131,8 @@ int fastface_set_shortcut_fusion(FastFace* ff, int on);
 
 /* ---------------- introspection (tests, bench) ---------------------------- */
 typedef struct {
-    int kind;                 /* 1 conv, 2 FC                                   */
+    int kind;                 /* 1 conv, 2 FC, 3 stand-alone BN / PReLU (a
+                                 per-channel table), 4 stand-alone Add          */
     int op_first, op_last;    /* reference op indices this launch covers        */
     int cin, cout, kh, kw, stride, pad, hin, win, hout, wout;   /* as launched:
                                  a 1x1 stride-2 shortcut over a tensor stored

@@ -269,6 +269,31 @@ int         ffk_conv_grid(const ffk_conv_desc* d);
 int    ffk_make_bn_lut(const float* s_in, const float* bn_s, const float* bn_o,
                        const float* bn_inv, int cout, int8_t* lut);
 
+/* ---- stand-alone elementwise ops --------------------------------------
+ * A BN or PReLU whose input is not a conv's output, and an Add after no conv,
+ * run as table lookups over int8 tensors (NHWC, 16-byte aligned).
+ *
+ * Replaces bn_prelu_requant_int8 (kernels/int8_epilogue.c:253-318, called by
+ * libfastface.c:401-424): lut[c*256 + q + 128] is that function's output for
+ * the int8 value q in channel c, with in-scale s_in[c], BN scale and offset
+ * bn_s[c] / bn_o[c] (both NULL: no BN), PReLU slope[c] (NULL: no PReLU) and
+ * output inverse scale inv[c] (host function; the reference's 8-channel
+ * vector path, which every channel count that is a multiple of 8 takes). */
+int    ffk_make_map_lut(const float* s_in, const float* bn_s, const float* bn_o,
+                        const float* slope, const float* inv, int c, int8_t* lut);
+/* Replaces add_requant_int8 (kernels/int8_epilogue.c:116-131, called by
+ * libfastface.c:429-434): lut[(a + 128)*256 + b + 128] =
+ * clamp((int)lrintf(fma(a, a_scale, b*b_scale) * (1/(out_scale + 1e-9f))))
+ * as the reference computes it on x86-64 (host function, 65536 bytes). */
+int    ffk_make_add_lut(float a_scale, float b_scale, float out_scale, int8_t* lut);
+/* out[p*c + ch] = lut[ch*256 + in[p*c + ch] + 128] for n_pix pixels of c
+ * channels (c a multiple of 64); `out` may not overlap `in`. */
+int    ffk_map_i8(const int8_t* in, int8_t* out, long long n_pix, int c, const int8_t* lut,
+                  void* stream);
+/* out[i] = lut[(a[i] + 128)*256 + b[i] + 128] for n bytes (a multiple of 16). */
+int    ffk_add_i8(const int8_t* a, const int8_t* b, int8_t* out, long long n, const int8_t* lut,
+                  void* stream);
+
 /* uint8 RGB input as a table: lut[c*256 + x] is the reference's input
  * quantization (quantize_fp32_nhwc_to_int8_per_channel,
  * kernels/int8_epilogue.c:231-247) of the pixel value its SDKs feed it,

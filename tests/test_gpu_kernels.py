@@ -1056,3 +1056,62 @@ def test_fma_tail_window_is_real(gpu_lib, oracle):
     assert np.array_equal(plain, exp)
     assert (forced[..., 0] == 0).all()
     assert np.array_equal(forced[..., 1:], exp[..., 1:])
+
+
+MAP_CASES = [  # (C, pixels, bn, prelu): ragged pixel counts, and more passes than the grid has workgroups
+    (64, 1, True, False), (128, 37, False, True), (256, 1001, True, True), (512, 49, False, False),
+    (64, 3 * 2048 * 64 + 5, True, True),
+]
+
+
+@pytest.mark.parametrize("C_,pix,bn,prelu", MAP_CASES)
+def test_standalone_map_kernel(gpu_lib, oracle, C_, pix, bn, prelu):
+    """A stand-alone BN / PReLU through its per-channel table on the device
+    equals the oracle's bn_prelu_requant (itself pinned to the reference's
+    bn_prelu_requant_int8) on every element, special parameters included."""
+    lib = gpu_lib
+    r = rng(1700 + C_ + pix)
+    x = r.integers(-128, 128, size=(pix, C_), dtype=np.int8)
+    x[0, :] = np.arange(C_) % 256 - 128                  # every value in some channel
+    s_in = r.uniform(1e-3, 5e-2, C_).astype(F32)
+    bns = r.uniform(0.5, 1.5, C_).astype(F32)
+    bno = r.normal(0, 0.05, C_).astype(F32)
+    slope = r.uniform(0.0, 0.3, C_).astype(F32)
+    inv = (1.0 / r.uniform(0.01, 0.1, C_)).astype(F32)
+    s_in[0], bns[1], slope[2], inv[3], bno[4] = np.float32(3e-45), np.nan, -0.5, 3e38, -0.0
+    lut = np.empty((C_, 256), np.int8)
+    gpu_util.check(lib, lib.ffk_make_map_lut(s_in.ctypes.data, bns.ctypes.data if bn else None,
+                                             bno.ctypes.data if bn else None,
+                                             slope.ctypes.data if prelu else None, inv.ctypes.data,
+                                             C_, lut.ctypes.data))
+    d_in, d_lut = gpu_util.Dev(lib, host=x), gpu_util.Dev(lib, host=lut)
+    d_out = gpu_util.Dev(lib, nbytes=x.nbytes)
+    gpu_util.check(lib, lib.ffk_map_i8(d_in.ptr, d_out.ptr, pix, C_, d_lut.ptr, None))
+    gpu_util.check(lib, lib.ffk_stream_sync(None))
+    got = d_out.get(np.int8, x.shape)
+    exp = oracle.bn_prelu_requant(x, in_scale_pc=s_in, bn_scale=bns if bn else None,
+                                  bn_offset=bno if bn else None, prelu=slope if prelu else None,
+                                  inv_pc=inv)
+    assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("n,scales", [(16, (0.013, 0.021, 0.03)), (65536 * 16, (0.5, 0.5, 1.0)),
+                                      (4 * 1024 * 256 * 16 + 48, (3e38, 3e38, 1e-30))])
+def test_standalone_add_kernel(gpu_lib, oracle, n, scales):
+    """A stand-alone Add through its pair table on the device equals the
+    oracle's add_requant (pinned to the reference's add_requant_int8); the
+    largest case takes more passes than the grid has workgroups."""
+    lib = gpu_lib
+    r = rng(1800 + n)
+    a = r.integers(-128, 128, size=n, dtype=np.int8)
+    b = r.integers(-128, 128, size=n, dtype=np.int8)
+    if n >= 65536:                                       # every pair once
+        a[:65536] = np.repeat(np.arange(-128, 128, dtype=np.int8), 256)
+        b[:65536] = np.tile(np.arange(-128, 128, dtype=np.int8), 256)
+    lut = np.empty(65536, np.int8)
+    gpu_util.check(lib, lib.ffk_make_add_lut(*scales, lut.ctypes.data))
+    da, db, dl = gpu_util.Dev(lib, host=a), gpu_util.Dev(lib, host=b), gpu_util.Dev(lib, host=lut)
+    do = gpu_util.Dev(lib, nbytes=n)
+    gpu_util.check(lib, lib.ffk_add_i8(da.ptr, db.ptr, do.ptr, n, dl.ptr, None))
+    gpu_util.check(lib, lib.ffk_stream_sync(None))
+    assert np.array_equal(do.get(np.int8, n), oracle.add_requant(a, scales[0], b, scales[1], scales[2]))

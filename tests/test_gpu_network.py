@@ -162,6 +162,50 @@ def test_other_formats_end_to_end(gpu_lib, oracle, version, with_opsc2):
         oracle.free_model(m)
 
 
+@pytest.mark.parametrize("with_opsc2", [True, False], ids=["opsc2", "noopsc2"])
+def test_standalone_elementwise_ops_end_to_end(gpu_lib, oracle, with_opsc2):
+    """A model with elementwise ops that no conv absorbs (synth
+    `iresnet_schedule(standalone=True)`: a PReLU after a residual Add, whose
+    output is a block input that a 1x1 stride-2 shortcut reads, a BN after
+    that PReLU, an Add after a BN, a BN after that Add, a second BN and a
+    PReLU after the last one;
+    libfastface.c:401-434).  The plan runs them as table steps (five maps, one
+    Add); embeddings equal the oracle's (itself equal to the reference's
+    fastface_embed on this model) at b=1 and on faces of both halves of a split
+    batch; every intermediate int8 tensor equals the oracle's at 2 faces."""
+    d = synth.synthetic_standalone_dir()
+    ffw = os.path.join(d, "model.ffw4")
+    opsc = os.path.join(d, "models", "op_scales.bin")
+    opsc2 = os.path.join(d, "models", "op_scales_v2.bin" if with_opsc2 else "no_such_v2.bin")
+    m = oracle.load_model(ffw, opsc, opsc2 if with_opsc2 else None)
+    f = fa.FastFace(ffw, scale_files=(opsc, opsc2))
+    try:
+        info = fa.fastface_step_info()
+        kinds = []
+        for s in range(gpu_lib.fastface_num_steps(f.ff)):
+            assert gpu_lib.fastface_get_step(f.ff, s, C.byref(info)) == 0
+            kinds.append(info.kind)
+        assert kinds.count(3) == 5 and kinds.count(4) == 1 and kinds.count(1) == 53
+        x = synth.faces_uniform(50, 70)
+        batch = f.embed_batch(x)                        # two halves of 25 faces
+        idx = [0, 24, 25, 49]
+        exp, _ = oracle.forward(m, x[idx])
+        assert np.array_equal(batch[idx], exp)
+        assert np.array_equal(f.embed(x[0]), exp[0])
+        assert gpu_lib.fastface_debug_keep_tensors(f.ff, 1) == 0
+        exp2, dumps = oracle.forward(m, x[:2], dump_ops=set(range(183)))
+        assert np.array_equal(f.embed_batch(x[:2]), exp2)
+        for op in (53, 55, 70, 71, 74, 179, 180):      # the inserted ops, the BNs after them
+            assert op in dumps
+        for op, t in sorted(dumps.items()):
+            buf = np.empty(t.size, np.int8)
+            assert gpu_lib.fastface_debug_read(f.ff, op, 2, buf.ctypes.data, buf.nbytes) == t.size, op
+            assert np.array_equal(buf.reshape(t.shape), t), "op %d differs" % op
+    finally:
+        f.close()
+        oracle.free_model(m)
+
+
 def test_stage_outputs_stored_at_even_pixels(ff, gpu_lib):
     """The stem's output X and each stage's last X are read only by the next
     stage's 1x1 stride-2 shortcut: the plan stores them at their even pixels

@@ -85,6 +85,129 @@ def test_bn_table_matches_oracle_bn_requant(oracle):
     assert np.array_equal(lut.T, exp)
 
 
+def _map_params(r, C_):
+    """Per-channel parameters of a stand-alone BN / PReLU with the delicate
+    values: denormal and tiny scales, NaN, -0, huge inverses, negative and
+    > 1 slopes, exact .5 ties (q * 0.5 * 1.0)."""
+    s_in = r.uniform(1e-3, 5e-2, C_).astype(np.float32)
+    s_in[0], s_in[1], s_in[8] = np.float32(3e-45), np.float32(1.2e-38), 0.5
+    bns = r.uniform(0.5, 1.5, C_).astype(np.float32)
+    bns[2], bns[8] = np.nan, 1.0
+    bno = r.normal(0, 0.05, C_).astype(np.float32)
+    bno[3], bno[8] = -0.0, 0.0
+    slope = r.uniform(0.0, 0.3, C_).astype(np.float32)
+    slope[4], slope[5], slope[6], slope[8] = -0.7, 2.5, np.nan, 1.0
+    inv = (1.0 / r.uniform(0.01, 0.1, C_)).astype(np.float32)
+    inv[4], inv[5], inv[7], inv[8] = 1e9, 3e38, 1e30, 1.0
+    return s_in, bns, bno, slope, inv
+
+
+MAP_FORMS = [(True, False), (False, True), (True, True), (False, False)]   # (bn, prelu)
+
+
+def _make_map_lut(lib, s_in, bns, bno, slope, inv, bn, prelu):
+    C_ = s_in.size
+    lut = np.empty((C_, 256), np.int8)
+    assert lib.ffk_make_map_lut(s_in.ctypes.data, bns.ctypes.data if bn else None,
+                                bno.ctypes.data if bn else None, slope.ctypes.data if prelu else None,
+                                inv.ctypes.data, C_, lut.ctypes.data) == 0
+    return lut
+
+
+@pytest.mark.parametrize("bn,prelu", MAP_FORMS)
+def test_map_table_matches_oracle(oracle, bn, prelu):
+    """A stand-alone BN / PReLU is a per-channel table over the 256 int8
+    values: every entry equals the oracle's bn_prelu_requant of that value."""
+    lib = fa.load()
+    C_ = 72
+    s_in, bns, bno, slope, inv = _map_params(np.random.default_rng(31), C_)
+    lut = _make_map_lut(lib, s_in, bns, bno, slope, inv, bn, prelu)
+    q = np.arange(-128, 128, dtype=np.int8).reshape(256, 1).repeat(C_, axis=1)
+    exp = oracle.bn_prelu_requant(q, in_scale_pc=s_in, bn_scale=bns if bn else None,
+                                  bn_offset=bno if bn else None, prelu=slope if prelu else None,
+                                  inv_pc=inv)
+    assert np.array_equal(lut.T, exp)
+    assert lib.ffk_make_map_lut(s_in.ctypes.data, bns.ctypes.data, None, None, inv.ctypes.data,
+                                C_, lut.ctypes.data) != 0
+
+
+@pytest.mark.parametrize("bn,prelu", MAP_FORMS)
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_map_table_matches_reference(ref, bn, prelu, per_channel):
+    """The same tables against the reference's own bn_prelu_requant_int8,
+    with per-channel scales and with the scalar in-scale and 1/(s + 1e-9f)
+    inverse the reference falls back to (libfastface.c:401-424)."""
+    lib = fa.load()
+    C_ = 72
+    s_in, bns, bno, slope, inv = _map_params(np.random.default_rng(32), C_)
+    kw = dict(bn_scale=bns if bn else None, bn_offset=bno if bn else None,
+              prelu=slope if prelu else None)
+    if per_channel:
+        kw.update(in_scale_pc=s_in, inv_pc=inv)
+    else:
+        s, out_s = np.float32(0.0213), np.float32(0.0371)
+        s_in = np.full(C_, s, np.float32)
+        inv = np.full(C_, np.float32(1.0) / (out_s + np.float32(1e-9)), np.float32)
+        kw.update(in_scale=float(s), out_scale=float(out_s))
+    lut = _make_map_lut(lib, s_in, bns, bno, slope, inv, bn, prelu)
+    q = np.arange(-128, 128, dtype=np.int8).reshape(256, 1).repeat(C_, axis=1)
+    assert np.array_equal(lut.T, ref.bn_prelu_requant(q, **kw))
+
+
+ADD_SCALES = [  # (a_scale, b_scale, out_scale)
+    (0.013, 0.021, 0.03),            # the residual sum's usual range
+    (0.5, 0.5, 1.0),                 # exact halves: round-half-even ties
+    (1.0, -1.0, 0.5),                # saturation both ways
+    (3e38, 3e38, 1e-30),             # inf and NaN sums, then lrintf's out-of-range long
+    (2.0 ** 20, 1.0, 2.0 ** -12),    # values in [2^31, 2^63): the int cast keeps 32 bits
+    (np.nan, 0.01, 0.02),
+    (1e-40, -2e-39, 1e-38),          # denormal scales
+]
+
+
+def _add_table(lib, sa, sb, so):
+    lut = np.empty(65536, np.int8)
+    assert lib.ffk_make_add_lut(sa, sb, so, lut.ctypes.data) == 0
+    return lut.reshape(256, 256)
+
+
+def _all_pairs():
+    v = np.arange(-128, 128, dtype=np.int8)
+    return np.repeat(v, 256), np.tile(v, 256)
+
+
+@pytest.mark.parametrize("sa,sb,so", ADD_SCALES)
+def test_add_table_matches_oracle(oracle, sa, sb, so):
+    """A stand-alone Add is one 256 x 256 table (its scales are per tensor):
+    every entry equals the oracle's add_requant of that pair."""
+    lib = fa.load()
+    a, b = _all_pairs()
+    exp = oracle.add_requant(a, sa, b, sb, so).reshape(256, 256)
+    assert np.array_equal(_add_table(lib, sa, sb, so), exp)
+
+
+@pytest.mark.parametrize("sa,sb,so", ADD_SCALES)
+def test_add_table_matches_reference(ref, sa, sb, so):
+    lib = fa.load()
+    a, b = _all_pairs()
+    exp = ref.add_requant(a, sa, b, sb, so).reshape(256, 256)
+    assert np.array_equal(_add_table(lib, sa, sb, so), exp)
+
+
+def test_eltwise_launch_argument_checks():
+    """The launchers reject what their kernels assume away, before touching
+    the device (pointers are never dereferenced on these paths)."""
+    lib = fa.load()
+    p = C.c_void_p(4096)
+    assert lib.ffk_map_i8(p, p, 10, 96, p, None) == -1           # channels not a multiple of 64
+    assert lib.ffk_map_i8(C.c_void_p(4100), p, 10, 64, p, None) == -1   # misaligned
+    assert lib.ffk_map_i8(None, p, 10, 64, p, None) == -1
+    assert lib.ffk_add_i8(p, p, p, 24, p, None) == -1            # not a multiple of 16 bytes
+    assert lib.ffk_add_i8(p, C.c_void_p(4104), p, 32, p, None) == -1
+    assert lib.ffk_map_i8(p, p, 0, 64, p, None) == 0             # nothing to do
+    assert lib.ffk_add_i8(p, p, p, 0, p, None) == 0
+
+
 def test_every_iresnet_conv_has_a_kernel():
     lib = fa.load()
     H = 112

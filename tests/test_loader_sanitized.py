@@ -187,8 +187,9 @@ def test_opsc2_errors_degrade_to_per_tensor(checker, synth_ffw4, tmp_path):
 
 
 def test_unsupported_op_sequence_fails_plan(checker, tmp_path):
-    """A stand-alone PReLU (no conv before it) is a valid file the planner
-    rejects with a message: create fails instead of running it otherwise."""
+    """A PReLU on the fp32 input faces (no conv before it; only the stem conv
+    reads them, quantizing on the fly) is a valid file the planner rejects
+    with a message: create fails instead of running it otherwise."""
     ffw = b"FFW4" + struct.pack("<I", 1) + bytes([synth.OP_PRELU]) + struct.pack("<H", 3) + \
         np.full(3, 0.25, np.float32).tobytes()
     opsc = b"OPSC" + struct.pack("<I", 1) + np.float32(1 / 127).tobytes() + \
@@ -282,3 +283,82 @@ def test_launch_lists_without_a_gpu(checker, synth_ffw4):
     variants = lambda tag: {t[4] for t in chains[tag]}
     assert "splitk" in variants("1") and "splitk" not in variants("1024/h0")
     assert "patch_kg" not in variants("1024/h0") and "patch" in variants("1024/h0")
+
+
+def test_standalone_ops_plan_and_tables(checker, oracle, tmp_path):
+    """The model with stand-alone elementwise ops (synth
+    `iresnet_schedule(standalone=True)`) plans under the sanitizers with and
+    without OPSC2: 53 convs + 5 table maps + 1 table Add + the FC, each map or
+    Add in every chain's launch list at its tensor's pixel count; each map's
+    table is the oracle's bn_prelu_requant of the 256 int8 values with the
+    step's rows, whose BN / PReLU rows are the file's; the Add's table is
+    the oracle's add_requant of every pair with the per-tensor scales the
+    reference passes (libfastface.c:429-434: the current scale, the saved
+    tensor's, the op's own)."""
+    import fastface_amd as fa
+    d = synth.synthetic_standalone_dir()
+    ffw = os.path.join(d, "model.ffw4")
+    opsc, opsc2 = os.path.join(d, "models", "op_scales.bin"), os.path.join(d, "models", "op_scales_v2.bin")
+    with open(ffw, "rb") as f:
+        blob = f.read()
+    offs, _ = op_offsets(blob)
+    _, sc = synth.read_opsc(opsc)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0")
+    for v2 in (opsc2, "-"):
+        dump = str(tmp_path / ("arena" + ("2" if v2 != "-" else "")))
+        r = subprocess.run([checker, ffw, opsc, v2, dump], capture_output=True, text=True, env=env,
+                           timeout=120)
+        assert r.returncode == 0, r.stderr[-2000:]
+        assert "plan 0 steps 60 " in r.stdout, r.stdout
+        arena = np.fromfile(dump + ".bin", np.int8)
+        params = np.fromfile(dump + ".params.bin", np.float32)
+        maps = []
+        for line in open(dump + ".txt"):
+            kind, op, off, n, *rest = line.split()
+            if kind not in ("map", "add"):
+                continue
+            op, off, n, p_off = int(op), int(off), int(n), int(rest[0])
+            got = arena[off:off + n]
+            if kind == "add":
+                assert op == 71 and n == 65536
+                a_s, b_s, o_s = params[p_off:p_off + 3]
+                assert (a_s, b_s, o_s) == (sc[68], sc[68], sc[71])
+                v = np.arange(-128, 128, dtype=np.int8)
+                exp = oracle.add_requant(np.repeat(v, 256), a_s, np.tile(v, 256), b_s, o_s)
+                assert np.array_equal(got, exp)
+                continue
+            maps.append(op)
+            C_ = n // 256
+            rows = params[p_off:p_off + fa.FFK_NPARAM * C_].reshape(fa.FFK_NPARAM, C_)
+            t = blob[offs[op]]
+            file_vals = np.frombuffer(blob, np.float32, (2 if t == synth.OP_BN else 1) * C_, offs[op] + 3)
+            if t == synth.OP_BN:
+                assert np.array_equal(rows[fa.FFK_P_BN_S], file_vals[:C_])
+                assert np.array_equal(rows[fa.FFK_P_BN_O], file_vals[C_:])
+            else:
+                assert np.array_equal(rows[fa.FFK_P_SLOPE], file_vals)
+            q = np.arange(-128, 128, dtype=np.int8).reshape(256, 1).repeat(C_, axis=1)
+            bn = t == synth.OP_BN
+            exp = oracle.bn_prelu_requant(q, in_scale_pc=rows[fa.FFK_P_BN_SIN],
+                                          bn_scale=rows[fa.FFK_P_BN_S] if bn else None,
+                                          bn_offset=rows[fa.FFK_P_BN_O] if bn else None,
+                                          prelu=None if bn else rows[fa.FFK_P_SLOPE],
+                                          inv_pc=rows[fa.FFK_P_BN_INV]).T.reshape(-1)
+            assert np.array_equal(got, exp), op
+        assert maps == [53, 55, 74, 179, 180]
+    r = subprocess.run([checker, ffw, opsc, opsc2, "-", "--launches", "1", "50"], capture_output=True,
+                       text=True, env=env, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    chains = {}
+    for line in r.stdout.splitlines():
+        t = line.split()
+        if t[0] == "launch":
+            chains.setdefault(t[1], []).append(t)
+    assert sorted(chains) == ["1", "50/h0", "50/h1"]
+    for tag, launches in chains.items():
+        faces = 1 if tag == "1" else 25
+        assert len(launches) == 60
+        tables = [(t[3], int(t[4]), int(t[5])) for t in launches if t[3] in ("map", "add")]
+        assert tables == [("map", 128, 784 * faces), ("map", 128, 784 * faces), ("add", 256, 196 * faces),
+                          ("map", 256, 196 * faces), ("map", 512, 49 * faces), ("map", 512, 49 * faces)]
+

@@ -257,15 +257,16 @@ def test_forward_vs_reference_embed(oracle, ref, oracle_model, synth_ffw4):
 OTHER_FORMATS = [(3, True), (3, False), (2, True), (2, False), (4, False)]
 
 
-def ref_embed_without_opsc2(ref, ffw, faces):
+def ref_embed_without_opsc2(ref, ffw, faces, cwd=None):
     """The reference's fastface_embed with no OPSC2 file to load ($OPSC2_PATH
     naming a missing file: libfastface.c:238-240 then keeps the per-tensor
-    OPSC scales)."""
+    OPSC scales); `cwd` holds models/op_scales.bin (default: the repo's)."""
     from fastface_amd import synth
+    cwd = cwd or synth.REPO_ROOT
     old = os.environ.get("OPSC2_PATH")
-    os.environ["OPSC2_PATH"] = os.path.join(synth.REPO_ROOT, "models", "no_such_op_scales_v2.bin")
+    os.environ["OPSC2_PATH"] = os.path.join(cwd, "models", "no_such_op_scales_v2.bin")
     try:
-        return ref.embed(ffw, faces, cwd=synth.REPO_ROOT)
+        return ref.embed(ffw, faces, cwd=cwd)
     finally:
         if old is None:
             del os.environ["OPSC2_PATH"]
@@ -300,6 +301,32 @@ def test_forward_vs_reference_embed_other_formats(oracle, ref, version, with_ops
     # the model is not degenerate: its activations spread over the int8 range
     for a in acts.values():
         assert a.astype(np.float32).std() > 5 and (a == 0).mean() < 0.2
+
+
+@pytest.mark.parametrize("with_opsc2", [True, False], ids=["opsc2", "noopsc2"])
+def test_forward_vs_reference_embed_standalone_ops(oracle, ref, with_opsc2):
+    """Whole network with elementwise ops that no conv absorbs (synth
+    `iresnet_schedule(standalone=True)`: stand-alone PReLU, BN after PReLU,
+    BN after an Add, an Add after a BN, a second BN; libfastface.c:401-434),
+    on its own OPSC / OPSC2 files.  Oracle interpreter == reference
+    fastface_embed, bit for bit, and the inserted ops' outputs are not
+    degenerate."""
+    from fastface_amd import synth
+    d = synth.synthetic_standalone_dir()
+    ffw = os.path.join(d, "model.ffw4")
+    faces = np.concatenate([synth.faces_uniform(1, 0), synth.faces_normal_clipped(1, 2)])
+    m = oracle.load_model(ffw, os.path.join(d, "models", "op_scales.bin"),
+                          os.path.join(d, "models", "op_scales_v2.bin") if with_opsc2 else None)
+    try:
+        emb, acts = oracle.forward(m, faces, dump_ops=[53, 55, 70, 71, 74, 179, 180])
+    finally:
+        oracle.free_model(m)
+    emb_ref = ref.embed(ffw, faces, cwd=d) if with_opsc2 else ref_embed_without_opsc2(ref, ffw, faces, cwd=d)
+    assert np.array_equal(emb, emb_ref)
+    if with_opsc2:
+        for op, a in acts.items():
+            a = a.astype(np.float32)
+            assert a.std() > 5 and (a == 0).mean() < 0.2 and (np.abs(a) >= 127).mean() < 0.2, op
 
 
 def test_synthetic_formats_share_their_weights():

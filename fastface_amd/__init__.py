@@ -110,6 +110,7 @@ EXPORTS = [
     ("ffk_graph_launch", C.c_int, [_p, _p]),
     ("ffk_graph_destroy", C.c_int, [_p]),
     ("ffk_conv_supported", C.c_int, [C.c_int] * 8),
+    ("ffk_conv_runnable", C.c_int, [C.c_int] * 8),
     ("ffk_prelu_le1_ok", C.c_int, [_p, C.c_int, C.c_int, C.c_int]),
     ("ffk_requant_in_range", C.c_int, [_p, C.c_int, C.c_int, C.c_int]),
     ("ffk_requant_fma_ok", C.c_int, [_p, C.c_int, C.c_int, C.c_int]),

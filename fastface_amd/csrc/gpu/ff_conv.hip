@@ -122,6 +122,16 @@ long long conv_pixels(const ffk_conv_desc* d) {
     return (long long)d->batch * hout * wout;
 }
 
+// A geometry the generic kernel runs: positive sizes, a stride, no negative
+// padding, at least one output pixel, and sizes whose products stay in range.
+bool generic_geometry(int cin, int cout, int kh, int kw, int stride, int pad, int hin, int win) {
+    if (cin <= 0 || cout <= 0 || kh <= 0 || kw <= 0 || stride <= 0 || pad < 0 || hin <= 0 || win <= 0)
+        return false;
+    if (cin > 65535 || cout > 65535 || kh > 255 || kw > 255 || pad > 255 || hin > 65535 || win > 65535)
+        return false;
+    return hin + 2 * pad >= kh && win + 2 * pad >= kw;
+}
+
 // kernel arguments of a descriptor (M, tiles_n and the split-K workspace are
 // set per launch)
 ConvArgs conv_args(const ffk_conv_desc* d) {
@@ -151,6 +161,11 @@ extern "C" {
 
 int ffk_conv_supported(int cin, int cout, int kh, int kw, int stride, int pad, int hin, int win) {
     return find_conv(cin, cout, kh, kw, stride, pad, hin, win) != nullptr;
+}
+
+int ffk_conv_runnable(int cin, int cout, int kh, int kw, int stride, int pad, int hin, int win) {
+    return find_conv(cin, cout, kh, kw, stride, pad, hin, win) != nullptr ||
+           generic_geometry(cin, cout, kh, kw, stride, pad, hin, win);
 }
 
 int ffk_prelu_le1_ok(const float* params, int cout, int ktotal, int with_add) {
@@ -299,9 +314,9 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
         return FFK_ERR_ARG;
     }
     const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);
-    if (!e) {
-        ffk_set_error("conv: no kernel for this layer geometry%s%s", nullptr, nullptr);
-        return FFK_ERR_UNSUPPORTED;
+    if (!e && !generic_geometry(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win)) {
+        ffk_set_error("conv: invalid layer geometry%s%s", nullptr, nullptr);
+        return FFK_ERR_ARG;
     }
     const long long M = conv_pixels(d);
     if (M > 0x7fffffffLL) {
@@ -344,6 +359,11 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     if (M == 0) return FFK_OK;
     if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_conv(d, (hipStream_t)stream);
     const ConvArgs a = conv_args(d);
+    if (!e) {                              // no tuned kernel: the generic one (64-bit addressing)
+        ConvArgs as = a;
+        as.M = (int)M;
+        return ff_conv_generic_launch(as, d, (hipStream_t)stream);
+    }
     // The direct-to-LDS kernels address the int8 input and the residual
     // tensor with 32-bit offsets: a batch whose input or output tensor
     // reaches 2 GiB runs as several launches over consecutive image ranges
@@ -493,7 +513,12 @@ size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d) {
 int ffk_conv_grid(const ffk_conv_desc* d) {
     if (!d || d->batch <= 0 || (d->flags & FFK_ALGO_WINOGRAD)) return -1;
     const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);
-    if (!e || e->cin == 3) return -1;                // (the stem sizes its persistent grid itself)
+    if (!e) {
+        if (!generic_geometry(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win)) return -1;
+        const long long g = ff_conv_generic_grid(conv_pixels(d), d->cout);
+        return g > 0x7fffffffLL ? -1 : (int)g;
+    }
+    if (e->cin == 3) return -1;                      // (the stem sizes its persistent grid itself)
     const long long M = conv_pixels(d);
     if (M > 0x7fffffffLL) return -1;
     return choose_launch(e, M, d->workspace ? d->workspace_bytes : 0, (d->flags & FFK_SHARED_GPU) != 0).grid;
@@ -502,8 +527,9 @@ int ffk_conv_grid(const ffk_conv_desc* d) {
 const char* ffk_conv_variant(const ffk_conv_desc* d) {
     if (!d || d->batch <= 0) return nullptr;
     const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);
-    if (!e) return nullptr;
     if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_eligible(d) ? "winograd" : nullptr;
+    if (!e) return generic_geometry(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win)
+                       ? "generic" : nullptr;
     const long long M = conv_pixels(d);
     if (M > 0x7fffffffLL) return nullptr;
     return choose_launch(e, M, d->workspace ? d->workspace_bytes : 0, (d->flags & FFK_SHARED_GPU) != 0).kind;

@@ -25,9 +25,10 @@
  *   - every scalar fallback of the reference (no OPSC2 entry, length
  *     mismatch) is resolved into explicit per-channel parameter rows,
  *     computed in fp32 exactly as the reference computes them.
- * Op sequences outside this pattern (ops on the fp32 input faces other than
- * the 3-channel stem conv, conv geometries without a kernel, ops after the
- * GEMM) are rejected (create fails) instead of being run some other way.
+ * A conv geometry without a tuned kernel runs on the generic one.  Op
+ * sequences outside this pattern (ops on the fp32 input faces other than a
+ * 3-channel conv, invalid conv geometries, ops after the GEMM) are rejected
+ * (create fails) instead of being run some other way.
  */
 #include <math.h>
 #include <pthread.h>
@@ -342,8 +343,8 @@ int ff_plan_build(const FfModel* m, FfPlan* p)
             if ((in_t == FF_T_INPUT) != (op->Cin == 3)) {
                 rc = fail(p, "only a 3-channel stem conv may read the input faces", i); break;
             }
-            if (!ffk_conv_supported(op->Cin, op->Cout, op->Kh, op->Kw, op->stride, op->pad, si.H, si.W)) {
-                rc = fail(p, "no kernel for this conv geometry", i); break;
+            if (!ffk_conv_runnable(op->Cin, op->Cout, op->Kh, op->Kw, op->stride, op->pad, si.H, si.W)) {
+                rc = fail(p, "invalid conv geometry", i); break;
             }
             const uint8_t* slope = NULL;
             int add_k = -1, eff = i, skip = 0;

@@ -48,7 +48,7 @@ OPSC_PATH = os.path.join(REPO_ROOT, "models", "op_scales.bin")
 OPSC2_PATH = os.path.join(REPO_ROOT, "models", "op_scales_v2.bin")
 
 
-def iresnet_schedule(stages=STAGES, standalone=False):
+def iresnet_schedule(stages=STAGES, standalone=False, generic=False):
     """List of op dicts in FFW4 order (types and conv geometry only).
 
     standalone=True inserts elementwise ops that no conv absorbs (each marked
@@ -57,14 +57,21 @@ def iresnet_schedule(stages=STAGES, standalone=False):
     SAVE_ID, a BN (the conv's second output) and an Add of the two (an Add
     after no conv), so that the next block's leading BN reads an Add's
     output; and a second BN and a PReLU after the final BN.  The reference's
-    interpreter runs them one by one (libfastface.c:401-434)."""
-    ops = [dict(type=OP_CONV, Cin=3, Cout=64, k=3, s=1, p=1), dict(type=OP_PRELU, C=64)]
+    interpreter runs them one by one (libfastface.c:401-434).
+
+    generic=True changes three convs to geometries without a tuned kernel,
+    keeping every tensor's shape (so the committed scale files still apply):
+    the stem and stage 3's fifth block's first conv as 5x5 pad 2, and stage
+    4's second block's second conv (the one adding the residual) as 1x1."""
+    ops = [dict(type=OP_CONV, Cin=3, Cout=64, k=5 if generic else 3, s=1, p=2 if generic else 1),
+           dict(type=OP_PRELU, C=64)]
     cin = 64
     for si, (nblocks, c) in enumerate(stages):
         for bi in range(nblocks):
             ops.append(dict(type=OP_BLOCK_START))
             ops.append(dict(type=OP_BN, C=cin))
-            ops.append(dict(type=OP_CONV, Cin=cin, Cout=c, k=3, s=1, p=1))
+            k1 = 5 if generic and si == 2 and bi == 4 else 3
+            ops.append(dict(type=OP_CONV, Cin=cin, Cout=c, k=k1, s=1, p=k1 // 2))
             ops.append(dict(type=OP_PRELU, C=c))
             if bi == 0:
                 ops.append(dict(type=OP_CONV, Cin=c, Cout=c, k=3, s=2, p=1))
@@ -72,7 +79,8 @@ def iresnet_schedule(stages=STAGES, standalone=False):
                 ops.append(dict(type=OP_CONV, Cin=cin, Cout=c, k=1, s=2, p=0))
                 ops.append(dict(type=OP_ADD))
             else:
-                ops.append(dict(type=OP_CONV, Cin=c, Cout=c, k=3, s=1, p=1))
+                k2 = 1 if generic and si == 3 and bi == 1 else 3
+                ops.append(dict(type=OP_CONV, Cin=c, Cout=c, k=k2, s=1, p=k2 // 2))
                 ops.append(dict(type=OP_ADD))
             if standalone and si == 1 and bi == nblocks - 1:
                 ops.append(dict(type=OP_PRELU, C=c, extra="copy"))
@@ -318,6 +326,17 @@ def synthetic_ffw4_path(seed=3, cache_dir=None, version=4):
     path = os.path.join(cache_dir, name)
     if not os.path.exists(path):
         write_synthetic_ffw4(path, seed=seed, version=version)
+    return path
+
+
+def synthetic_generic_path(seed=6, cache_dir=None):
+    """Path of a synthetic FFW4 of `iresnet_schedule(generic=True)` (the
+    committed scale files apply to it), generated on first use."""
+    cache_dir = cache_dir or os.environ.get("FASTFACE_CACHE", "/tmp/fastface_cache")
+    os.makedirs(cache_dir, exist_ok=True)
+    path = os.path.join(cache_dir, "synthetic_r50_generic_seed%d.ffw4" % seed)
+    if not os.path.exists(path):
+        write_synthetic_ffw4(path, seed=seed, ops=iresnet_schedule(generic=True))
     return path
 
 

@@ -207,9 +207,18 @@ int    ffk_requant_in_range(const float* params, int cout, int ktotal, int flags
  * a zero weight scale). */
 int    ffk_requant_fma_ok(const float* params, int cout, int ktotal, int flags);
 
-/* 1 if a kernel is compiled for this layer geometry, else 0. */
+/* 1 if a tuned kernel is compiled for this layer geometry (the IResNet
+ * layers at 112x112 input), else 0. */
 int    ffk_conv_supported(int cin, int cout, int kh, int kw, int stride, int pad,
                           int hin, int win);
+/* 1 if ffk_conv runs this geometry at all: a tuned kernel, or else the
+ * generic implicit GEMM that takes any kernel size, stride, padding and
+ * channel count (the reference's im2col path takes every shape,
+ * kernels/conv2d_nhwc.c:150-220; the same integers and int8 results, at a
+ * fraction of the tuned kernels' speed); 0 for an invalid geometry (a size
+ * or stride below 1, negative padding, no output pixel). */
+int    ffk_conv_runnable(int cin, int cout, int kh, int kw, int stride, int pad,
+                         int hin, int win);
 /* Bytes of the packed weights and the packing itself (host memory). */
 size_t ffk_conv_packed_bytes(int cin, int cout, int kh, int kw);
 int    ffk_pack_conv_weights(const int8_t* w_oihw, int cout, int cin, int kh, int kw,
@@ -254,12 +263,13 @@ int    ffk_conv_noalloc(const ffk_conv_desc* d, void* stream);
  * stride-2 layers as four phase images), "direct" (direct-to-LDS tiles),
  * "staged" / "staged128" (register-staged tiles), "splitk" (64x64 tiles
  * with the K reduction split over workgroups), "tile64" (64x64 tiles, whole
- * K: tiny grids), "winograd"; NULL when no kernel applies.  No counterpart in the reference: it lets
+ * K: tiny grids), "winograd", "generic" (any other geometry); NULL when no
+ * kernel applies.  No counterpart in the reference: it lets
  * tests and benchmarks name the code path they exercise. */
 const char* ffk_conv_variant(const ffk_conv_desc* d);
 /* Workgroups that launch would have (host function, no device involved);
- * -1 for the input layer (a persistent grid sized at launch), Winograd or
- * unsupported descriptors.  No counterpart in the reference: it lets a
+ * -1 for the tuned input layer (a persistent grid sized at launch), Winograd
+ * or invalid descriptors.  No counterpart in the reference: it lets a
  * launch list be built without a GPU. */
 int         ffk_conv_grid(const ffk_conv_desc* d);
 

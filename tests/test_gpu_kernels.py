@@ -1115,3 +1115,110 @@ def test_standalone_add_kernel(gpu_lib, oracle, n, scales):
     gpu_util.check(lib, lib.ffk_add_i8(da.ptr, db.ptr, do.ptr, n, dl.ptr, None))
     gpu_util.check(lib, lib.ffk_stream_sync(None))
     assert np.array_equal(do.get(np.int8, n), oracle.add_requant(a, scales[0], b, scales[1], scales[2]))
+
+
+GENERIC_CASES = [  # (cin, cout, kh, kw, stride, pad, H, W, B): no tuned kernel for any of them
+    (96, 64, 3, 3, 1, 1, 15, 13, 2),      # channel count, non-square image
+    (64, 64, 3, 3, 1, 0, 9, 9, 3),        # no padding
+    (17, 40, 5, 5, 2, 2, 23, 23, 2),      # odd channels, 5x5 stride 2, a partial channel tile
+    (256, 130, 1, 1, 1, 0, 7, 7, 5),      # 1x1, ragged output channels
+    (64, 72, 7, 1, 1, 3, 12, 12, 1),      # 7x1 kernel
+    (128, 64, 3, 3, 3, 1, 20, 20, 3),     # stride 3
+]
+
+
+def _generic_variant(lib, cin, cout, kh, kw, s, pad, H, W, B):
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, kh, kw
+    d.stride, d.pad, d.hin, d.win = s, pad, H, W
+    return lib.ffk_conv_variant(C.byref(d))
+
+
+@pytest.mark.parametrize("cin,cout,kh,kw,s,pad,H,W,B", GENERIC_CASES)
+def test_generic_conv_int32_accumulators(gpu_lib, oracle, cin, cout, kh, kw, s, pad, H, W, B):
+    """A geometry without a tuned kernel runs on the generic implicit GEMM:
+    int32 accumulators equal the oracle's convolution (pinned to brute force
+    on these shapes), extreme values included."""
+    assert _generic_variant(gpu_lib, cin, cout, kh, kw, s, pad, H, W, B) == b"generic"
+    r = rng(1900 + cin + cout + kh * 7 + kw + s)
+    x = r.integers(-128, 128, size=(B, H, W, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, kh, kw), dtype=np.int8)
+    x[0, 0] = -128
+    w[0] = -128
+    got = run_conv(gpu_lib, x, w, s, pad, raw=True)
+    assert np.array_equal(got, oracle.conv_i32(x, w, s, pad))
+
+
+@pytest.mark.parametrize("mode", ["prelu", "add_bn", "prelu_bn_even", "inscale_prelu_le1"])
+@pytest.mark.parametrize("case", [0, 2, 3])
+def test_generic_conv_epilogue(gpu_lib, oracle, mode, case):
+    """The generic kernel's epilogue (the tuned kernels' general form per
+    element: in-scale, ws, bias, residual, PReLU, round half away with the
+    x86 out-of-range case; X at even pixels; BN(X) through the table) equals
+    the oracle's fused epilogue and BN requant, special parameters included.
+    The shorter-form flags change nothing there."""
+    cin, cout, kh, kw, s, pad, H, W, B = GENERIC_CASES[case]
+    r = rng(2000 + case * 10 + len(mode))
+    x = r.integers(-128, 128, size=(B, H, W, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, kh, kw), dtype=np.int8)
+    Ho, Wo = (H + 2 * pad - kh) // s + 1, (W + 2 * pad - kw) // s + 1
+    ws, bias, inv = _special_params(r, cout)
+    rows = dict(ws=ws, bias=bias, inv=inv)
+    ekw = dict(ws=ws, bias=bias, inv_pc=inv)
+    flags = fa.FFK_EPI_BIAS
+    add = None
+    in_scale = 1.0
+    if "prelu" in mode:
+        slope = r.uniform(0, 0.3, cout).astype(F32)
+        slope[7] = -0.5
+        rows["slope"] = slope; ekw["prelu"] = slope; flags |= fa.FFK_EPI_PRELU
+    if "le1" in mode:
+        flags |= fa.FFK_EPI_PRELU_LE1 | fa.FFK_EPI_IN_RANGE
+    if "inscale" in mode:
+        in_scale = 0.0173
+        ekw["in_scale"] = in_scale; flags |= fa.FFK_EPI_INSCALE
+    if "add" in mode:
+        add = r.integers(-128, 128, size=(B, Ho, Wo, cout), dtype=np.int8)
+        adds = r.uniform(1e-3, 5e-2, cout).astype(F32)
+        rows["adds"] = adds; ekw.update(add_src=add, add_scale_pc=adds); flags |= fa.FFK_EPI_ADD
+    want_bn = "bn" in mode
+    if want_bn:
+        bsin = r.uniform(1e-3, 5e-2, cout).astype(F32)
+        bns = r.uniform(0.5, 1.5, cout).astype(F32)
+        bno = r.normal(0, 0.05, cout).astype(F32)
+        binv = (1.0 / r.uniform(0.01, 0.1, cout)).astype(F32)
+        rows.update(bn_sin=bsin, bn_s=bns, bn_o=bno, bn_inv=binv)
+        flags |= fa.FFK_EPI_BN
+    x_even = "even" in mode and Ho % 2 == 0 and Wo % 2 == 0
+    exp_x = oracle.fused_epilogue(oracle.conv_i32(x, w, s, pad), **ekw)
+    got_x, got_bn = run_conv(gpu_lib, x, w, s, pad, params=params_block(cout, **rows), flags=flags,
+                             add=add, want_bn=want_bn, in_scale=in_scale, x_even=x_even)
+    assert np.array_equal(got_x, exp_x[:, ::2, ::2] if x_even else exp_x)
+    if want_bn:
+        exp_bn = oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno, inv_pc=binv)
+        assert np.array_equal(got_bn, exp_bn)
+
+
+@pytest.mark.parametrize("rgb8", [False, True], ids=["fp32", "rgb8"])
+def test_generic_input_layer(gpu_lib, oracle, rgb8):
+    """A 3-channel input layer without a tuned kernel (5x5 stride 2, 32
+    channels): the faces are quantized on load (fp32, the reference's
+    lrintf semantics incl. ties and out-of-range values) or mapped through
+    the uint8 table, then the same int32 accumulators as the oracle's."""
+    r = rng(2100)
+    B = 2
+    w = r.integers(-128, 128, size=(32, 3, 5, 5), dtype=np.int8)
+    inv = np.array([127.0, 126.9, 127.3], F32)
+    if rgb8:
+        imgs = r.integers(0, 256, size=(B, 112, 112, 3), dtype=np.uint8)
+        lut = np.empty((3, 256), np.int8)
+        assert gpu_lib.ffk_make_rgb8_lut(inv.ctypes.data, lut.ctypes.data) == 0
+        got = run_conv(gpu_lib, imgs, w, 2, 2, raw=True, in_lut=lut, flags=fa.FFK_IN_RGB8)
+        q = oracle.quant_input((imgs.astype(F32) - 127.5) / 127.5, inv)
+    else:
+        x = r.uniform(-1, 1, size=(B, 112, 112, 3)).astype(F32)
+        x[0, 0, :4, 0] = [0.5 / 127, 1.5 / 127, 1e10, np.nan]
+        x[0, 1, :2, 1] = [-2.5 / 126.9, np.inf]
+        got = run_conv(gpu_lib, x, w, 2, 2, raw=True, in_inv=inv)
+        q = oracle.quant_input(x, inv)
+    assert np.array_equal(got, oracle.conv_i32(q, w, 2, 2))

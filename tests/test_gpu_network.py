@@ -206,6 +206,45 @@ def test_standalone_elementwise_ops_end_to_end(gpu_lib, oracle, with_opsc2):
         oracle.free_model(m)
 
 
+def test_generic_geometries_end_to_end(gpu_lib, oracle):
+    """A model with three convs of geometries no tuned kernel has (synth
+    `iresnet_schedule(generic=True)`: a 5x5 input layer, a 5x5 stage-3 conv
+    with its PReLU, a 1x1 stage-4 conv adding the residual and storing BN of
+    the sum): they run on the generic kernel, the rest as before.
+    Embeddings equal the oracle's (itself equal to the reference's
+    fastface_embed on this model) at b=1 and on faces of both halves of a
+    split batch; every intermediate int8 tensor equals the oracle's at 2
+    faces."""
+    ffw = synth.synthetic_generic_path()
+    m = oracle.load_model(ffw, synth.OPSC_PATH, synth.OPSC2_PATH)
+    f = fa.FastFace(ffw, cwd=synth.REPO_ROOT)
+    try:
+        info = fa.fastface_step_info()
+        generic = []
+        for s in range(gpu_lib.fastface_num_steps(f.ff)):
+            assert gpu_lib.fastface_get_step(f.ff, s, C.byref(info)) == 0
+            if info.kind == 1 and not gpu_lib.ffk_conv_supported(info.cin, info.cout, info.kh, info.kw,
+                                                                  info.stride, info.pad, info.hin, info.win):
+                generic.append((info.cin, info.cout, info.kh))
+        assert generic == [(3, 64, 5), (256, 256, 5), (512, 512, 1)]
+        x = synth.faces_uniform(50, 80)
+        batch = f.embed_batch(x)                        # two halves of 25 faces
+        idx = [0, 24, 25, 49]
+        exp, _ = oracle.forward(m, x[idx])
+        assert np.array_equal(batch[idx], exp)
+        assert np.array_equal(f.embed(x[0]), exp[0])
+        assert gpu_lib.fastface_debug_keep_tensors(f.ff, 1) == 0
+        exp2, dumps = oracle.forward(m, x[:2], dump_ops=set(range(177)))
+        assert np.array_equal(f.embed_batch(x[:2]), exp2)
+        for op, t in sorted(dumps.items()):
+            buf = np.empty(t.size, np.int8)
+            assert gpu_lib.fastface_debug_read(f.ff, op, 2, buf.ctypes.data, buf.nbytes) == t.size, op
+            assert np.array_equal(buf.reshape(t.shape), t), "op %d differs" % op
+    finally:
+        f.close()
+        oracle.free_model(m)
+
+
 def test_stage_outputs_stored_at_even_pixels(ff, gpu_lib):
     """The stem's output X and each stage's last X are read only by the next
     stage's 1x1 stride-2 shortcut: the plan stores them at their even pixels

@@ -267,8 +267,37 @@ def test_split_workspace_only_for_small_batches():
     assert need(64, 64, 3, 1, 56, 1) == 0             # short K chains never split
     assert need(64, 128, 3, 1, 56, 1) == 0
     assert need(64, 64, 1, 2, 112, 1) == 0            # 1x1: one K stage, nothing to split
-    assert need(96, 64, 3, 1, 112, 1) == 0            # no kernel
+    assert need(96, 64, 3, 1, 112, 1) == 0            # no tuned kernel: the generic one, no split
     assert lib.ffk_conv_workspace_bytes(None) == 0
+
+
+def test_generic_geometries_are_runnable():
+    """Geometries outside the tuned table run on the generic kernel (variant
+    "generic", one workgroup per 64x64 output tile, no workspace); invalid
+    geometries are refused before any launch."""
+    lib = fa.load()
+    d = fa.ffk_conv_desc()
+
+    def desc(cin, cout, kh, kw, s, pad, H, W, B):
+        d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, kh, kw
+        d.stride, d.pad, d.hin, d.win = s, pad, H, W
+        return C.byref(d)
+    for g in [(96, 64, 3, 3, 1, 1, 15, 13), (17, 40, 5, 5, 2, 2, 23, 23), (64, 72, 7, 1, 1, 3, 12, 12),
+              (3, 64, 5, 5, 1, 2, 112, 112), (64, 64, 3, 3, 1, 0, 56, 56)]:
+        assert lib.ffk_conv_runnable(*g) == 1 and lib.ffk_conv_supported(*g) == 0, g
+        cin, cout, kh, kw, s, pad, H, W = g
+        ho, wo = (H + 2 * pad - kh) // s + 1, (W + 2 * pad - kw) // s + 1
+        assert lib.ffk_conv_variant(desc(*g, 3)) == b"generic"
+        assert lib.ffk_conv_grid(desc(*g, 3)) == -(-3 * ho * wo // 64) * -(-cout // 64)
+        assert lib.ffk_conv_workspace_bytes(desc(*g, 3)) == 0
+    assert lib.ffk_conv_runnable(64, 64, 3, 3, 1, 1, 56, 56) == 1          # tuned
+    for bad in [(0, 64, 3, 3, 1, 1, 8, 8), (64, 64, 3, 3, 0, 1, 8, 8), (64, 64, 3, 3, 1, -1, 8, 8),
+                (64, 64, 9, 9, 1, 0, 8, 8), (64, 64, 3, 3, 1, 1, 0, 8)]:
+        assert lib.ffk_conv_runnable(*bad) == 0, bad
+        assert lib.ffk_conv_variant(desc(*bad, 1)) is None
+        d.in_ = d.w = d.params = d.out = 4096                     # (never dereferenced)
+        d.flags = 0
+        assert lib.ffk_conv(desc(*bad, 1), None) == -1
 
 
 def test_conv_variant_policy():
@@ -299,7 +328,7 @@ def test_conv_variant_policy():
     assert lib.ffk_conv_variant(C.byref(d)) == b"splitk" and lib.ffk_conv_grid(C.byref(d)) == 7 * 8 * 3
     d.batch = 1
     assert lib.ffk_conv_grid(C.byref(d)) == 1 * 8 * 9
-    assert variant(96, 64, 3, 1, 112, 1) is None
+    assert variant(96, 64, 3, 1, 112, 1) == "generic"             # no tuned kernel
     assert lib.ffk_conv_variant(None) is None
     # The large tiles where there are at least as many as CUs (512->512 @7 at
     # 512 faces: 392), the 128x128 K-group tiles below (at 256 faces: 196).

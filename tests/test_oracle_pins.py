@@ -161,6 +161,64 @@ def test_conv_i32_brute_force(oracle):
         assert np.array_equal(got, exp)
 
 
+def _conv_brute(x, w, s, pad):
+    B, H, W, _ = x.shape
+    cout, _, kh, kw = w.shape
+    xp = np.pad(x.astype(np.int64), ((0, 0), (pad, pad), (pad, pad), (0, 0)))
+    Ho, Wo = (H + 2 * pad - kh) // s + 1, (W + 2 * pad - kw) // s + 1
+    exp = np.zeros((B, Ho, Wo, cout), np.int64)
+    for oh in range(Ho):
+        for ow in range(Wo):
+            patch = xp[:, oh * s:oh * s + kh, ow * s:ow * s + kw, :]
+            exp[:, oh, ow, :] = np.einsum("bhwc,ochw->bo", patch, w.astype(np.int64))
+    return exp
+
+
+# geometries outside the IResNet table (the generic GPU kernel's cases):
+# (cin, cout, kh, kw, stride, pad, H, W)
+ODD_GEOMETRIES = [(96, 64, 3, 3, 1, 1, 7, 6), (17, 40, 5, 5, 2, 2, 9, 9), (64, 72, 7, 1, 1, 3, 8, 8),
+                  (128, 64, 3, 3, 3, 1, 10, 10), (3, 32, 5, 5, 2, 0, 11, 11)]
+
+
+@pytest.mark.parametrize("cin,cout,kh,kw,s,pad,H,W", ODD_GEOMETRIES)
+def test_conv_i32_other_geometries(oracle, cin, cout, kh, kw, s, pad, H, W):
+    """The oracle's convolution on shapes no tuned kernel has (channel counts,
+    kernel sizes, non-square kernels, strides, paddings): the definition by
+    brute force."""
+    r = rng(17 + cin + kh * 3 + kw + s)
+    x = r.integers(-128, 128, size=(2, H, W, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, kh, kw), dtype=np.int8)
+    x[0, 0, 0, :] = -128
+    w[0] = -128
+    assert np.array_equal(oracle.conv_i32(x, w, s, pad), _conv_brute(x, w, s, pad))
+
+
+@pytest.mark.parametrize("cin,cout,kh,kw,s,pad,H,W", [g for g in ODD_GEOMETRIES if g[2] == g[3]])
+def test_conv_i32_other_geometries_vs_reference(oracle, ref, cin, cout, kh, kw, s, pad, H, W):
+    """The same shapes (square kernels: the reference's packer takes one
+    kernel size per axis as given) against the reference's im2col + VNNI."""
+    r = rng(18 + cin + kh + s)
+    x = r.integers(-128, 128, size=(2, H, W, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, kh, kw), dtype=np.int8)
+    assert np.array_equal(oracle.conv_i32(x, w, s, pad), ref.conv_i32(x, w, s, pad))
+
+
+def test_forward_vs_reference_embed_generic_geometries(oracle, ref):
+    """Whole network with three convs of geometries no tuned kernel has (synth
+    `iresnet_schedule(generic=True)`: a 5x5 stem, a 5x5 stage-3 conv, a 1x1
+    stage-4 conv adding the residual): oracle interpreter == reference
+    fastface_embed, bit for bit."""
+    from fastface_amd import synth
+    ffw = synth.synthetic_generic_path()
+    faces = np.concatenate([synth.faces_uniform(1, 0), synth.faces_normal_clipped(1, 2)])
+    m = oracle.load_model(ffw, synth.OPSC_PATH, synth.OPSC2_PATH)
+    try:
+        emb, _ = oracle.forward(m, faces)
+    finally:
+        oracle.free_model(m)
+    assert np.array_equal(emb, ref.embed(ffw, faces, cwd=synth.REPO_ROOT))
+
+
 WINO_SHAPES = [(64, 64, 56, 1), (64, 64, 112, 1), (16, 8, 6, 2)]
 
 

@@ -132,14 +132,17 @@ def cpu_baseline(ffw, runs=5, cooldown=1.0):
                         if r1:
                             b1.append(r1[1])
                     if b1:
+                        log("cpu baseline: reference fastface_int8 b=1, %d threads: median of %d runs %.3f ms"
+                            % (threads, len(b1), statistics.median(b1)))
                         rec["b1_ms_" + tag] = min(b1)
                         rec["b1_stable_" + tag] = {
                             "threads": threads, "runs": len(b1), "cooldown_s": cooldown,
                             "median_ms": round(statistics.median(b1), 3),
                             "min_ms": round(min(b1), 3), "max_ms": round(max(b1), 3),
                             "protocol": "bench_stable_int8_ffw4.py:7-13 (median of runs, each the binary's "
-                                        "best of 5x30), %d runs / %.1f s cooldown instead of 20 / 3 s"
-                                        % (len(b1), cooldown)}
+                                        "best of 5x30), %d runs / %.1f s cooldown%s"
+                                        % (len(b1), cooldown, "" if (len(b1), cooldown) == (20, 3.0)
+                                           else " instead of 20 / 3 s")}
             return rec
     from fastface_amd import synth
     from oracle.oracle import Oracle

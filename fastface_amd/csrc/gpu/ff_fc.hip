@@ -43,7 +43,8 @@ __global__ __launch_bounds__(FC_NT) void fc_matvec_kernel(const int8_t* __restri
                                                           const float* __restrict__ ws,
                                                           const float* __restrict__ bias,
                                                           float a_scale, float* out,
-                                                          const ffk_io* io, int B, int N, int K) {
+                                                          const ffk_io* io, int io_face, int B, int N,
+                                                          int K) {
     __shared__ int part[FC_ROWS][FC_KSPLIT][FC_MAXB];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -84,7 +85,7 @@ __global__ __launch_bounds__(FC_NT) void fc_matvec_kernel(const int8_t* __restri
         int v = 0;
 #pragma unroll
         for (int k = 0; k < FC_KSPLIT; k++) v += part[r][k][lane];
-        float* o = out ? out : io->out;
+        float* o = out ? out : io->out + (size_t)io_face * N;
         o[(size_t)lane * N + n] = ff::fc_out(v, a_scale, ws[n], bias[n]);
     }
 }
@@ -153,18 +154,16 @@ int ffk_fc(const ffk_fc_desc* d, void* stream) {
     if (d->batch == 0) return FFK_OK;
     hipStream_t s = (hipStream_t)stream;
     int path = d->path;
-    if (path == 0) path = d->batch <= FC_MAXB ? 1 : 2;
+    // the MFMA GEMM is compiled for the IResNet head (25088 -> 512); any
+    // other shape takes the matvec in chunks of FC_MAXB faces at every batch
+    const bool gemm_shape = d->n == 512 && d->k == 25088;
+    if (path == 0) path = (d->batch <= FC_MAXB || !gemm_shape) ? 1 : 2;
     if (path == 2) return ffk_fc_gemm_launch(d, s);
-    // matvec: chunks of FC_MAXB faces
     for (int b0 = 0; b0 < d->batch; b0 += FC_MAXB) {
         const int nb = d->batch - b0 < FC_MAXB ? d->batch - b0 : FC_MAXB;
         float* out = d->out ? d->out + (size_t)b0 * d->n : nullptr;
-        if (!out && b0 != 0) {
-            ffk_set_error("fc: io output needs batch <= 16 on the matvec path%s%s", nullptr, nullptr);
-            return FFK_ERR_ARG;
-        }
         hipLaunchKernelGGL(fc_matvec_kernel, dim3((d->n + FC_ROWS - 1) / FC_ROWS), dim3(FC_NT), 0, s,
-                           d->a + (size_t)b0 * d->k, d->w, d->ws, d->bias, d->a_scale, out, d->io,
+                           d->a + (size_t)b0 * d->k, d->w, d->ws, d->bias, d->a_scale, out, d->io, b0,
                            nb, d->n, d->k);
         int rc = ffk_check_launch("fc matvec launch");
         if (rc) return rc;

@@ -35,7 +35,12 @@ extern "C" {
 typedef struct FastFace FastFace;
 
 /* Reference fastface.h:31.  Loads FFW4 (also FFW3/FFW2) weights, builds the
- * fused launch plan, packs and uploads the weights once. */
+ * fused launch plan, packs and uploads the weights once.  Any op list the
+ * reference's interpreter runs is accepted (convs of any geometry, BN /
+ * PReLU / Add with or without a conv before them), except ops on the fp32
+ * input faces other than a 3-channel conv, ops after the GEMM head, and a
+ * GEMM head whose K is not a multiple of 64 or whose N is not 512; those make
+ * create return NULL with a message on stderr. */
 FastFace* fastface_create(const char* ffw4_path);
 
 /* Reference fastface.h:35.  One face: 37632 fp32 in, 512 fp32 out. */

@@ -326,7 +326,10 @@ typedef struct {
     float          a_scale;
     float*         out;      /* [batch][n] fp32, or NULL: io->out             */
     const ffk_io*  io;
-    int            path;     /* 0 auto, 1 matvec, 2 MFMA GEMM                 */
+    int            path;     /* 0 auto (the matvec up to 16 faces, the GEMM
+                                above; a head other than 25088 -> 512 takes
+                                the matvec, 16 faces per launch), 1 matvec,
+                                2 MFMA GEMM (25088 -> 512 only)               */
     /* Optional workspace (device memory, zero-filled once, the same rules as
      * ffk_conv_desc.workspace; one workspace can serve both): the MFMA GEMM
      * path then shares each output tile's K reduction among several

@@ -383,6 +383,40 @@ def test_fc_head(gpu_lib, oracle, B, path, split):
         assert np.array_equal(got[b], oracle.fc(a[b], W, ws, bias)), "face %d" % b
 
 
+@pytest.mark.parametrize("B,via_io", [(40, False), (40, True), (3, True)])
+def test_fc_other_head_shapes(gpu_lib, oracle, B, via_io):
+    """A head other than 25088 -> 512 (here K = 4096) takes the matvec at
+    every batch, 16 faces per launch, writing to `out` or, as a captured
+    chain does, through the I/O descriptor (each launch at its first face's
+    rows); the GEMM path refuses the shape."""
+    lib = gpu_lib
+    r = rng(570 + B)
+    K, N = 4096, 512
+    a = r.integers(-128, 128, size=(B, K), dtype=np.int8)
+    W = r.integers(-127, 128, size=(N, K), dtype=np.int8)
+    ws = r.uniform(1e-7, 1e-5, N).astype(F32)
+    bias = r.normal(0, 0.05, N).astype(F32)
+    exp = np.stack([oracle.fc(a[b], W, ws, bias) for b in range(B)])
+    if not via_io:
+        assert np.array_equal(run_fc(lib, a, W, ws, bias), exp)
+        with pytest.raises(RuntimeError):
+            run_fc(lib, a, W, ws, bias, path=2)
+        return
+    packed = np.empty(lib.ffk_fc_packed_bytes(N, K), np.int8)
+    gpu_util.check(lib, lib.ffk_pack_fc_weights(W.ctypes.data, N, K, packed.ctypes.data))
+    da, dw = gpu_util.Dev(lib, host=a), gpu_util.Dev(lib, host=packed)
+    dws, db = gpu_util.Dev(lib, host=ws), gpu_util.Dev(lib, host=bias)
+    do = gpu_util.Dev(lib, nbytes=B * N * 4)
+    dio = gpu_util.Dev(lib, host=np.array([0, do.ptr], np.uint64))
+    d = fa.ffk_fc_desc()
+    d.batch, d.n, d.k = B, N, K
+    d.a, d.w, d.ws, d.bias, d.out, d.io = da.ptr, dw.ptr, dws.ptr, db.ptr, None, dio.ptr
+    d.a_scale = 1.0
+    gpu_util.check(lib, lib.ffk_fc(C.byref(d), None))
+    gpu_util.check(lib, lib.ffk_stream_sync(None))
+    assert np.array_equal(do.get(np.float32, (B, N)), exp)
+
+
 @pytest.mark.parametrize("B", [1, 2, 16])
 def test_fc_matvec_extreme_values(gpu_lib, oracle, B):
     """Matvec path (each row's K range split over several waves, partial sums

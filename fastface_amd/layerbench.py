@@ -39,8 +39,8 @@ def time_layer(lib, cin=256, cout=256, k=3, stride=1, hin=14, batch=64, iters=20
     the host's launch gaps, as a kernel trace's durations do."""
     pad = k // 2
     ho = (hin + 2 * pad - k) // stride + 1
-    if not lib.ffk_conv_supported(cin, cout, k, k, stride, pad, hin, hin):
-        raise ValueError("unsupported layer geometry")
+    if not lib.ffk_conv_runnable(cin, cout, k, k, stride, pad, hin, hin):
+        raise ValueError("invalid layer geometry")
     r = np.random.default_rng(1)
     if cin == 3:        # the input layer reads fp32 faces in [-1, 1]
         x = r.uniform(-1, 1, size=(batch, hin, hin, cin)).astype(np.float32)
@@ -266,6 +266,61 @@ def time_pair(lib, cin=64, cout=64, hin=112, cx=64, batch=1024, iters=10, fused=
             "fused": fused, "ms": round(ms.value / iters, 5)}
 
 
+def time_eltwise(lib, op="map", channels=256, hin=14, batch=1024, iters=20):
+    """Mean launch time of a stand-alone BN / PReLU (`op` "map": the
+    per-channel table kernel) or Add ("add": the pair table kernel) over
+    batch x hin x hin pixels of `channels` int8 channels (HIP events on the
+    launch stream; seeded int8 data and tables).  Reports the HBM rate of
+    the algorithmic bytes (2 or 3 per element) against 8 TB/s."""
+    r = np.random.default_rng(11)
+    n = batch * hin * hin * channels
+    held = []
+
+    def dev(arr=None, nbytes=None):
+        m = arr.nbytes if arr is not None else nbytes
+        p = lib.ffk_malloc(m)
+        if not p:
+            raise MemoryError(fa.last_error())
+        held.append(p)
+        if arr is not None:
+            lib.ffk_memcpy_h2d(p, arr.ctypes.data, m, None)
+        return p
+    a = dev(r.integers(-128, 128, size=n, dtype=np.int8))
+    out = dev(nbytes=n)
+    if op == "map":
+        lut = dev(r.integers(-128, 128, size=channels * 256, dtype=np.int8))
+        run = lambda s: lib.ffk_map_i8(a, out, batch * hin * hin, channels, lut, s)
+        per_elem = 2
+    else:
+        b = dev(r.integers(-128, 128, size=n, dtype=np.int8))
+        lut = dev(r.integers(-128, 128, size=65536, dtype=np.int8))
+        run = lambda s: lib.ffk_add_i8(a, b, out, n, lut, s)
+        per_elem = 3
+    stream, e0, e1, ms = C.c_void_p(), C.c_void_p(), C.c_void_p(), C.c_float()
+    lib.ffk_stream_create(C.byref(stream))
+    lib.ffk_event_create(C.byref(e0))
+    lib.ffk_event_create(C.byref(e1))
+    try:
+        for _ in range(3):
+            assert run(stream) == 0, fa.last_error()
+        lib.ffk_event_record(e0, stream)
+        for _ in range(iters):
+            run(stream)
+        lib.ffk_event_record(e1, stream)
+        assert lib.ffk_event_elapsed_ms(e0, e1, C.byref(ms)) == 0, fa.last_error()
+    finally:
+        lib.ffk_stream_sync(stream)
+        lib.ffk_event_destroy(e0)
+        lib.ffk_event_destroy(e1)
+        lib.ffk_stream_destroy(stream)
+        for p in held:
+            lib.ffk_free(p)
+    per = ms.value / iters
+    gbs = per_elem * n / (per * 1e-3) / 1e9
+    return {"op": op, "channels": channels, "pixels": batch * hin * hin, "bytes": per_elem * n,
+            "ms_per_launch": round(per, 5), "hbm_gbs": round(gbs, 1), "frac_of_hbm": round(gbs / 8000.0, 4)}
+
+
 def time_fc(lib, batch=1, iters=50, path=0):
     """Mean launch time of the FC head 25088 -> 512 at `batch` faces (the
     path and split-K workspace ffk_fc chooses, or with path 1 / 2 the matvec
@@ -354,6 +409,9 @@ def main():
                     help="instead: the stride-2 conv (--cin/--cout/--hin, k3 s2) and its 1x1 shortcut "
                          "over this many compact input channels, as one launch")
     ap.add_argument("--unfused", action="store_true", help="with --pair-cx: as two launches")
+    ap.add_argument("--eltwise", choices=["map", "add"],
+                    help="instead: a stand-alone BN / PReLU (map) or Add over --batch x --hin x --hin "
+                         "pixels of --cout channels")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="instead: device-to-device copies of this many MiB (the calibration "
                          "workload for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -371,6 +429,9 @@ def main():
         return
     if a.fc:
         print(json.dumps(time_fc(lib, a.batch, a.iters, a.fc_path)), flush=True)
+        return
+    if a.eltwise:
+        print(json.dumps(time_eltwise(lib, a.eltwise, a.cout, a.hin, a.batch, a.iters)), flush=True)
         return
     if a.pair_cx:
         print(json.dumps(time_pair(lib, a.cin, a.cout, a.hin, a.pair_cx, a.batch, a.iters,

@@ -235,8 +235,28 @@ def _fill_scales(ops, opsc2):
     return out
 
 
+def hostile_channels(ops):
+    """Parameter values that no shorter epilogue form survives, for
+    `write_synthetic_ffw4(hostile=True)`: {op index: (field, channel, value)}.
+    The input layer's channel 0 gets a NaN weight scale, the first 256-channel
+    conv with a PReLU a bias of 3e38 on channel 1 (its requant value
+    overflows: the x86 out-of-range case), the first 512-channel conv that
+    adds a residual a bias of -3e38 on channel 3, and the first 128-channel
+    conv's PReLU a slope of 1.5 on channel 2 (PReLU is then no max)."""
+    out = {0: ("scales", 0, np.float32(np.nan))}
+    conv = lambda i, c, nxt: (ops[i]["type"] == OP_CONV and ops[i]["Cout"] == c and
+                              ops[i + 1]["type"] == nxt)
+    i256 = next(i for i in range(len(ops) - 1) if conv(i, 256, OP_PRELU))
+    i512 = next(i for i in range(len(ops) - 1) if conv(i, 512, OP_ADD))
+    i128 = next(i for i in range(len(ops) - 1) if conv(i, 128, OP_PRELU))
+    out[i256] = ("bias", 1, np.float32(3e38))
+    out[i512] = ("bias", 3, np.float32(-3e38))
+    out[i128 + 1] = ("slope", 2, np.float32(1.5))
+    return out
+
+
 def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPSC2_PATH, version=4,
-                         ops=None, opsc2=None):
+                         ops=None, opsc2=None, hostile=False):
     """Write a synthetic FFW4 file (about 43.7 MB) and return its path.
 
     version 3 or 2 writes the same network as an FFW3 / FFW2 file
@@ -247,12 +267,14 @@ def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPS
     scales are sized from the OPSC per-tensor scales instead of the OPSC2
     per-channel ones.  The random draws are the same for every version: the
     int8 weights, biases and slopes are identical.  `ops` / `opsc2`: another
-    schedule and its OPSC2 contents (FFW4 only)."""
+    schedule and its OPSC2 contents (FFW4 only).  hostile: the values of
+    `hostile_channels` written into a few convs and one PReLU."""
     assert version in (2, 3, 4)
     assert ops is None or version == 4
     rng = np.random.default_rng(seed)
     ops = ops if ops is not None else iresnet_schedule()
     opsc2 = opsc2 if opsc2 is not None else read_opsc2(opsc2_path)
+    special = hostile_channels(ops) if hostile else {}
     _, per_op = opsc2
     track = _fill_scales(ops, opsc2)
     pt_in, pt_out = _per_tensor_scales(ops, read_opsc()) if version < 4 else (None, None)
@@ -278,6 +300,9 @@ def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPS
                 jitter = rng.uniform(0.5, 1.5, size=cout)
                 scales = (base * jitter).astype(np.float32)
                 bias = rng.normal(0.0, 0.05, size=cout).astype(np.float32)
+                if i in special:
+                    field, ch, v = special[i]
+                    (scales if field == "scales" else bias)[ch] = v
                 f.write(struct.pack("<6H", cin, cout, k, k, op["s"], op["p"]))
                 f.write(w.tobytes())
                 f.write(scales.tobytes())
@@ -298,6 +323,8 @@ def write_synthetic_ffw4(path, seed=3, act_sigma=40.0, gain=0.35, opsc2_path=OPS
             elif t == OP_PRELU:
                 c = op["C"]
                 slope = rng.uniform(0.0, 0.3, size=c).astype(np.float32)
+                if i in special:
+                    slope[special[i][1]] = special[i][2]
                 f.write(struct.pack("<H", c))
                 f.write(slope.tobytes())
             elif t == OP_GEMM:
@@ -326,6 +353,17 @@ def synthetic_ffw4_path(seed=3, cache_dir=None, version=4):
     path = os.path.join(cache_dir, name)
     if not os.path.exists(path):
         write_synthetic_ffw4(path, seed=seed, version=version)
+    return path
+
+
+def synthetic_hostile_path(seed=7, cache_dir=None):
+    """Path of a synthetic FFW4 with `hostile_channels` (the committed scale
+    files apply to it), generated on first use."""
+    cache_dir = cache_dir or os.environ.get("FASTFACE_CACHE", "/tmp/fastface_cache")
+    os.makedirs(cache_dir, exist_ok=True)
+    path = os.path.join(cache_dir, "synthetic_r50_hostile_seed%d.ffw4" % seed)
+    if not os.path.exists(path):
+        write_synthetic_ffw4(path, seed=seed, hostile=True)
     return path
 
 

@@ -245,6 +245,56 @@ def test_generic_geometries_end_to_end(gpu_lib, oracle):
         oracle.free_model(m)
 
 
+def test_hostile_parameters_end_to_end(gpu_lib, oracle):
+    """A model whose parameters defeat the shorter epilogue forms in a few
+    layers (synth `hostile_channels`: a NaN weight scale in the input layer,
+    +-3e38 biases whose requant values overflow, a PReLU slope of 1.5): the
+    plan gives exactly those launches the general forms (no FFK_EPI_IN_RANGE
+    where a value can leave the int32 range or is NaN, no FFK_EPI_PRELU_LE1
+    there or for the slope above 1) and every other launch its shorter
+    forms.  Embeddings
+    equal the oracle's (itself equal to the reference's fastface_embed on
+    this model) at b=1 and on faces of both halves of a split batch; every
+    intermediate int8 tensor equals the oracle's at 2 faces."""
+    ffw = synth.synthetic_hostile_path()
+    special = synth.hostile_channels(synth.iresnet_schedule())
+    m = oracle.load_model(ffw, synth.OPSC_PATH, synth.OPSC2_PATH)
+    f = fa.FastFace(ffw, cwd=synth.REPO_ROOT)
+    try:
+        info = fa.fastface_step_info()
+        no_range, no_le1 = [], []
+        for s in range(gpu_lib.fastface_num_steps(f.ff)):
+            assert gpu_lib.fastface_get_step(f.ff, s, C.byref(info)) == 0
+            if info.kind != 1:
+                continue
+            if not info.flags & fa.FFK_EPI_IN_RANGE:
+                no_range.append(info.op_first)
+            if info.flags & fa.FFK_EPI_PRELU and not info.flags & fa.FFK_EPI_PRELU_LE1:
+                no_le1.append(info.op_first)
+        ops = synth.iresnet_schedule()
+        convs = sorted(i for i, v in special.items() if v[0] != "slope")
+        assert sorted(no_range) == convs                  # the NaN scale and the +-3e38 biases
+        # PReLU as a max needs finite, bounded parameters and slopes <= 1
+        assert sorted(no_le1) == sorted([i for i in convs if ops[i + 1]["type"] == synth.OP_PRELU] +
+                                        [i - 1 for i, v in special.items() if v[0] == "slope"])
+        x = synth.faces_uniform(50, 90)
+        batch = f.embed_batch(x)                        # two halves of 25 faces
+        idx = [0, 24, 25, 49]
+        exp, _ = oracle.forward(m, x[idx])
+        assert np.array_equal(batch[idx], exp)
+        assert np.array_equal(f.embed(x[0]), exp[0])
+        assert gpu_lib.fastface_debug_keep_tensors(f.ff, 1) == 0
+        exp2, dumps = oracle.forward(m, x[:2], dump_ops=set(range(177)))
+        assert np.array_equal(f.embed_batch(x[:2]), exp2)
+        for op, t in sorted(dumps.items()):
+            buf = np.empty(t.size, np.int8)
+            assert gpu_lib.fastface_debug_read(f.ff, op, 2, buf.ctypes.data, buf.nbytes) == t.size, op
+            assert np.array_equal(buf.reshape(t.shape), t), "op %d differs" % op
+    finally:
+        f.close()
+        oracle.free_model(m)
+
+
 def test_stage_outputs_stored_at_even_pixels(ff, gpu_lib):
     """The stem's output X and each stage's last X are read only by the next
     stage's 1x1 stride-2 shortcut: the plan stores them at their even pixels

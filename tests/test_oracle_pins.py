@@ -387,6 +387,24 @@ def test_forward_vs_reference_embed_standalone_ops(oracle, ref, with_opsc2):
             assert a.std() > 5 and (a == 0).mean() < 0.2 and (np.abs(a) >= 127).mean() < 0.2, op
 
 
+def test_forward_vs_reference_embed_hostile_parameters(oracle, ref):
+    """Whole network with parameter values no shorter epilogue form survives
+    (synth `hostile_channels`: a NaN weight scale in the input layer, +-3e38
+    biases whose requant values overflow, a PReLU slope of 1.5): oracle
+    interpreter == reference fastface_embed, bit for bit, and the
+    overflowing channel is the x86 out-of-range -128 everywhere."""
+    from fastface_amd import synth
+    ffw = synth.synthetic_hostile_path()
+    faces = np.concatenate([synth.faces_uniform(1, 0), synth.faces_normal_clipped(1, 2)])
+    m = oracle.load_model(ffw, synth.OPSC_PATH, synth.OPSC2_PATH)
+    try:
+        emb, acts = oracle.forward(m, faces, dump_ops=[1])
+    finally:
+        oracle.free_model(m)
+    assert np.array_equal(emb, ref.embed(ffw, faces, cwd=synth.REPO_ROOT))
+    assert (acts[1][..., 0] == -128).all()
+
+
 def test_synthetic_formats_share_their_weights():
     """FFW3 / FFW2 variants hold the FFW4 model's int8 weights (the same
     draws); FFW2 lacks exactly the 53 conv biases."""

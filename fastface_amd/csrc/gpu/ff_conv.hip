@@ -504,7 +504,7 @@ size_t ffk_conv_workspace_bytes(const ffk_conv_desc* d) {
     if (!d || d->batch <= 0) return 0;
     const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);
     if (!e) return 0;
-    if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_ws_bytes(d);
+    if (d->flags & FFK_ALGO_WINOGRAD) return 0;       // (its transformed input stays on chip)
     const long long M = conv_pixels(d);
     if (M > 0x7fffffffLL) return 0;
     return choose_launch(e, M, (size_t)-1, (d->flags & FFK_SHARED_GPU) != 0).ws_bytes;

@@ -25,12 +25,10 @@ static inline int ffk_check_launch(const char* what) {
 static constexpr int FF_KSTEP = 64;
 
 // A conv workspace starts with the split-K arrival counters, which every
-// split launch leaves at zero for the next one; other users of a workspace
-// (the Winograd path) keep out of these first bytes.
+// split launch leaves at zero for the next one.
 static constexpr size_t FF_WS_COUNTER_AREA = 2048;
 
 // Integer Winograd F(2,3) path of the 64-channel 3x3 stride-1 layers
 // (ff_winograd.hip), taken by ffk_conv for FFK_ALGO_WINOGRAD.
 int ffk_winograd_eligible(const ffk_conv_desc* d);
-size_t ffk_winograd_ws_bytes(const ffk_conv_desc* d);
 int ffk_winograd_conv(const ffk_conv_desc* d, hipStream_t s);

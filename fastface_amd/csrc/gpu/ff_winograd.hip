@@ -21,12 +21,12 @@
 // than the transform saves, so this path is an exact alternative (BASELINE
 // config 5 runs the stage-1 layers both ways), not the default.
 //
-// Two kernels per layer:
-//   wino_in_kernel   input transform: int8 NHWC -> V limbs [cell][tile][K'],
-//                    K' = [v1 of 64 channels | v0 of 64 channels]
-//   wino_gemm_kernel per 64-tile x 64-channel block: the 16 cell GEMMs on
-//                    MFMA, the output transform in registers, the fused
-//                    requant epilogue (PReLU / residual / BN second output)
+// One kernel per layer (wino_conv_kernel), per 64-block x 64-channel tile:
+// the input transform of the tile's 4x4 windows into LDS, one row of four
+// cells at a time (V limbs [cell][block][K'], K' = [v1 of 64 channels | v0
+// of 64 channels]), the cell GEMMs on MFMA, the output transform in
+// registers, and the fused requant epilogue (PReLU / residual / BN second
+// output).  The transformed input, 8x the int8 input, never leaves the CU.
 #include <algorithm>
 
 #include "ff_internal.h"
@@ -45,8 +45,7 @@ typedef short s16x16 __attribute__((ext_vector_type(16)));
 typedef signed char c16 __attribute__((ext_vector_type(16)));
 
 struct WinoArgs {
-    const int8_t* x;          // int8 NHWC input of the slice
-    int8_t* V;                // transformed input limbs (workspace)
+    const int8_t* x;          // int8 NHWC input
     const int8_t* U;          // packed weight limbs (ffk_pack_winograd_weights)
     const float* params;      // [FFK_NPARAM][64]
     const int8_t* add_src;
@@ -54,73 +53,26 @@ struct WinoArgs {
     int8_t* out;
     int8_t* out_bn;
     int32_t* out_i32;
-    int n_tiles;              // 2x2 output blocks in the slice
+    int n_tiles;              // 2x2 output blocks of the launch
     int flags;
     float in_scale;
 };
 
 // ---------------------------------------------------------------------------
-// Input transform.  One thread = one 2x2 output block and 16 channels: the
-// 4x4 window at (2ty-1, 2tx-1) (zero outside the image), V = B^T d B in int16,
-// then the two limbs of each of the 16 cells go to their cell planes.
+// Input transform + cell GEMMs + output transform + epilogue.  Workgroup = 8
+// waves: wave (wm, wn) takes output blocks t0 + wm*32 .. +31 (MFMA rows) and
+// channels wn*32 .. +31 (MFMA columns).  Per row of four cells every thread
+// transforms one block's 4x4 window for 16 channels (two of its input rows,
+// 16-byte loads that the neighbouring blocks' windows share in L2) into the
+// LDS A stage, and the cell row's U limbs (32 KB, contiguous in the packed
+// weights) are copied into the LDS B stage; both operands are read from
+// there in fragment order: lane (row/column lane%32, K half lane/32) holds
+// 16 bytes of each 32-byte K step.  (Reading U straight from global memory
+// in every wave cost a quarter of the layer's time: each 32x32 block
+// re-read it from L2.)
 // ---------------------------------------------------------------------------
-template <int H, int W>
-__global__ __launch_bounds__(256) void wino_in_kernel(const int8_t* __restrict__ x, int8_t* __restrict__ V,
-                                                      int n_tiles) {
-    constexpr int TH = H / 2, TW = W / 2, G = WC / 16;
-    const int idx = blockIdx.x * 256 + threadIdx.x;
-    if (idx >= n_tiles * G) return;
-    const int t = idx / G, g = idx - t * G;
-    const int b = t / (TH * TW);
-    const int rr = t - b * (TH * TW);
-    const int ty = rr / TW, tx = rr - ty * TW;
-    s16x16 d[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int ih = 2 * ty - 1 + i, iw = 2 * tx - 1 + j;
-            const bool in = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
-            const int8_t* src = in ? x + ((size_t)(b * H + ih) * W + iw) * WC + g * 16 : wg_zero;
-            d[i][j] = __builtin_convertvector(*reinterpret_cast<const c16*>(src), s16x16);
-        }
-    s16x16 e[4][4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {           // rows: B^T d
-        e[0][j] = d[0][j] - d[2][j];
-        e[1][j] = d[1][j] + d[2][j];
-        e[2][j] = d[2][j] - d[1][j];
-        e[3][j] = d[1][j] - d[3][j];
-    }
-    const size_t plane = (size_t)n_tiles * KP;
-    int8_t* dst = V + (size_t)t * KP + g * 16;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {           // columns: (B^T d) B
-        s16x16 v[4];
-        v[0] = e[i][0] - e[i][2];
-        v[1] = e[i][1] + e[i][2];
-        v[2] = e[i][2] - e[i][1];
-        v[3] = e[i][1] - e[i][3];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const s16x16 v1 = v[j] >> (short)6;               // floor(v / 64)
-            const s16x16 v0 = v[j] & (short)63;               // v - 64*v1
-            int8_t* p = dst + (size_t)(i * 4 + j) * plane;
-            *reinterpret_cast<c16*>(p) = __builtin_convertvector(v1, c16);
-            *reinterpret_cast<c16*>(p + WC) = __builtin_convertvector(v0, c16);
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Cell GEMMs + output transform + epilogue.  Workgroup = 4 waves: wave
-// (wm, wn) takes output blocks t0 + wm*32 .. +31 (MFMA rows) and channels
-// wn*32 .. +31 (MFMA columns).  Per cell the A operand (V limbs of 32 blocks)
-// and the B operand (U limbs of 32 channels) come straight from global
-// memory in fragment order: lane (row/column lane%32, K half lane/32) holds
-// 16 bytes of each 32-byte K step.
-// ---------------------------------------------------------------------------
-constexpr int GW_TILES = 64;
+constexpr int GW_TILES = 128;     // 2x2 output blocks per workgroup
+constexpr int GW_NT = 512;        // threads per workgroup: 8 waves
 constexpr int AT[2][4] = {{1, 1, 1, 0}, {0, 1, -1, -1}};
 
 __device__ __forceinline__ v16i mfma(const v4i& a, const v4i& b, const v16i& c) {
@@ -156,20 +108,45 @@ __device__ __forceinline__ void wino_requant(const v16i (&y)[4], const WinoArgs&
 }
 
 template <int H, int W>
-__global__ __launch_bounds__(256, 2) void wino_gemm_kernel(WinoArgs a) {
+__global__ __launch_bounds__(GW_NT, 1) void wino_conv_kernel(WinoArgs a) {
     constexpr int TH = H / 2, TW = W / 2;
-    __shared__ __align__(16) int8_t T8[GW_TILES * 4 * PX_PITCH];
+    // the A operand of one cell row (4 cells x 128 blocks x K' bytes, row
+    // pitch AP); the epilogue's byte tile reuses it after the last cell row
+    constexpr int AP = KP + 16;
+    static_assert(GW_TILES * 4 * PX_PITCH <= 4 * GW_TILES * AP, "the epilogue tile must fit the A stage");
+    static_assert(GW_NT == GW_TILES * (WC / 16), "one thread per block and 16 channels");
+    __shared__ __align__(16) int8_t As[4 * GW_TILES * AP];
+    __shared__ __align__(16) int8_t Bs[4 * WC * AP];     // the B operand of one cell row
     __shared__ __align__(16) int8_t Ls[WC * LUT_PITCH];
+    int8_t* T8 = As;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
     const int lc = lane & 31, kh = lane >> 5;
     const int blk0 = blockIdx.x * GW_TILES;
-    const int t = blk0 + wm * 32 + lc;                     // this lane's A row (output block)
     const int c = wn * 32 + lc;                            // this lane's B column (channel)
-    const size_t plane = (size_t)a.n_tiles * KP;
-    const int8_t* arow = t < a.n_tiles ? a.V + (size_t)t * KP + kh * 16 : nullptr;
-    const int8_t* brow = a.U + (size_t)c * KP + kh * 16;
+    const int8_t* brow = Bs + c * AP + kh * 16;            // ... in a cell of the B stage
+    const int8_t* arow = As + (wm * 32 + lc) * AP + kh * 16;   // this lane's A row (block) in a cell
+
+    // input transform: thread (tb, tg) = local block tb, channels 16*tg ..
+    const int tb = tid >> 2, tg = tid & 3;
+    const int gblk = blk0 + tb;
+    const bool tvalid = gblk < a.n_tiles;
+    int ib = 0, ty = 0, tx = 0;
+    if (tvalid) {
+        ib = gblk / (TH * TW);
+        const int rr = gblk - ib * (TH * TW);
+        ty = rr / TW;
+        tx = rr - ty * TW;
+    }
+    // row r of the 4x4 window (input row 2ty - 1 + r), column j, this thread's
+    // 16 channels as int16 (zero outside the image)
+    auto win = [&](int r, int j) -> s16x16 {
+        const int ih = 2 * ty - 1 + r, iw = 2 * tx - 1 + j;
+        const bool in = tvalid && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+        const int8_t* src = in ? a.x + ((size_t)(ib * H + ih) * W + iw) * WC + tg * 16 : wg_zero;
+        return __builtin_convertvector(*reinterpret_cast<const c16*>(src), s16x16);
+    };
 
     v16i y[4];
 #pragma unroll
@@ -177,69 +154,88 @@ __global__ __launch_bounds__(256, 2) void wino_gemm_kernel(WinoArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; r++) y[p][r] = 0;
 
-    // fragments of cell `cell` into buffer `buf` (cell c+1 loads while cell c
-    // computes)
-    v4i A1[2][2], A0[2][2], B1[2][2], B0[2][2];
-    auto load = [&](int cell, int buf) {
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            if (arow) {
-                A1[buf][s] = *reinterpret_cast<const v4i*>(arow + cell * plane + s * 32);
-                A0[buf][s] = *reinterpret_cast<const v4i*>(arow + cell * plane + WC + s * 32);
-            } else {
-                A1[buf][s] = v4i{0, 0, 0, 0};
-                A0[buf][s] = v4i{0, 0, 0, 0};
-            }
-            const int8_t* bc = brow + (size_t)cell * WC * KP;
-            B1[buf][s] = *reinterpret_cast<const v4i*>(bc + s * 32);
-            B0[buf][s] = *reinterpret_cast<const v4i*>(bc + WC + s * 32);
+    for (int ci = 0; ci < 4; ci++) {                       // cell row: cells 4ci .. 4ci+3
+        // row ci of B^T d: d0 - d2, d1 + d2, d2 - d1, d1 - d3
+        s16x16 e[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (ci == 0) e[j] = win(0, j) - win(2, j);
+            if (ci == 1) e[j] = win(1, j) + win(2, j);
+            if (ci == 2) e[j] = win(2, j) - win(1, j);
+            if (ci == 3) e[j] = win(1, j) - win(3, j);
         }
-    };
-    load(0, 0);
+        // columns: (B^T d) B, then the two limbs of each cell into the A stage
+        s16x16 v[4];
+        v[0] = e[0] - e[2];
+        v[1] = e[1] + e[2];
+        v[2] = e[2] - e[1];
+        v[3] = e[1] - e[3];
+        // the cell row's U limbs: 4 cells x 64 channels x K' bytes, contiguous
+        // in the packed weights, 64 bytes per thread
+        v4i u[4];
+        const int8_t* usrc = a.U + (size_t)ci * 4 * WC * KP + (size_t)tid * 64;
 #pragma unroll
-    for (int cell = 0; cell < 16; cell++) {
-        if (cell + 1 < 16) load(cell + 1, (cell + 1) & 1);
-        const v4i* a1 = A1[cell & 1];
-        const v4i* a0 = A0[cell & 1];
-        const v4i* b1 = B1[cell & 1];
-        const v4i* b0 = B0[cell & 1];
-        v16i m;
+        for (int q = 0; q < 4; q++) u[q] = *reinterpret_cast<const v4i*>(usrc + q * 16);
+        __syncthreads();                                   // the previous cell row's fragments are read
 #pragma unroll
-        for (int r = 0; r < 16; r++) m[r] = 0;
-        m = mfma(a1[0], b1[0], m);
-        m = mfma(a1[1], b1[1], m);
+        for (int q = 0; q < 4; q++) {
+            const int byte = tid * 64 + q * 16;            // (cell, channel) row byte / KP, offset % KP
+            *reinterpret_cast<v4i*>(Bs + (byte / KP) * AP + byte % KP) = u[q];
+        }
 #pragma unroll
-        for (int r = 0; r < 16; r++) m[r] <<= 6;
-        m = mfma(a1[0], b0[0], m);
-        m = mfma(a1[1], b0[1], m);
-        m = mfma(a0[0], b1[0], m);
-        m = mfma(a0[1], b1[1], m);
+        for (int j = 0; j < 4; j++) {
+            const s16x16 v1 = v[j] >> (short)6;            // floor(v / 64)
+            const s16x16 v0 = v[j] & (short)63;            // v - 64*v1
+            int8_t* dst = As + (j * GW_TILES + tb) * AP + tg * 16;
+            *reinterpret_cast<c16*>(dst) = __builtin_convertvector(v1, c16);
+            *reinterpret_cast<c16*>(dst + WC) = __builtin_convertvector(v0, c16);
+        }
+        __syncthreads();
 #pragma unroll
-        for (int r = 0; r < 16; r++) m[r] <<= 6;
-        m = mfma(a0[0], b0[0], m);
-        m = mfma(a0[1], b0[1], m);
-        // output transform: y(p, q) += A^T[p][i] A^T[q][j] M(i, j)
-        const int ci = cell >> 2, cj = cell & 3;
+        for (int cj = 0; cj < 4; cj++) {
+            const int8_t* ar = arow + cj * GW_TILES * AP;
+            const int8_t* bc = brow + cj * WC * AP;
+            v4i a1[2], a0[2], b1[2], b0[2];
 #pragma unroll
-        for (int p = 0; p < 2; p++)
-#pragma unroll
-            for (int q = 0; q < 2; q++) {
-                const int k = AT[p][ci] * AT[q][cj];
-                if (k == 1) {
-#pragma unroll
-                    for (int r = 0; r < 16; r++) y[p * 2 + q][r] += m[r];
-                } else if (k == -1) {
-#pragma unroll
-                    for (int r = 0; r < 16; r++) y[p * 2 + q][r] -= m[r];
-                }
+            for (int s = 0; s < 2; s++) {
+                a1[s] = *reinterpret_cast<const v4i*>(ar + s * 32);
+                a0[s] = *reinterpret_cast<const v4i*>(ar + WC + s * 32);
+                b1[s] = *reinterpret_cast<const v4i*>(bc + s * 32);
+                b0[s] = *reinterpret_cast<const v4i*>(bc + WC + s * 32);
             }
-        // keep the later cells' loads out of this one, and the output
-        // transform here: without these the compiler keeps every cell's M live
-        // to sum them at the end
-        asm volatile("" ::: "memory");
+            v16i m;
 #pragma unroll
-        for (int p = 0; p < 4; p++) asm volatile("" : "+v"(y[p]));
+            for (int r = 0; r < 16; r++) m[r] = 0;
+            m = mfma(a1[0], b1[0], m);
+            m = mfma(a1[1], b1[1], m);
+#pragma unroll
+            for (int r = 0; r < 16; r++) m[r] <<= 6;
+            m = mfma(a1[0], b0[0], m);
+            m = mfma(a1[1], b0[1], m);
+            m = mfma(a0[0], b1[0], m);
+            m = mfma(a0[1], b1[1], m);
+#pragma unroll
+            for (int r = 0; r < 16; r++) m[r] <<= 6;
+            m = mfma(a0[0], b0[0], m);
+            m = mfma(a0[1], b0[1], m);
+            // output transform: y(p, q) += A^T[p][ci] A^T[q][cj] M(ci, cj)
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const int k = AT[p][ci] * AT[q][cj];
+                    if (k == 1) {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) y[p * 2 + q][r] += m[r];
+                    } else if (k == -1) {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) y[p * 2 + q][r] -= m[r];
+                    }
+                }
+        }
     }
+    __syncthreads();                                       // the A stage becomes the epilogue tile
     // Y = 4 x the direct conv, exactly
 #pragma unroll
     for (int p = 0; p < 4; p++)
@@ -271,11 +267,11 @@ __global__ __launch_bounds__(256, 2) void wino_gemm_kernel(WinoArgs a) {
     const bool bn = (a.flags & FFK_EPI_BN) != 0;
     const bool x_even = (a.flags & FFK_OUT_X_EVEN) != 0;
     if (bn)
-        for (int i = tid; i < WC * 16; i += 256)
+        for (int i = tid; i < WC * 16; i += GW_NT)
             *reinterpret_cast<v4i*>(Ls + (i >> 4) * LUT_PITCH + (i & 15) * 16) =
                 *reinterpret_cast<const v4i*>(a.bn_lut + (size_t)i * 16);
     if (add)
-        for (int i = tid; i < GW_TILES * 2 * 8; i += 256) {
+        for (int i = tid; i < GW_TILES * 2 * 8; i += GW_NT) {
             const int row = i >> 4, pr = (i >> 3) & 1, k = i & 7;
             const int blk = blk0 + row;
             const int8_t* src = blk < a.n_tiles ? a.add_src + pix(blk, pr * 2) * WC + k * 16 : wg_zero;
@@ -293,7 +289,7 @@ __global__ __launch_bounds__(256, 2) void wino_gemm_kernel(WinoArgs a) {
         else wino_requant<H, W, 2, false>(y, a, T8, c, row0);
     }
     __syncthreads();
-    for (int i = tid; i < GW_TILES * 2 * 8; i += 256) {
+    for (int i = tid; i < GW_TILES * 2 * 8; i += GW_NT) {
         const int row = i >> 4, pr = (i >> 3) & 1, k = i & 7;
         const int blk = blk0 + row;
         if (blk >= a.n_tiles) continue;
@@ -324,17 +320,6 @@ __global__ __launch_bounds__(256, 2) void wino_gemm_kernel(WinoArgs a) {
     }
 }
 
-// images per launch pair: the transformed input of a slice (written by the
-// input transform, read right after by the cell GEMMs) is sized to stay in
-// the 256 MB memory-side cache instead of round-tripping through HBM
-#ifndef FF_WINO_SLICE_MB
-#define FF_WINO_SLICE_MB 192
-#endif
-template <int H, int W>
-constexpr int slice_images() {
-    return (int)(((long long)FF_WINO_SLICE_MB << 20) / ((long long)(H / 2) * (W / 2) * 16 * KP));
-}
-
 int eligible(const ffk_conv_desc* d) {
     return d && d->cin == WC && d->cout == WC && d->kh == 3 && d->kw == 3 && d->stride == 1 && d->pad == 1 &&
            d->hin == d->win && (d->hin == 56 || d->hin == 112);
@@ -342,48 +327,25 @@ int eligible(const ffk_conv_desc* d) {
 
 template <int H, int W>
 int launch(const ffk_conv_desc* d, hipStream_t s) {
-    constexpr int per_img = (H / 2) * (W / 2);
-    constexpr int SLICE = slice_images<H, W>();
-    for (int b0 = 0; b0 < d->batch; b0 += SLICE) {
-        const int nb = std::min(SLICE, d->batch - b0);
-        const size_t pix0 = (size_t)b0 * H * W;
-        WinoArgs a = {};
-        a.x = (const int8_t*)d->in + pix0 * WC;
-        a.V = (int8_t*)d->workspace + FF_WS_COUNTER_AREA;     // the split-K counters stay untouched
-        a.U = d->w;
-        a.params = d->params;
-        a.add_src = d->add_src ? d->add_src + pix0 * WC : nullptr;
-        a.bn_lut = d->bn_lut;
-        // FFK_OUT_X_EVEN: one pixel of four (the top left of each 2x2 block)
-        a.out = d->out ? d->out + ((d->flags & FFK_OUT_X_EVEN) ? pix0 / 4 : pix0) * WC : nullptr;
-        a.out_bn = d->out_bn ? d->out_bn + pix0 * WC : nullptr;
-        a.out_i32 = d->out_i32 ? d->out_i32 + pix0 * WC : nullptr;
-        a.n_tiles = nb * per_img;
-        a.flags = d->flags;
-        a.in_scale = d->in_scale;
-        const int n_thr = a.n_tiles * (WC / 16);
-        hipLaunchKernelGGL((wino_in_kernel<H, W>), dim3((n_thr + 255) / 256), dim3(256), 0, s, a.x, a.V,
-                           a.n_tiles);
-        int rc = ffk_check_launch("winograd input transform");
-        if (rc) return rc;
-        hipLaunchKernelGGL((wino_gemm_kernel<H, W>), dim3((a.n_tiles + GW_TILES - 1) / GW_TILES), dim3(256), 0,
-                           s, a);
-        rc = ffk_check_launch("winograd gemm");
-        if (rc) return rc;
-    }
-    return FFK_OK;
+    WinoArgs a = {};
+    a.x = (const int8_t*)d->in;
+    a.U = d->w;
+    a.params = d->params;
+    a.add_src = d->add_src;
+    a.bn_lut = d->bn_lut;
+    a.out = d->out;                 // FFK_OUT_X_EVEN: the top left pixel of each 2x2 block
+    a.out_bn = d->out_bn;
+    a.out_i32 = d->out_i32;
+    a.n_tiles = d->batch * (H / 2) * (W / 2);
+    a.flags = d->flags;
+    a.in_scale = d->in_scale;
+    hipLaunchKernelGGL((wino_conv_kernel<H, W>), dim3((a.n_tiles + GW_TILES - 1) / GW_TILES), dim3(GW_NT), 0, s, a);
+    return ffk_check_launch("winograd conv");
 }
 
 }  // namespace
 
 int ffk_winograd_eligible(const ffk_conv_desc* d) { return eligible(d); }
-
-size_t ffk_winograd_ws_bytes(const ffk_conv_desc* d) {
-    if (!eligible(d) || d->batch <= 0) return 0;
-    const long long per_img = (long long)(d->hin / 2) * (d->win / 2) * 16 * KP;
-    const int slice = d->hin == 56 ? slice_images<56, 56>() : slice_images<112, 112>();
-    return FF_WS_COUNTER_AREA + (size_t)per_img * (size_t)std::min(d->batch, slice);
-}
 
 int ffk_winograd_conv(const ffk_conv_desc* d, hipStream_t s) {
     if (!eligible(d)) {
@@ -395,10 +357,8 @@ int ffk_winograd_conv(const ffk_conv_desc* d, hipStream_t s) {
         ffk_set_error("conv: FFK_ALGO_WINOGRAD needs an int8 input tensor%s%s", nullptr, nullptr);
         return FFK_ERR_ARG;
     }
-    const size_t need = ffk_winograd_ws_bytes(d);
-    if (!d->workspace || d->workspace_bytes < need) {
-        ffk_set_error("conv: FFK_ALGO_WINOGRAD needs the workspace ffk_conv_workspace_bytes reports%s%s",
-                      nullptr, nullptr);
+    if ((long long)d->batch * (d->hin / 2) * (d->win / 2) > 0x7fffffffLL - GW_TILES) {
+        ffk_set_error("conv: batch too large for the Winograd path%s%s", nullptr, nullptr);
         return FFK_ERR_ARG;
     }
     return d->hin == 56 ? launch<56, 56>(d, s) : launch<112, 112>(d, s);

@@ -127,7 +127,6 @@ def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=Fa
     keep.append(dw)
     if winograd:
         flags |= fa.FFK_ALGO_WINOGRAD
-        split = True            # the transformed input lives in the workspace
     d.w = dw.ptr
     if in_inv is not None:
         di = Dev(lib, host=np.asarray(list(in_inv) + [0.0], np.float32)); keep.append(di)
@@ -166,7 +165,7 @@ def run_conv(lib, x, w_oihw, stride, pad, params=None, flags=0, add=None, raw=Fa
         keep.append(ws)
         d.workspace, d.workspace_bytes = ws.ptr, ws.nbytes
     if winograd:
-        assert ws is not None and lib.ffk_conv_variant(C.byref(d)) == b"winograd"
+        assert lib.ffk_conv_variant(C.byref(d)) == b"winograd"
     check(lib, lib.ffk_conv(C.byref(d), None))
     check(lib, lib.ffk_stream_sync(None))
     if ws is not None:

@@ -271,6 +271,35 @@ def test_split_workspace_only_for_small_batches():
     assert lib.ffk_conv_workspace_bytes(None) == 0
 
 
+def test_noalloc_scratch_covers_every_workspace():
+    """ffk_conv_noalloc's device array holds the workspace of every layer the
+    library runs, at any batch: the split-K grids are capped at the array's
+    size (small batches), larger batches and the Winograd and generic paths
+    need none; so the no-allocation entry point serves every layer."""
+    lib = fa.load()
+    d = fa.ffk_conv_desc()
+    layers, cur, blk = set(), (3, 112), (3, 112)        # (cin, cout, k, stride, input size)
+    ops = synth.iresnet_schedule()
+    for i, op in enumerate(ops):
+        if op["type"] == synth.OP_CONV:
+            src = blk if ops[i - 1]["type"] == synth.OP_SAVE_ID else cur
+            layers.add((op["Cin"], op["Cout"], op["k"], op["s"], src[1]))
+            cur = (op["Cout"], (src[1] + 2 * op["p"] - op["k"]) // op["s"] + 1)
+        elif op["type"] == synth.OP_BLOCK_START:
+            blk = cur
+    layers |= {(64, 64, 1, 1, 56), (64, 128, 1, 1, 28), (128, 256, 1, 1, 14), (256, 512, 1, 1, 7)}
+    sizes = set()
+    for cin, cout, k, s, hin in sorted(layers):
+        for B in list(range(1, 33)) + [64, 256, 1024]:
+            for wino in (0, fa.FFK_ALGO_WINOGRAD):
+                d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, k, k
+                d.stride, d.pad, d.hin, d.win, d.flags = s, k // 2, hin, hin, wino
+                n = lib.ffk_conv_workspace_bytes(C.byref(d))
+                sizes.add(n)
+                assert n <= fa.FFK_NOALLOC_SCRATCH_BYTES, (cin, cout, k, s, hin, B, wino, n)
+    assert max(sizes) > fa.FFK_NOALLOC_SCRATCH_BYTES // 2          # the array is not oversized
+
+
 def test_generic_geometries_are_runnable():
     """Geometries outside the tuned table run on the generic kernel (variant
     "generic", one workgroup per 64x64 output tile, no workspace); invalid

@@ -79,19 +79,41 @@ def test_conv_noalloc_equals_conv_with_workspace(gpu_lib, cin, cout, k, stride, 
             assert kind == b"splitk"
 
 
-def test_conv_noalloc_rejects_what_exceeds_the_scratch(gpu_lib):
-    """A Winograd launch needs its transformed input as workspace (far above
-    the device array): rejected with a clear error, nothing launched."""
+def test_conv_noalloc_winograd_and_generic(gpu_lib):
+    """Layers that need no workspace at all (the Winograd path, whose
+    transformed input stays on chip, and a geometry on the generic kernel)
+    run through the no-allocation entry point too, equal to ffk_conv, on two
+    calls in a row, the second with a smaller batch."""
     lib = gpu_lib
-    d = fa.ffk_conv_desc()
-    d.batch, d.cin, d.cout, d.kh, d.kw, d.stride, d.pad, d.hin, d.win = 64, 64, 64, 3, 3, 1, 1, 56, 56
-    d.flags = fa.FFK_ALGO_WINOGRAD | fa.FFK_EPI_BIAS
-    assert lib.ffk_conv_workspace_bytes(C.byref(d)) > fa.FFK_NOALLOC_SCRATCH_BYTES
-    # real buffers of the layer's sizes, so that nothing could fault even if
-    # the call went ahead
-    n = 64 * 56 * 56 * 64
-    bufs = [Dev(lib, nbytes=n), Dev(lib, nbytes=lib.ffk_winograd_packed_bytes(64, 64)),
-            Dev(lib, nbytes=fa.FFK_NPARAM * 64 * 4), Dev(lib, nbytes=n)]
-    d.in_, d.w, d.params, d.out = (b.ptr for b in bufs)
-    assert lib.ffk_conv_noalloc(C.byref(d), None) == -1          # FFK_ERR_ARG
-    assert b"device scratch" in lib.ffk_last_error()
+    r = np.random.default_rng(760)
+    P = params_block(64, ws=r.uniform(1e-3, 1e-2, 64), bias=r.normal(0, 0.1, 64), slope=0.25, adds=0.02,
+                     inv=1 / 40.0, bn_sin=0.02, bn_s=1.0, bn_o=0.01, bn_inv=50.0)
+    flags = fa.FFK_EPI_BIAS | fa.FFK_EPI_PRELU | fa.FFK_EPI_BN
+    for case, (cin, H, extra) in enumerate([(64, 56, fa.FFK_ALGO_WINOGRAD), (96, 20, 0)]):
+        for call, B in enumerate((3, 1)):
+            x = r.integers(-128, 128, size=(B, H, H, cin), dtype=np.int8)
+            w = r.integers(-128, 128, size=(64, cin, 3, 3), dtype=np.int8)
+            print("noalloc case %d batch %d call %d" % (case, B, call), flush=True)
+            keep = []
+            d1, o1, b1, shp = _desc(lib, keep, x, w, P, flags, None, 64, 3, 1)
+            d2, o2, b2, _ = _desc(lib, keep, x, w, P, flags, None, 64, 3, 1)
+            if extra:
+                wp = Dev(lib, host=_wino_pack(lib, w))
+                keep.append(wp)
+                d1.w = d2.w = wp.ptr
+                d1.flags = d2.flags = flags | extra
+            assert lib.ffk_conv_workspace_bytes(C.byref(d1)) == 0
+            kind = lib.ffk_conv_variant(C.byref(d1))
+            assert kind == (b"winograd" if extra else b"generic")
+            check(lib, lib.ffk_conv(C.byref(d1), None))
+            check(lib, lib.ffk_conv_noalloc(C.byref(d2), None))
+            check(lib, lib.ffk_stream_sync(None))
+            assert np.array_equal(o1.get(np.int8, shp), o2.get(np.int8, shp))
+            assert np.array_equal(b1.get(np.int8, shp), b2.get(np.int8, shp))
+
+
+def _wino_pack(lib, w):
+    cout, cin = w.shape[:2]
+    packed = np.empty(lib.ffk_winograd_packed_bytes(cin, cout), np.int8)
+    check(lib, lib.ffk_pack_winograd_weights(np.ascontiguousarray(w).ctypes.data, cout, cin, packed.ctypes.data))
+    return packed

@@ -161,9 +161,8 @@ typedef struct {
  * (kernels/winograd_int8_ref.c:36-179: G' = 2G, output = 4 x direct, here
  * divided back exactly) instead of the direct implicit GEMM.  Same int32
  * accumulators and outputs bit for bit; `w` must hold
- * ffk_pack_winograd_weights output, and the call needs the workspace
- * ffk_conv_workspace_bytes reports (the transformed input of up to 2 GiB of
- * images at a time).  ffk_conv_variant names it "winograd". */
+ * ffk_pack_winograd_weights output; the transformed input stays on chip, so
+ * the call needs no workspace.  ffk_conv_variant names it "winograd". */
 #define FFK_ALGO_WINOGRAD 0x80
 /* 1 if FFK_ALGO_WINOGRAD serves this layer geometry, else 0. */
 int    ffk_winograd_supported(int cin, int cout, int kh, int kw, int stride, int pad,
@@ -249,8 +248,9 @@ int    ffk_conv_s2_shortcut(const ffk_conv_desc* c, const ffk_conv_desc* s, void
  * forbid hipMalloc.  The small-batch split-K path takes its workspace from a
  * device array inside the library, FFK_NOALLOC_SCRATCH_BYTES per GPU, held
  * until the process ends (the descriptor's workspace fields are ignored).
- * Layers whose launch needs more (the FFK_ALGO_WINOGRAD path) are rejected
- * with FFK_ERR_ARG.  Every call on one GPU shares that GPU's array: calls that
+ * Every layer the library runs fits it (the split-K grids are capped at its
+ * size; larger batches, the Winograd and the generic paths need none); a
+ * launch that would need more is rejected with FFK_ERR_ARG.  Every call on one GPU shares that GPU's array: calls that
  * overlap in time on one GPU (other streams, other threads) race and must be
  * ordered by the caller; each launch leaves the array's counter area zero for
  * the next.  Results are bit-identical to ffk_conv's. */

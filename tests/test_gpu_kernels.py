@@ -725,8 +725,8 @@ def test_stem_epilogue_forms(gpu_lib, oracle, mode, form, x_even, B):
 
 @pytest.mark.parametrize("B", [2, 341])
 def test_x_even_winograd(gpu_lib, oracle, B):
-    """The Winograd path keeps pixel (0, 0) of each 2x2 output block; at 341
-    faces the 112x112 layer runs as two slices of transformed input."""
+    """The Winograd path keeps pixel (0, 0) of each 2x2 output block, also at
+    341 faces of 112x112 (a ragged last tile)."""
     r = rng(960 + B)
     H = 112 if B > 2 else 56
     x = r.integers(-128, 128, size=(B, H, H, 64), dtype=np.int8)

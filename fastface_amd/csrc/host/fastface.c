@@ -230,10 +230,10 @@ static int step_flags(const FastFace* ff, const FfStep* st)
 static void step_desc(FastFace* ff, int s, int batch, int fmt, int part, size_t off, int shared, ffk_conv_desc* d);
 
 /* Largest workspace any conv step asks for at 1..max_batch faces.  Only
- * small batches split K (the split grid is capped at a few thousand 64x64
- * tiles, i.e. below ~4096 faces for every IResNet layer); the Winograd
- * layers' transformed input grows with the batch up to a fixed slice, so
- * max_batch covers it. */
+ * small batches split K (the split grid is capped at FF_SPLIT_MAX_WG 64x64
+ * tiles, far below 4096 faces for every layer); the Winograd and generic
+ * paths need none.  max_batch itself is checked too (the FC head's split-K
+ * workspace grows with the batch up to its own cap). */
 static size_t workspace_bytes(FastFace* ff, int max_batch)
 {
     size_t best = 0;

@@ -240,10 +240,10 @@ static size_t workspace_bytes(FastFace* ff, int max_batch)
     const int top = max_batch < 4096 ? max_batch : 4096;
     for (int s = 0; s < ff->plan.n_steps; s++) {
         if (ff->plan.steps[s].kind == FF_STEP_FC) {          /* FC head: split-K of mid-size batches */
-            for (int b = 1; b <= top; b++) {
+            for (int b = 1; b <= top + 1; b++) {
                 ffk_fc_desc f;
                 memset(&f, 0, sizeof f);
-                f.batch = b; f.n = ff->plan.steps[s].fc_n; f.k = ff->plan.steps[s].fc_k;
+                f.batch = b <= top ? b : max_batch; f.n = ff->plan.steps[s].fc_n; f.k = ff->plan.steps[s].fc_k;
                 const size_t n = ffk_fc_workspace_bytes(&f);
                 if (n > best) best = n;
             }

@@ -362,3 +362,51 @@ def test_standalone_ops_plan_and_tables(checker, oracle, tmp_path):
         assert tables == [("map", 128, 784 * faces), ("map", 128, 784 * faces), ("add", 256, 196 * faces),
                           ("map", 256, 196 * faces), ("map", 512, 49 * faces), ("map", 512, 49 * faces)]
 
+
+
+def _tiny_model(tmp_path, name, ops):
+    """A small FFW4 of `ops` (synth op dicts) with OPSC / OPSC2 files whose
+    entries are flat 0.02 scales of each op's channel count."""
+    per_op, sc, c = [], [], 3
+    for op in ops:
+        if op["type"] == synth.OP_CONV:
+            c = op["Cout"]
+        n = op.get("C", c)
+        has = op["type"] in (synth.OP_CONV, synth.OP_BN, synth.OP_PRELU)
+        per_op.append(np.full(n, 0.02, np.float32) if has else None)
+        sc.append(0.02 if has else 0.0)
+    opsc2 = (np.full(3, 1 / 127, np.float32), per_op)
+    ffw = str(tmp_path / (name + ".ffw4"))
+    synth.write_synthetic_ffw4(ffw, seed=1, ops=ops, opsc2=opsc2)
+    opsc, opsc2p = str(tmp_path / (name + "_opsc.bin")), str(tmp_path / (name + "_opsc2.bin"))
+    synth.write_opsc(opsc, 1 / 127, sc)
+    synth.write_opsc2(opsc2p, *opsc2)
+    return ffw, opsc, opsc2p
+
+
+def test_standalone_op_rejections(checker, tmp_path):
+    """Op sequences the plan refuses even with stand-alone ops supported, each
+    a valid file: the plan fails with its message (under the sanitizers), and
+    create would return NULL."""
+    conv = lambda ci, co, s=1: dict(type=synth.OP_CONV, Cin=ci, Cout=co, k=3, s=s, p=1)
+    cases = {
+        "prelu_size": ([conv(3, 64), dict(type=synth.OP_PRELU, C=64), dict(type=synth.OP_BN, C=64),
+                        dict(type=synth.OP_PRELU, C=32)], "PReLU size != channels"),
+        "add_shapes": ([conv(3, 64), dict(type=synth.OP_PRELU, C=64), dict(type=synth.OP_SAVE_ID),
+                        dict(type=synth.OP_BN, C=64), conv(64, 64, 2), dict(type=synth.OP_PRELU, C=64),
+                        dict(type=synth.OP_BN, C=64), dict(type=synth.OP_ADD)],
+                       "Add operands differ in shape"),
+        "map_channels": ([conv(3, 96), dict(type=synth.OP_PRELU, C=96), dict(type=synth.OP_BN, C=96),
+                          dict(type=synth.OP_BN, C=96)], "multiple of 64 channels"),
+        "input_op": ([dict(type=synth.OP_BN, C=3), conv(3, 64), dict(type=synth.OP_PRELU, C=64)],
+                     "input faces"),
+        "add_no_slot": ([conv(3, 64), dict(type=synth.OP_PRELU, C=64), dict(type=synth.OP_BN, C=64),
+                         dict(type=synth.OP_ADD)], "Add before any SAVE_ID"),
+    }
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0")
+    for name, (ops, msg) in cases.items():
+        ffw, opsc, opsc2 = _tiny_model(tmp_path, name, ops)
+        r = subprocess.run([checker, ffw, opsc, opsc2], capture_output=True, text=True, env=env, timeout=120)
+        assert r.returncode == 0, r.stderr[-2000:]
+        assert "runtime error" not in r.stderr and "AddressSanitizer" not in r.stderr, r.stderr[-2000:]
+        assert "load 0 " in r.stdout and "plan -1 " in r.stdout and msg in r.stdout, (name, r.stdout)

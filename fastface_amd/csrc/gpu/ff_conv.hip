@@ -359,7 +359,7 @@ int ffk_conv(const ffk_conv_desc* d, void* stream) {
     if (M == 0) return FFK_OK;
     if (d->flags & FFK_ALGO_WINOGRAD) return ffk_winograd_conv(d, (hipStream_t)stream);
     const ConvArgs a = conv_args(d);
-    if (!e) {                              // no tuned kernel: the generic one (64-bit addressing)
+    if (!e) {                              // no tuned kernel: the generic one
         ConvArgs as = a;
         as.M = (int)M;
         return ff_conv_generic_launch(as, d, (hipStream_t)stream);
@@ -515,7 +515,7 @@ int ffk_conv_grid(const ffk_conv_desc* d) {
     const ConvEntry* e = find_conv(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win);
     if (!e) {
         if (!generic_geometry(d->cin, d->cout, d->kh, d->kw, d->stride, d->pad, d->hin, d->win)) return -1;
-        const long long g = ff_conv_generic_grid(conv_pixels(d), d->cout);
+        const long long g = ff_conv_generic_grid(conv_pixels(d), d->cin, d->cout);
         return g > 0x7fffffffLL ? -1 : (int)g;
     }
     if (e->cin == 3) return -1;                      // (the stem sizes its persistent grid itself)

@@ -3,9 +3,9 @@
 // kernels/conv2d_nhwc.c:150-220): an implicit GEMM with the geometry in
 // registers instead of template parameters.
 //
-// 64x64 output tiles, four waves of two 32x32x32 i8 MFMAs each per 64-byte
-// K step; the A operand is gathered from the NHWC input in 16- or 8-byte
-// channel runs where the channel count allows, byte by byte otherwise (any
+// 64- or 128-wide output tiles, four waves of 32x32x32 i8 MFMAs; the A
+// operand is gathered from the NHWC input in 16- or 8-byte channel runs
+// where the channel count allows, byte by byte otherwise (any
 // channel count, kernel size, stride and padding; the 3-channel input layer
 // quantizes fp32 faces or maps uint8 pixels on the fly), the B operand read
 // from the packed weights.  The epilogue is the general form of the tuned
@@ -16,174 +16,288 @@
 #include "ff_conv_table.h"
 #include "ff_numerics.h"
 
+#include <algorithm>
+
 namespace {
 
 struct GenGeom {
     int cin, cout, kh, kw, stride, pad, hin, win, hout, wout;
     int ktot;       // kh * kw * cin
     int kpad;       // ktot rounded up to whole 64-byte weight steps
+    unsigned in_bytes;   // the launch's int8 input tensor (below 2 GiB)
 };
 
-constexpr int GEN_PITCH = 80;    // LDS row pitch of the staged operands (one 64-byte K step + 16)
+// A thread's position k in the reduction order (kh*KW + kw)*Cin + ci: tap
+// row th, tap column tw, channel ci, and off = (th*Win + tw)*Cin + ci, the
+// input element's offset from the output pixel's tap (0, 0) element.
+struct KCursor {
+    int k, ci, th, tw, off;
+};
 
-// The 16 A-operand bytes k .. k+15 of output pixel (b, ih0, iw0) (input
-// pixel of tap (0, 0)), k in reduction order (kh*KW + kw)*Cin + ci.
+__device__ __forceinline__ KCursor kcursor_at(const GenGeom& g, int k) {
+    KCursor c;
+    const int tap = k / g.cin;
+    c.k = k;
+    c.ci = k - tap * g.cin;
+    c.th = tap / g.kw;
+    c.tw = tap - c.th * g.kw;
+    c.off = (c.th * g.win + c.tw) * g.cin + c.ci;
+    return c;
+}
+
+// Moves the cursor n elements on without a division: each channel wrap is
+// the next tap (the next pixel of the row: off runs on), each tap-column
+// wrap the next tap row (off skips Win - KW pixels).
+__device__ __forceinline__ void kcursor_step(KCursor& c, const GenGeom& g, int n) {
+    c.k += n;
+    c.ci += n;
+    c.off += n;
+    while (c.ci >= g.cin) {
+        c.ci -= g.cin;
+        if (++c.tw == g.kw) {
+            c.tw = 0;
+            c.th++;
+            c.off += (g.win - g.kw) * g.cin;
+        }
+    }
+}
+
+// The 16 A-operand bytes from cursor c on of the output pixel whose tap (0, 0)
+// is input pixel (ih0, iw0) at element offset base.
 // RUN 16: they are one tap's channel run (Cin % 16 == 0), one 16-byte load;
-// RUN 8: two taps' 8-byte runs (Cin % 8 == 0); RUN 0: byte by byte (any Cin,
-// and the 3-channel input layer, which quantizes fp32 faces or maps uint8
-// pixels).  Padding, rows past the batch and k past K give zeros.
+// RUN 8: two taps' 8-byte runs (Cin % 8 == 0); both through the int8 input's
+// buffer resource r_in, where padding, rows past the batch and k past K take
+// the out-of-range offset and read zeros.  RUN 0: byte by byte (any Cin, and
+// the 3-channel input layer, which quantizes fp32 faces or maps uint8
+// pixels), zeros there by branch.
 template <int RUN>
-__device__ __forceinline__ v4i gather_a(const ConvArgs& a, const GenGeom& g, const void* x, bool mrow, int b,
-                                        int ih0, int iw0, int k) {
-    v4i v = {0, 0, 0, 0};
-    if (!mrow) return v;
+__device__ __forceinline__ v4i gather_a(const ConvArgs& a, const GenGeom& g, __amdgpu_buffer_rsrc_t r_in,
+                                        const void* x, bool mrow, long long base, int ih0, int iw0, KCursor c) {
     if constexpr (RUN == 16 || RUN == 8) {
+        v4i v;
 #pragma unroll
         for (int h = 0; h < 16 / RUN; h++) {
-            const int kk = k + h * RUN;
-            if (kk >= g.ktot) continue;
-            const int tap = kk / g.cin, ci = kk - tap * g.cin;
-            const int th = tap / g.kw;
-            const int ih = ih0 + th, iw = iw0 + (tap - th * g.kw);
-            if (ih < 0 || ih >= g.hin || iw < 0 || iw >= g.win) continue;
-            const int8_t* src = (const int8_t*)x + (((size_t)b * g.hin + ih) * g.win + iw) * g.cin + ci;
+            if (h) kcursor_step(c, g, RUN);
+            const int ih = ih0 + c.th, iw = iw0 + c.tw;
+            const bool in = mrow && c.k < g.ktot && ih >= 0 && ih < g.hin && iw >= 0 && iw < g.win;
+            const unsigned off = in ? (unsigned)(base + c.off) : FF_OOB;
             if constexpr (RUN == 16) {
-                v = *reinterpret_cast<const v4i*>(src);
+                v = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r_in, off, 0, 0));
             } else {
-                const uint2 u = *reinterpret_cast<const uint2*>(src);
-                v[2 * h] = (int)u.x;
-                v[2 * h + 1] = (int)u.y;
+                const auto u = __builtin_amdgcn_raw_buffer_load_b64(r_in, off, 0, 0);
+                v[2 * h] = (int)u[0];
+                v[2 * h + 1] = (int)u[1];
             }
         }
+        return v;
     } else {
+        v4i v = {0, 0, 0, 0};
+        if (!mrow) return v;
         const bool stem = g.cin == 3;
         const bool rgb8 = stem && (a.flags & FFK_IN_RGB8);
-        int tap = k / g.cin, ci = k - tap * g.cin;
-        for (int e = 0; e < 16; e++, k++) {
+        // (global-space pointers: the input may come through the I/O
+        // descriptor, whose pointer the compiler cannot place)
+        typedef const __attribute__((address_space(1))) int8_t* gi8;
+        typedef const __attribute__((address_space(1))) uint8_t* gu8;
+        typedef const __attribute__((address_space(1))) float* gf32;
+        for (int e = 0; e < 16; e++) {
+            if (e) kcursor_step(c, g, 1);
             int q = 0;
-            if (k < g.ktot) {
-                const int th = tap / g.kw;
-                const int ih = ih0 + th, iw = iw0 + (tap - th * g.kw);
+            if (c.k < g.ktot) {
+                const int ih = ih0 + c.th, iw = iw0 + c.tw;
                 if (ih >= 0 && ih < g.hin && iw >= 0 && iw < g.win) {
-                    const size_t off = (((size_t)b * g.hin + ih) * g.win + iw) * g.cin + ci;
-                    if (!stem) q = ((const int8_t*)x)[off];
-                    else if (rgb8) q = a.in_lut[ci * 256 + ((const uint8_t*)x)[off]];
-                    else q = ff::quant_input(((const float*)x)[off], a.in_inv[ci]);
+                    const long long off = base + c.off;
+                    if (!stem) q = ((gi8)x)[off];
+                    else if (rgb8) q = a.in_lut[c.ci * 256 + ((gu8)x)[off]];
+                    else q = ff::quant_input(((gf32)x)[off], a.in_inv[c.ci]);
                 }
             }
             v[e >> 2] |= (int)((uint32_t)(uint8_t)q << (8 * (e & 3)));
-            if (++ci == g.cin) { ci = 0; tap++; }
         }
+        return v;
     }
-    return v;
 }
 
-// 64x64 output tiles of four waves (one 32x32 block each); per 64-byte K
-// step every thread stages 16 bytes of one A row (output pixel) and of one B
-// row (output channel) in LDS, then each wave runs two 32x32x32 MFMAs; the
-// next step's loads are in flight meanwhile.
-template <int RUN>
+// BM x BN output tiles (64 or 128 each) of four waves in a 2 x 2 grid, each
+// wave MI x NJ 32x32 blocks; per 64-byte K step every thread stages 16 bytes
+// of BM/64 A rows (output pixels) and of BN/64 B rows (output channels) in
+// LDS, then each wave runs 2 * MI * NJ 32x32x32 MFMAs; the next step's loads
+// are in flight meanwhile.  A 128-wide tile halves the gathers of the other
+// operand per MAC: every staged A row serves BN output channels, every B row
+// BM output pixels.
+template <int RUN, int BM, int BN>
 __global__ __launch_bounds__(256) void conv_generic_kernel(ConvArgs a, GenGeom g) {
-    __shared__ __align__(16) int8_t As[64 * GEN_PITCH];
-    __shared__ __align__(16) int8_t Bs[64 * GEN_PITCH];
+    constexpr int AR = BM / 64, BR = BN / 64;          // operand rows each thread stages
+    constexpr int MI = BM / 64, NJ = BN / 64;          // 32x32 blocks per wave (2 x 2 waves)
+    // one 64-byte K step per barrier pair (two or four steps' pieces staged
+    // at once, their loads in flight together, measured 7-48 % slower:
+    // fewer waves per SIMD, the gathers' VALU work back to back)
+    constexpr int PITCH = 80;                          // LDS row pitch of the staged operands
+    __shared__ __align__(16) int8_t As[BM * PITCH];
+    __shared__ __align__(16) int8_t Bs[BN * PITCH];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tiles_n = (g.cout + 63) / 64;
-    const long long m0 = (long long)(blockIdx.x / tiles_n) * 64;
-    const int n0 = (int)(blockIdx.x % tiles_n) * 64;
+    const int tiles_n = (g.cout + BN - 1) / BN;
+    // Workgroups go round-robin over the 8 XCDs: give each XCD a contiguous
+    // run of tiles (N fastest), so the tiles that gather the same pixels
+    // share one L2.
+    const unsigned nb = gridDim.x, bid = blockIdx.x;
+    const unsigned t = (nb & 7) == 0 ? (bid & 7) * (nb >> 3) + (bid >> 3) : bid;
+    const long long m0 = (long long)(t / tiles_n) * BM;
+    const int n0 = (int)(t % tiles_n) * BN;
     const int hw = g.hout * g.wout;
     const void* x = g.cin != 3 ? (const void*)a.in : a.in_f32 ? (const void*)a.in_f32 : (const void*)a.io->in;
 
     const int r = tid >> 2, kq = (tid & 3) * 16;
-    const long long m = m0 + r;
-    const bool mrow = m < a.M;
-    int b = 0, ih0 = 0, iw0 = 0;
-    if (mrow) {
-        b = (int)(m / hw);
-        const int rem = (int)(m - (long long)b * hw);
-        const int oh = rem / g.wout;
-        ih0 = oh * g.stride - g.pad;
-        iw0 = (rem - oh * g.wout) * g.stride - g.pad;
+    bool mrow[AR];
+    int ih0[AR], iw0[AR];
+    long long base[AR];          // element offset of the row's tap (0, 0) input pixel
+#pragma unroll
+    for (int i = 0; i < AR; i++) {
+        const long long m = m0 + r + 64 * i;
+        mrow[i] = m < a.M;
+        ih0[i] = 0; iw0[i] = 0; base[i] = 0;
+        if (mrow[i]) {
+            const int b = (int)(m / hw);
+            const int rem = (int)(m - (long long)b * hw);
+            const int oh = rem / g.wout;
+            ih0[i] = oh * g.stride - g.pad;
+            iw0[i] = (rem - oh * g.wout) * g.stride - g.pad;
+            base[i] = (((long long)b * g.hin + ih0[i]) * g.win + iw0[i]) * g.cin;
+        }
     }
-    const int ncol = n0 + r;
-    const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
-    auto load_b = [&](int k0) {
+    KCursor cur = kcursor_at(g, kq);
+    const __amdgpu_buffer_rsrc_t r_in = ff_rsrc(a.in, RUN ? g.in_bytes : 0u);
+    const int wr = (wave >> 1) * (BM / 2), wc = (wave & 1) * (BN / 2);
+    auto load_b = [&](int k0, int i) {
+        const int ncol = n0 + r + 64 * i;
         v4i v = {0, 0, 0, 0};
         if (ncol < g.cout) v = *reinterpret_cast<const v4i*>(a.w + ((size_t)(k0 >> 6) * g.cout + ncol) * 64 + kq);
         return v;
     };
 
-    v16i acc;
+    v16i acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < 16; i++) acc[i] = 0;
-    v4i ra = gather_a<RUN>(a, g, x, mrow, b, ih0, iw0, kq);
-    v4i rb = load_b(0);
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+    v4i ra[AR], rb[BR];
+#pragma unroll
+    for (int i = 0; i < AR; i++) ra[i] = gather_a<RUN>(a, g, r_in, x, mrow[i], base[i], ih0[i], iw0[i], cur);
+#pragma unroll
+    for (int i = 0; i < BR; i++) rb[i] = load_b(0, i);
     for (int k0 = 0; k0 < g.kpad; k0 += 64) {
         __syncthreads();                                  // the previous step's fragments are read
-        *reinterpret_cast<v4i*>(As + r * GEN_PITCH + kq) = ra;
-        *reinterpret_cast<v4i*>(Bs + r * GEN_PITCH + kq) = rb;
+#pragma unroll
+        for (int i = 0; i < AR; i++) *reinterpret_cast<v4i*>(As + (r + 64 * i) * PITCH + kq) = ra[i];
+#pragma unroll
+        for (int i = 0; i < BR; i++) *reinterpret_cast<v4i*>(Bs + (r + 64 * i) * PITCH + kq) = rb[i];
         __syncthreads();
         if (k0 + 64 < g.kpad) {
-            ra = gather_a<RUN>(a, g, x, mrow, b, ih0, iw0, k0 + 64 + kq);
-            rb = load_b(k0 + 64);
+            kcursor_step(cur, g, 64);
+#pragma unroll
+            for (int i = 0; i < AR; i++) ra[i] = gather_a<RUN>(a, g, r_in, x, mrow[i], base[i], ih0[i], iw0[i], cur);
+#pragma unroll
+            for (int i = 0; i < BR; i++) rb[i] = load_b(k0 + 64, i);
         }
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const v4i A = *reinterpret_cast<const v4i*>(As + (wr + (lane & 31)) * GEN_PITCH + h * 32 + (lane >> 5) * 16);
-            const v4i B = *reinterpret_cast<const v4i*>(Bs + (wc + (lane & 31)) * GEN_PITCH + h * 32 + (lane >> 5) * 16);
-            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, acc, 0, 0, 0);
+            v4i A[MI], B[NJ];
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+                A[i] = *reinterpret_cast<const v4i*>(As + (wr + i * 32 + (lane & 31)) * PITCH + h * 32 + (lane >> 5) * 16);
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                B[j] = *reinterpret_cast<const v4i*>(Bs + (wc + j * 32 + (lane & 31)) * PITCH + h * 32 + (lane >> 5) * 16);
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], B[j], acc[i][j], 0, 0, 0);
         }
     }
 
-    // epilogue: lane owns column wc + lane%32 and 16 rows of the wave's block
-    const int n = n0 + wc + (lane & 31);
-    if (n >= g.cout) return;
+    // epilogue: lane owns column wc + 32j + lane%32 and 16 rows of each of
+    // the wave's blocks
     const int C = g.cout;
     const float* P = a.params;
     const bool raw = a.out_i32 != nullptr;
-    float ws = 0.0f, bias = 0.0f, inv = 0.0f, slope = 0.0f, adds = 0.0f;
-    if (!raw) {
-        ws = P[FFK_P_WS * C + n];
-        bias = P[FFK_P_BIAS * C + n];
-        inv = P[FFK_P_INV * C + n];
-        slope = P[FFK_P_SLOPE * C + n];
-        adds = P[FFK_P_ADDSCALE * C + n];
-    }
     const bool x_even = (a.flags & FFK_OUT_X_EVEN) != 0;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const long long mm = m0 + wr + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-        if (mm >= a.M) continue;
-        const size_t o = (size_t)mm * C + n;
-        if (raw) {
-            a.out_i32[o] = acc[i];
-            continue;
+    for (int j = 0; j < NJ; j++) {
+        const int n = n0 + wc + j * 32 + (lane & 31);
+        if (n >= C) continue;
+        float ws = 0.0f, bias = 0.0f, inv = 0.0f, slope = 0.0f, adds = 0.0f;
+        if (!raw) {
+            ws = P[FFK_P_WS * C + n];
+            bias = P[FFK_P_BIAS * C + n];
+            inv = P[FFK_P_INV * C + n];
+            slope = P[FFK_P_SLOPE * C + n];
+            adds = P[FFK_P_ADDSCALE * C + n];
         }
-        float f = (float)acc[i];
-        if (a.flags & FFK_EPI_INSCALE) f = f * a.in_scale;
-        f = f * ws;
-        f = f + bias;
-        if (a.flags & FFK_EPI_ADD) f = ff::add_residual(f, (int32_t)a.add_src[o], adds);
-        if (a.flags & FFK_EPI_PRELU) f = ff::prelu(f, slope);
-        const int q = ff::requant_haz(f * inv);
-        if (a.out) {
-            if (!x_even) {
-                a.out[o] = (int8_t)q;
-            } else {
-                const int bb = (int)(mm / hw);
-                const int rem = (int)(mm - (long long)bb * hw);
-                const int oh = rem / g.wout, ow = rem - oh * g.wout;
-                if (!((oh | ow) & 1))
-                    a.out[(((size_t)bb * (g.hout / 2) + (oh >> 1)) * (g.wout / 2) + (ow >> 1)) * C + n] = (int8_t)q;
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const long long mm = m0 + wr + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+                if (mm >= a.M) continue;
+                const size_t o = (size_t)mm * C + n;
+                if (raw) {
+                    a.out_i32[o] = acc[i][j][e];
+                    continue;
+                }
+                float f = (float)acc[i][j][e];
+                if (a.flags & FFK_EPI_INSCALE) f = f * a.in_scale;
+                f = f * ws;
+                f = f + bias;
+                if (a.flags & FFK_EPI_ADD) f = ff::add_residual(f, (int32_t)a.add_src[o], adds);
+                if (a.flags & FFK_EPI_PRELU) f = ff::prelu(f, slope);
+                const int q = ff::requant_haz(f * inv);
+                if (a.out) {
+                    if (!x_even) {
+                        a.out[o] = (int8_t)q;
+                    } else {
+                        const int bb = (int)(mm / hw);
+                        const int rem = (int)(mm - (long long)bb * hw);
+                        const int oh = rem / g.wout, ow = rem - oh * g.wout;
+                        if (!((oh | ow) & 1))
+                            a.out[(((size_t)bb * (g.hout / 2) + (oh >> 1)) * (g.wout / 2) + (ow >> 1)) * C + n] = (int8_t)q;
+                    }
+                }
+                if (a.flags & FFK_EPI_BN) a.out_bn[o] = a.bn_lut[n * 256 + q + 128];
             }
-        }
-        if (a.flags & FFK_EPI_BN) a.out_bn[o] = a.bn_lut[n * 256 + q + 128];
     }
+}
+
+// Tile shape of a launch: 128-wide in N above 64 output channels, 128-high
+// in M where that still gives the 256 CUs a workgroup each, except for the
+// 3-channel input layer, whose byte gather runs faster on 64-row tiles.
+struct GenTile { int bm, bn; };
+
+GenTile gen_tile(long long M, int cin, int cout) {
+    GenTile t;
+    t.bn = cout > 64 ? 128 : 64;
+    const long long tiles_n = (cout + t.bn - 1) / t.bn;
+    t.bm = cin != 3 && ((M + 127) / 128) * tiles_n >= 256 ? 128 : 64;
+    return t;
+}
+
+template <int RUN>
+void launch_run(GenTile t, dim3 gd, hipStream_t s, const ConvArgs& a, const GenGeom& g) {
+    const dim3 bd(256);
+    if (t.bm == 128 && t.bn == 128) hipLaunchKernelGGL((conv_generic_kernel<RUN, 128, 128>), gd, bd, 0, s, a, g);
+    else if (t.bm == 128) hipLaunchKernelGGL((conv_generic_kernel<RUN, 128, 64>), gd, bd, 0, s, a, g);
+    else if (t.bn == 128) hipLaunchKernelGGL((conv_generic_kernel<RUN, 64, 128>), gd, bd, 0, s, a, g);
+    else hipLaunchKernelGGL((conv_generic_kernel<RUN, 64, 64>), gd, bd, 0, s, a, g);
 }
 
 }  // namespace
 
-// Workgroups of the generic kernel for M output pixels (one per 64x64 tile).
-long long ff_conv_generic_grid(long long M, int cout) { return ((M + 63) / 64) * ((cout + 63) / 64); }
+// Workgroups of the generic kernel for M output pixels (one per tile).
+long long ff_conv_generic_grid(long long M, int cin, int cout) {
+    const GenTile t = gen_tile(M, cin, cout);
+    return ((M + t.bm - 1) / t.bm) * ((cout + t.bn - 1) / t.bn);
+}
 
 int ff_conv_generic_launch(const ConvArgs& a, const ffk_conv_desc* d, hipStream_t s) {
     GenGeom g;
@@ -193,18 +307,46 @@ int ff_conv_generic_launch(const ConvArgs& a, const ffk_conv_desc* d, hipStream_
     g.wout = (d->win + 2 * d->pad - d->kw) / d->stride + 1;
     g.ktot = d->kh * d->kw * d->cin;
     g.kpad = (g.ktot + FF_KSTEP - 1) / FF_KSTEP * FF_KSTEP;
-    const long long grid = ff_conv_generic_grid(a.M, d->cout);
-    if (grid > 0x7fffffffLL) {
-        ffk_set_error("conv: batch too large for the generic kernel%s%s", nullptr, nullptr);
-        return FFK_ERR_ARG;
-    }
-    const dim3 gd((unsigned)grid), bd(256);
     // channel runs are read as 8- / 16-byte vectors: they need the run's
     // alignment in memory (a tensor base that is not 16-byte aligned takes
     // the byte gather)
-    if (d->cin == 3 || d->cin % 8 || ((uintptr_t)d->in & 15))
-        hipLaunchKernelGGL(conv_generic_kernel<0>, gd, bd, 0, s, a, g);
-    else if (d->cin % 16) hipLaunchKernelGGL(conv_generic_kernel<8>, gd, bd, 0, s, a, g);
-    else hipLaunchKernelGGL(conv_generic_kernel<16>, gd, bd, 0, s, a, g);
-    return ffk_check_launch("generic conv launch");
+    const int run = (d->cin == 3 || d->cin % 8 || ((uintptr_t)d->in & 15)) ? 0 : d->cin % 16 ? 8 : 16;
+    // The channel-run gathers address the int8 input with 32-bit offsets: a
+    // batch whose input or output tensor reaches 2 GiB runs as several
+    // launches over consecutive image ranges (images are independent).  The
+    // byte gather uses 64-bit addresses and takes the batch in one launch.
+    const long long px_out = (long long)g.hout * g.wout;
+    const long long in_img = (long long)d->hin * d->win * d->cin;
+    const long long img = std::max<long long>(in_img, px_out * d->cout);
+    const int slice = run == 0 ? d->batch : (int)std::min<long long>(d->batch, 0x7fffffffLL / img);
+    if (slice < 1) {
+        ffk_set_error("conv: one image's tensors reach 2 GiB%s%s", nullptr, nullptr);
+        return FFK_ERR_ARG;
+    }
+    const bool x_even = (d->flags & FFK_OUT_X_EVEN) != 0;
+    for (int b0 = 0; b0 < d->batch; b0 += slice) {
+        const int nb = std::min(slice, d->batch - b0);
+        ConvArgs as = a;
+        as.M = (int)((long long)nb * px_out);
+        const size_t o = (size_t)b0 * px_out * d->cout;
+        if (run) as.in = a.in + (size_t)b0 * in_img;
+        if (a.add_src) as.add_src = a.add_src + o;
+        if (a.out) as.out = a.out + (x_even ? o / 4 : o);     // even/even pixels: a quarter
+        if (a.out_bn) as.out_bn = a.out_bn + o;
+        if (a.out_i32) as.out_i32 = a.out_i32 + o;
+        g.in_bytes = run ? (unsigned)(nb * in_img) : 0u;
+        const long long grid = ff_conv_generic_grid(as.M, d->cin, d->cout);
+        if (grid > 0x7fffffffLL) {
+            ffk_set_error("conv: batch too large for the generic kernel%s%s", nullptr, nullptr);
+            return FFK_ERR_ARG;
+        }
+        const GenTile t = gen_tile(as.M, d->cin, d->cout);
+        const dim3 gd((unsigned)grid);
+        if (run == 0) launch_run<0>(t, gd, s, as, g);
+        else if (run == 8) launch_run<8>(t, gd, s, as, g);
+        else launch_run<16>(t, gd, s, as, g);
+        const int rc = ffk_check_launch("generic conv launch");
+        if (rc != FFK_OK) return rc;
+    }
+    return FFK_OK;
 }

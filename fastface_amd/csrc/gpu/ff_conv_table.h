@@ -341,7 +341,7 @@ const ConvEntry* ff_conv_table_c256(int* n);
 const ConvEntry* ff_conv_table_c512(int* n);
 // Any other conv geometry (ff_conv_generic.hip): one workgroup per 64x64
 // output tile; a.M holds the launch's output pixels.
-long long ff_conv_generic_grid(long long M, int cout);
+long long ff_conv_generic_grid(long long M, int cin, int cout);
 int ff_conv_generic_launch(const ConvArgs& a, const ffk_conv_desc* d, hipStream_t s);
 // FC head as an MFMA GEMM (ff_conv_fc.hip)
 constexpr int FC_SPLIT = 8;

@@ -1232,6 +1232,44 @@ def test_generic_conv_epilogue(gpu_lib, oracle, mode, case):
         assert np.array_equal(got_bn, exp_bn)
 
 
+GENERIC_WIDE_CASES = [  # batches large enough for 128-pixel tiles (at least 256 workgroups)
+    (96, 72, 3, 3, 1, 1, 28, 28, 48),     # 128x128 tiles, 16-byte channel runs, ragged channels
+    (40, 64, 3, 3, 1, 1, 28, 28, 48),     # 128x64 tiles, 8-byte channel runs
+]
+
+
+@pytest.mark.parametrize("case", range(len(GENERIC_WIDE_CASES)))
+def test_generic_conv_wide_tiles(gpu_lib, oracle, case):
+    """The generic kernel's 128-wide tiles: int32 accumulators and the fused
+    PReLU + residual + BN epilogue equal the oracle's."""
+    cin, cout, kh, kw, s, pad, H, W, B = GENERIC_WIDE_CASES[case]
+    assert _generic_variant(gpu_lib, cin, cout, kh, kw, s, pad, H, W, B) == b"generic"
+    r = rng(2150 + case)
+    x = r.integers(-128, 128, size=(B, H, W, cin), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, kh, kw), dtype=np.int8)
+    acc = oracle.conv_i32(x, w, s, pad)
+    assert np.array_equal(run_conv(gpu_lib, x, w, s, pad, raw=True), acc)
+    Ho, Wo = (H + 2 * pad - kh) // s + 1, (W + 2 * pad - kw) // s + 1
+    ws = r.uniform(1e-4, 1e-3, cout).astype(F32)
+    bias = r.normal(0, 0.1, cout).astype(F32)
+    inv = (1.0 / r.uniform(0.01, 0.05, cout)).astype(F32)
+    slope = r.uniform(0, 0.3, cout).astype(F32)
+    add = r.integers(-128, 128, size=(B, Ho, Wo, cout), dtype=np.int8)
+    adds = r.uniform(1e-3, 5e-2, cout).astype(F32)
+    bsin = r.uniform(1e-3, 5e-2, cout).astype(F32)
+    bns = r.uniform(0.5, 1.5, cout).astype(F32)
+    bno = r.normal(0, 0.05, cout).astype(F32)
+    binv = (1.0 / r.uniform(0.01, 0.1, cout)).astype(F32)
+    flags = fa.FFK_EPI_BIAS | fa.FFK_EPI_PRELU | fa.FFK_EPI_ADD | fa.FFK_EPI_BN
+    prm = params_block(cout, ws=ws, bias=bias, inv=inv, slope=slope, adds=adds, bn_sin=bsin, bn_s=bns, bn_o=bno,
+                       bn_inv=binv)
+    got_x, got_bn = run_conv(gpu_lib, x, w, s, pad, params=prm, flags=flags, add=add, want_bn=True)
+    exp_x = oracle.fused_epilogue(acc, ws=ws, bias=bias, inv_pc=inv, prelu=slope, add_src=add, add_scale_pc=adds)
+    assert np.array_equal(got_x, exp_x)
+    assert np.array_equal(got_bn, oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns, bn_offset=bno,
+                                                          inv_pc=binv))
+
+
 @pytest.mark.parametrize("rgb8", [False, True], ids=["fp32", "rgb8"])
 def test_generic_input_layer(gpu_lib, oracle, rgb8):
     """A 3-channel input layer without a tuned kernel (5x5 stride 2, 32

@@ -302,8 +302,10 @@ def test_noalloc_scratch_covers_every_workspace():
 
 def test_generic_geometries_are_runnable():
     """Geometries outside the tuned table run on the generic kernel (variant
-    "generic", one workgroup per 64x64 output tile, no workspace); invalid
-    geometries are refused before any launch."""
+    "generic", no workspace, one workgroup per output tile: 128 channels
+    wide above 64 output channels, 128 pixels high where that still gives
+    256 workgroups, except on the 3-channel input layer); invalid geometries
+    are refused before any launch."""
     lib = fa.load()
     d = fa.ffk_conv_desc()
 
@@ -316,9 +318,14 @@ def test_generic_geometries_are_runnable():
         assert lib.ffk_conv_runnable(*g) == 1 and lib.ffk_conv_supported(*g) == 0, g
         cin, cout, kh, kw, s, pad, H, W = g
         ho, wo = (H + 2 * pad - kh) // s + 1, (W + 2 * pad - kw) // s + 1
-        assert lib.ffk_conv_variant(desc(*g, 3)) == b"generic"
-        assert lib.ffk_conv_grid(desc(*g, 3)) == -(-3 * ho * wo // 64) * -(-cout // 64)
-        assert lib.ffk_conv_workspace_bytes(desc(*g, 3)) == 0
+        for B in (3, 64):
+            assert lib.ffk_conv_variant(desc(*g, B)) == b"generic"
+            M = B * ho * wo
+            bn = 128 if cout > 64 else 64
+            tn = -(-cout // bn)
+            bm = 128 if cin != 3 and -(-M // 128) * tn >= 256 else 64
+            assert lib.ffk_conv_grid(desc(*g, B)) == -(-M // bm) * tn, (g, B)
+            assert lib.ffk_conv_workspace_bytes(desc(*g, B)) == 0
     assert lib.ffk_conv_runnable(64, 64, 3, 3, 1, 1, 56, 56) == 1          # tuned
     for bad in [(0, 64, 3, 3, 1, 1, 8, 8), (64, 64, 3, 3, 0, 1, 8, 8), (64, 64, 3, 3, 1, -1, 8, 8),
                 (64, 64, 9, 9, 1, 0, 8, 8), (64, 64, 3, 3, 1, 1, 0, 8)]:

@@ -2083,11 +2083,17 @@ __global__ __launch_bounds__(STEM_NT, (STEM_WG_PER_CU * STEM_WAVES + 3) / 4) voi
             const int iw = pc - 1;
             const bool in = px < NPIX && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
             const size_t off = ((size_t)b * HW + ih * W + iw) * 3;
+            // global-space loads: as generic-address (flat) loads, which the
+            // compiler emits for a pointer read from the I/O descriptor, they
+            // would count against the LDS wait counter, and the patch reads
+            // of this tile would wait for the next tile's fetch
             if constexpr (RGB8) {
-                const uint8_t* src = (const uint8_t*)x + off;
+                const __attribute__((address_space(1))) uint8_t* src =
+                    (const __attribute__((address_space(1))) uint8_t*)x + off;
                 pq[j] = in ? (int)(src[0] | (src[1] << 8) | (src[2] << 16)) : -1;
             } else {
-                const float* src = (const float*)x + off;
+                const __attribute__((address_space(1))) float* src =
+                    (const __attribute__((address_space(1))) float*)x + off;
 #pragma unroll
                 for (int c = 0; c < 3; c++) pv[j][c] = in ? src[c] : 0.0f;
             }

@@ -1270,6 +1270,63 @@ def test_generic_conv_wide_tiles(gpu_lib, oracle, case):
                                                           inv_pc=binv))
 
 
+SLICE_CASES = [  # (kind, cin, cout, kh, kw, stride, pad, H, W): images per 2 GiB launch slice
+    ("tuned", 64, 64, 3, 3, 1, 1, 56, 56),          # 200,704 bytes per image: 10,699 per slice
+    ("generic", 16, 16, 1, 1, 1, 0, 512, 512),      # 4 MiB per image: 511 per slice
+]
+
+
+@pytest.mark.parametrize("case", SLICE_CASES, ids=[c[0] for c in SLICE_CASES])
+def test_conv_batch_slices_at_2gib(gpu_lib, oracle, case):
+    """A batch whose int8 tensors reach 2 GiB runs as several launches over
+    consecutive image ranges (32-bit buffer offsets): the images at both ends
+    and on both sides of the slice boundary, with a residual input and the BN
+    second output, equal the oracle's."""
+    kind, cin, cout, kh, kw, s, pad, H, W = case
+    Ho, Wo = (H + 2 * pad - kh) // s + 1, (W + 2 * pad - kw) // s + 1
+    img = max(H * W * cin, Ho * Wo * cout)
+    per = 0x7FFFFFFF // img                                # images per launch slice
+    B = per + 2
+    r = rng(2300 + cin)
+    block = r.integers(-128, 128, size=(4, H, W, cin), dtype=np.int8)
+    x = np.empty((B, H, W, cin), np.int8)
+    for i in range(0, B, 4):
+        x[i:i + 4] = block[:min(4, B - i)]
+    add = np.empty((B, Ho, Wo, cout), np.int8)
+    ablock = r.integers(-128, 128, size=(4, Ho, Wo, cout), dtype=np.int8)
+    for i in range(0, B, 4):
+        add[i:i + 4] = ablock[:min(4, B - i)]
+    picks = [0, per - 1, per, B - 1]
+    for i in picks[1:]:                                  # fresh content around the boundary
+        x[i] = r.integers(-128, 128, size=(H, W, cin), dtype=np.int8)
+        add[i] = r.integers(-128, 128, size=(Ho, Wo, cout), dtype=np.int8)
+    w = r.integers(-128, 128, size=(cout, cin, kh, kw), dtype=np.int8)
+    d = fa.ffk_conv_desc()
+    d.batch, d.cin, d.cout, d.kh, d.kw = B, cin, cout, kh, kw
+    d.stride, d.pad, d.hin, d.win = s, pad, H, W
+    assert (gpu_lib.ffk_conv_variant(C.byref(d)) == b"generic") == (kind == "generic")
+    ws = r.uniform(1e-4, 1e-3, cout).astype(F32)
+    bias = r.normal(0, 0.1, cout).astype(F32)
+    inv = (1.0 / r.uniform(0.01, 0.05, cout)).astype(F32)
+    slope = r.uniform(0, 0.3, cout).astype(F32)
+    adds = r.uniform(1e-3, 5e-2, cout).astype(F32)
+    bsin = r.uniform(1e-3, 5e-2, cout).astype(F32)
+    bns = r.uniform(0.5, 1.5, cout).astype(F32)
+    bno = r.normal(0, 0.05, cout).astype(F32)
+    binv = (1.0 / r.uniform(0.01, 0.1, cout)).astype(F32)
+    flags = fa.FFK_EPI_BIAS | fa.FFK_EPI_PRELU | fa.FFK_EPI_ADD | fa.FFK_EPI_BN
+    prm = params_block(cout, ws=ws, bias=bias, inv=inv, slope=slope, adds=adds, bn_sin=bsin, bn_s=bns, bn_o=bno,
+                       bn_inv=binv)
+    got_x, got_bn = run_conv(gpu_lib, x, w, s, pad, params=prm, flags=flags, add=add, want_bn=True, split=False)
+    xs = x[picks]
+    acc = oracle.conv_i32(xs, w, s, pad)
+    exp_x = oracle.fused_epilogue(acc, ws=ws, bias=bias, inv_pc=inv, prelu=slope, add_src=add[picks],
+                                  add_scale_pc=adds)
+    assert np.array_equal(got_x[picks], exp_x)
+    assert np.array_equal(got_bn[picks], oracle.bn_prelu_requant(exp_x, in_scale_pc=bsin, bn_scale=bns,
+                                                                 bn_offset=bno, inv_pc=binv))
+
+
 @pytest.mark.parametrize("rgb8", [False, True], ids=["fp32", "rgb8"])
 def test_generic_input_layer(gpu_lib, oracle, rgb8):
     """A 3-channel input layer without a tuned kernel (5x5 stride 2, 32

@@ -3,16 +3,17 @@
 // kernels/conv2d_nhwc.c:150-220): an implicit GEMM with the geometry in
 // registers instead of template parameters.
 //
-// 64- or 128-wide output tiles, four waves of 32x32x32 i8 MFMAs; the A
-// operand is gathered from the NHWC input in 16- or 8-byte channel runs
-// where the channel count allows, byte by byte otherwise (any
-// channel count, kernel size, stride and padding; the 3-channel input layer
-// quantizes fp32 faces or maps uint8 pixels on the fly), the B operand read
-// from the packed weights.  The epilogue is the general form of the tuned
-// kernels' per element (in-scale, ws, bias, residual, PReLU, round half away
-// with the x86 out-of-range case), then X, its even pixels only or BN(X)
-// through the channel's table.  No LDS reuse of the input patch: each tap's
-// run is read from L2 / HBM for every output pixel.
+// 64- or 128-wide output tiles, four waves of 32x32x32 i8 MFMAs.  Channel
+// counts that are multiples of 16 load the A operand (16-byte channel runs
+// of the NHWC input) and the B operand (packed weights) straight into a
+// double-buffered LDS ring (conv_generic_dma_kernel); other channel counts
+// stage it through registers, in 8-byte runs or byte by byte (any channel
+// count; the 3-channel input layer quantizes fp32 faces or maps uint8 pixels
+// on the fly).  The epilogue is the general form of the tuned kernels' per
+// element (in-scale, ws, bias, residual, PReLU, round half away with the x86
+// out-of-range case), then X, its even pixels only or BN(X) through the
+// channel's table.  No LDS reuse of the input patch: each tap's run is read
+// from L2 / HBM for every output pixel.
 #include "ff_conv_table.h"
 #include "ff_numerics.h"
 
@@ -118,6 +119,66 @@ __device__ __forceinline__ v4i gather_a(const ConvArgs& a, const GenGeom& g, __a
     }
 }
 
+// The general epilogue per element (the tuned kernels' general form: in-scale,
+// ws, bias, residual, PReLU, round half away with the x86 out-of-range
+// case), then X, its even pixels only or BN(X) through the channel's table,
+// stored straight from registers: lane owns column wc + 32j + lane%32 and 16
+// rows of each of the wave's MI x NJ blocks at tile (m0, n0).
+template <int MI, int NJ>
+__device__ __forceinline__ void gen_epilogue(const v16i (&acc)[MI][NJ], const ConvArgs& a, const GenGeom& g,
+                                             long long m0, int n0, int wr, int wc) {
+    const int lane = threadIdx.x & 63;
+    const int hw = g.hout * g.wout;
+    const int C = g.cout;
+    const float* P = a.params;
+    const bool raw = a.out_i32 != nullptr;
+    const bool x_even = (a.flags & FFK_OUT_X_EVEN) != 0;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int n = n0 + wc + j * 32 + (lane & 31);
+        if (n >= C) continue;
+        float ws = 0.0f, bias = 0.0f, inv = 0.0f, slope = 0.0f, adds = 0.0f;
+        if (!raw) {
+            ws = P[FFK_P_WS * C + n];
+            bias = P[FFK_P_BIAS * C + n];
+            inv = P[FFK_P_INV * C + n];
+            slope = P[FFK_P_SLOPE * C + n];
+            adds = P[FFK_P_ADDSCALE * C + n];
+        }
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const long long mm = m0 + wr + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+                if (mm >= a.M) continue;
+                const size_t o = (size_t)mm * C + n;
+                if (raw) {
+                    a.out_i32[o] = acc[i][j][e];
+                    continue;
+                }
+                float f = (float)acc[i][j][e];
+                if (a.flags & FFK_EPI_INSCALE) f = f * a.in_scale;
+                f = f * ws;
+                f = f + bias;
+                if (a.flags & FFK_EPI_ADD) f = ff::add_residual(f, (int32_t)a.add_src[o], adds);
+                if (a.flags & FFK_EPI_PRELU) f = ff::prelu(f, slope);
+                const int q = ff::requant_haz(f * inv);
+                if (a.out) {
+                    if (!x_even) {
+                        a.out[o] = (int8_t)q;
+                    } else {
+                        const int bb = (int)(mm / hw);
+                        const int rem = (int)(mm - (long long)bb * hw);
+                        const int oh = rem / g.wout, ow = rem - oh * g.wout;
+                        if (!((oh | ow) & 1))
+                            a.out[(((size_t)bb * (g.hout / 2) + (oh >> 1)) * (g.wout / 2) + (ow >> 1)) * C + n] = (int8_t)q;
+                    }
+                }
+                if (a.flags & FFK_EPI_BN) a.out_bn[o] = a.bn_lut[n * 256 + q + 128];
+            }
+    }
+}
+
 // BM x BN output tiles (64 or 128 each) of four waves in a 2 x 2 grid, each
 // wave MI x NJ 32x32 blocks; per 64-byte K step every thread stages 16 bytes
 // of BM/64 A rows (output pixels) and of BN/64 B rows (output channels) in
@@ -217,56 +278,123 @@ __global__ __launch_bounds__(256) void conv_generic_kernel(ConvArgs a, GenGeom g
         }
     }
 
-    // epilogue: lane owns column wc + 32j + lane%32 and 16 rows of each of
-    // the wave's blocks
-    const int C = g.cout;
-    const float* P = a.params;
-    const bool raw = a.out_i32 != nullptr;
-    const bool x_even = (a.flags & FFK_OUT_X_EVEN) != 0;
+    gen_epilogue<MI, NJ>(acc, a, g, m0, n0, wr, wc);
+}
+
+// Cin % 16 == 0 (16-byte channel runs): the same tiles with the operands
+// loaded straight into a GEN_NST-deep LDS ring (direct-to-LDS buffer loads:
+// no register staging, the loads of GEN_NST - 1 steps in flight; two stages,
+// 16-32 KB, leave room for four or five workgroups per CU, which measured
+// 15-25 % faster than three or four stages with fewer workgroups).  A stage is
+// BM + BN 64-byte rows in 256-byte lines of four rows, the 16-byte slot of
+// (row r, piece p) ((r%4)*4 + p) XOR (r/4 % 4), as in conv_dma_kernel: the
+// 16 rows a ds_read_b128 lane group reads land in 16 distinct slots.  A lane
+// fetches the same piece p of its rows at every step (the swizzle picks
+// which), so one K cursor per thread serves all its A rows; padding, rows
+// past the batch, k past K and channels past Cout read zeros through the
+// out-of-range offset.
+constexpr int GEN_NST = 2;
+
+template <int BM, int BN>
+__global__ __launch_bounds__(256, 2) void conv_generic_dma_kernel(ConvArgs a, GenGeom g) {
+    constexpr int MI = BM / 64, NJ = BN / 64;          // 32x32 blocks per wave (2 x 2 waves)
+    constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64, STAGE = A_BYTES + B_BYTES;
+    constexpr int A_LD = A_BYTES / (256 * 16), B_LD = B_BYTES / (256 * 16);
+    constexpr int LPS = A_LD + B_LD;                   // loads per thread and stage
+    static_assert((GEN_NST - 2) * LPS < 64, "vmcnt range");
+    __shared__ __align__(1024) int8_t smem[GEN_NST * STAGE];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int tiles_n = (g.cout + BN - 1) / BN;
+    const unsigned nb = gridDim.x, bid = blockIdx.x;
+    const unsigned t = (nb & 7) == 0 ? (bid & 7) * (nb >> 3) + (bid >> 3) : bid;
+    const long long m0 = (long long)(t / tiles_n) * BM;
+    const int n0 = (int)(t % tiles_n) * BN;
+    const int hw = g.hout * g.wout;
+    const int nsteps = g.kpad / 64;
+    const __amdgpu_buffer_rsrc_t r_in = ff_rsrc(a.in, g.in_bytes);
+    const __amdgpu_buffer_rsrc_t r_w = ff_rsrc(a.w, (unsigned)(nsteps * g.cout * 64));
+
+    // this thread's pieces: wave load j of wave w fills lines (4j + w)*4 ..
+    // +3 of a stage's A (B) rows; lane L takes line +L/16, slot L%16, which
+    // holds piece p = slot%4 XOR ... of row 4*line + slot/4
+    const int sl = (lane & 15) ^ ((lane >> 4) & 3);
+    const int p = sl & 3;
+    int a_base[A_LD], a_ih0[A_LD], a_iw0[A_LD];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int n = n0 + wc + j * 32 + (lane & 31);
-        if (n >= C) continue;
-        float ws = 0.0f, bias = 0.0f, inv = 0.0f, slope = 0.0f, adds = 0.0f;
-        if (!raw) {
-            ws = P[FFK_P_WS * C + n];
-            bias = P[FFK_P_BIAS * C + n];
-            inv = P[FFK_P_INV * C + n];
-            slope = P[FFK_P_SLOPE * C + n];
-            adds = P[FFK_P_ADDSCALE * C + n];
+    for (int j = 0; j < A_LD; j++) {
+        const int r = ((j * 4 + wave) * 4 + (lane >> 4)) * 4 + (sl >> 2);
+        const long long m = m0 + r;
+        a_base[j] = 0; a_iw0[j] = 0;
+        a_ih0[j] = -(1 << 28);                         // a row past the batch fails every bounds check
+        if (m < a.M) {
+            const int b = (int)(m / hw);
+            const int rem = (int)(m - (long long)b * hw);
+            const int oh = rem / g.wout;
+            a_ih0[j] = oh * g.stride - g.pad;
+            a_iw0[j] = (rem - oh * g.wout) * g.stride - g.pad;
+            a_base[j] = ((b * g.hin + a_ih0[j]) * g.win + a_iw0[j]) * g.cin;
         }
-#pragma unroll
-        for (int i = 0; i < MI; i++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const long long mm = m0 + wr + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-                if (mm >= a.M) continue;
-                const size_t o = (size_t)mm * C + n;
-                if (raw) {
-                    a.out_i32[o] = acc[i][j][e];
-                    continue;
-                }
-                float f = (float)acc[i][j][e];
-                if (a.flags & FFK_EPI_INSCALE) f = f * a.in_scale;
-                f = f * ws;
-                f = f + bias;
-                if (a.flags & FFK_EPI_ADD) f = ff::add_residual(f, (int32_t)a.add_src[o], adds);
-                if (a.flags & FFK_EPI_PRELU) f = ff::prelu(f, slope);
-                const int q = ff::requant_haz(f * inv);
-                if (a.out) {
-                    if (!x_even) {
-                        a.out[o] = (int8_t)q;
-                    } else {
-                        const int bb = (int)(mm / hw);
-                        const int rem = (int)(mm - (long long)bb * hw);
-                        const int oh = rem / g.wout, ow = rem - oh * g.wout;
-                        if (!((oh | ow) & 1))
-                            a.out[(((size_t)bb * (g.hout / 2) + (oh >> 1)) * (g.wout / 2) + (ow >> 1)) * C + n] = (int8_t)q;
-                    }
-                }
-                if (a.flags & FFK_EPI_BN) a.out_bn[o] = a.bn_lut[n * 256 + q + 128];
-            }
     }
+    unsigned b_off[B_LD];
+#pragma unroll
+    for (int j = 0; j < B_LD; j++) {
+        const int n = n0 + ((j * 4 + wave) * 4 + (lane >> 4)) * 4 + (sl >> 2);
+        b_off[j] = n < g.cout ? (unsigned)(n * 64 + p * 16) : FF_OOB;
+    }
+    KCursor cur = kcursor_at(g, p * 16);
+    auto issue = [&](int st, int buf) {
+        int8_t* sb = smem + buf * STAGE;
+        const bool kin = cur.k < g.ktot;
+#pragma unroll
+        for (int j = 0; j < A_LD; j++) {
+            const int ih = a_ih0[j] + cur.th, iw = a_iw0[j] + cur.tw;
+            const bool v = kin && ih >= 0 && ih < g.hin && iw >= 0 && iw < g.win;
+            bdma16(r_in, v ? (unsigned)(a_base[j] + cur.off) : FF_OOB, 0u, sb + (j * 4 + wave) * 1024);
+        }
+        const unsigned wst = (unsigned)(st * g.cout * 64);
+#pragma unroll
+        for (int j = 0; j < B_LD; j++)
+            bdma16(r_w, b_off[j] == FF_OOB ? FF_OOB : b_off[j] + wst, 0u, sb + A_BYTES + (j * 4 + wave) * 1024);
+        kcursor_step(cur, g, 64);
+    };
+
+    const int wm = wave >> 1, wn = wave & 1;
+    const int a_rd = dma_slot(wm * MI * 32 + (lane & 31), lane >> 5);
+    const int b_rd = A_BYTES + dma_slot(wn * NJ * 32 + (lane & 31), lane >> 5);
+    v16i acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+#pragma unroll
+    for (int u = 0; u < GEN_NST - 1; u++)
+        if (u < nsteps) issue(u, u);
+    int rbuf = 0;                                      // ring slot of step s
+    for (int st = 0; st < nsteps; st++) {
+        if (st + GEN_NST - 2 < nsteps) dma_wait_barrier<(GEN_NST - 2) * LPS>();
+        else dma_wait_barrier<0>();
+        if (st + GEN_NST - 1 < nsteps) issue(st + GEN_NST - 1, rbuf == 0 ? GEN_NST - 1 : rbuf - 1);
+        const int8_t* sb = smem + rbuf * STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            v4i af[MI], bf[NJ];
+#pragma unroll
+            for (int i = 0; i < MI; i++) af[i] = *reinterpret_cast<const v4i*>(sb + ((a_rd + i * 2048) ^ (ks * 32)));
+#pragma unroll
+            for (int j = 0; j < NJ; j++) bf[j] = *reinterpret_cast<const v4i*>(sb + ((b_rd + j * 2048) ^ (ks * 32)));
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        rbuf = rbuf == GEN_NST - 1 ? 0 : rbuf + 1;
+    }
+    gen_epilogue<MI, NJ>(acc, a, g, m0, n0, wm * (BM / 2), wn * (BN / 2));
 }
 
 // Tile shape of a launch: 128-wide in N above 64 output channels, 128-high
@@ -285,10 +413,17 @@ GenTile gen_tile(long long M, int cin, int cout) {
 template <int RUN>
 void launch_run(GenTile t, dim3 gd, hipStream_t s, const ConvArgs& a, const GenGeom& g) {
     const dim3 bd(256);
-    if (t.bm == 128 && t.bn == 128) hipLaunchKernelGGL((conv_generic_kernel<RUN, 128, 128>), gd, bd, 0, s, a, g);
-    else if (t.bm == 128) hipLaunchKernelGGL((conv_generic_kernel<RUN, 128, 64>), gd, bd, 0, s, a, g);
-    else if (t.bn == 128) hipLaunchKernelGGL((conv_generic_kernel<RUN, 64, 128>), gd, bd, 0, s, a, g);
-    else hipLaunchKernelGGL((conv_generic_kernel<RUN, 64, 64>), gd, bd, 0, s, a, g);
+    if constexpr (RUN == 16) {
+        if (t.bm == 128 && t.bn == 128) hipLaunchKernelGGL((conv_generic_dma_kernel<128, 128>), gd, bd, 0, s, a, g);
+        else if (t.bm == 128) hipLaunchKernelGGL((conv_generic_dma_kernel<128, 64>), gd, bd, 0, s, a, g);
+        else if (t.bn == 128) hipLaunchKernelGGL((conv_generic_dma_kernel<64, 128>), gd, bd, 0, s, a, g);
+        else hipLaunchKernelGGL((conv_generic_dma_kernel<64, 64>), gd, bd, 0, s, a, g);
+    } else {
+        if (t.bm == 128 && t.bn == 128) hipLaunchKernelGGL((conv_generic_kernel<RUN, 128, 128>), gd, bd, 0, s, a, g);
+        else if (t.bm == 128) hipLaunchKernelGGL((conv_generic_kernel<RUN, 128, 64>), gd, bd, 0, s, a, g);
+        else if (t.bn == 128) hipLaunchKernelGGL((conv_generic_kernel<RUN, 64, 128>), gd, bd, 0, s, a, g);
+        else hipLaunchKernelGGL((conv_generic_kernel<RUN, 64, 64>), gd, bd, 0, s, a, g);
+    }
 }
 
 }  // namespace

@@ -55,6 +55,13 @@
 #define FF_STAGE_BYTES ((size_t)FF_STAGE_MB << 20)
 /* a one-chunk host batch of at least this many bytes is staged too */
 #define FF_STAGE_MIN_BYTES ((size_t)8 << 20)
+/* Small host batches bounce through one pinned buffer instead (a DMA from
+ * pinned memory skips the runtime's own staging of pageable memory): the
+ * input up to FF_SMALL_IN bytes (one fp32 face, six uint8 faces), the
+ * embeddings up to FF_SMALL_OUT bytes (eight faces).  Measured at b=1: the
+ * 2 KB embedding 21.4 -> 11.9 us, the 147 KB face 14.7 -> 13.1 us. */
+#define FF_SMALL_IN ((size_t)256 << 10)
+#define FF_SMALL_OUT ((size_t)16 << 10)
 
 /* Batches of FF_SPLIT_MIN faces or more run as two halves, each on its own
  * stream inside the one captured graph (a fork and a join), both launched
@@ -113,6 +120,8 @@ struct FastFace {
     void* ev_fork, *ev_join;    /* (recorded only inside graph capture) */
     void* ev_chunk[FF_MAX_CHUNKS];
     void* h_stage[2];           /* pinned staging of streamed input pieces (on first use) */
+    void* h_small;              /* pinned bounce buffer of small host batches (on first use):
+                                   FF_SMALL_IN input bytes, then FF_SMALL_OUT output bytes */
     void* ev_stage[2];          /* the last DMA out of each staging buffer */
     Stager* stager;             /* its copy threads (on first use), or NULL */
     ffk_io io_cur[2];           /* what d_io holds now */
@@ -589,6 +598,7 @@ void fastface_destroy(FastFace* ff)
         if (ff->ev_stage[b]) ffk_event_destroy(ff->ev_stage[b]);
         if (ff->h_stage[b]) ffk_host_free(ff->h_stage[b]);
     }
+    if (ff->h_small) ffk_host_free(ff->h_small);
     if (ff->stream) ffk_stream_destroy(ff->stream);
     ff_plan_free(&ff->plan);
     ff_model_free(&ff->model);
@@ -751,6 +761,14 @@ static int stage_h2d(FastFace* ff, Stager* st, int8_t* d_in, const int8_t* in, s
     return 0;
 }
 
+/* the pinned bounce buffer of small host batches, NULL if it cannot be
+ * had (the copies then go from and to the caller's memory directly) */
+static int8_t* small_buffer(FastFace* ff)
+{
+    if (!ff->h_small) ff->h_small = ffk_host_alloc(FF_SMALL_IN + FF_SMALL_OUT);
+    return (int8_t*)ff->h_small;
+}
+
 static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, int batch, float* out)
 {
     /* a host call is synchronous: first let any device call still running
@@ -779,7 +797,16 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
             if (!rc) rc = ffk_stream_wait_event(ff->stream, ff->ev_chunk[0]);
             if (rc) ffk_stream_sync(ff->cstream);
         } else if (!rc) {
-            rc = ffk_memcpy_h2d(d_in, in, bytes, ff->stream);
+            int8_t* hs = bytes <= FF_SMALL_IN ? small_buffer(ff) : NULL;
+            /* (the stream is idle here after a completed call; the sync
+             * covers a call that failed with its copy still in flight) */
+            if (hs) rc = ffk_stream_sync(ff->stream);
+            if (!rc && hs) {
+                memcpy(hs, in, bytes);
+                rc = ffk_memcpy_h2d(d_in, hs, bytes, ff->stream);
+            } else if (!rc) {
+                rc = ffk_memcpy_h2d(d_in, in, bytes, ff->stream);
+            }
         }
         if (!rc) rc = enqueue(ff, batch, ff->stream, fmt);
     } else {
@@ -811,8 +838,11 @@ static int embed_host(FastFace* ff, const void* in, size_t face_bytes, int fmt, 
             memset(ff->io_cur, 0, sizeof ff->io_cur);
         }
     }
-    if (!rc) rc = ffk_memcpy_d2h(out, ff->d_output, out_bytes, ff->stream);
+    int8_t* ho = out_bytes <= FF_SMALL_OUT ? small_buffer(ff) : NULL;
+    if (ho) ho += FF_SMALL_IN;
+    if (!rc) rc = ffk_memcpy_d2h(ho ? (void*)ho : (void*)out, ff->d_output, out_bytes, ff->stream);
     if (!rc) rc = ffk_stream_sync(ff->stream);
+    if (!rc && ho) memcpy(out, ho, out_bytes);
     if (!rc) ff->last_stream = NULL;        /* all of it has finished */
     if (rc) { report("embed", rc); return -3; }
     return 0;

@@ -64,9 +64,9 @@ __device__ __forceinline__ void kcursor_step(KCursor& c, const GenGeom& g, int n
 }
 
 // The 16 A-operand bytes from cursor c on of the output pixel whose tap (0, 0)
-// is input pixel (ih0, iw0) at element offset base.
-// RUN 16: they are one tap's channel run (Cin % 16 == 0), one 16-byte load;
-// RUN 8: two taps' 8-byte runs (Cin % 8 == 0); both through the int8 input's
+// is input pixel (ih0, iw0) at element offset base (channel counts that are
+// multiples of 16 take conv_generic_dma_kernel instead).
+// RUN 8: two taps' 8-byte runs (Cin % 8 == 0) through the int8 input's
 // buffer resource r_in, where padding, rows past the batch and k past K take
 // the out-of-range offset and read zeros.  RUN 0: byte by byte (any Cin, and
 // the 3-channel input layer, which quantizes fp32 faces or maps uint8
@@ -74,21 +74,18 @@ __device__ __forceinline__ void kcursor_step(KCursor& c, const GenGeom& g, int n
 template <int RUN>
 __device__ __forceinline__ v4i gather_a(const ConvArgs& a, const GenGeom& g, __amdgpu_buffer_rsrc_t r_in,
                                         const void* x, bool mrow, long long base, int ih0, int iw0, KCursor c) {
-    if constexpr (RUN == 16 || RUN == 8) {
+    static_assert(RUN == 8 || RUN == 0, "16-byte runs: conv_generic_dma_kernel");
+    if constexpr (RUN == 8) {
         v4i v;
 #pragma unroll
-        for (int h = 0; h < 16 / RUN; h++) {
-            if (h) kcursor_step(c, g, RUN);
+        for (int h = 0; h < 2; h++) {
+            if (h) kcursor_step(c, g, 8);
             const int ih = ih0 + c.th, iw = iw0 + c.tw;
             const bool in = mrow && c.k < g.ktot && ih >= 0 && ih < g.hin && iw >= 0 && iw < g.win;
             const unsigned off = in ? (unsigned)(base + c.off) : FF_OOB;
-            if constexpr (RUN == 16) {
-                v = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r_in, off, 0, 0));
-            } else {
-                const auto u = __builtin_amdgcn_raw_buffer_load_b64(r_in, off, 0, 0);
-                v[2 * h] = (int)u[0];
-                v[2 * h + 1] = (int)u[1];
-            }
+            const auto u = __builtin_amdgcn_raw_buffer_load_b64(r_in, off, 0, 0);
+            v[2 * h] = (int)u[0];
+            v[2 * h + 1] = (int)u[1];
         }
         return v;
     } else {
@@ -179,7 +176,8 @@ __device__ __forceinline__ void gen_epilogue(const v16i (&acc)[MI][NJ], const Co
     }
 }
 
-// BM x BN output tiles (64 or 128 each) of four waves in a 2 x 2 grid, each
+// Channel counts that are not multiples of 16: BM x BN output tiles (64 or
+// 128 each) of four waves in a 2 x 2 grid, each
 // wave MI x NJ 32x32 blocks; per 64-byte K step every thread stages 16 bytes
 // of BM/64 A rows (output pixels) and of BN/64 B rows (output channels) in
 // LDS, then each wave runs 2 * MI * NJ 32x32x32 MFMAs; the next step's loads
